@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the uncertain-gpt layer-kernel set on one MI355X.
+
+Workload: one GPT-2-124M Bayesian step's layer-kernel path,
+fp32, L=12 H=12 C=768 V=50257 B=8 T=1024, on the reference's buffer layout:
+    bayes_materialize over n = 124,439,808 parameters (tied-head count)
+    -> the layer kernels of gpt2_forward (encoder, 25 LayerNorm, 24 residual,
+       12 GELU) -> the layer kernels of gpt2_backward (same, backward).
+The dense ops between them (GEMMs, attention) are not part of the path; their
+output buffers hold synthetic data. A "step" is that sequence, queued by the
+native step driver of libugk.so (ugk_gpt2_layers_forward/backward).
+
+Printed JSON line (the last line of stdout):
+    value        algorithmic bytes of the step / step time, GB/s
+    ms_per_step  layer-kernel milliseconds per step (median-free mean over --steps)
+    kernels      each kernel at its step shape, cold (a 1 GiB buffer is written
+                 between repetitions so the 256 MB MALL cannot serve it): median ms,
+                 GB/s from algorithmic bytes, fraction of 8 TB/s
+    roofline     the dominant kernel (most HBM bytes per step: GELU backward),
+                 achieved = algorithmic bytes per launch / mean launch time from
+                 HIP events on the stream it runs on
+    cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this
+                 repo's bit-identical restatement) on one host core, timed per op
+                 at the step shapes and composed by launch count
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "uncertain-gpt_amd"))
+
+METRIC = "achieved HBM GB/s (% of peak) per layer kernel fwd+bwd; layer-kernel ms/step"
+PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def step_bytes(B, T, C, L, n_mat):
+    """Algorithmic bytes: each fp32 input read once, each output written once, += = read+write."""
+    BT, N = B * T, B * T * C
+    per = {
+        "encoder_forward": 12 * N + 4 * BT,
+        "encoder_backward": 20 * N + 4 * BT,
+        "layernorm_forward": 8 * N + 8 * BT + 8 * C,
+        "layernorm_backward": 16 * N + 8 * BT + 20 * C,
+        "gelu_forward": 8 * 4 * N,
+        "gelu_backward": 16 * 4 * N,
+        "residual_forward": 12 * N,
+        "residual_backward": 20 * N,
+        "bayes_materialize": 16 * n_mat,
+    }
+    count = {"encoder_forward": 1, "encoder_backward": 1, "layernorm_forward": 2 * L + 1,
+             "layernorm_backward": 2 * L + 1, "gelu_forward": L, "gelu_backward": L,
+             "residual_forward": 2 * L, "residual_backward": 2 * L, "bayes_materialize": 1}
+    return per, count, sum(per[k] * count[k] for k in per)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=25, help="cold repetitions per kernel")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the layer kernels shard by rows with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ugk
+
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    B, T, C, V, NH, maxT, L = 8, 1024, 768, 50257, 12, 1024, 12
+    cfg = ugk.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=maxT, L=L)
+    P = ugk.param_count(cfg)
+    n_mat = P - (C * V + V)  # GPT-2-124M with the head tied to wte: 124,439,808
+    A = ugk.act_count(cfg)
+    per, count, total_bytes = step_bytes(B, T, C, L, n_mat)
+    log(f"bench: params {P} (materialize {n_mat}), acts {A}, algorithmic bytes/step {total_bytes / 1e9:.3f} GB")
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    mu = torch.randn(P, generator=g, device=dev) * 0.02
+    rho = torch.randn(P, generator=g, device=dev) * 0.1 - 5.0
+    eps = torch.randn(P, generator=g, device=dev)
+    w = torch.empty(P, device=dev)
+    acts = torch.randn(A, generator=g, device=dev)
+    grads = torch.zeros(P, device=dev)
+    grads_acts = torch.randn(A, generator=g, device=dev)
+    inputs = torch.randint(0, V, (B * T,), generator=g, device=dev, dtype=torch.int32)
+    flush = torch.empty(256 * 1024 * 1024, device=dev)  # 1 GiB, beyond L2 + MALL
+    torch.cuda.synchronize()
+    lib = ugk.lib
+    ugk.set_stream(None)  # the null stream: torch's default stream too, so its events bracket our kernels
+
+    def chk(rc):
+        if rc != 0:
+            raise ugk.UgkError(rc, lib.ugk_last_error().decode())
+
+    wp, mup, rhop, epsp = w.data_ptr(), mu.data_ptr(), rho.data_ptr(), eps.data_ptr()
+    ap_, gp, gap, ip = acts.data_ptr(), grads.data_ptr(), grads_acts.data_ptr(), inputs.data_ptr()
+
+    def step():
+        chk(lib.ugk_bayes_materialize(wp, mup, rhop, epsp, n_mat))
+        chk(lib.ugk_gpt2_layers_forward(ap_, wp, ip, cfg, None))
+        chk(lib.ugk_gpt2_layers_backward(gp, gap, ap_, wp, ip, cfg, None))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_step = e0.elapsed_time(e1) / args.steps
+    value = total_bytes / (ms_step * 1e-3) / 1e9
+    log(f"bench: step {ms_step:.4f} ms (host wall {wall:.4f} ms) -> {value:.1f} GB/s algorithmic")
+
+    # ---- each kernel alone at its step shape, cold ----------------------------
+    N = B * T * C
+    blk = lambda: torch.empty(N, device=dev)
+    x1, x2, x3, x4 = (torch.randn(N, generator=g, device=dev) for _ in range(4))
+    h1, h2, h3 = (torch.randn(4 * N, generator=g, device=dev) for _ in range(3))
+    lw, lb = torch.ones(C, device=dev), torch.zeros(C, device=dev)
+    mean, rstd = torch.empty(B * T, device=dev), torch.empty(B * T, device=dev)
+    dlw, dlb = torch.zeros(C, device=dev), torch.zeros(C, device=dev)
+    wte, wpe = mu[: V * C], mu[V * C: V * C + maxT * C]
+    dwte, dwpe = grads[: V * C], grads[V * C: V * C + maxT * C]
+    out = blk()
+    ugk.layernorm_forward(out, mean, rstd, x1, lw, lb, B, T, C)
+    launch = {
+        "encoder_forward": lambda: chk(lib.ugk_encoder_forward(out.data_ptr(), ip, wte.data_ptr(), wpe.data_ptr(), B, T, C)),
+        "encoder_backward": lambda: chk(lib.ugk_encoder_backward(dwte.data_ptr(), dwpe.data_ptr(), x1.data_ptr(), ip, B, T, C)),
+        "layernorm_forward": lambda: chk(lib.ugk_layernorm_forward(out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                                                                   x1.data_ptr(), lw.data_ptr(), lb.data_ptr(), B, T, C)),
+        "layernorm_backward": lambda: chk(lib.ugk_layernorm_backward(x2.data_ptr(), dlw.data_ptr(), dlb.data_ptr(),
+                                                                     x3.data_ptr(), x1.data_ptr(), lw.data_ptr(),
+                                                                     mean.data_ptr(), rstd.data_ptr(), B, T, C)),
+        "gelu_forward": lambda: chk(lib.ugk_gelu_forward(h2.data_ptr(), h1.data_ptr(), 4 * N)),
+        "gelu_backward": lambda: chk(lib.ugk_gelu_backward(h3.data_ptr(), h1.data_ptr(), h2.data_ptr(), 4 * N)),
+        "residual_forward": lambda: chk(lib.ugk_residual_forward(out.data_ptr(), x1.data_ptr(), x2.data_ptr(), N)),
+        "residual_backward": lambda: chk(lib.ugk_residual_backward(x3.data_ptr(), x4.data_ptr(), x1.data_ptr(), N)),
+        "bayes_materialize": lambda: chk(lib.ugk_bayes_materialize(wp, mup, rhop, epsp, n_mat)),
+    }
+    kernels = {}
+    for name, fn in launch.items():
+        fn()
+        times = []
+        for r in range(args.reps):
+            flush.fill_(float(r))
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            times.append(s.elapsed_time(e))
+        med = statistics.median(times)
+        gbs = per[name] / (med * 1e-3) / 1e9
+        kernels[name] = {"ms": round(med, 5), "p25_ms": round(statistics.quantiles(times, n=4)[0], 5),
+                         "p75_ms": round(statistics.quantiles(times, n=4)[2], 5), "GBps": round(gbs, 1),
+                         "frac": round(gbs / PEAK_GBS, 4), "bytes": per[name], "per_step": count[name]}
+        log(f"bench: {name:20s} {med * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak")
+
+    # ---- roofline of the dominant kernel: HIP events over back-to-back cold launches
+    dom = max(per, key=lambda k: per[k] * count[k])
+    ev = []
+    for r in range(args.steps):
+        flush.fill_(float(r))
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch[dom]()
+        e.record()
+        ev.append((s, e))
+    torch.cuda.synchronize()
+    dom_ms = statistics.mean(s.elapsed_time(e) for s, e in ev)
+    achieved = per[dom] / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "launch_ms": round(dom_ms, 5),
+                "bytes_per_launch": per[dom]}
+
+    cpu = None if args.no_cpu else cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes)
+
+    rec = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "BASELINE config 5: GPT-2-124M Bayesian step, layer-kernel path "
+                               "(materialize + encoder/LN/GELU/residual fwd+bwd)",
+                   "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
+                   "param_layout_n": P, "parallelism": "single GPU"},
+        "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
+    """Each CPU op once at the step shape (materialize on a 1/16 slice, scaled),
+    composed by launch count; single-threaded, like train_bnn.c."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, REF_SO
+    kind = "reference" if os.path.exists(REF_SO) else "port"
+    o = Oracle(reference=(kind == "reference"))
+    rng = np.random.Generator(np.random.Philox(key=7))
+    N = B * T * C
+    f = lambda n: rng.standard_normal(n, dtype=np.float32)
+    x, y, d = f(N), f(N), f(N)
+    h, hd = f(4 * N), f(4 * N)
+    wv, bv = np.ones(C, np.float32), np.zeros(C, np.float32)
+    mean, rstd = np.zeros(B * T, np.float32), np.zeros(B * T, np.float32)
+    out, out4 = np.zeros(N, np.float32), np.zeros(4 * N, np.float32)
+    inp = rng.integers(0, V, B * T, dtype=np.int32)
+    wte, wpe = f(V * C) * np.float32(0.02), f(T * C) * np.float32(0.01)
+    dwte, dwpe = np.zeros(V * C, np.float32), np.zeros(T * C, np.float32)
+    dwl, dbl = np.zeros(C, np.float32), np.zeros(C, np.float32)
+    ns = n_mat // 16
+    mu, rh, ep, wm = f(ns) * np.float32(0.02), f(ns) * np.float32(0.1) - np.float32(5), f(ns), np.zeros(ns, np.float32)
+    ops = {
+        "encoder_forward": (lambda: o.encoder_forward(out, inp, wte, wpe, B, T, C), 1),
+        "encoder_backward": (lambda: o.encoder_backward(dwte, dwpe, d, inp, B, T, C), 1),
+        "layernorm_forward": (lambda: o.layernorm_forward(out, mean, rstd, x, wv, bv, B, T, C), 1),
+        "layernorm_backward": (lambda: o.layernorm_backward(y, dwl, dbl, d, x, wv, mean, rstd, B, T, C), 1),
+        "gelu_forward": (lambda: o.gelu_forward(out4, h, 4 * N), 1),
+        "gelu_backward": (lambda: o.gelu_backward(hd, h, out4, 4 * N), 1),
+        "residual_forward": (lambda: o.residual_forward(out, x, y, N), 1),
+        "residual_backward": (lambda: o.residual_backward(y, out, d, N), 1),
+        "bayes_materialize": (lambda: o.bayes_materialize(wm, mu, rh, ep, ns), n_mat / ns),
+    }
+    t_op, t_sample = {}, 0.0
+    for name, (fn, scale) in ops.items():
+        best = None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            fn()
+            dt = time.perf_counter() - t0
+            t_sample += dt
+            best = dt if best is None else min(best, dt)
+        t_op[name] = best * scale
+    step_s = sum(t_op[k] * count[k] for k in t_op)
+    gbs = total_bytes / step_s / 1e9
+    log(f"bench: cpu ({kind}, 1 core) step {step_s * 1e3:.1f} ms -> {gbs:.2f} GB/s; sample {t_sample:.1f} s")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": kind, "ms_per_step": round(step_s * 1e3, 1),
+            "per_op_ms": {k: round(v * 1e3, 2) for k, v in t_op.items()},
+            "sample": "each train_bnn.c op once per rep (best of 2) at the config-5 step shape "
+                      "(materialize on a 1/16 slice, scaled), summed by launch count per step; "
+                      f"{t_sample:.1f} s of CPU work"}
+
+
+if __name__ == "__main__":
+    main()

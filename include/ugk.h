@@ -1,0 +1,170 @@
+/*
+ * ugk.h - C-ABI of libugk.so, the MI355X (gfx950) layer-kernel set of
+ * uncertain-gpt: LayerNorm, GELU, residual, encoder and bayes_materialize.
+ *
+ * Every entry point keeps the parameter list and parameter order of the CPU
+ * op it replaces in the reference oracle train_bnn.c, so a caller swaps
+ *     layernorm_forward(out, mean, rstd, inp, w, b, B, T, C);
+ * for
+ *     UGK_CHECK(ugk_layernorm_forward(out, mean, rstd, inp, w, b, B, T, C));
+ * The differences are:
+ *   - all pointers are DEVICE pointers (hipMalloc / torch device memory);
+ *   - each call returns an int status (UGK_OK = 0) instead of void; the text
+ *     of the last failure on the calling thread is ugk_last_error();
+ *   - work is queued on the library's stream (ugk_set_stream, default the
+ *     null stream, which is also what the reference's <<<>>> launches use),
+ *     and a call returns before the GPU has finished.
+ * Semantics are the reference's: backward outputs ACCUMULATE (+=) into the
+ * caller's buffers, and the caller zeroes them when it wants plain gradients.
+ * Results: encoder fwd/bwd, residual fwd/bwd, GELU fwd/bwd and
+ * bayes_materialize are bit-identical to train_bnn.c on a host with glibc 2.35
+ * and FMA; LayerNorm row statistics and dinp are within fp32 rounding of it,
+ * and LayerNorm dweight/dbias are reduced in a fixed, run-to-run deterministic
+ * order.
+ *
+ * The library never allocates inside a kernel. It owns one scratch buffer per
+ * device (LayerNorm-backward partial sums, the encoder-backward bucket table),
+ * allocated on the first call that needs it and grown only when a larger
+ * shape arrives; ugk_reserve() allocates it up front.
+ */
+#ifndef UGK_H
+#define UGK_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UGK_OK 0
+#define UGK_EINVAL 1  /* invalid argument: NULL pointer, negative size, ... */
+#define UGK_EHIP 2    /* the HIP runtime reported an error */
+#define UGK_ENOMEM 3  /* scratch allocation failed */
+
+/* train_bnn.c:41-65 / gpt2_kernels.cuh:245-252 (k_encoder_forward).
+ * out[b,t,:] = wte[inp[b,t],:] + wpe[t,:].  0 <= inp[i] < V is the caller's
+ * contract, as in the reference. */
+int ugk_encoder_forward(float *out, const int *inp, const float *wte,
+                        const float *wpe, int B, int T, int C);
+
+/* train_bnn.c:647-662 / gpt2_kernels.cuh:254-263 (k_encoder_backward).
+ * dwte[inp[b,t],:] += dout[b,t,:];  dwpe[t,:] += dout[b,t,:].
+ * Each row's contributions are added in ascending (b,t) order, the order of
+ * the CPU loop, so the result is deterministic and bit-identical to it. Rows
+ * with a negative token are skipped. */
+int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout,
+                         const int *inp, int B, int T, int C);
+
+/* train_bnn.c:81-115 / gpt2_kernels.cuh:265-288 (k_layernorm_forward).
+ * eps = 1e-5; writes out (B,T,C), mean (B,T), rstd (B,T). */
+int ugk_layernorm_forward(float *out, float *mean, float *rstd,
+                          const float *inp, const float *weight,
+                          const float *bias, int B, int T, int C);
+
+/* train_bnn.c:439-477 / gpt2_kernels.cuh:290-316 (k_layernorm_backward).
+ * dinp += ..., dweight += sum_rows dout*xhat, dbias += sum_rows dout. */
+int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias,
+                           const float *dout, const float *inp,
+                           const float *weight, const float *mean,
+                           const float *rstd, int B, int T, int C);
+
+/* train_bnn.c:163-170 / gpt2_kernels.cuh:318-325 (k_gelu_forward). */
+int ugk_gelu_forward(float *out, const float *inp, int N);
+
+/* train_bnn.c:520-533 / gpt2_kernels.cuh:327-338 (k_gelu_backward).
+ * dinp += gelu'(inp) * dout. */
+int ugk_gelu_backward(float *dinp, const float *inp, const float *dout, int N);
+
+/* train_bnn.c:182-186 / gpt2_kernels.cuh:340-344 (k_residual_forward). */
+int ugk_residual_forward(float *out, const float *x, const float *y, int N);
+
+/* train_bnn.c:491-496 / gpt2_kernels.cuh:346-350 (k_residual_backward).
+ * dx += dout; dy += dout. */
+int ugk_residual_backward(float *dx, float *dy, const float *dout, int N);
+
+/* train_bnn.c:831-835 with softplus :814-816 / dev/bayes_materialize.cu:64-75.
+ * w = mu + softplus(rho) * eps, eps given. */
+int ugk_bayes_materialize(float *w, const float *mu, const float *rho,
+                          const float *eps, size_t n);
+
+/* ---- library control (no counterpart in the reference: its kernels run on
+ * the CUDA legacy default stream and abort on error, gpt2_kernels.cuh:88-101) */
+
+/* Text of the last failure on this thread ("" if none). */
+const char *ugk_last_error(void);
+/* Stream for subsequent calls from any thread (a hipStream_t; NULL = the
+ * null stream). */
+int ugk_set_stream(void *stream);
+void *ugk_get_stream(void);
+/* Allocate the current device's scratch for shapes up to (rows = B*T, C)
+ * now instead of on first use. */
+int ugk_reserve(int rows, int C);
+/* Bytes of scratch currently held on the current device. */
+size_t ugk_scratch_bytes(void);
+/* Wait for all work queued on the library's stream. */
+int ugk_synchronize(void);
+/* Library version, major*10000 + minor*100 + patch. */
+int ugk_version(void);
+
+/* ---- GPT-2 layer-kernel step driver ------------------------------------
+ * gpt2_kernels.cuh:634-719 (Config, param_offsets, act_offsets) and the
+ * launch sequence of gpt2_forward / gpt2_backward (:756-896), restricted to
+ * this library's kernels. The dense ops between them (QKV / proj / fc / fc2
+ * GEMMs and attention) are the caller's: pass them as callbacks in
+ * ugk_dense_ops, or pass NULL to run the layer kernels alone over whatever
+ * those ops' output buffers already hold (what the benchmark does). Buffers
+ * use the reference's flat layout, so the same params/acts/grads pointers
+ * the reference allocates work unchanged. */
+typedef struct {
+  int B, T, C, V, NH, maxT, L;
+} ugk_config;
+
+typedef struct {
+  void *ctx;
+  /* out (M,OC) = inp (M,C) @ weight (C,OC) + bias */
+  int (*matmul_forward)(void *ctx, float *out, const float *inp,
+                        const float *weight, const float *bias, int M, int C,
+                        int OC);
+  /* dinp += dout @ weight^T; dweight += inp^T @ dout; dbias += colsum(dout) */
+  int (*matmul_backward)(void *ctx, float *dinp, float *dweight, float *dbias,
+                         const float *inp, const float *weight,
+                         const float *dout, int M, int C, int OC);
+  int (*attention_forward)(void *ctx, float *out, const float *qkv, int B,
+                           int T, int C, int NH);
+  int (*attention_backward)(void *ctx, float *dqkv, const float *dout,
+                            const float *qkv, int B, int T, int C, int NH);
+} ugk_dense_ops;
+
+/* Float counts of the reference's parameter and activation buffers. */
+size_t ugk_param_count(ugk_config cfg);
+size_t ugk_act_count(ugk_config cfg);
+
+/* Forward from the encoder to the final LayerNorm (gpt2_kernels.cuh:775-813).
+ * The head GEMM and softmax/cross-entropy are not part of it. */
+int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
+                            ugk_config cfg, const ugk_dense_ops *ops);
+
+/* Backward from the final LayerNorm down to the encoder
+ * (gpt2_kernels.cuh:846-894). On entry grads_acts holds d(final LN output)
+ * at the reference's flo offset; accumulates into grads and grads_acts. */
+int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
+                             const float *params, const int *inputs,
+                             ugk_config cfg, const ugk_dense_ops *ops);
+
+#ifdef __cplusplus
+}
+#endif
+
+/* Abort-on-error wrapper with the reference's UNCERTAIN_ABORT behaviour
+ * (gpt2_kernels.cuh:88-101): print file:line and the message, then exit. */
+#define UGK_CHECK(call)                                                      \
+  do {                                                                       \
+    int ugk_status_ = (call);                                                \
+    if (ugk_status_ != UGK_OK) {                                             \
+      fprintf(stderr, "[UGK ERROR] at %s:%d\n%s\n", __FILE__, __LINE__,      \
+              ugk_last_error());                                             \
+      exit(EXIT_FAILURE);                                                    \
+    }                                                                        \
+  } while (0)
+
+#endif /* UGK_H */

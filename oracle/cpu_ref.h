@@ -1,0 +1,40 @@
+/* cpu_ref.h - CPU oracle (test infrastructure only; see cpu_ref.c). */
+#ifndef UGK_ORACLE_CPU_REF_H
+#define UGK_ORACLE_CPU_REF_H
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void oracle_encoder_forward(float *out, const int *inp, const float *wte,
+                            const float *wpe, int B, int T, int C);
+void oracle_encoder_backward(float *dwte, float *dwpe, const float *dout,
+                             const int *inp, int B, int T, int C);
+void oracle_layernorm_forward(float *out, float *mean, float *rstd,
+                              const float *inp, const float *weight,
+                              const float *bias, int B, int T, int C);
+void oracle_layernorm_backward(float *dinp, float *dweight, float *dbias,
+                               const float *dout, const float *inp,
+                               const float *weight, const float *mean,
+                               const float *rstd, int B, int T, int C);
+void oracle_gelu_forward(float *out, const float *inp, int N);
+void oracle_gelu_backward(float *dinp, const float *inp, const float *dout, int N);
+void oracle_residual_forward(float *out, const float *x, const float *y, int N);
+void oracle_residual_backward(float *dx, float *dy, const float *dout, int N);
+float oracle_softplus(float x);
+void oracle_bayes_materialize(float *w, const float *mu, const float *rho,
+                              const float *eps, size_t n);
+
+void oracle_expf_n(float *y, const float *x, size_t n);
+void oracle_log1pf_n(float *y, const float *x, size_t n);
+void oracle_tanhf_n(float *y, const float *x, size_t n);
+void oracle_softplus_n(float *y, const float *x, size_t n);
+void oracle_float_range(float *x, unsigned lo, size_t n);
+size_t oracle_count_bit_mismatch(const float *a, const float *b, size_t n,
+                                 size_t *first);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,458 @@
+"""GPU parity: every kernel of libugk.so, called through the C-ABI (ugk binding),
+against the CPU oracle on the same seeded inputs.
+
+Bars (from the benchmark contract):
+  * bit-exact: encoder fwd/bwd, residual fwd/bwd, GELU fwd/bwd, bayes_materialize;
+  * LayerNorm out/mean/rstd/dinp: |gpu - cpu| <= 1e-6 + 1e-5 |cpu| (the literal bar);
+  * LayerNorm dweight/dbias (column sums over all rows, whose fp32 value depends
+    on the summation order): deterministic run to run, within 1e-5 of the
+    computation's scale (sum of |terms|), at least as close to a float64
+    recomputation as the CPU's own serial sum, and the literal bar where the
+    CPU's rounding error allows it (reported).
+"""
+import numpy as np
+import pytest
+import torch
+
+import gen
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    same = (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+    return bool(same.all())
+
+
+def assert_bits(gpu_arr, cpu_arr, what):
+    if not bits_equal(gpu_arr, cpu_arr):
+        g = np.ascontiguousarray(gpu_arr, np.float32).ravel()
+        c = np.ascontiguousarray(cpu_arr, np.float32).ravel()
+        bad = np.nonzero((g.view(np.uint32) != c.view(np.uint32)) & ~(np.isnan(g) & np.isnan(c)))[0]
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {g.size} differ; first at {i}: gpu {g[i]!r} cpu {c[i]!r}")
+
+
+def assert_close(g, c, what, rtol=1e-5, atol=1e-6):
+    g = np.asarray(g, np.float64)
+    c = np.asarray(c, np.float64)
+    err = np.abs(g - c)
+    lim = atol + rtol * np.abs(c)
+    if not (err <= lim).all():
+        i = int(np.argmax(err - lim))
+        raise AssertionError(f"{what}: {(err > lim).sum()} of {err.size} beyond {rtol}/{atol}; "
+                             f"worst at {i}: gpu {g.flat[i]!r} cpu {c.flat[i]!r}")
+
+
+# ---- residual -------------------------------------------------------------------
+
+@pytest.mark.parametrize("N", [1, 3, 4, 5, 1000, 98304, (1 << 20) + 3])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_residual(gpu, oracle, N, offset):
+    g = gen.rng(N + offset)
+    x, y, dout = gen.normal(g, (N,)), gen.normal(g, (N,)), gen.normal(g, (N,))
+    dx0, dy0 = gen.normal(g, (N,)), gen.normal(g, (N,))
+    # offset=1 places every buffer 4 bytes past a 16-byte boundary (scalar path)
+    big = lambda a: dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
+    tx, ty, tout, tdo, tdx, tdy = big(x), big(y), big(np.zeros(N, np.float32)), big(dout), big(dx0), big(dy0)
+    gpu.residual_forward(tout, tx, ty, N)
+    gpu.residual_backward(tdx, tdy, tdo, N)
+    out = np.zeros(N, np.float32)
+    oracle.residual_forward(out, x, y, N)
+    dx, dy = dx0.copy(), dy0.copy()
+    oracle.residual_backward(dx, dy, dout, N)
+    assert_bits(host(tout), out, "residual_forward")
+    assert_bits(host(tdx), dx, "residual_backward dx")
+    assert_bits(host(tdy), dy, "residual_backward dy")
+
+
+def test_residual_backward_aliased(gpu, oracle):
+    """dx and dy the same buffer: the CPU loop adds dout twice."""
+    N = 4099
+    g = gen.rng(77)
+    d0, dout = gen.normal(g, (N,)), gen.normal(g, (N,))
+    t = dev(d0)
+    gpu.residual_backward(t, t, dev(dout), N)
+    d = d0.copy()
+    oracle.residual_backward(d, d, dout, N)
+    assert_bits(host(t), d, "aliased residual_backward")
+
+
+# ---- GELU -------------------------------------------------------------------------
+
+def gelu_pair(gpu, oracle, x, seed):
+    N = x.size
+    g = gen.rng(seed)
+    dout, dinp0 = gen.normal(g, (N,)), gen.normal(g, (N,))
+    tx, tout, tdi = dev(x), torch.empty(N, device=DEV), dev(dinp0)
+    gpu.gelu_forward(tout, tx, N)
+    gpu.gelu_backward(tdi, tx, dev(dout), N)
+    out = np.zeros(N, np.float32)
+    oracle.gelu_forward(out, x, N)
+    dinp = dinp0.copy()
+    oracle.gelu_backward(dinp, x, dout, N)
+    assert_bits(host(tout), out, "gelu_forward")
+    assert_bits(host(tdi), dinp, "gelu_backward")
+
+
+@pytest.mark.parametrize("N", [1, 7, 393216, 1000003])
+def test_gelu_normal(gpu, oracle, N):
+    x = gen.normal(gen.rng(N), (N,), 0, 2.0)
+    gelu_pair(gpu, oracle, x, N + 1)
+
+
+def test_gelu_special_and_sweeps(gpu, oracle):
+    """Every 257th float bit pattern, plus every 7th pattern with 0.25 <= |x| <= 10."""
+    strided = (np.arange(0, 1 << 32, 257, dtype=np.uint64).astype(np.uint32)).view(np.float32)
+    dense = np.arange(0x3E800000, 0x41200000, 7, dtype=np.uint32).view(np.float32)
+    x = np.concatenate([gen.special_floats(), strided, dense, -dense]).astype(np.float32)
+    gelu_pair(gpu, oracle, x, 5)
+
+
+# ---- bayes_materialize ------------------------------------------------------------
+
+def materialize_check(gpu, oracle, mu, rho, eps, what):
+    n = rho.size
+    tw = torch.empty(n, device=DEV)
+    gpu.bayes_materialize(tw, dev(mu), dev(rho), dev(eps), n)
+    w = np.zeros(n, np.float32)
+    oracle.bayes_materialize(w, mu, rho, eps, n)
+    assert_bits(host(tw), w, what)
+
+
+@pytest.mark.parametrize("n", [1, 5, 65536 + 3, 11_061_531])
+def test_materialize(gpu, oracle, n):
+    g = gen.rng(n)
+    materialize_check(gpu, oracle, gen.normal(g, (n,), 0, 0.02), gen.normal(g, (n,), -5, 0.1),
+                      gen.normal(g, (n,)), f"materialize n={n}")
+
+
+def test_materialize_softplus_sweeps(gpu, oracle):
+    """mu = 0, eps = 1, so w = softplus(rho): every 61st float pattern, and every
+    pattern in [-8, -2] (the rho the benchmark draws)."""
+    strided = (np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)).view(np.float32)
+    dense = np.arange(0xC0000000, 0xC1000000 + 1, dtype=np.uint32).view(np.float32)
+    rho = np.concatenate([gen.special_floats(), strided, dense]).astype(np.float32)
+    n = rho.size
+    materialize_check(gpu, oracle, np.zeros(n, np.float32), rho, np.ones(n, np.float32), "softplus sweep")
+
+
+def test_materialize_special_cases(gpu, oracle):
+    sp = gen.special_floats()
+    n = sp.size
+    g = gen.rng(3)
+    mu = gen.normal(g, (n,))
+    materialize_check(gpu, oracle, mu, sp, np.zeros(n, np.float32), "eps=0")
+    materialize_check(gpu, oracle, mu, sp, gen.normal(g, (n,)), "special rho")
+
+
+# ---- LayerNorm ------------------------------------------------------------------------
+
+def ln_case(gpu, oracle, B, T, C, seed, offset=0, reps=1):
+    g = gen.rng(seed)
+    x = gen.normal(g, (B, T, C))
+    w, b = gen.normal(g, (C,), 1, 0.1), gen.normal(g, (C,), 0, 0.1)
+    dout = gen.normal(g, (B, T, C))
+    dinp0, dw0, db0 = gen.normal(g, (B, T, C)), gen.normal(g, (C,)), gen.normal(g, (C,))
+    n = B * T * C
+
+    def put(a):
+        flat = np.concatenate([np.zeros(offset, np.float32), a.ravel()])
+        return dev(flat)[offset:]
+
+    tx, tw, tb, tdo = put(x), put(w), put(b), put(dout)
+    tout, tm, tr = put(np.zeros(n, np.float32)), put(np.zeros(B * T, np.float32)), put(np.zeros(B * T, np.float32))
+    gpu.layernorm_forward(tout, tm, tr, tx, tw, tb, B, T, C)
+    results = []
+    for _ in range(reps):
+        tdi, tdw, tdb = put(dinp0), put(dw0), put(db0)
+        gpu.layernorm_backward(tdi, tdw, tdb, tdo, tx, tw, tm, tr, B, T, C)
+        results.append((host(tdi), host(tdw), host(tdb)))
+    out = np.zeros_like(x)
+    mean, rstd = np.zeros((B, T), np.float32), np.zeros((B, T), np.float32)
+    oracle.layernorm_forward(out, mean, rstd, x, w, b, B, T, C)
+    # backward on the CPU from the GPU's saved statistics (the step passes them on)
+    gm, gr = host(tm).reshape(B, T), host(tr).reshape(B, T)
+    dinp, dw, db = dinp0.copy(), dw0.copy(), db0.copy()
+    oracle.layernorm_backward(dinp, dw, db, dout, x, w, gm, gr, B, T, C)
+    assert_close(host(tout).reshape(B, T, C), out, "ln out")
+    assert_close(gm, mean, "ln mean")
+    assert_close(gr, rstd, "ln rstd")
+    gdi, gdw, gdb = results[0]
+    assert_close(gdi.reshape(B, T, C), dinp, "ln dinp")
+    for r in results[1:]:
+        assert all(bits_equal(a, b) for a, b in zip(r, results[0])), "LN backward not deterministic"
+    # column sums: scale-aware bar and float64 accuracy
+    xhat = (x.astype(np.float64) - gm[..., None]) * gr[..., None]
+    terms_b = dout.astype(np.float64).reshape(-1, C)
+    terms_w = (dout.astype(np.float64) * xhat).reshape(-1, C)
+    literal = {}
+    for name, got, cpu, init, terms in (("dbias", gdb, db, db0, terms_b), ("dweight", gdw, dw, dw0, terms_w)):
+        f64 = init.astype(np.float64) + terms.sum(0)
+        scale = np.abs(init) + np.abs(terms).sum(0)
+        e_gpu, e_cpu = np.abs(got - f64), np.abs(cpu - f64)
+        assert (np.abs(got - cpu) <= 1e-5 * scale).all(), f"{name}: beyond the scale-aware bar"
+        assert e_gpu.max() <= e_cpu.max() + 1e-6 * scale.max(), f"{name}: less accurate than the CPU sum"
+        literal[name] = float(((np.abs(got - cpu) <= 1e-6 + 1e-5 * np.abs(cpu))).mean())
+    return literal
+
+
+@pytest.mark.parametrize("B,T,C", [(4, 64, 384), (1, 3, 768), (2, 5, 16), (1, 2, 2048), (1, 4, 13),
+                                   (1, 2, 3000), (3, 7, 4)])
+def test_layernorm(gpu, oracle, B, T, C):
+    literal = ln_case(gpu, oracle, B, T, C, seed=B * 1000 + T * 10 + C, reps=2)
+    print(f"literal-bar pass fraction for the column sums: {literal}")
+
+
+def test_layernorm_misaligned(gpu, oracle):
+    ln_case(gpu, oracle, 2, 8, 384, seed=9, offset=1)
+
+
+# ---- encoder ------------------------------------------------------------------------
+
+def enc_case(gpu, oracle, B, T, C, V, inp, seed, reps=1):
+    g = gen.rng(seed)
+    wte, wpe = gen.normal(g, (V, C), 0, 0.02), gen.normal(g, (T, C), 0, 0.01)
+    dout = gen.normal(g, (B, T, C))
+    dwte0, dwpe0 = gen.normal(g, (V, C)), gen.normal(g, (T, C))
+    tinp = dev(inp)
+    tout = torch.empty(B * T * C, device=DEV)
+    gpu.encoder_forward(tout, tinp, dev(wte), dev(wpe), B, T, C)
+    out = np.zeros((B, T, C), np.float32)
+    oracle.encoder_forward(out, inp, wte, wpe, B, T, C)
+    assert_bits(host(tout).reshape(B, T, C), out, "encoder_forward")
+    dwte, dwpe = dwte0.copy(), dwpe0.copy()
+    oracle.encoder_backward(dwte, dwpe, dout, inp, B, T, C)
+    tdo = dev(dout)
+    for r in range(reps):
+        tdwte, tdwpe = dev(dwte0), dev(dwpe0)
+        gpu.encoder_backward(tdwte, tdwpe, tdo, tinp, B, T, C)
+        assert_bits(host(tdwte), dwte, f"encoder_backward dwte (rep {r})")
+        assert_bits(host(tdwpe), dwpe, f"encoder_backward dwpe (rep {r})")
+
+
+def test_encoder_repeated_token_case(gpu, oracle):
+    enc_case(gpu, oracle, 2, 3, 4, 7, np.array([5, 2, 5, 0, 5, 6], np.int32), 1)
+
+
+@pytest.mark.parametrize("B,T,C,V", [(4, 64, 384, 27), (1, 1, 4, 3), (3, 5, 13, 11), (2, 33, 768, 100)])
+def test_encoder_uniform(gpu, oracle, B, T, C, V):
+    enc_case(gpu, oracle, B, T, C, V, gen.tokens_uniform(gen.rng(V), B * T, V), C, reps=2)
+
+
+def test_encoder_one_token(gpu, oracle):
+    """Every row is the same token: one bucket of B*T rows (the longest serial chain)."""
+    B, T, C, V = 4, 256, 128, 9
+    enc_case(gpu, oracle, B, T, C, V, np.full(B * T, 3, np.int32), 2)
+
+
+def test_encoder_zipf_cfg4_shape(gpu, oracle):
+    B, T, C, V = 16, 1024, 768, 50257
+    enc_case(gpu, oracle, B, T, C, V, gen.tokens_zipf(gen.rng(11), B * T, V), 3, reps=2)
+
+
+def test_encoder_uniform_cfg4_shape(gpu, oracle):
+    B, T, C, V = 16, 1024, 768, 50257
+    enc_case(gpu, oracle, B, T, C, V, gen.tokens_uniform(gen.rng(12), B * T, V), 4)
+
+
+def test_encoder_multi_chunk(gpu, oracle):
+    """More than 65,536 rows: buckets are built chunk by chunk, order must hold across chunks."""
+    B, T, C, V = 70, 1024, 8, 50
+    enc_case(gpu, oracle, B, T, C, V, gen.tokens_zipf(gen.rng(13), B * T, V), 5)
+
+
+# ---- golden fixtures ----------------------------------------------------------------------
+
+def test_golden_fixtures(gpu):
+    import os
+    gd = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    ld = lambda n: dict(np.load(os.path.join(gd, n + ".npz"), allow_pickle=False))
+    d = ld("encoder")
+    B, T, C = int(d["B"]), int(d["T"]), int(d["C"])
+    t = torch.empty(B * T * C, device=DEV)
+    gpu.encoder_forward(t, dev(d["inp"]), dev(d["wte"]), dev(d["wpe"]), B, T, C)
+    assert_bits(host(t).reshape(d["out"].shape), d["out"], "golden encoder out")
+    tw, tp = dev(d["dwte0"]), dev(d["dwpe0"])
+    gpu.encoder_backward(tw, tp, dev(d["dout"]), dev(d["inp"]), B, T, C)
+    assert_bits(host(tw), d["dwte"], "golden dwte")
+    assert_bits(host(tp), d["dwpe"], "golden dwpe")
+    kw, kp = torch.zeros(28, device=DEV), torch.zeros(12, device=DEV)
+    gpu.encoder_backward(kw, kp, dev(d["k_dout"]), dev(d["k_inp"]), 2, 3, 4)
+    assert_bits(host(kw).reshape(7, 4), d["k_dwte"], "golden repeated-token dwte")
+    g = ld("gelu")
+    n = g["x"].size
+    t = torch.empty(n, device=DEV)
+    gpu.gelu_forward(t, dev(g["x"]), n)
+    assert_bits(host(t), g["out"], "golden gelu out")
+    td = dev(g["dinp0"])
+    gpu.gelu_backward(td, dev(g["x"]), dev(g["dout"]), n)
+    assert_bits(host(td), g["dinp"], "golden gelu dinp")
+    r = ld("residual")
+    n = r["x"].size
+    t = torch.empty(n, device=DEV)
+    gpu.residual_forward(t, dev(r["x"]), dev(r["y"]), n)
+    assert_bits(host(t), r["out"], "golden residual out")
+    tx, ty = dev(r["dx0"]), dev(r["dy0"])
+    gpu.residual_backward(tx, ty, dev(r["dout"]), n)
+    assert_bits(host(tx), r["dx"], "golden dx")
+    assert_bits(host(ty), r["dy"], "golden dy")
+    m = ld("materialize")
+    n = m["w"].size
+    t = torch.empty(n, device=DEV)
+    gpu.bayes_materialize(t, dev(m["mu"]), dev(m["rho"]), dev(m["eps"]), n)
+    assert_bits(host(t), m["w"], "golden materialize")
+    L = ld("layernorm")
+    B, T, C = int(L["B"]), int(L["T"]), int(L["C"])
+    to, tm, tr = torch.empty(B * T * C, device=DEV), torch.empty(B * T, device=DEV), torch.empty(B * T, device=DEV)
+    gpu.layernorm_forward(to, tm, tr, dev(L["x"]), dev(L["w"]), dev(L["b"]), B, T, C)
+    assert_close(host(to).reshape(B, T, C), L["out"], "golden ln out")
+    assert_close(host(tm).reshape(B, T), L["mean"], "golden ln mean")
+    assert_close(host(tr).reshape(B, T), L["rstd"], "golden ln rstd")
+    tdi, tdw, tdb = dev(L["dinp0"]), dev(L["dw0"]), dev(L["db0"])
+    gpu.layernorm_backward(tdi, tdw, tdb, dev(L["dout"]), dev(L["x"]), dev(L["w"]), dev(L["mean"]),
+                           dev(L["rstd"]), B, T, C)
+    assert_close(host(tdi).reshape(B, T, C), L["dinp"], "golden ln dinp")
+    assert_close(host(tdw), L["dw"], "golden ln dweight", rtol=1e-5, atol=2e-5)
+    assert_close(host(tdb), L["db"], "golden ln dbias", rtol=1e-5, atol=2e-5)
+
+
+# ---- full benchmark shapes ------------------------------------------------------------
+
+def test_full_cfg2_layernorm(gpu, oracle):
+    literal = ln_case(gpu, oracle, 16, 1024, 768, seed=22, reps=2)
+    print(f"16384x768 literal-bar pass fraction for the column sums: {literal}")
+
+
+def test_full_cfg3_gelu_residual(gpu, oracle):
+    N = 16 * 1024 * 3072
+    g = gen.rng(33)
+    x = gen.normal(g, (N,))
+    gelu_pair(gpu, oracle, x, 34)
+    y = gen.normal(g, (N,))
+    t = torch.empty(N, device=DEV)
+    gpu.residual_forward(t, dev(x), dev(y), N)
+    out = np.zeros(N, np.float32)
+    oracle.residual_forward(out, x, y, N)
+    assert_bits(host(t), out, "residual cfg3")
+
+
+def test_full_cfg5_materialize(gpu, oracle):
+    n = 124_439_808
+    g = gen.rng(55)
+    materialize_check(gpu, oracle, gen.normal(g, (n,), 0, 0.02), gen.normal(g, (n,), -5, 0.1),
+                      gen.normal(g, (n,)), "materialize cfg5")
+
+
+# ---- the step driver --------------------------------------------------------------------
+
+def ref_offsets(B, T, C, V, maxT, L):
+    """Independent restatement of gpt2_kernels.cuh:656-719 for the driver test."""
+    p = {"wte": 0, "wpe": V * C}
+    p["blk0"] = p["wpe"] + maxT * C
+    rel, o = {}, 0
+    for k, sz in (("lng", C), ("lnb", C), ("qw", 3 * C * C), ("qb", 3 * C), ("pw", C * C), ("pb", C),
+                  ("ln2g", C), ("ln2b", C), ("w1", 4 * C * C), ("b1", 4 * C), ("w2", 4 * C * C), ("b2", C)):
+        rel[k] = o
+        o += sz
+    p["bstride"] = o
+    p.update({"flng": p["blk0"] + L * o})
+    p["flnb"] = p["flng"] + C
+    p["total"] = p["flnb"] + C + C * V + V
+    BT = B * T
+    a = {"enc": 0, "blk0": BT * C}
+    arel, o = {}, 0
+    for k, sz in (("lno", BT * C), ("lnm", BT), ("lnr", BT), ("qkv", 3 * BT * C), ("atty", BT * C),
+                  ("apr", BT * C), ("resa", BT * C), ("ln2o", BT * C), ("ln2m", BT), ("ln2r", BT),
+                  ("fch", 4 * BT * C), ("gelu", 4 * BT * C), ("mlpo", BT * C), ("res1", BT * C)):
+        arel[k] = o
+        o += sz
+    a["bstride"] = o
+    a["flo"] = a["blk0"] + L * o
+    a["flm"] = a["flo"] + BT * C
+    a["flr"] = a["flm"] + BT
+    a["total"] = a["flr"] + BT + 2 * BT * V + BT
+    return p, rel, a, arel
+
+
+def test_step_driver_matches_oracle_replay(gpu, oracle):
+    B, T, C, V, NH, maxT, L = 2, 16, 64, 11, 2, 16, 2
+    cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=maxT, L=L)
+    p, prel, a, arel = ref_offsets(B, T, C, V, maxT, L)
+    assert gpu.param_count(cfg) == p["total"] and gpu.act_count(cfg) == a["total"]
+    g = gen.rng(66)
+    params = gen.normal(g, (p["total"],), 0, 0.02)
+    for l in range(L):  # LN gains near 1
+        for k in ("lng", "ln2g"):
+            s = p["blk0"] + l * p["bstride"] + prel[k]
+            params[s:s + C] += 1.0
+    params[p["flng"]:p["flng"] + C] += 1.0
+    acts = gen.normal(g, (a["total"],))  # GEMM/attention outputs are whatever the buffer holds
+    inputs = gen.tokens_uniform(g, B * T, V)
+    tacts, tpar, tin = dev(acts), dev(params), dev(inputs)
+    gpu.gpt2_layers_forward(tacts, tpar, tin, cfg)
+    gacts = host(tacts)
+
+    # CPU replay of gpt2_kernels.cuh:775-813 with the oracle ops
+    cacts = acts.copy()
+    A = lambda l, k, n: cacts[a["blk0"] + l * a["bstride"] + arel[k]:][:n]
+    P = lambda l, k, n: params[p["blk0"] + l * p["bstride"] + prel[k]:][:n]
+    NB = B * T * C
+    enc = cacts[:NB]
+    oracle.encoder_forward(enc, inputs, params[:V * C], params[V * C:V * C + maxT * C], B, T, C)
+    stream = enc
+    for l in range(L):
+        oracle.layernorm_forward(A(l, "lno", NB), A(l, "lnm", B * T), A(l, "lnr", B * T), stream,
+                                 P(l, "lng", C), P(l, "lnb", C), B, T, C)
+        oracle.residual_forward(A(l, "resa", NB), stream, A(l, "apr", NB), NB)
+        oracle.layernorm_forward(A(l, "ln2o", NB), A(l, "ln2m", B * T), A(l, "ln2r", B * T), A(l, "resa", NB),
+                                 P(l, "ln2g", C), P(l, "ln2b", C), B, T, C)
+        oracle.gelu_forward(A(l, "gelu", 4 * NB), A(l, "fch", 4 * NB), 4 * NB)
+        oracle.residual_forward(A(l, "res1", NB), A(l, "resa", NB), A(l, "mlpo", NB), NB)
+        stream = A(l, "res1", NB)
+    oracle.layernorm_forward(cacts[a["flo"]:][:NB], cacts[a["flm"]:][:B * T], cacts[a["flr"]:][:B * T], stream,
+                             params[p["flng"]:][:C], params[p["flnb"]:][:C], B, T, C)
+    assert_bits(gacts[:NB], cacts[:NB], "driver encoder output")
+    assert_close(gacts, cacts, "driver forward activations", rtol=1e-5, atol=1e-5)
+
+    # backward from identical activations (the GPU forward's)
+    grads = np.zeros(p["total"], np.float32)
+    gacts_grad = np.zeros(a["total"], np.float32)
+    gacts_grad[a["flo"]:a["flo"] + NB] = gen.normal(g, (NB,))
+    tg, tga = dev(grads), dev(gacts_grad)
+    gpu.gpt2_layers_backward(tg, tga, tacts, tpar, tin, cfg)
+    cg, cga, ca = grads.copy(), gacts_grad.copy(), gacts
+    GA = lambda off, n: cga[off:][:n]
+    AO = lambda l, k: a["blk0"] + l * a["bstride"] + arel[k]
+    PO = lambda l, k: p["blk0"] + l * p["bstride"] + prel[k]
+    last = AO(L - 1, "res1")
+    oracle.layernorm_backward(GA(last, NB), cg[p["flng"]:][:C], cg[p["flnb"]:][:C], GA(a["flo"], NB),
+                              ca[last:][:NB], params[p["flng"]:][:C], ca[a["flm"]:][:B * T], ca[a["flr"]:][:B * T],
+                              B, T, C)
+    for l in range(L - 1, -1, -1):
+        st = a["enc"] if l == 0 else AO(l - 1, "res1")
+        oracle.residual_backward(GA(AO(l, "resa"), NB), GA(AO(l, "mlpo"), NB), GA(AO(l, "res1"), NB), NB)
+        oracle.gelu_backward(GA(AO(l, "fch"), 4 * NB), ca[AO(l, "fch"):][:4 * NB], GA(AO(l, "gelu"), 4 * NB), 4 * NB)
+        oracle.layernorm_backward(GA(AO(l, "resa"), NB), cg[PO(l, "ln2g"):][:C], cg[PO(l, "ln2b"):][:C],
+                                  GA(AO(l, "ln2o"), NB), ca[AO(l, "resa"):][:NB], params[PO(l, "ln2g"):][:C],
+                                  ca[AO(l, "ln2m"):][:B * T], ca[AO(l, "ln2r"):][:B * T], B, T, C)
+        oracle.residual_backward(GA(st, NB), GA(AO(l, "apr"), NB), GA(AO(l, "resa"), NB), NB)
+        oracle.layernorm_backward(GA(st, NB), cg[PO(l, "lng"):][:C], cg[PO(l, "lnb"):][:C], GA(AO(l, "lno"), NB),
+                                  ca[st:][:NB], params[PO(l, "lng"):][:C], ca[AO(l, "lnm"):][:B * T],
+                                  ca[AO(l, "lnr"):][:B * T], B, T, C)
+    oracle.encoder_backward(cg[:V * C], cg[V * C:V * C + maxT * C], GA(a["enc"], NB), inputs, B, T, C)
+    assert_close(host(tga), cga, "driver grads_acts", rtol=1e-5, atol=1e-5)
+    assert_close(host(tg), cg, "driver grads", rtol=1e-4, atol=1e-5)

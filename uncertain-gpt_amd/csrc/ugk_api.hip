@@ -1,0 +1,428 @@
+// ugk_api.hip - the C-ABI of libugk.so: argument checks, error reporting,
+// stream and scratch management, and the GPT-2 layer-kernel step driver.
+//
+// Every entry point validates its arguments on the host before it touches the
+// HIP runtime, so invalid calls are reported (UGK_EINVAL + message) without a
+// GPU, and no kernel is ever launched with a shape it does not expect.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <atomic>
+#include <climits>
+#include <mutex>
+
+#include "../../include/ugk.h"
+#include "ugk_internal.h"
+
+namespace ugk {
+
+namespace {
+thread_local char g_err[512] = "";
+std::atomic<hipStream_t> g_stream{nullptr};
+std::mutex g_mu;
+constexpr int kMaxDevices = 64;
+struct Scratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+Scratch g_scratch[kMaxDevices];
+}  // namespace
+
+hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+
+int set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(UGK_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return UGK_OK;
+}
+
+void *scratch(size_t bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error(UGK_EHIP, "scratch: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  Scratch &s = g_scratch[dev];
+  if (s.bytes >= bytes && s.ptr) return s.ptr;
+  if (s.ptr) {
+    // queued kernels may still read the old buffer
+    (void)hipStreamSynchronize(stream());
+    (void)hipFree(s.ptr);
+    s.ptr = nullptr;
+    s.bytes = 0;
+  }
+  size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+  if (hipMalloc(&s.ptr, want) != hipSuccess) {
+    (void)hipGetLastError();
+    s.ptr = nullptr;
+    set_error(UGK_ENOMEM, "scratch: cannot allocate %zu bytes", want);
+    return nullptr;
+  }
+  s.bytes = want;
+  return s.ptr;
+}
+
+size_t scratch_bytes_current() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  std::lock_guard<std::mutex> lock(g_mu);
+  return g_scratch[dev].bytes;
+}
+
+}  // namespace ugk
+
+using namespace ugk;
+
+namespace {
+
+int ok() {
+  g_err[0] = '\0';
+  return UGK_OK;
+}
+
+int bad(const char *fn, const char *what) { return set_error(UGK_EINVAL, "%s: %s", fn, what); }
+
+// B, T, C >= 0 and B*T*C addressable; B*T fits an int (the reference indexes
+// rows with int).
+int check_btc(const char *fn, int B, int T, int C) {
+  if (B < 0 || T < 0 || C < 0) return bad(fn, "B, T and C must be >= 0");
+  if ((long long)B * T > INT_MAX) return bad(fn, "B*T exceeds INT_MAX");
+  return UGK_OK;
+}
+
+bool any_null(std::initializer_list<const void *> ps) {
+  for (const void *p : ps)
+    if (!p) return true;
+  return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ugk_encoder_forward(float *out, const int *inp, const float *wte, const float *wpe, int B, int T,
+                        int C) {
+  const char *fn = "ugk_encoder_forward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T * C == 0) return ok();
+  if (any_null({out, inp, wte, wpe})) return bad(fn, "NULL pointer");
+  if (int e = launch_encoder_forward(out, inp, wte, wpe, B, T, C)) return e;
+  return ok();
+}
+
+int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout, const int *inp, int B, int T,
+                         int C) {
+  const char *fn = "ugk_encoder_backward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T * C == 0) return ok();
+  if (any_null({dwte, dwpe, dout, inp})) return bad(fn, "NULL pointer");
+  if (int e = launch_encoder_backward(dwte, dwpe, dout, inp, B, T, C)) return e;
+  return ok();
+}
+
+int ugk_layernorm_forward(float *out, float *mean, float *rstd, const float *inp, const float *weight,
+                          const float *bias, int B, int T, int C) {
+  const char *fn = "ugk_layernorm_forward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T == 0) return ok();
+  if (C == 0) return bad(fn, "C must be > 0 when B*T > 0 (mean over an empty row)");
+  if (any_null({out, mean, rstd, inp, weight, bias})) return bad(fn, "NULL pointer");
+  if (int e = launch_layernorm_forward(out, mean, rstd, inp, weight, bias, B * T, C)) return e;
+  return ok();
+}
+
+int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias, const float *dout,
+                           const float *inp, const float *weight, const float *mean, const float *rstd,
+                           int B, int T, int C) {
+  const char *fn = "ugk_layernorm_backward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T * C == 0) return ok();
+  if (any_null({dinp, dweight, dbias, dout, inp, weight, mean, rstd})) return bad(fn, "NULL pointer");
+  if (int e = launch_layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, B * T, C))
+    return e;
+  return ok();
+}
+
+int ugk_gelu_forward(float *out, const float *inp, int N) {
+  const char *fn = "ugk_gelu_forward";
+  if (N < 0) return bad(fn, "N must be >= 0");
+  if (N == 0) return ok();
+  if (any_null({out, inp})) return bad(fn, "NULL pointer");
+  if (int e = launch_gelu_forward(out, inp, (size_t)N)) return e;
+  return ok();
+}
+
+int ugk_gelu_backward(float *dinp, const float *inp, const float *dout, int N) {
+  const char *fn = "ugk_gelu_backward";
+  if (N < 0) return bad(fn, "N must be >= 0");
+  if (N == 0) return ok();
+  if (any_null({dinp, inp, dout})) return bad(fn, "NULL pointer");
+  if (int e = launch_gelu_backward(dinp, inp, dout, (size_t)N)) return e;
+  return ok();
+}
+
+int ugk_residual_forward(float *out, const float *x, const float *y, int N) {
+  const char *fn = "ugk_residual_forward";
+  if (N < 0) return bad(fn, "N must be >= 0");
+  if (N == 0) return ok();
+  if (any_null({out, x, y})) return bad(fn, "NULL pointer");
+  if (int e = launch_residual_forward(out, x, y, (size_t)N)) return e;
+  return ok();
+}
+
+int ugk_residual_backward(float *dx, float *dy, const float *dout, int N) {
+  const char *fn = "ugk_residual_backward";
+  if (N < 0) return bad(fn, "N must be >= 0");
+  if (N == 0) return ok();
+  if (any_null({dx, dy, dout})) return bad(fn, "NULL pointer");
+  if (int e = launch_residual_backward(dx, dy, dout, (size_t)N)) return e;
+  return ok();
+}
+
+int ugk_bayes_materialize(float *w, const float *mu, const float *rho, const float *eps, size_t n) {
+  const char *fn = "ugk_bayes_materialize";
+  if (n == 0) return ok();
+  if (any_null({w, mu, rho, eps})) return bad(fn, "NULL pointer");
+  if (int e = launch_bayes_materialize(w, mu, rho, eps, n)) return e;
+  return ok();
+}
+
+const char *ugk_last_error(void) { return g_err; }
+
+int ugk_set_stream(void *s) {
+  g_stream.store(static_cast<hipStream_t>(s));
+  return ok();
+}
+
+void *ugk_get_stream(void) { return g_stream.load(); }
+
+int ugk_reserve(int rows, int C) {
+  if (rows < 0 || C < 0) return bad("ugk_reserve", "rows and C must be >= 0");
+  size_t need = layernorm_backward_scratch(rows, C);
+  if (!scratch(need)) return UGK_ENOMEM;
+  return ok();
+}
+
+size_t ugk_scratch_bytes(void) { return scratch_bytes_current(); }
+
+int ugk_synchronize(void) {
+  const hipError_t e = hipStreamSynchronize(stream());
+  if (e != hipSuccess) return set_error(UGK_EHIP, "ugk_synchronize: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int ugk_version(void) { return 100; }
+
+}  // extern "C"
+
+// ---- GPT-2 layer-kernel step driver -----------------------------------------
+namespace {
+
+// Offsets of the reference's flat parameter buffer (gpt2_kernels.cuh:656-685).
+struct POff {
+  size_t wte, wpe, blk0, bstride;
+  size_t lng, lnb, qw, qb, pw, pb, ln2g, ln2b, w1, b1, w2, b2;
+  size_t flng, flnb, hw, hb, total;
+};
+
+// Offsets of the reference's flat activation buffer (gpt2_kernels.cuh:687-719).
+struct AOff {
+  size_t enc, blk0, bstride;
+  size_t lno, lnm, lnr, qkv, atty, apr, resa, ln2o, ln2m, ln2r, fch, gelu, mlpo, res1;
+  size_t flo, flm, flr, log, prb, los, total;
+};
+
+POff poff(const ugk_config &c) {
+  const size_t C = c.C, V = c.V, maxT = c.maxT;
+  POff p{};
+  p.wte = 0;
+  p.wpe = V * C;
+  p.blk0 = p.wpe + maxT * C;
+  size_t o = 0;
+  p.lng = o; o += C;
+  p.lnb = o; o += C;
+  p.qw = o; o += C * 3 * C;
+  p.qb = o; o += 3 * C;
+  p.pw = o; o += C * C;
+  p.pb = o; o += C;
+  p.ln2g = o; o += C;
+  p.ln2b = o; o += C;
+  p.w1 = o; o += C * 4 * C;
+  p.b1 = o; o += 4 * C;
+  p.w2 = o; o += 4 * C * C;
+  p.b2 = o; o += C;
+  p.bstride = o;
+  const size_t after = p.blk0 + (size_t)c.L * p.bstride;
+  p.flng = after;
+  p.flnb = p.flng + C;
+  p.hw = p.flnb + C;
+  p.hb = p.hw + C * V;
+  p.total = p.hb + V;
+  return p;
+}
+
+AOff aoff(const ugk_config &c) {
+  const size_t BT = (size_t)c.B * c.T, C = c.C, V = c.V;
+  AOff a{};
+  a.enc = 0;
+  a.blk0 = BT * C;
+  size_t o = 0;
+  a.lno = o; o += BT * C;
+  a.lnm = o; o += BT;
+  a.lnr = o; o += BT;
+  a.qkv = o; o += BT * 3 * C;
+  a.atty = o; o += BT * C;
+  a.apr = o; o += BT * C;
+  a.resa = o; o += BT * C;
+  a.ln2o = o; o += BT * C;
+  a.ln2m = o; o += BT;
+  a.ln2r = o; o += BT;
+  a.fch = o; o += BT * 4 * C;
+  a.gelu = o; o += BT * 4 * C;
+  a.mlpo = o; o += BT * C;
+  a.res1 = o; o += BT * C;
+  a.bstride = o;
+  const size_t after = a.blk0 + (size_t)c.L * a.bstride;
+  a.flo = after;
+  a.flm = a.flo + BT * C;
+  a.flr = a.flm + BT;
+  a.log = a.flr + BT;
+  a.prb = a.log + BT * V;
+  a.los = a.prb + BT * V;
+  a.total = a.los + BT;
+  return a;
+}
+
+int check_cfg(const char *fn, const ugk_config &c) {
+  if (c.B < 0 || c.T < 0 || c.C <= 0 || c.V <= 0 || c.L < 0 || c.maxT < c.T)
+    return bad(fn, "config needs B,T,L >= 0, C,V > 0 and maxT >= T");
+  if ((long long)c.B * c.T * 4 * c.C > INT_MAX)
+    return bad(fn, "B*T*4C exceeds INT_MAX (the element counts are int, as in train_bnn.c)");
+  return UGK_OK;
+}
+
+#define UGK_TRY(x) \
+  do {             \
+    int e_ = (x);  \
+    if (e_) return e_; \
+  } while (0)
+
+int dense(int rc, const char *what) {
+  return rc ? set_error(rc, "dense op callback %s returned %d", what, rc) : UGK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ugk_param_count(ugk_config cfg) { return poff(cfg).total; }
+size_t ugk_act_count(ugk_config cfg) { return aoff(cfg).total; }
+
+// gpt2_kernels.cuh:756-813
+int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs, ugk_config cfg,
+                            const ugk_dense_ops *ops) {
+  const char *fn = "ugk_gpt2_layers_forward";
+  UGK_TRY(check_cfg(fn, cfg));
+  if (any_null({acts, params, inputs})) return bad(fn, "NULL pointer");
+  const POff p = poff(cfg);
+  const AOff a = aoff(cfg);
+  const int B = cfg.B, T = cfg.T, C = cfg.C, M = B * T;
+  const int NBTC = M * C;
+  auto A = [&](size_t l, size_t rel) { return acts + a.blk0 + l * a.bstride + rel; };
+  auto P = [&](size_t l, size_t rel) { return params + p.blk0 + l * p.bstride + rel; };
+  UGK_TRY(ugk_encoder_forward(acts + a.enc, inputs, params + p.wte, params + p.wpe, B, T, C));
+  const float *stream_in = acts + a.enc;
+  for (int l = 0; l < cfg.L; l++) {
+    UGK_TRY(ugk_layernorm_forward(A(l, a.lno), A(l, a.lnm), A(l, a.lnr), stream_in, P(l, p.lng),
+                                  P(l, p.lnb), B, T, C));
+    if (ops && ops->matmul_forward)
+      UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.qkv), A(l, a.lno), P(l, p.qw), P(l, p.qb), M, C,
+                                        3 * C), "matmul_forward(qkv)"));
+    if (ops && ops->attention_forward)
+      UGK_TRY(dense(ops->attention_forward(ops->ctx, A(l, a.atty), A(l, a.qkv), B, T, C, cfg.NH),
+                    "attention_forward"));
+    if (ops && ops->matmul_forward)
+      UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.apr), A(l, a.atty), P(l, p.pw), P(l, p.pb), M, C, C),
+                    "matmul_forward(proj)"));
+    UGK_TRY(ugk_residual_forward(A(l, a.resa), stream_in, A(l, a.apr), NBTC));
+    UGK_TRY(ugk_layernorm_forward(A(l, a.ln2o), A(l, a.ln2m), A(l, a.ln2r), A(l, a.resa), P(l, p.ln2g),
+                                  P(l, p.ln2b), B, T, C));
+    if (ops && ops->matmul_forward)
+      UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.fch), A(l, a.ln2o), P(l, p.w1), P(l, p.b1), M, C,
+                                        4 * C), "matmul_forward(fc)"));
+    UGK_TRY(ugk_gelu_forward(A(l, a.gelu), A(l, a.fch), NBTC * 4));
+    if (ops && ops->matmul_forward)
+      UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.mlpo), A(l, a.gelu), P(l, p.w2), P(l, p.b2), M,
+                                        4 * C, C), "matmul_forward(fc2)"));
+    UGK_TRY(ugk_residual_forward(A(l, a.res1), A(l, a.resa), A(l, a.mlpo), NBTC));
+    stream_in = A(l, a.res1);
+  }
+  UGK_TRY(ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
+                                params + p.flnb, B, T, C));
+  return ok();
+}
+
+// gpt2_kernels.cuh:846-894
+int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts, const float *params,
+                             const int *inputs, ugk_config cfg, const ugk_dense_ops *ops) {
+  const char *fn = "ugk_gpt2_layers_backward";
+  UGK_TRY(check_cfg(fn, cfg));
+  if (any_null({grads, grads_acts, acts, params, inputs})) return bad(fn, "NULL pointer");
+  const POff p = poff(cfg);
+  const AOff a = aoff(cfg);
+  const int B = cfg.B, T = cfg.T, C = cfg.C, M = B * T;
+  const int NBTC = M * C;
+  auto A = [&](size_t l, size_t rel) { return a.blk0 + l * a.bstride + rel; };
+  auto P = [&](size_t l, size_t rel) { return p.blk0 + l * p.bstride + rel; };
+  const size_t last = cfg.L > 0 ? A(cfg.L - 1, a.res1) : a.enc;
+  UGK_TRY(ugk_layernorm_backward(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + a.flo,
+                                 acts + last, params + p.flng, acts + a.flm, acts + a.flr, B, T, C));
+  for (int l = cfg.L - 1; l >= 0; l--) {
+    const size_t st = (l == 0) ? a.enc : A(l - 1, a.res1);
+    UGK_TRY(ugk_residual_backward(grads_acts + A(l, a.resa), grads_acts + A(l, a.mlpo),
+                                  grads_acts + A(l, a.res1), NBTC));
+    if (ops && ops->matmul_backward)
+      UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.gelu), grads + P(l, p.w2),
+                                         grads + P(l, p.b2), acts + A(l, a.gelu), params + P(l, p.w2),
+                                         grads_acts + A(l, a.mlpo), M, 4 * C, C), "matmul_backward(fc2)"));
+    UGK_TRY(ugk_gelu_backward(grads_acts + A(l, a.fch), acts + A(l, a.fch), grads_acts + A(l, a.gelu),
+                              NBTC * 4));
+    if (ops && ops->matmul_backward)
+      UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.ln2o), grads + P(l, p.w1),
+                                         grads + P(l, p.b1), acts + A(l, a.ln2o), params + P(l, p.w1),
+                                         grads_acts + A(l, a.fch), M, C, 4 * C), "matmul_backward(fc)"));
+    UGK_TRY(ugk_layernorm_backward(grads_acts + A(l, a.resa), grads + P(l, p.ln2g), grads + P(l, p.ln2b),
+                                   grads_acts + A(l, a.ln2o), acts + A(l, a.resa), params + P(l, p.ln2g),
+                                   acts + A(l, a.ln2m), acts + A(l, a.ln2r), B, T, C));
+    UGK_TRY(ugk_residual_backward(grads_acts + st, grads_acts + A(l, a.apr), grads_acts + A(l, a.resa),
+                                  NBTC));
+    if (ops && ops->matmul_backward)
+      UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.atty), grads + P(l, p.pw),
+                                         grads + P(l, p.pb), acts + A(l, a.atty), params + P(l, p.pw),
+                                         grads_acts + A(l, a.apr), M, C, C), "matmul_backward(proj)"));
+    if (ops && ops->attention_backward)
+      UGK_TRY(dense(ops->attention_backward(ops->ctx, grads_acts + A(l, a.qkv), grads_acts + A(l, a.atty),
+                                            acts + A(l, a.qkv), B, T, C, cfg.NH), "attention_backward"));
+    if (ops && ops->matmul_backward)
+      UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.lno), grads + P(l, p.qw),
+                                         grads + P(l, p.qb), acts + A(l, a.lno), params + P(l, p.qw),
+                                         grads_acts + A(l, a.qkv), M, C, 3 * C), "matmul_backward(qkv)"));
+    UGK_TRY(ugk_layernorm_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
+                                   grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
+                                   acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
+  }
+  UGK_TRY(ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C));
+  return ok();
+}
+
+}  // extern "C"

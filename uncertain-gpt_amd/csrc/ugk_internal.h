@@ -1,0 +1,56 @@
+// ugk_internal.h - shared by the libugk translation units (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ugk {
+
+constexpr int kWave = 64;      // CDNA wavefront width
+constexpr int kBlock = 256;    // 4 waves per workgroup for streaming kernels
+
+// Library state, defined in ugk_api.hip.
+hipStream_t stream();
+int set_error(int code, const char *fmt, ...);
+int check_launch(const char *what);
+// Scratch of at least `bytes` on the current device (nullptr on failure,
+// with the error already set).
+void *scratch(size_t bytes);
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline unsigned grid_for(size_t work, size_t per_block) {
+  return (unsigned)((work + per_block - 1) / per_block);
+}
+
+// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Launchers, one per kernel family. Each validates nothing (ugk_api.hip does)
+// and returns the launch status through check_launch.
+int launch_residual_forward(float *out, const float *x, const float *y, size_t n);
+int launch_residual_backward(float *dx, float *dy, const float *dout, size_t n);
+int launch_gelu_forward(float *out, const float *inp, size_t n);
+int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n);
+int launch_bayes_materialize(float *w, const float *mu, const float *rho,
+                             const float *eps, size_t n);
+int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
+                             const float *weight, const float *bias, int rows, int C);
+int launch_layernorm_backward(float *dinp, float *dweight, float *dbias,
+                              const float *dout, const float *inp, const float *weight,
+                              const float *mean, const float *rstd, int rows, int C);
+int launch_encoder_forward(float *out, const int *inp, const float *wte,
+                           const float *wpe, int B, int T, int C);
+int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
+                            const int *inp, int B, int T, int C);
+
+// Scratch sizes, for ugk_reserve.
+size_t layernorm_backward_scratch(int rows, int C);
+size_t encoder_backward_scratch(int rows);
+
+}  // namespace ugk

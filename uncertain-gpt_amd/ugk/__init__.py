@@ -1,0 +1,251 @@
+"""ugk - Python binding of libugk.so, the MI355X layer-kernel set of uncertain-gpt.
+
+The functions mirror the CPU ops of the reference oracle ``train_bnn.c``
+(names, argument order and ``+=`` semantics for every backward output) and run
+the hand-written gfx950 HIP kernels of ``libugk.so`` through its C-ABI
+(``include/ugk.h``). Arguments are torch tensors on the GPU (fp32, int32 for
+token ids), or raw device addresses (``int``) for callers that manage memory
+themselves. Every tensor argument is checked on the host for device, dtype,
+contiguity and size before the call, so a kernel never sees a buffer smaller
+than the shape it is told; a failing call raises :class:`UgkError` with the
+library's message.
+
+There is no CPU fallback: if ``libugk.so`` is missing this module raises on
+import, and on a machine without a GPU the calls fail in the HIP runtime.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+__all__ = [
+    "UgkError", "lib", "library_path",
+    "encoder_forward", "encoder_backward", "layernorm_forward", "layernorm_backward",
+    "gelu_forward", "gelu_backward", "residual_forward", "residual_backward",
+    "bayes_materialize", "set_stream", "synchronize", "reserve", "scratch_bytes",
+    "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
+    "gpt2_layers_backward", "version",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+library_path = os.path.normpath(os.path.join(_HERE, "..", "libugk.so"))
+
+if not os.path.exists(library_path):
+    raise ImportError(
+        f"libugk.so not found at {library_path}; build it with "
+        "`make -C uncertain-gpt_amd/csrc` or `python -c 'import __graft_entry__ as g; g.build()'`")
+
+lib = ctypes.CDLL(library_path)
+
+_fp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+
+
+class Config(ctypes.Structure):
+    """``Config`` of gpt2_kernels.cuh:634 (ugk_config)."""
+    _fields_ = [("B", _i), ("T", _i), ("C", _i), ("V", _i), ("NH", _i), ("maxT", _i), ("L", _i)]
+
+
+_MATMUL_FWD = ctypes.CFUNCTYPE(_i, _fp, _fp, _fp, _fp, _fp, _i, _i, _i)
+_MATMUL_BWD = ctypes.CFUNCTYPE(_i, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i)
+_ATTN_FWD = ctypes.CFUNCTYPE(_i, _fp, _fp, _fp, _i, _i, _i, _i)
+_ATTN_BWD = ctypes.CFUNCTYPE(_i, _fp, _fp, _fp, _fp, _i, _i, _i, _i)
+
+
+class DenseOps(ctypes.Structure):
+    """``ugk_dense_ops``: callbacks for the GEMM/attention steps between layer kernels."""
+    _fields_ = [("ctx", _fp), ("matmul_forward", _MATMUL_FWD), ("matmul_backward", _MATMUL_BWD),
+                ("attention_forward", _ATTN_FWD), ("attention_backward", _ATTN_BWD)]
+
+
+_SIGS = {
+    "ugk_encoder_forward": [_fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_encoder_backward": [_fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_layernorm_forward": [_fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_layernorm_backward": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_gelu_forward": [_fp, _fp, _i],
+    "ugk_gelu_backward": [_fp, _fp, _fp, _i],
+    "ugk_residual_forward": [_fp, _fp, _fp, _i],
+    "ugk_residual_backward": [_fp, _fp, _fp, _i],
+    "ugk_bayes_materialize": [_fp, _fp, _fp, _fp, _sz],
+    "ugk_set_stream": [_fp],
+    "ugk_get_stream": [],
+    "ugk_reserve": [_i, _i],
+    "ugk_scratch_bytes": [],
+    "ugk_synchronize": [],
+    "ugk_version": [],
+    "ugk_last_error": [],
+    "ugk_param_count": [Config],
+    "ugk_act_count": [Config],
+    "ugk_gpt2_layers_forward": [_fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
+    "ugk_gpt2_layers_backward": [_fp, _fp, _fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
+}
+_RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz,
+        "ugk_param_count": _sz, "ugk_act_count": _sz}
+for _name, _args in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.argtypes = _args
+    _f.restype = _RET.get(_name, _i)
+
+
+class UgkError(RuntimeError):
+    """A libugk call returned a nonzero status (1 invalid argument, 2 HIP error, 3 out of memory)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[ugk status {status}] {message}")
+        self.status = status
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise UgkError(status, lib.ugk_last_error().decode(errors="replace"))
+
+
+def _ptr(x, what: str, need: int, dtype: str):
+    """Device address of ``x`` after checking it can hold ``need`` elements of ``dtype``."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    import torch  # plumbing only: device memory
+    want = {"f32": torch.float32, "i32": torch.int32}[dtype]
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{what}: expected a torch tensor or a device address, got {type(x)!r}")
+    if x.device.type != "cuda":
+        raise ValueError(f"{what}: tensor must be on the GPU, got {x.device}")
+    if x.dtype != want:
+        raise TypeError(f"{what}: dtype must be {want}, got {x.dtype}")
+    if not x.is_contiguous():
+        raise ValueError(f"{what}: tensor must be contiguous")
+    if x.numel() < need:
+        raise ValueError(f"{what}: needs at least {need} elements, has {x.numel()}")
+    return x.data_ptr()
+
+
+def _check_tokens(inp, table, C: int, what: str) -> None:
+    """Token ids must index rows of ``table`` (the reference's contract); checked when both are tensors."""
+    import torch
+    if isinstance(inp, torch.Tensor) and isinstance(table, torch.Tensor) and inp.numel() and C:
+        rows = table.numel() // C
+        lo, hi = int(inp.min()), int(inp.max())
+        if lo < 0 or hi >= rows:
+            raise ValueError(f"{what}: token ids must lie in [0, {rows}), got [{lo}, {hi}]")
+
+
+def encoder_forward(out, inp, wte, wpe, B: int, T: int, C: int) -> None:
+    """train_bnn.c:41-65. ``out[b,t,:] = wte[inp[b,t],:] + wpe[t,:]``."""
+    _check_tokens(inp, wte, C, "encoder_forward")
+    _check(lib.ugk_encoder_forward(_ptr(out, "out", B * T * C, "f32"), _ptr(inp, "inp", B * T, "i32"),
+                                   _ptr(wte, "wte", C, "f32"), _ptr(wpe, "wpe", T * C, "f32"), B, T, C))
+
+
+def encoder_backward(dwte, dwpe, dout, inp, B: int, T: int, C: int) -> None:
+    """train_bnn.c:647-662. ``dwte[inp[b,t],:] += dout[b,t,:]``; ``dwpe[t,:] += dout[b,t,:]``."""
+    _check_tokens(inp, dwte, C, "encoder_backward")
+    _check(lib.ugk_encoder_backward(_ptr(dwte, "dwte", C, "f32"), _ptr(dwpe, "dwpe", T * C, "f32"),
+                                    _ptr(dout, "dout", B * T * C, "f32"), _ptr(inp, "inp", B * T, "i32"),
+                                    B, T, C))
+
+
+def layernorm_forward(out, mean, rstd, inp, weight, bias, B: int, T: int, C: int) -> None:
+    """train_bnn.c:81-115."""
+    n, r = B * T * C, B * T
+    _check(lib.ugk_layernorm_forward(_ptr(out, "out", n, "f32"), _ptr(mean, "mean", r, "f32"),
+                                     _ptr(rstd, "rstd", r, "f32"), _ptr(inp, "inp", n, "f32"),
+                                     _ptr(weight, "weight", C, "f32"), _ptr(bias, "bias", C, "f32"),
+                                     B, T, C))
+
+
+def layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, B: int, T: int, C: int) -> None:
+    """train_bnn.c:439-477 (all three gradients accumulate)."""
+    n, r = B * T * C, B * T
+    _check(lib.ugk_layernorm_backward(_ptr(dinp, "dinp", n, "f32"), _ptr(dweight, "dweight", C, "f32"),
+                                      _ptr(dbias, "dbias", C, "f32"), _ptr(dout, "dout", n, "f32"),
+                                      _ptr(inp, "inp", n, "f32"), _ptr(weight, "weight", C, "f32"),
+                                      _ptr(mean, "mean", r, "f32"), _ptr(rstd, "rstd", r, "f32"), B, T, C))
+
+
+def gelu_forward(out, inp, N: int) -> None:
+    """train_bnn.c:163-170 (tanh approximation)."""
+    _check(lib.ugk_gelu_forward(_ptr(out, "out", N, "f32"), _ptr(inp, "inp", N, "f32"), N))
+
+
+def gelu_backward(dinp, inp, dout, N: int) -> None:
+    """train_bnn.c:520-533. ``dinp += gelu'(inp) * dout``."""
+    _check(lib.ugk_gelu_backward(_ptr(dinp, "dinp", N, "f32"), _ptr(inp, "inp", N, "f32"),
+                                 _ptr(dout, "dout", N, "f32"), N))
+
+
+def residual_forward(out, x, y, N: int) -> None:
+    """train_bnn.c:182-186."""
+    _check(lib.ugk_residual_forward(_ptr(out, "out", N, "f32"), _ptr(x, "x", N, "f32"),
+                                    _ptr(y, "y", N, "f32"), N))
+
+
+def residual_backward(dx, dy, dout, N: int) -> None:
+    """train_bnn.c:491-496. ``dx += dout``; ``dy += dout``."""
+    _check(lib.ugk_residual_backward(_ptr(dx, "dx", N, "f32"), _ptr(dy, "dy", N, "f32"),
+                                     _ptr(dout, "dout", N, "f32"), N))
+
+
+def bayes_materialize(w, mu, rho, eps, n: int) -> None:
+    """train_bnn.c:831-835. ``w = mu + softplus(rho) * eps``."""
+    _check(lib.ugk_bayes_materialize(_ptr(w, "w", n, "f32"), _ptr(mu, "mu", n, "f32"),
+                                     _ptr(rho, "rho", n, "f32"), _ptr(eps, "eps", n, "f32"), n))
+
+
+def set_stream(stream: Optional[int]) -> None:
+    """Queue later calls on ``stream`` (a hipStream_t address, e.g. ``torch.cuda.Stream().cuda_stream``)."""
+    _check(lib.ugk_set_stream(stream or None))
+
+
+def synchronize() -> None:
+    _check(lib.ugk_synchronize())
+
+
+def reserve(rows: int, C: int) -> None:
+    _check(lib.ugk_reserve(rows, C))
+
+
+def scratch_bytes() -> int:
+    return int(lib.ugk_scratch_bytes())
+
+
+def version() -> int:
+    return int(lib.ugk_version())
+
+
+def param_count(cfg: Config) -> int:
+    return int(lib.ugk_param_count(cfg))
+
+
+def act_count(cfg: Config) -> int:
+    return int(lib.ugk_act_count(cfg))
+
+
+def _cfg_check(cfg: Config) -> None:
+    if cfg.B < 0 or cfg.T < 0 or cfg.C <= 0 or cfg.V <= 0 or cfg.L < 0 or cfg.maxT < cfg.T:
+        raise ValueError(f"bad config {[(f, getattr(cfg, f)) for f, _ in Config._fields_]}")
+
+
+def gpt2_layers_forward(acts, params, inputs, cfg: Config, ops: Optional[DenseOps] = None) -> None:
+    """Layer-kernel half of gpt2_forward (gpt2_kernels.cuh:756-813) on the reference's buffer layout."""
+    _cfg_check(cfg)
+    _check(lib.ugk_gpt2_layers_forward(_ptr(acts, "acts", act_count(cfg), "f32"),
+                                       _ptr(params, "params", param_count(cfg), "f32"),
+                                       _ptr(inputs, "inputs", cfg.B * cfg.T, "i32"), cfg,
+                                       ctypes.byref(ops) if ops is not None else None))
+
+
+def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
+                         ops: Optional[DenseOps] = None) -> None:
+    """Layer-kernel half of gpt2_backward (gpt2_kernels.cuh:846-894)."""
+    _cfg_check(cfg)
+    na, npar = act_count(cfg), param_count(cfg)
+    _check(lib.ugk_gpt2_layers_backward(_ptr(grads, "grads", npar, "f32"),
+                                        _ptr(grads_acts, "grads_acts", na, "f32"),
+                                        _ptr(acts, "acts", na, "f32"), _ptr(params, "params", npar, "f32"),
+                                        _ptr(inputs, "inputs", cfg.B * cfg.T, "i32"), cfg,
+                                        ctypes.byref(ops) if ops is not None else None))
