@@ -18,8 +18,7 @@
 //                  slot and an arrival rank from atomicAdd on the slot count.
 //                  The same launch also runs the dwpe threads (first chunk).
 //     K2 place   - one workgroup: exclusive scan of the slot counts gives each
-//                  bucket's start; row i goes to start[slot]+rank; the table is
-//                  then reset to empty for the next call.
+//                  bucket's start; row i goes to start[slot]+rank.
 //     K3 add     - one wavefront per placed position. A bucket of n rows is
 //                  handled by the wavefront at its first position when
 //                  n <= 64: the n row ids are ranked by comparison (ids are
@@ -29,6 +28,7 @@
 //                  so the long serial chains of a frequent token run 64-wide on
 //                  12 wavefronts at C=768; each builds an LDS bitmap of the
 //                  bucket's row ids and walks it in ascending order.
+//     K4 reset   - returns the used table slots to empty for the next chunk.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
 #include "ugk_internal.h"
@@ -83,6 +83,7 @@ struct EncState {
   int *rank_of;    // [kChunk] arrival rank of row i within its slot
   int *placed;     // [kChunk] row ids grouped by bucket
   int *pos_slot;   // [kChunk] slot of each placed position
+  int *total;      // [1] number of placed rows
 };
 
 __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift) {
@@ -146,7 +147,8 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int
   }
 }
 
-// K2: one workgroup of 1024 threads. Scan slots [0, tsize), place rows, reset.
+// K2: one workgroup of 1024 threads. Scan slots [0, tsize) and place the rows.
+// keys/cnt stay as they are: K3 reads them, K4 clears them.
 constexpr int kPlaceThreads = 1024;
 __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int n, int tsize) {
   __shared__ int wsum[kPlaceThreads / kWave];
@@ -173,6 +175,7 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
       wpre[w] = run;
       run += wsum[w];
     }
+    s.total[0] = run;
   }
   __syncthreads();
   int start = wpre[wave] + inc - local;
@@ -189,9 +192,6 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
     s.placed[p] = i;
     s.pos_slot[p] = h;
   }
-  __syncthreads();
-  // K3 reads keys/cnt through bstart's copies below, so keep them until K3:
-  // the reset happens in K3 by the owner wave of each bucket.
 }
 
 // K3: add the buckets. Dynamic LDS: per wave max(kSmall, words) ints.
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int p = blockIdx.x * kWavesPerBlock + wave;
-  if (p >= n) return;
+  if (p >= n || p >= s.total[0]) return;
   const int per_wave = words > kSmall ? words : kSmall;
   unsigned *mine = lds + (size_t)wave * per_wave;
   const int h = s.pos_slot[p];
@@ -300,7 +300,7 @@ __global__ void k_enc_init(EncState s) {
   }
 }
 
-size_t state_bytes() { return ((size_t)3 * kTableMax + (size_t)4 * kChunk) * sizeof(int); }
+size_t state_bytes() { return ((size_t)3 * kTableMax + (size_t)4 * kChunk + 64) * sizeof(int); }
 
 EncState carve(void *base) {
   int *p = static_cast<int *>(base);
@@ -312,6 +312,7 @@ EncState carve(void *base) {
   s.rank_of = p; p += kChunk;
   s.placed = p; p += kChunk;
   s.pos_slot = p; p += kChunk;
+  s.total = p;
   return s;
 }
 
