@@ -13,12 +13,13 @@ native step driver of libugk.so (ugk_gpt2_layers_forward/backward).
 Printed JSON line (the last line of stdout):
     value        algorithmic bytes of the step / step time, GB/s
     ms_per_step  layer-kernel milliseconds per step (median-free mean over --steps)
-    kernels      each kernel at its step shape, cold (a 1 GiB buffer is written
-                 between repetitions so the 256 MB MALL cannot serve it): median ms,
-                 GB/s from algorithmic bytes, fraction of 8 TB/s
-    roofline     the dominant kernel (most HBM bytes per step: GELU backward),
-                 achieved = algorithmic bytes per launch / mean launch time from
-                 HIP events on the stream it runs on
+    kernels      each kernel at its step shape, cold (launches rotate over buffer
+                 sets totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds
+                 the operands): mean ms from HIP events, GB/s from algorithmic
+                 bytes, fraction of 8 TB/s
+    roofline     the dominant kernel (most algorithmic bytes per step: GELU
+                 backward), achieved = algorithmic bytes per launch / its mean
+                 launch time above
     cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this
                  repo's bit-identical restatement) on one host core, timed per op
                  at the step shapes and composed by launch count
@@ -26,7 +27,6 @@ Printed JSON line (the last line of stdout):
 import argparse
 import json
 import os
-import statistics
 import sys
 import time
 
@@ -66,7 +66,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--reps", type=int, default=25, help="cold repetitions per kernel")
+    ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -131,66 +131,98 @@ def main():
     log(f"bench: step {ms_step:.4f} ms (host wall {wall:.4f} ms) -> {value:.1f} GB/s algorithmic")
 
     # ---- each kernel alone at its step shape, cold ----------------------------
+    # Each kernel cycles through k private buffer sets whose total exceeds
+    # 1.5 GiB, so every launch finds its operands outside the L2 and the 256 MB
+    # MALL; R*k back-to-back launches sit between two HIP events on the stream
+    # the kernels run on, and the mean launch time is (t1 - t0) / (R*k).
     N = B * T * C
-    blk = lambda: torch.empty(N, device=dev)
-    x1, x2, x3, x4 = (torch.randn(N, generator=g, device=dev) for _ in range(4))
-    h1, h2, h3 = (torch.randn(4 * N, generator=g, device=dev) for _ in range(3))
-    lw, lb = torch.ones(C, device=dev), torch.zeros(C, device=dev)
-    mean, rstd = torch.empty(B * T, device=dev), torch.empty(B * T, device=dev)
-    dlw, dlb = torch.zeros(C, device=dev), torch.zeros(C, device=dev)
-    wte, wpe = mu[: V * C], mu[V * C: V * C + maxT * C]
-    dwte, dwpe = grads[: V * C], grads[V * C: V * C + maxT * C]
-    out = blk()
-    ugk.layernorm_forward(out, mean, rstd, x1, lw, lb, B, T, C)
-    launch = {
-        "encoder_forward": lambda: chk(lib.ugk_encoder_forward(out.data_ptr(), ip, wte.data_ptr(), wpe.data_ptr(), B, T, C)),
-        "encoder_backward": lambda: chk(lib.ugk_encoder_backward(dwte.data_ptr(), dwpe.data_ptr(), x1.data_ptr(), ip, B, T, C)),
-        "layernorm_forward": lambda: chk(lib.ugk_layernorm_forward(out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
-                                                                   x1.data_ptr(), lw.data_ptr(), lb.data_ptr(), B, T, C)),
-        "layernorm_backward": lambda: chk(lib.ugk_layernorm_backward(x2.data_ptr(), dlw.data_ptr(), dlb.data_ptr(),
-                                                                     x3.data_ptr(), x1.data_ptr(), lw.data_ptr(),
-                                                                     mean.data_ptr(), rstd.data_ptr(), B, T, C)),
-        "gelu_forward": lambda: chk(lib.ugk_gelu_forward(h2.data_ptr(), h1.data_ptr(), 4 * N)),
-        "gelu_backward": lambda: chk(lib.ugk_gelu_backward(h3.data_ptr(), h1.data_ptr(), h2.data_ptr(), 4 * N)),
-        "residual_forward": lambda: chk(lib.ugk_residual_forward(out.data_ptr(), x1.data_ptr(), x2.data_ptr(), N)),
-        "residual_backward": lambda: chk(lib.ugk_residual_backward(x3.data_ptr(), x4.data_ptr(), x1.data_ptr(), N)),
-        "bayes_materialize": lambda: chk(lib.ugk_bayes_materialize(wp, mup, rhop, epsp, n_mat)),
-    }
-    kernels = {}
-    for name, fn in launch.items():
-        fn()
-        times = []
-        for r in range(args.reps):
-            flush.fill_(float(r))
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            fn()
-            e.record()
-            e.synchronize()
-            times.append(s.elapsed_time(e))
-        med = statistics.median(times)
-        gbs = per[name] / (med * 1e-3) / 1e9
-        kernels[name] = {"ms": round(med, 5), "p25_ms": round(statistics.quantiles(times, n=4)[0], 5),
-                         "p75_ms": round(statistics.quantiles(times, n=4)[2], 5), "GBps": round(gbs, 1),
-                         "frac": round(gbs / PEAK_GBS, 4), "bytes": per[name], "per_step": count[name]}
-        log(f"bench: {name:20s} {med * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak")
+    rnd = lambda n: torch.randn(n, generator=g, device=dev)
 
-    # ---- roofline of the dominant kernel: HIP events over back-to-back cold launches
-    dom = max(per, key=lambda k: per[k] * count[k])
-    ev = []
-    for r in range(args.steps):
-        flush.fill_(float(r))
+    def sets_for(make, set_bytes):
+        k = max(2, -(-int(1.5 * 2 ** 30) // set_bytes))
+        return [make() for _ in range(k)]
+
+    def mk_enc():
+        return {"out": torch.empty(N, device=dev), "wte": rnd(V * C) * 0.02, "wpe": rnd(maxT * C) * 0.01,
+                "dout": rnd(N), "inp": torch.randint(0, V, (B * T,), generator=g, device=dev, dtype=torch.int32)}
+
+    def mk_ln():
+        d = {"x": rnd(N), "out": torch.empty(N, device=dev), "mean": torch.empty(B * T, device=dev),
+             "rstd": torch.empty(B * T, device=dev), "w": torch.ones(C, device=dev), "b": torch.zeros(C, device=dev),
+             "dout": rnd(N), "dinp": rnd(N), "dw": torch.zeros(C, device=dev), "db": torch.zeros(C, device=dev)}
+        ugk.layernorm_forward(d["out"], d["mean"], d["rstd"], d["x"], d["w"], d["b"], B, T, C)
+        return d
+
+    def mk_gelu():
+        return {"x": rnd(4 * N), "out": torch.empty(4 * N, device=dev), "dout": rnd(4 * N), "dinp": rnd(4 * N)}
+
+    def mk_res():
+        return {"x": rnd(N), "y": rnd(N), "out": torch.empty(N, device=dev), "dout": rnd(N)}
+
+    def mk_mat():
+        return {"mu": rnd(n_mat) * 0.02, "rho": rnd(n_mat) * 0.1 - 5.0, "eps": rnd(n_mat),
+                "w": torch.empty(n_mat, device=dev)}
+
+    P_ = lambda t: t.data_ptr()
+    plan = {
+        "encoder_forward": (mk_enc, 16 * N, lambda d: chk(lib.ugk_encoder_forward(
+            P_(d["out"]), P_(d["inp"]), P_(d["wte"]), P_(d["wpe"]), B, T, C))),
+        "encoder_backward": (mk_enc, 16 * N, lambda d: chk(lib.ugk_encoder_backward(
+            P_(d["wte"]), P_(d["wpe"]), P_(d["dout"]), P_(d["inp"]), B, T, C))),
+        "layernorm_forward": (mk_ln, 20 * N, lambda d: chk(lib.ugk_layernorm_forward(
+            P_(d["out"]), P_(d["mean"]), P_(d["rstd"]), P_(d["x"]), P_(d["w"]), P_(d["b"]), B, T, C))),
+        "layernorm_backward": (mk_ln, 20 * N, lambda d: chk(lib.ugk_layernorm_backward(
+            P_(d["dinp"]), P_(d["dw"]), P_(d["db"]), P_(d["dout"]), P_(d["x"]), P_(d["w"]), P_(d["mean"]),
+            P_(d["rstd"]), B, T, C))),
+        "gelu_forward": (mk_gelu, 64 * N, lambda d: chk(lib.ugk_gelu_forward(P_(d["out"]), P_(d["x"]), 4 * N))),
+        "gelu_backward": (mk_gelu, 64 * N, lambda d: chk(lib.ugk_gelu_backward(
+            P_(d["dinp"]), P_(d["x"]), P_(d["dout"]), 4 * N))),
+        "residual_forward": (mk_res, 16 * N, lambda d: chk(lib.ugk_residual_forward(
+            P_(d["out"]), P_(d["x"]), P_(d["y"]), N))),
+        "residual_backward": (mk_res, 16 * N, lambda d: chk(lib.ugk_residual_backward(
+            P_(d["x"]), P_(d["y"]), P_(d["dout"]), N))),
+        "bayes_materialize": (mk_mat, 16 * n_mat, lambda d: chk(lib.ugk_bayes_materialize(
+            P_(d["w"]), P_(d["mu"]), P_(d["rho"]), P_(d["eps"]), n_mat))),
+    }
+    kernels, mean_ms = {}, {}
+    for name, (make, set_bytes, fn) in plan.items():
+        sets = sets_for(make, set_bytes)
+        for d in sets:
+            fn(d)
+        torch.cuda.synchronize()
+        rounds = max(1, args.reps // len(sets))
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        launch[dom]()
+        for _ in range(rounds):
+            for d in sets:
+                fn(d)
         e.record()
-        ev.append((s, e))
-    torch.cuda.synchronize()
-    dom_ms = statistics.mean(s.elapsed_time(e) for s, e in ev)
-    achieved = per[dom] / (dom_ms * 1e-3) / 1e9
+        e.synchronize()
+        ms = s.elapsed_time(e) / (rounds * len(sets))
+        mean_ms[name] = ms
+        gbs = per[name] / (ms * 1e-3) / 1e9
+        kernels[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                         "bytes": per[name], "per_step": count[name], "launches_timed": rounds * len(sets),
+                         "buffer_sets": len(sets)}
+        log(f"bench: {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak"
+            f"  ({rounds * len(sets)} launches over {len(sets)} buffer sets)")
+        del sets
+        torch.cuda.empty_cache()
+
+    # ---- roofline of the dominant kernel (most algorithmic bytes per step)
+    dom = max(per, key=lambda k: per[k] * count[k])
+    achieved = per[dom] / (mean_ms[dom] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "launch_ms": round(dom_ms, 5),
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "launch_ms": round(mean_ms[dom], 5),
                 "bytes_per_launch": per[dom]}
+
+    # a plain 1 GiB device-to-device copy (torch's copy kernel): the known-size
+    # reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings
+    calib = torch.empty_like(flush)
+    for _ in range(3):
+        calib.copy_(flush)
+    torch.cuda.synchronize()
+    del calib
 
     cpu = None if args.no_cpu else cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes)
 

@@ -106,6 +106,20 @@ int ugk_synchronize(void);
 /* Library version, major*10000 + minor*100 + patch. */
 int ugk_version(void);
 
+/* ---- diagnostics of the kernels' float math (no counterpart in the
+ * reference; used by the parity tests). fn: 0 expf, 1 log1pf, 2 expm1f,
+ * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it. */
+
+/* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
+ * those where the kernels' SIMD-shaped math differs from its line-by-line
+ * restatement of the host C library; *first gets the smallest such pattern
+ * (0xffffffff if none). Synchronous. */
+int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
+                           unsigned long long *mismatches, unsigned *first);
+/* out[i] = f(in[i]) on the device; variant 0 = the kernels' math, 1 = the
+ * line-by-line restatement. */
+int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n);
+
 /* ---- GPT-2 layer-kernel step driver ------------------------------------
  * gpt2_kernels.cuh:634-719 (Config, param_offsets, act_offsets) and the
  * launch sequence of gpt2_forward / gpt2_backward (:756-896), restricted to

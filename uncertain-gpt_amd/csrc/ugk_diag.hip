@@ -1,0 +1,112 @@
+// ugk_diag.hip - diagnostics of the kernels' float math (no reference
+// counterpart): exhaustive comparison of the SIMD-shaped math in
+// ugk_libm_dev.h with its IEEE restatement in ugk_libm.h, and elementwise
+// evaluation of either for comparison with the host C library.
+#include "../../include/ugk.h"
+#include "ugk_internal.h"
+#include "ugk_libm_dev.h"
+
+namespace ugk {
+namespace {
+
+template <int FN>
+__device__ __forceinline__ float kernel_math(float x) {
+  if (FN == 0) return ugk_expf(x);
+  if (FN == 1) return ugk_dev_log1pf(x);
+  if (FN == 2) return ugk_dev_expm1f(x);
+  if (FN == 3) return ugk_dev_tanhf(x);
+  return ugk_dev_softplusf(x);
+}
+
+template <int FN>
+__device__ __forceinline__ float reference_math(float x) {
+  if (FN == 0) return ugk_expf(x);
+  if (FN == 1) return ugk_log1pf(x);
+  if (FN == 2) return ugk_expm1f(x);
+  if (FN == 3) return ugk_tanhf(x);
+  return ugk_softplusf(x);
+}
+
+template <int FN>
+__global__ __launch_bounds__(kBlock) void k_math_mismatch(unsigned long long lo, unsigned long long count,
+                                                          unsigned long long *nbad, unsigned *first) {
+  unsigned long long local = 0;
+  unsigned lfirst = 0xffffffffu;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * kBlock + threadIdx.x; i < count;
+       i += (unsigned long long)gridDim.x * kBlock) {
+    const unsigned u = (unsigned)(lo + i);
+    const float x = ugk_u2f(u);
+    const float a = kernel_math<FN>(x), b = reference_math<FN>(x);
+    if (ugk_f2u(a) != ugk_f2u(b) && !(a != a && b != b)) {
+      local++;
+      lfirst = min(lfirst, u);
+    }
+  }
+  if (local) {
+    atomicAdd(nbad, local);
+    atomicMin(first, lfirst);
+  }
+}
+
+template <int FN>
+__global__ __launch_bounds__(kBlock) void k_math_eval(int variant, float *out, const float *in, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock)
+    out[i] = variant == 0 ? kernel_math<FN>(in[i]) : reference_math<FN>(in[i]);
+}
+
+int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: fn must be 0..4", fn); }
+
+}  // namespace
+}  // namespace ugk
+
+using namespace ugk;
+
+extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
+                                      unsigned long long *mismatches, unsigned *first) {
+  if (fn < 0 || fn > 4) return bad_fn("ugk_diag_math_mismatch");
+  if (!mismatches || !first) return set_error(UGK_EINVAL, "ugk_diag_math_mismatch: NULL result pointer");
+  if (count > (1ull << 32) - lo) return set_error(UGK_EINVAL, "ugk_diag_math_mismatch: range beyond 2^32");
+  struct Res {
+    unsigned long long n;
+    unsigned first;
+  } h{0, 0xffffffffu};
+  Res *d = nullptr;
+  if (hipMalloc(&d, sizeof(Res)) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_ENOMEM, "ugk_diag_math_mismatch: hipMalloc failed");
+  }
+  int rc = UGK_OK;
+  if (hipMemcpyAsync(d, &h, sizeof h, hipMemcpyHostToDevice, stream()) != hipSuccess) rc = UGK_EHIP;
+  const dim3 grid(8192), block(kBlock);
+  if (rc == UGK_OK && count) {
+    switch (fn) {
+#define UGK_MM(f) \
+  case f: hipLaunchKernelGGL(k_math_mismatch<f>, grid, block, 0, stream(), (unsigned long long)lo, count, &d->n, &d->first); break;
+      UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4)
+#undef UGK_MM
+    }
+    rc = check_launch("ugk_diag_math_mismatch");
+  }
+  if (rc == UGK_OK && hipMemcpyAsync(&h, d, sizeof h, hipMemcpyDeviceToHost, stream()) != hipSuccess) rc = UGK_EHIP;
+  if (rc == UGK_OK && hipStreamSynchronize(stream()) != hipSuccess) rc = UGK_EHIP;
+  (void)hipFree(d);
+  if (rc != UGK_OK) return rc == UGK_EHIP ? set_error(rc, "ugk_diag_math_mismatch: HIP error") : rc;
+  *mismatches = h.n;
+  *first = h.first;
+  return UGK_OK;
+}
+
+extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n) {
+  if (fn < 0 || fn > 4) return bad_fn("ugk_diag_math_eval");
+  if (n == 0) return UGK_OK;
+  if (!out || !in) return set_error(UGK_EINVAL, "ugk_diag_math_eval: NULL pointer");
+  unsigned g = grid_for(n, kBlock);
+  if (g > 65536u) g = 65536u;
+  switch (fn) {
+#define UGK_EV(f) \
+  case f: hipLaunchKernelGGL(k_math_eval<f>, dim3(g), dim3(kBlock), 0, stream(), variant, out, in, n); break;
+    UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4)
+#undef UGK_EV
+  }
+  return check_launch("ugk_diag_math_eval");
+}

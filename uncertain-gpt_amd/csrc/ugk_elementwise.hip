@@ -10,9 +10,10 @@
 //
 // Arithmetic follows train_bnn.c operation by operation (the library is built
 // with -ffp-contract=off) and the transcendental functions come from
-// ugk_libm.h, so every result is bit-identical to the CPU oracle.
+// ugk_libm_dev.h, which equals the host glibc on every input, so every result
+// is bit-identical to the CPU oracle.
 #include "ugk_internal.h"
-#include "ugk_libm.h"
+#include "ugk_libm_dev.h"
 
 namespace ugk {
 namespace {
@@ -48,7 +49,7 @@ struct GeluFwd {  // train_bnn.c:163-170
     const float k = 0.7978845608f;
     const float x = ld[0];
     const float inner = k * (x + 0.044715f * x * x * x);
-    st[0] = 0.5f * x * (1.0f + ugk_tanhf(inner));
+    st[0] = 0.5f * x * (1.0f + ugk_dev_tanhf(inner));
   }
 };
 
@@ -58,7 +59,7 @@ struct GeluBwd {  // train_bnn.c:520-533; loads inp, dout, dinp
     const float k = 0.7978845608f;
     const float x = ld[0];
     const float u = k * (x + 0.044715f * x * x * x);
-    const float tanh_u = ugk_tanhf(u);
+    const float tanh_u = ugk_dev_tanhf(u);
     const float sech2 = 1.0f - tanh_u * tanh_u;
     const float du_dx = k * (1.0f + 3.0f * 0.044715f * x * x);
     const float local_grad = 0.5f * (1.0f + tanh_u) + 0.5f * x * sech2 * du_dx;
@@ -69,7 +70,7 @@ struct GeluBwd {  // train_bnn.c:520-533; loads inp, dout, dinp
 struct Materialize {  // train_bnn.c:831-835; loads mu, rho, eps
   static constexpr int kLoads = 3, kStores = 1;
   __device__ static void apply(const float *ld, float *st) {
-    st[0] = ld[0] + ugk_softplusf(ld[1]) * ld[2];
+    st[0] = ld[0] + ugk_dev_softplusf(ld[1]) * ld[2];
   }
 };
 

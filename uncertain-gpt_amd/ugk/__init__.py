@@ -81,6 +81,9 @@ _SIGS = {
     "ugk_act_count": [Config],
     "ugk_gpt2_layers_forward": [_fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
     "ugk_gpt2_layers_backward": [_fp, _fp, _fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
+    "ugk_diag_math_mismatch": [_i, ctypes.c_uint, ctypes.c_ulonglong, ctypes.POINTER(ctypes.c_ulonglong),
+                               ctypes.POINTER(ctypes.c_uint)],
+    "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
 }
 _RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz,
         "ugk_param_count": _sz, "ugk_act_count": _sz}
@@ -249,3 +252,20 @@ def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
                                         _ptr(acts, "acts", na, "f32"), _ptr(params, "params", npar, "f32"),
                                         _ptr(inputs, "inputs", cfg.B * cfg.T, "i32"), cfg,
                                         ctypes.byref(ops) if ops is not None else None))
+
+
+MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4}
+
+
+def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
+    """(mismatches, first) of the kernels' float math against its IEEE restatement over bit patterns."""
+    n, first = ctypes.c_ulonglong(0), ctypes.c_uint(0)
+    _check(lib.ugk_diag_math_mismatch(MATH_FUNCTIONS[fn], lo, count, ctypes.byref(n), ctypes.byref(first)))
+    return int(n.value), int(first.value)
+
+
+def diag_math_eval(fn: str, out, inp, variant: int = 0) -> None:
+    """``out = f(inp)`` on the device (variant 0 the kernels' math, 1 the restatement)."""
+    n = inp.numel()
+    _check(lib.ugk_diag_math_eval(MATH_FUNCTIONS[fn], variant, _ptr(out, "out", n, "f32"),
+                                  _ptr(inp, "inp", n, "f32"), n))
