@@ -108,7 +108,8 @@ int ugk_version(void);
 
 /* ---- diagnostics of the kernels' float math (no counterpart in the
  * reference; used by the parity tests). fn: 0 expf, 1 log1pf, 2 expm1f,
- * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it. */
+ * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it; 10+s, 20+s, 30+s:
+ * tanhf, log1pf, expm1f with the candidate division sequence s = 0..3. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

@@ -9,22 +9,28 @@
 namespace ugk {
 namespace {
 
+// fn codes: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf, 4 softplus (the kernels'
+// math); 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
+// (ugk_div_t<s>), to compare the candidate sequences.
 template <int FN>
 __device__ __forceinline__ float kernel_math(float x) {
   if (FN == 0) return ugk_expf(x);
   if (FN == 1) return ugk_dev_log1pf(x);
   if (FN == 2) return ugk_dev_expm1f(x);
   if (FN == 3) return ugk_dev_tanhf(x);
-  return ugk_dev_softplusf(x);
+  if (FN == 4) return ugk_dev_softplusf(x);
+  if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
+  if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
+  return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
 template <int FN>
 __device__ __forceinline__ float reference_math(float x) {
   if (FN == 0) return ugk_expf(x);
-  if (FN == 1) return ugk_log1pf(x);
-  if (FN == 2) return ugk_expm1f(x);
-  if (FN == 3) return ugk_tanhf(x);
-  return ugk_softplusf(x);
+  if (FN == 1 || (FN >= 20 && FN < 24)) return ugk_log1pf(x);
+  if (FN == 3 || (FN >= 10 && FN < 14)) return ugk_tanhf(x);
+  if (FN == 4) return ugk_softplusf(x);
+  return ugk_expm1f(x);
 }
 
 template <int FN>
@@ -54,7 +60,8 @@ __global__ __launch_bounds__(kBlock) void k_math_eval(int variant, float *out, c
     out[i] = variant == 0 ? kernel_math<FN>(in[i]) : reference_math<FN>(in[i]);
 }
 
-int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: fn must be 0..4", fn); }
+bool fn_ok(int fn) { return (fn >= 0 && fn <= 4) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
+int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
 }  // namespace
 }  // namespace ugk
@@ -63,7 +70,7 @@ using namespace ugk;
 
 extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
                                       unsigned long long *mismatches, unsigned *first) {
-  if (fn < 0 || fn > 4) return bad_fn("ugk_diag_math_mismatch");
+  if (!fn_ok(fn)) return bad_fn("ugk_diag_math_mismatch");
   if (!mismatches || !first) return set_error(UGK_EINVAL, "ugk_diag_math_mismatch: NULL result pointer");
   if (count > (1ull << 32) - lo) return set_error(UGK_EINVAL, "ugk_diag_math_mismatch: range beyond 2^32");
   struct Res {
@@ -83,6 +90,8 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
 #define UGK_MM(f) \
   case f: hipLaunchKernelGGL(k_math_mismatch<f>, grid, block, 0, stream(), (unsigned long long)lo, count, &d->n, &d->first); break;
       UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4)
+      UGK_MM(10) UGK_MM(11) UGK_MM(12) UGK_MM(13) UGK_MM(20) UGK_MM(21) UGK_MM(22) UGK_MM(23)
+      UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -97,7 +106,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
 }
 
 extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n) {
-  if (fn < 0 || fn > 4) return bad_fn("ugk_diag_math_eval");
+  if (!fn_ok(fn)) return bad_fn("ugk_diag_math_eval");
   if (n == 0) return UGK_OK;
   if (!out || !in) return set_error(UGK_EINVAL, "ugk_diag_math_eval: NULL pointer");
   unsigned g = grid_for(n, kBlock);
@@ -106,6 +115,8 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
 #define UGK_EV(f) \
   case f: hipLaunchKernelGGL(k_math_eval<f>, dim3(g), dim3(kBlock), 0, stream(), variant, out, in, n); break;
     UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4)
+    UGK_EV(10) UGK_EV(11) UGK_EV(12) UGK_EV(13) UGK_EV(20) UGK_EV(21) UGK_EV(22) UGK_EV(23)
+    UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

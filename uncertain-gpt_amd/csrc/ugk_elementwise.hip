@@ -1,10 +1,13 @@
 // ugk_elementwise.hip - streaming elementwise kernels: residual fwd/bwd,
 // GELU fwd/bwd and bayes_materialize.
 //
-// All five are HBM-bound maps over flat fp32 arrays. Each thread owns kUnroll
-// float4 (16-byte) slots strided by the workgroup size, so every load and
-// store instruction of a wavefront covers one contiguous 1 KiB span, and all
-// of a thread's loads are issued before its first arithmetic instruction.
+// All five are maps over flat fp32 arrays. Each thread owns kUnroll float4
+// (16-byte) slots strided by the workgroup size, so every load and store
+// instruction of a wavefront covers one contiguous 1 KiB span, all of a
+// thread's loads are issued before its first arithmetic instruction, and every
+// access is non-temporal (each byte is touched once). A launch-shape sweep on
+// MI355X (unroll 1-8, 256-1024 threads, flat or grid-stride, with and without
+// nt) put unroll 1-2 of 256 threads with nt loads and stores on top.
 // Arrays whose pointers are not all 16-byte aligned, and the n % 4 tail, take
 // a scalar grid-stride path with identical arithmetic.
 //
@@ -18,7 +21,7 @@
 namespace ugk {
 namespace {
 
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 2;
 
 // ---- per-element operators ------------------------------------------------
 // `ld` are the loaded operands in the order of the launcher's load list, `st`
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
     const size_t i = base + (size_t)u * kBlock;
     if (i < n4) {
 #pragma unroll
-      for (int l = 0; l < Op::kLoads; l++) v[u][l] = reinterpret_cast<const float4 *>(s.ld[l])[i];
+      for (int l = 0; l < Op::kLoads; l++) v[u][l] = ld_nt(reinterpret_cast<const float4 *>(s.ld[l]) + i);
     }
   }
 #pragma unroll
@@ -106,8 +109,7 @@ __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
       for (int e = 0; e < 4; e++) Op::apply(in[e], out[e]);
 #pragma unroll
       for (int o = 0; o < Op::kStores; o++)
-        reinterpret_cast<float4 *>(s.st[o])[i] =
-            make_float4(out[0][o], out[1][o], out[2][o], out[3][o]);
+        st_nt(reinterpret_cast<float4 *>(s.st[o]) + i, make_float4(out[0][o], out[1][o], out[2][o], out[3][o]));
     }
   }
 }

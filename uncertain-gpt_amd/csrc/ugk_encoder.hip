@@ -18,7 +18,9 @@
 //                  slot and an arrival rank from atomicAdd on the slot count.
 //                  The same launch also runs the dwpe threads (first chunk).
 //     K2 place   - one workgroup: exclusive scan of the slot counts gives each
-//                  bucket's start; row i goes to start[slot]+rank.
+//                  bucket's start; row i goes to start[slot]+rank together
+//                  with its bucket's start, size and token; the table is then
+//                  cleared for the next chunk.
 //     K3 add     - one wavefront per placed position. A bucket of n rows is
 //                  handled by the wavefront at its first position when
 //                  n <= 64: the n row ids are ranked by comparison (ids are
@@ -28,7 +30,6 @@
 //                  so the long serial chains of a frequent token run 64-wide on
 //                  12 wavefronts at C=768; each builds an LDS bitmap of the
 //                  bucket's row ids and walks it in ascending order.
-//     K4 reset   - returns the used table slots to empty for the next chunk.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
 #include "ugk_internal.h"
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_vec(float4 *__restrict__ out
   float4 *o = out + (size_t)bt * C4;
   for (int c = lane; c < C4; c += kWave) {
     const float4 x = a[c], y = p[c];
-    o[c] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    st_nt(o + c, make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w));
   }
 }
 
@@ -76,13 +77,12 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_scalar(float *out, const int
 // ---- backward --------------------------------------------------------------
 
 struct EncState {
-  int *keys;       // [kTableMax] token per slot, kEmpty when free
-  int *cnt;        // [kTableMax] rows per slot
-  int *bstart;     // [kTableMax] bucket start (valid for non-empty slots)
+  int *keys;       // [kTableMax] token per slot, kEmpty when free (kept clean between calls)
+  int *cnt;        // [kTableMax] rows per slot (kept zero between calls)
+  int *bstart;     // [kTableMax] bucket start of a slot (valid during a call)
   int *slot_of;    // [kChunk] slot of row i of the chunk (-1: skipped)
   int *rank_of;    // [kChunk] arrival rank of row i within its slot
-  int *placed;     // [kChunk] row ids grouped by bucket
-  int *pos_slot;   // [kChunk] slot of each placed position
+  int4 *meta;      // [kChunk] per placed position: {bucket start, bucket size, token, row}
   int *total;      // [1] number of placed rows
 };
 
@@ -124,8 +124,9 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int
     s.rank_of[i] = atomicAdd(&s.cnt[h], 1);
     return;
   }
-  // dwpe[t, c] += dout[b, t, c] for b = 0..B-1, in order.
+  // dwpe[t, c] += dout[b, t, c] for b = 0..B-1, in order; 8 rows in flight.
   const size_t j = (size_t)(blockIdx.x - ins_blocks) * kBlock + threadIdx.x;
+  constexpr int kB = 8;
   if (kVec) {
     const int C4 = C >> 2;
     if (j >= (size_t)T * C4) return;
@@ -133,23 +134,41 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int
     float4 *p = reinterpret_cast<float4 *>(dwpe) + j;
     const float4 *g = reinterpret_cast<const float4 *>(dout) + (size_t)t * C4 + c4;
     float4 acc = *p;
-    for (int b = 0; b < B; b++) {
-      const float4 d = g[(size_t)b * T * C4];
-      acc.x += d.x; acc.y += d.y; acc.z += d.z; acc.w += d.w;
+    for (int b0 = 0; b0 < B; b0 += kB) {
+      float4 d[kB];
+#pragma unroll
+      for (int q = 0; q < kB; q++)
+        if (b0 + q < B) d[q] = ld_nt(g + (size_t)(b0 + q) * T * C4);
+#pragma unroll
+      for (int q = 0; q < kB; q++)
+        if (b0 + q < B) {
+          acc.x += d[q].x; acc.y += d[q].y; acc.z += d[q].z; acc.w += d[q].w;
+        }
     }
     *p = acc;
   } else {
     if (j >= (size_t)T * C) return;
     const int t = (int)(j / C), c = (int)(j % C);
     float acc = dwpe[j];
-    for (int b = 0; b < B; b++) acc += dout[((size_t)b * T + t) * C + c];
+    for (int b0 = 0; b0 < B; b0 += kB) {
+      float d[kB];
+#pragma unroll
+      for (int q = 0; q < kB; q++)
+        if (b0 + q < B) d[q] = dout[((size_t)(b0 + q) * T + t) * C + c];
+#pragma unroll
+      for (int q = 0; q < kB; q++)
+        if (b0 + q < B) acc += d[q];
+    }
     dwpe[j] = acc;
   }
 }
 
-// K2: one workgroup of 1024 threads. Scan slots [0, tsize) and place the rows.
-// keys/cnt stay as they are: K3 reads them, K4 clears them.
+// K2: one workgroup of 1024 threads. Exclusive scan of the slot counts over
+// [0, tsize) gives each bucket's start; every row i is placed at
+// start[slot] + rank with its bucket's metadata; the table is then returned
+// to empty for the next chunk or call.
 constexpr int kPlaceThreads = 1024;
+constexpr int kPlaceBatch = 8;
 __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int n, int tsize) {
   __shared__ int wsum[kPlaceThreads / kWave];
   __shared__ int wpre[kPlaceThreads / kWave];
@@ -157,9 +176,15 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
   const int per = (tsize + kPlaceThreads - 1) / kPlaceThreads;
   const int lo = min(tid * per, tsize), hi = min(lo + per, tsize);
   int local = 0;
-  for (int h = lo; h < hi; h++) local += s.cnt[h];
+  for (int h0 = lo; h0 < hi; h0 += kPlaceBatch) {
+    int c[kPlaceBatch];
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++) c[q] = (h0 + q < hi) ? s.cnt[h0 + q] : 0;
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++) local += c[q];
+  }
   // exclusive scan of `local` over the workgroup: wave inclusive scan, then
-  // wave totals.
+  // wave totals
   const int lane = tid & (kWave - 1), wave = tid >> 6;
   int inc = local;
 #pragma unroll
@@ -179,22 +204,44 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
   }
   __syncthreads();
   int start = wpre[wave] + inc - local;
-  for (int h = lo; h < hi; h++) {
-    const int c = s.cnt[h];
-    s.bstart[h] = start;
-    start += c;
+  for (int h0 = lo; h0 < hi; h0 += kPlaceBatch) {
+    int c[kPlaceBatch];
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++) c[q] = (h0 + q < hi) ? s.cnt[h0 + q] : 0;
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++)
+      if (h0 + q < hi) {
+        s.bstart[h0 + q] = start;
+        start += c[q];
+      }
   }
   __syncthreads();
-  for (int i = tid; i < n; i += kPlaceThreads) {
-    const int h = s.slot_of[i];
-    if (h < 0) continue;
-    const int p = s.bstart[h] + s.rank_of[i];
-    s.placed[p] = i;
-    s.pos_slot[p] = h;
+  for (int i0 = tid * kPlaceBatch; i0 < n; i0 += kPlaceThreads * kPlaceBatch) {
+    int h[kPlaceBatch], rk[kPlaceBatch], st[kPlaceBatch], ct[kPlaceBatch], tk[kPlaceBatch];
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++) {
+      h[q] = (i0 + q < n) ? s.slot_of[i0 + q] : -1;
+      rk[q] = (i0 + q < n) ? s.rank_of[i0 + q] : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++) {
+      st[q] = h[q] >= 0 ? s.bstart[h[q]] : 0;
+      ct[q] = h[q] >= 0 ? s.cnt[h[q]] : 0;
+      tk[q] = h[q] >= 0 ? s.keys[h[q]] : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kPlaceBatch; q++)
+      if (h[q] >= 0) s.meta[st[q] + rk[q]] = make_int4(st[q], ct[q], tk[q], i0 + q);
+  }
+  __syncthreads();
+  for (int h = lo; h < hi; h++) {
+    s.keys[h] = kEmpty;
+    s.cnt[h] = 0;
   }
 }
 
-// K3: add the buckets. Dynamic LDS: per wave max(kSmall, words) ints.
+// K3: add the buckets, one wavefront per placed position. Dynamic LDS: per
+// wave max(kSmall, words) 32-bit words.
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__restrict__ dwte,
                                                         const float *__restrict__ dout, int n, int C,
@@ -206,21 +253,25 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
   if (p >= n || p >= s.total[0]) return;
   const int per_wave = words > kSmall ? words : kSmall;
   unsigned *mine = lds + (size_t)wave * per_wave;
-  const int h = s.pos_slot[p];
-  const int start = s.bstart[h];
-  const int cnt = s.cnt[h];
-  const int tok = s.keys[h];
+  const int4 mt = s.meta[p];
+  const int start = mt.x, cnt = mt.y, tok = mt.z;
   const int k = p - start;
   if (cnt <= kSmall) {
     if (k != 0) return;
-    // rank the bucket's row ids; ids are distinct, so ranks are a permutation
-    const int id = lane < cnt ? s.placed[start + lane] : 0x7fffffff;
-    int rank = 0;
-    for (int j = 0; j < cnt; j++) {
-      const int o = __shfl(id, j);
-      rank += (o < id) ? 1 : 0;
+    int nrow = 1;
+    if (cnt == 1) {
+      mine[0] = (unsigned)mt.w;
+    } else {
+      // rank the bucket's row ids; ids are distinct, so ranks are a permutation
+      const int id = lane < cnt ? s.meta[start + lane].w : 0x7fffffff;
+      int rank = 0;
+      for (int j = 0; j < cnt; j++) {
+        const int o = __shfl(id, j);
+        rank += (o < id) ? 1 : 0;
+      }
+      if (lane < cnt) mine[rank] = (unsigned)id;
+      nrow = cnt;
     }
-    if (lane < cnt) mine[rank] = (unsigned)id;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -230,8 +281,8 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
       const float4 *g = reinterpret_cast<const float4 *>(dout);
       for (int c4 = lane; c4 < C4; c4 += kWave) {
         float4 acc = row[c4];
-        for (int q = 0; q < cnt; q++) {
-          const float4 d = g[(size_t)mine[q] * C4 + c4];
+        for (int q = 0; q < nrow; q++) {
+          const float4 d = ld_nt(g + (size_t)mine[q] * C4 + c4);
           acc.x += d.x; acc.y += d.y; acc.z += d.z; acc.w += d.w;
         }
         row[c4] = acc;
@@ -240,7 +291,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
       float *row = dwte + (size_t)tok * C;
       for (int c = lane; c < C; c += kWave) {
         float acc = row[c];
-        for (int q = 0; q < cnt; q++) acc += dout[(size_t)mine[q] * C + c];
+        for (int q = 0; q < nrow; q++) acc += dout[(size_t)mine[q] * C + c];
         row[c] = acc;
       }
     }
@@ -254,7 +305,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   for (int j = lane; j < cnt; j += kWave) {
-    const int id = s.placed[start + j];
+    const int id = s.meta[start + j].w;
     atomicOr(&mine[id >> 5], 1u << (id & 31));
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -283,15 +334,6 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__res
   }
 }
 
-// K4: reset the table slots used by this chunk (after K3 has read them).
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_reset(EncState s, int tsize) {
-  const int h = blockIdx.x * kBlock + threadIdx.x;
-  if (h < tsize) {
-    s.keys[h] = kEmpty;
-    s.cnt[h] = 0;
-  }
-}
-
 __global__ void k_enc_init(EncState s) {
   const int h = blockIdx.x * kBlock + threadIdx.x;
   if (h < kTableMax) {
@@ -300,25 +342,27 @@ __global__ void k_enc_init(EncState s) {
   }
 }
 
-size_t state_bytes() { return ((size_t)3 * kTableMax + (size_t)4 * kChunk + 64) * sizeof(int); }
+size_t state_bytes() {
+  return ((size_t)3 * kTableMax + (size_t)2 * kChunk + 64) * sizeof(int) + (size_t)kChunk * sizeof(int4);
+}
 
 EncState carve(void *base) {
-  int *p = static_cast<int *>(base);
+  int4 *m = static_cast<int4 *>(base);
   EncState s;
+  s.meta = m;
+  int *p = reinterpret_cast<int *>(m + kChunk);
   s.keys = p; p += kTableMax;
   s.cnt = p; p += kTableMax;
   s.bstart = p; p += kTableMax;
   s.slot_of = p; p += kChunk;
   s.rank_of = p; p += kChunk;
-  s.placed = p; p += kChunk;
-  s.pos_slot = p; p += kChunk;
   s.total = p;
   return s;
 }
 
-// The table must start empty; it is returned to empty by K4 after each chunk.
-// State is kept per device in the encoder's own allocation (not the shared
-// scratch, which other ops overwrite).
+// The table must start empty; K2 returns it to empty after each chunk. State
+// is kept per device in the encoder's own allocation (not the shared scratch,
+// which other ops overwrite).
 struct DevState {
   void *mem = nullptr;
 };
@@ -387,8 +431,6 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     else
       hipLaunchKernelGGL(k_enc_bwd_add<false>, dim3(grid_for((size_t)n, kWavesPerBlock)), dim3(kBlock), lds,
                          stream(), s, dwte, dchunk, n, C, words);
-    hipLaunchKernelGGL(k_enc_bwd_reset, dim3(grid_for((size_t)tsize, kBlock)), dim3(kBlock), 0, stream(), s,
-                       tsize);
   }
   return check_launch("encoder_backward");
 }

@@ -24,6 +24,22 @@ inline unsigned grid_for(size_t work, size_t per_block) {
   return (unsigned)((work + per_block - 1) / per_block);
 }
 
+// Streaming access: loads and stores of data touched once per kernel use the
+// non-temporal (nt) cache policy, which on MI355X measured 5-12% more
+// bandwidth than the default policy for read-read-write streams.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_nt(const float4 *p) {
+  const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(float4 *p, float4 v) {
+  const v4f w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<v4f *>(p));
+}
+__device__ __forceinline__ float ld_nt(const float *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
+
 // Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

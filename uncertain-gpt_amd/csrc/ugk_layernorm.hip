@@ -10,12 +10,14 @@
 // the registers with 64-lane butterfly sums, rstd = 1/sqrtf(var/C + 1e-5)
 // with IEEE division and square root, exactly the CPU formula.
 //
-// Backward: one wavefront per row for dinp (two butterfly sums), and the
-// dweight/dbias column sums are carried in registers across the rows a
-// wavefront visits, then combined in a fixed order: 4 wavefronts through LDS
-// into one partial row per workgroup, then workgroups in index order by a
-// small second kernel that adds the totals into dweight/dbias. No atomics, so
-// the result is identical run to run.
+// Backward: one wavefront per row for dinp (two butterfly sums, two rows in
+// flight per wavefront), and the dweight/dbias column sums are carried in
+// registers across the rows a wavefront visits, then combined in a fixed
+// order: the 16 wavefronts of a workgroup through an LDS tree into one
+// partial row per workgroup (at most 256 workgroups, one per CU), then the
+// partial rows in index order by a small second kernel that adds the totals
+// into dweight/dbias. No atomics, so the result is identical run to run.
+// Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
 #include "ugk_internal.h"
 
 namespace ugk {
@@ -40,7 +42,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, 
 #pragma unroll
   for (int v = 0; v < V; v++) {
     const int c4 = lane + v * kWave;
-    xv[v] = (c4 < C4) ? x4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    xv[v] = (c4 < C4) ? ld_nt(x4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   float s = 0.0f;
 #pragma unroll
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, 
       o.y = (xv[v].y - m) * r * w.y + b.y;
       o.z = (xv[v].z - m) * r * w.z + b.z;
       o.w = (xv[v].w - m) * r * w.w + b.w;
-      o4[c4] = o;
+      st_nt(o4 + c4, o);
     }
   }
   if (lane == 0) {
@@ -111,18 +113,20 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
   }
 }
 
-// Backward, register-resident rows. Workgroup g handles rows
-// [g*rpb, min((g+1)*rpb, rows)); its wavefront w takes rows g*rpb + w + 4k.
-// partial: one row of 2*C floats per workgroup, dweight part then dbias part.
+// Backward, register-resident rows. A workgroup is 16 wavefronts; wavefront w
+// of workgroup g takes the rpw consecutive rows starting at (16 g + w) * rpw,
+// two at a time (both rows' loads are in flight together), writes dinp and
+// carries the dweight/dbias column sums of its rows in registers. The 16
+// wavefronts' sums are then folded pairwise through LDS (8+8, 4+4, 2+2, 1+1,
+// a fixed tree) and wavefront 0 writes the workgroup's partial row:
+// partial[g] = [dweight part (C floats) | dbias part (C floats)].
+constexpr int kBwdWaves = 16;
 template <int V>
-__global__ __launch_bounds__(kBlock) void k_ln_bwd_vec(float *__restrict__ dinp, float *__restrict__ partial,
-                                                       const float *__restrict__ dout,
-                                                       const float *__restrict__ inp,
-                                                       const float *__restrict__ weight,
-                                                       const float *__restrict__ mean,
-                                                       const float *__restrict__ rstd, int rows, int C,
-                                                       int rpb) {
-  __shared__ float red[kWavesPerBlock][2][V * kWave * 4];
+__global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
+    float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
+    const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
+    const float *__restrict__ rstd, int rows, int C, int rpw) {
+  __shared__ float4 red[kBwdWaves / 2][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int C4 = C >> 2;
@@ -136,79 +140,112 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_vec(float *__restrict__ dinp,
     dg[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     db[v] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const int row0 = blockIdx.x * rpb;
-  const int row1 = min(row0 + rpb, rows);
-  for (int row = row0 + wave; row < row1; row += kWavesPerBlock) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(inp + (size_t)row * C);
-    const float4 *dy4 = reinterpret_cast<const float4 *>(dout + (size_t)row * C);
-    float4 *dx4 = reinterpret_cast<float4 *>(dinp + (size_t)row * C);
-    float4 x[V], dy[V], dx[V];
+  const int row0 = (blockIdx.x * kBwdWaves + wave) * rpw;
+  const int row1 = min(row0 + rpw, rows);
+  for (int row = row0; row < row1; row += 2) {
+    const int nr = (row + 1 < row1) ? 2 : 1;
+    float4 x[2][V], dy[2][V], dx[2][V];
+    float m[2], r[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const int rq = q < nr ? row + q : row;
+      const float4 *x4 = reinterpret_cast<const float4 *>(inp + (size_t)rq * C);
+      const float4 *dy4 = reinterpret_cast<const float4 *>(dout + (size_t)rq * C);
+      const float4 *dx4 = reinterpret_cast<const float4 *>(dinp + (size_t)rq * C);
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        const int c4 = lane + v * kWave;
+        if (c4 < C4 && q < nr) {
+          x[q][v] = ld_nt(x4 + c4);
+          dy[q][v] = ld_nt(dy4 + c4);
+          dx[q][v] = ld_nt(dx4 + c4);
+        } else {
+          x[q][v] = dy[q][v] = dx[q][v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      m[q] = mean[rq];
+      r[q] = rstd[rq];
+    }
+    float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
+    float4 xh[2][V], dn[2][V];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        xh[q][v].x = (x[q][v].x - m[q]) * r[q]; dn[q][v].x = dy[q][v].x * w[v].x;
+        xh[q][v].y = (x[q][v].y - m[q]) * r[q]; dn[q][v].y = dy[q][v].y * w[v].y;
+        xh[q][v].z = (x[q][v].z - m[q]) * r[q]; dn[q][v].z = dy[q][v].z * w[v].z;
+        xh[q][v].w = (x[q][v].w - m[q]) * r[q]; dn[q][v].w = dy[q][v].w * w[v].w;
+        if (lane + v * kWave < C4) {
+          s1[q] += dn[q][v].x; s2[q] += dn[q][v].x * xh[q][v].x;
+          s1[q] += dn[q][v].y; s2[q] += dn[q][v].y * xh[q][v].y;
+          s1[q] += dn[q][v].z; s2[q] += dn[q][v].z * xh[q][v].z;
+          s1[q] += dn[q][v].w; s2[q] += dn[q][v].w * xh[q][v].w;
+        }
+      }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      s1[0] += __shfl_xor(s1[0], off);
+      s2[0] += __shfl_xor(s2[0], off);
+      s1[1] += __shfl_xor(s1[1], off);
+      s2[1] += __shfl_xor(s2[1], off);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      if (q >= nr) break;
+      const float dnm = s1[q] / Cf, dnxm = s2[q] / Cf;
+      float4 *dx4 = reinterpret_cast<float4 *>(dinp + (size_t)(row + q) * C);
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        const int c4 = lane + v * kWave;
+        if (c4 < C4) {
+          float4 o;
+          o.x = dx[q][v].x + r[q] * (dn[q][v].x - dnm - xh[q][v].x * dnxm);
+          o.y = dx[q][v].y + r[q] * (dn[q][v].y - dnm - xh[q][v].y * dnxm);
+          o.z = dx[q][v].z + r[q] * (dn[q][v].z - dnm - xh[q][v].z * dnxm);
+          o.w = dx[q][v].w + r[q] * (dn[q][v].w - dnm - xh[q][v].w * dnxm);
+          st_nt(dx4 + c4, o);
+          db[v].x += dy[q][v].x; dg[v].x += dy[q][v].x * xh[q][v].x;
+          db[v].y += dy[q][v].y; dg[v].y += dy[q][v].y * xh[q][v].y;
+          db[v].z += dy[q][v].z; dg[v].z += dy[q][v].z * xh[q][v].z;
+          db[v].w += dy[q][v].w; dg[v].w += dy[q][v].w * xh[q][v].w;
+        }
+      }
+    }
+  }
+  // fold the 16 wavefronts' column sums: upper half adds into lower half
+#pragma unroll
+  for (int half = kBwdWaves / 2; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        red[wave - half][0][v * kWave + lane] = dg[v];
+        red[wave - half][1][v * kWave + lane] = db[v];
+      }
+    }
+    __syncthreads();
+    if (wave < half) {
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        const float4 g = red[wave][0][v * kWave + lane], b = red[wave][1][v * kWave + lane];
+        dg[v].x += g.x; dg[v].y += g.y; dg[v].z += g.z; dg[v].w += g.w;
+        db[v].x += b.x; db[v].y += b.y; db[v].z += b.z; db[v].w += b.w;
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    float4 *pg = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C);
+    float4 *pb = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C + C);
 #pragma unroll
     for (int v = 0; v < V; v++) {
       const int c4 = lane + v * kWave;
       if (c4 < C4) {
-        x[v] = x4[c4];
-        dy[v] = dy4[c4];
-        dx[v] = dx4[c4];
-      } else {
-        x[v] = dy[v] = dx[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        pg[c4] = dg[v];
+        pb[c4] = db[v];
       }
     }
-    const float m = mean[row], r = rstd[row];
-    float s1 = 0.0f, s2 = 0.0f;
-    float4 xh[V], dn[V];
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      xh[v].x = (x[v].x - m) * r; dn[v].x = dy[v].x * w[v].x;
-      xh[v].y = (x[v].y - m) * r; dn[v].y = dy[v].y * w[v].y;
-      xh[v].z = (x[v].z - m) * r; dn[v].z = dy[v].z * w[v].z;
-      xh[v].w = (x[v].w - m) * r; dn[v].w = dy[v].w * w[v].w;
-      if (lane + v * kWave < C4) {
-        s1 += dn[v].x; s2 += dn[v].x * xh[v].x;
-        s1 += dn[v].y; s2 += dn[v].y * xh[v].y;
-        s1 += dn[v].z; s2 += dn[v].z * xh[v].z;
-        s1 += dn[v].w; s2 += dn[v].w * xh[v].w;
-      }
-    }
-    s1 = wave_sum(s1);
-    s2 = wave_sum(s2);
-    const float dnm = s1 / Cf, dnxm = s2 / Cf;
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      const int c4 = lane + v * kWave;
-      if (c4 < C4) {
-        float4 o;
-        o.x = dx[v].x + r * (dn[v].x - dnm - xh[v].x * dnxm);
-        o.y = dx[v].y + r * (dn[v].y - dnm - xh[v].y * dnxm);
-        o.z = dx[v].z + r * (dn[v].z - dnm - xh[v].z * dnxm);
-        o.w = dx[v].w + r * (dn[v].w - dnm - xh[v].w * dnxm);
-        dx4[c4] = o;
-        db[v].x += dy[v].x; dg[v].x += dy[v].x * xh[v].x;
-        db[v].y += dy[v].y; dg[v].y += dy[v].y * xh[v].y;
-        db[v].z += dy[v].z; dg[v].z += dy[v].z * xh[v].z;
-        db[v].w += dy[v].w; dg[v].w += dy[v].w * xh[v].w;
-      }
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < V; v++) {
-    const int c = (lane + v * kWave) * 4;
-    red[wave][0][c + 0] = dg[v].x; red[wave][0][c + 1] = dg[v].y;
-    red[wave][0][c + 2] = dg[v].z; red[wave][0][c + 3] = dg[v].w;
-    red[wave][1][c + 0] = db[v].x; red[wave][1][c + 1] = db[v].y;
-    red[wave][1][c + 2] = db[v].z; red[wave][1][c + 3] = db[v].w;
-  }
-  __syncthreads();
-  float *prow = partial + (size_t)blockIdx.x * 2 * C;
-  for (int c = threadIdx.x; c < C; c += kBlock) {
-    float g = red[0][0][c], b = red[0][1][c];
-#pragma unroll
-    for (int k = 1; k < kWavesPerBlock; k++) {
-      g += red[k][0][c];
-      b += red[k][1][c];
-    }
-    prow[c] = g;
-    prow[C + c] = b;
   }
 }
 
@@ -260,9 +297,11 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_scalar(float *dinp, float *pa
 
 // Column totals of the partial rows in workgroup order, added to dweight
 // (columns [0,C)) and dbias (columns [C,2C)). Block: 64 columns x 16 groups;
-// group k sums partial rows k, k+16, ...; the 16 group sums are then added in
-// group order.
+// group k sums the partial rows [k*J, (k+1)*J), J = ceil(nblk/16) <= 32, with
+// all its loads issued before the first add; the 16 group sums are then added
+// in group order.
 constexpr int kRedGroups = 16;
+constexpr int kRedMaxPer = 32;
 __global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dweight, float *dbias,
                                                                       const float *partial, int nblk,
                                                                       int C) {
@@ -271,9 +310,15 @@ __global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dwe
   const int g = threadIdx.x >> 6;
   const int col = blockIdx.x * kWave + cl;
   const int C2 = 2 * C;
+  const int J = (nblk + kRedGroups - 1) / kRedGroups;
+  const int j0 = g * J, j1 = min(j0 + J, nblk);
+  float v[kRedMaxPer];
+#pragma unroll
+  for (int q = 0; q < kRedMaxPer; q++)
+    v[q] = (col < C2 && j0 + q < j1) ? partial[(size_t)(j0 + q) * C2 + col] : 0.0f;
   float acc = 0.0f;
-  if (col < C2)
-    for (int j = g; j < nblk; j += kRedGroups) acc += partial[(size_t)j * C2 + col];
+#pragma unroll
+  for (int q = 0; q < kRedMaxPer; q++) acc += v[q];
   red[g][cl] = acc;
   __syncthreads();
   if (g == 0 && col < C2) {
@@ -294,6 +339,7 @@ bool vec_ok(int C, std::initializer_list<const void *> ptrs) {
   return true;
 }
 
+// Scalar path: workgroups of 4 wavefronts, at most 512 of them.
 void bwd_shape(int rows, int *nblk, int *rpb) {
   int nb = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
   if (nb > kMaxBwdBlocks) nb = kMaxBwdBlocks;
@@ -304,11 +350,21 @@ void bwd_shape(int rows, int *nblk, int *rpb) {
   *nblk = (rows + per - 1) / per;
 }
 
+// Vector path: 16 wavefronts per workgroup, rpw rows each, at most 256
+// workgroups (one per CU), so the reduce reads at most 16 rows per group.
+void bwd_shape_vec(int rows, int *nblk, int *rpw) {
+  const int per_wave = (rows + 256 * kBwdWaves - 1) / (256 * kBwdWaves);
+  *rpw = per_wave < 1 ? 1 : per_wave;
+  *nblk = (rows + kBwdWaves * *rpw - 1) / (kBwdWaves * *rpw);
+}
+
 }  // namespace
 
 size_t layernorm_backward_scratch(int rows, int C) {
-  int nblk, rpb;
+  int nblk, rpb, nv, rpw;
   bwd_shape(rows, &nblk, &rpb);
+  bwd_shape_vec(rows, &nv, &rpw);
+  if (nv > nblk) nblk = nv;
   return (size_t)nblk * 2 * (size_t)C * sizeof(float);
 }
 
@@ -336,22 +392,25 @@ int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const f
                               const float *inp, const float *weight, const float *mean,
                               const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
-  int nblk, rpb;
-  bwd_shape(rows, &nblk, &rpb);
   float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
   if (!partial) return 3;
-  const dim3 grid(nblk), block(kBlock);
+  int nblk;
   if (vec_ok(C, {dinp, dout, inp, weight})) {
+    int rpw;
+    bwd_shape_vec(rows, &nblk, &rpw);
     const int V = ((C >> 2) + kWave - 1) / kWave;
+    const dim3 grid(nblk), block(kBwdWaves * kWave);
     switch (V) {
 #define UGK_LN_BWD(v) \
-  case v: hipLaunchKernelGGL(k_ln_bwd_vec<v>, grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpb); break;
+  case v: hipLaunchKernelGGL(k_ln_bwd_vec<v>, grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw); break;
       UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
       UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
 #undef UGK_LN_BWD
     }
   } else {
-    hipLaunchKernelGGL(k_ln_bwd_scalar, grid, block, 0, stream(), dinp, partial, dout, inp, weight,
+    int rpb;
+    bwd_shape(rows, &nblk, &rpb);
+    hipLaunchKernelGGL(k_ln_bwd_scalar, dim3(nblk), dim3(kBlock), 0, stream(), dinp, partial, dout, inp, weight,
                        mean, rstd, rows, C, rpb);
   }
   hipLaunchKernelGGL(k_ln_bwd_reduce, dim3(grid_for((size_t)2 * C, kWave)), dim3(kWave * kRedGroups), 0,

@@ -2,34 +2,60 @@
 //
 // Same operations as ugk_libm.h (the line-by-line restatement of glibc's
 // expm1f/tanhf/log1pf), in the same order and with the same rounding, but
-// without data-dependent branches: every case of the reference is computed
-// and the right one selected, so a wavefront whose lanes fall in different
-// cases runs each piece of arithmetic once instead of once per case, and
-// tanhf evaluates one expm1f instead of two inlined copies. Divisions use
-// ugk_div, a reciprocal with Newton-Raphson correction.
+// arranged for wavefronts:
+//   * tanhf evaluates one expm1f instead of two inlined copies, and that
+//     expm1f is specialised to the arguments tanhf gives it (2|x| for
+//     |x| >= 1, -2|x| below), with the fdlibm cases computed side by side and
+//     selected rather than branched on, since neighbouring lanes of a GELU
+//     input routinely fall in different cases;
+//   * log1pf keeps branches, because the inputs softplus feeds it (expf of a
+//     weight's rho) are coherent across a wavefront and the common case then
+//     runs alone;
+//   * divisions are a reciprocal seed plus Newton-Raphson corrections
+//     (ugk_div) rather than the compiler's general IEEE sequence.
 //
-// That this equals ugk_libm.h on every one of the 2^32 inputs is checked on
-// the GPU by ugk_diag_math_mismatch (tests/test_parity_gpu.py); ugk_libm.h
-// itself equals the host glibc on every input (oracle/libm_exhaustive.cpp).
+// That each function here equals its ugk_libm.h counterpart on every one of
+// the 2^32 inputs is checked on the GPU by ugk_diag_math_mismatch
+// (tests/test_parity_gpu.py); ugk_libm.h itself equals the host glibc on
+// every input (oracle/libm_exhaustive.cpp).
 #pragma once
 
 #include "ugk_libm.h"
 
 // a / b rounded to nearest-even, for the operand ranges these functions
-// produce (b normal, quotient normal or zero): v_rcp_f32 seed, one Newton step
-// on the reciprocal, then two residual corrections of the quotient.
-__device__ __forceinline__ float ugk_div(float a, float b) {
+// produce (b normal, quotient normal or zero). kSteps selects the sequence:
+//   0 the compiler's IEEE division;
+//   1 v_rcp_f32 seed, q = a*r, one residual correction;
+//   2 as 1 with the reciprocal refined by one Newton step first;
+//   3 as 2 with a second residual correction.
+template <int kSteps>
+__device__ __forceinline__ float ugk_div_t(float a, float b) {
+  if (kSteps == 0) return a / b;
   float r = __builtin_amdgcn_rcpf(b);
-  const float t = __builtin_fmaf(-b, r, 1.0f);
-  r = __builtin_fmaf(t, r, r);
+  if (kSteps >= 2) {
+    const float t = __builtin_fmaf(-b, r, 1.0f);
+    r = __builtin_fmaf(t, r, r);
+  }
   float q = a * r;
   float e = __builtin_fmaf(-b, q, a);
   q = __builtin_fmaf(e, r, q);
-  e = __builtin_fmaf(-b, q, a);
-  return __builtin_fmaf(e, r, q);
+  if (kSteps >= 3) {
+    e = __builtin_fmaf(-b, q, a);
+    q = __builtin_fmaf(e, r, q);
+  }
+  return q;
 }
 
-__device__ __forceinline__ float ugk_dev_expm1f(float x) {
+#ifndef UGK_DIV_STEPS
+#define UGK_DIV_STEPS 1
+#endif
+
+__device__ __forceinline__ float ugk_div(float a, float b) { return ugk_div_t<UGK_DIV_STEPS>(a, b); }
+
+// expm1f for any input, branch-free (used by the exhaustive diagnostic and as
+// the general form of the specialised copy inside tanhf).
+template <int kDiv>
+__device__ __forceinline__ float ugk_dev_expm1f_t(float x) {
   const float o_threshold = 8.8721679688e+01f;
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
   const float invln2 = 1.4426950216e+00f;
@@ -55,7 +81,7 @@ __device__ __forceinline__ float ugk_dev_expm1f(float x) {
   const float hxs = xr * hfx;
   const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
   const float tt = 3.0f - r1 * hfx;
-  const float e = hxs * ugk_div(r1 - tt, 6.0f - xr * tt);
+  const float e = hxs * ugk_div_t<kDiv>(r1 - tt, 6.0f - xr * tt);
   const float y0 = xr - (xr * e - hxs);  // k == 0
   float e2 = (xr * (e - c) - c);
   e2 -= hxs;
@@ -90,22 +116,72 @@ __device__ __forceinline__ float ugk_dev_expm1f(float x) {
   return y;
 }
 
-__device__ __forceinline__ float ugk_dev_tanhf(float x) {
+// expm1f(a) for the arguments tanhf passes: a = 2|x| >= 2 (so k >= 3) when
+// big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3). Arguments
+// beyond 44 (|x| >= 22) and non-finite ones give values tanhf discards.
+template <int kDiv>
+__device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
+  const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
+  const float invln2 = 1.4426950216e+00f;
+  const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f,
+              Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
+              Q5 = -2.0109921195e-07f;
+  const uint32_t ha = ugk_f2u(a) & 0x7fffffffu;
+  const bool red = ha > 0x3eb17218u;   // |a| > ln2/2
+  const bool near = ha < 0x3F851592u;  // |a| < 1.5 ln2 (never when big)
+  const float kf = fminf(invln2 * a + (big ? 0.5f : -0.5f), 200.0f);
+  const int k = red ? ((near && !big) ? -1 : (int)kf) : 0;
+  const float t = (float)k;
+  const float hi = a - t * ln2_hi;
+  const float lo = t * ln2_lo;
+  const float xr = hi - lo;
+  const float c = (hi - xr) - lo;
+  const float hfx = 0.5f * xr;
+  const float hxs = xr * hfx;
+  const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  const float tt = 3.0f - r1 * hfx;
+  const float e = hxs * ugk_div_t<kDiv>(r1 - tt, 6.0f - xr * tt);
+  float e2 = (xr * (e - c) - c);
+  e2 -= hxs;
+  const float d = e2 - xr;
+  // scaled cases share "base - d, then add k to the exponent":
+  //   k <= -2 or k > 56: base 1 (and 1 is subtracted after scaling);
+  //   3 <= k < 23:       base 1 - 2^-k;
+  //   23 <= k <= 56:     (xr - (e2 + 2^-k)) + 1 instead.
+  const bool lo_k = big && k < 23;
+  const bool hi_k = big && k >= 23 && k <= 56;
+  const int ks = lo_k ? k : 31;
+  const float base = ugk_u2f(0x3f800000u - (0x1000000u >> ks));  // 1 - 2^-k, or 1 when ks = 31
+  float pre = base - d;
+  const float thi = ugk_u2f((uint32_t)(0x7f - k) << 23);
+  const float yhi = (xr - (e2 + thi)) + 1.0f;
+  pre = hi_k ? yhi : pre;
+  float y = ugk_u2f(ugk_f2u(pre) + ((uint32_t)k << 23));
+  y = (lo_k || hi_k) ? y : y - 1.0f;
+  y = (k == -1) ? 0.5f * (xr - e2) - 0.5f : y;
+  y = (k == 0) ? ((ha < 0x33000000u) ? a : xr - (xr * e - hxs)) : y;
+  return y;
+}
+
+template <int kDiv>
+__device__ __forceinline__ float ugk_dev_tanhf_t(float x) {
   const uint32_t jx = ugk_f2u(x);
   const uint32_t ix = jx & 0x7fffffffu;
-  const float ax = ugk_u2f(ix);
   const bool big = ix >= 0x3f800000u;  // |x| >= 1
-  const float t = ugk_dev_expm1f(big ? 2.0f * ax : -2.0f * ax);
-  const float q = ugk_div(big ? 2.0f : -t, t + 2.0f);
+  const float a2 = 2.0f * ugk_u2f(ix);
+  const float a = big ? a2 : -a2;
+  const float t = ugk_dev_expm1f_tanh<kDiv>(a, big);
+  const float q = ugk_div_t<kDiv>(big ? 2.0f : -t, t + 2.0f);
   float z = big ? 1.0f - q : q;
   z = (ix >= 0x41b00000u) ? 1.0f : z;  // |x| >= 22 and +-inf
-  float r = (jx >> 31) ? -z : z;
+  float r = ugk_u2f(ugk_f2u(z) ^ (jx & 0x80000000u));
   r = (ix < 0x24000000u) ? x * (1.0f + x) : r;  // |x| < 2^-55, and +-0
   r = (ix > 0x7f800000u) ? x + x : r;            // nan
   return r;
 }
 
-__device__ __forceinline__ float ugk_dev_log1pf(float x) {
+template <int kDiv>
+__device__ __forceinline__ float ugk_dev_log1pf_t(float x) {
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
   const float Lp1 = 6.6666668653e-01f, Lp2 = 4.0000000596e-01f,
               Lp3 = 2.8571429849e-01f, Lp4 = 2.2222198546e-01f,
@@ -113,39 +189,48 @@ __device__ __forceinline__ float ugk_dev_log1pf(float x) {
               Lp7 = 1.4798198640e-01f;
   const int32_t hx = (int32_t)ugk_f2u(x);
   const int32_t ax = hx & 0x7fffffff;
-  const bool low = hx < 0x3ed413d7;                              // x < 0.41422
-  const bool k0 = low && (hx > 0 || hx <= (int32_t)0xbe95f61fu);  // f = x, k = 0
-  // 1 + x = 2^k (1 + f)
-  const bool mid = hx < 0x5a000000;
-  const float u1 = 1.0f + x;
-  const float u = mid ? u1 : x;
-  int32_t hu = (int32_t)ugk_f2u(u);
-  int k = (hu >> 23) - 127;
-  float c = (k > 0) ? 1.0f - (u1 - x) : x - (u1 - 1.0f);
-  c = mid ? ugk_div(c, u1) : 0.0f;
-  hu &= 0x007fffff;
-  const bool lm = hu < 0x3504f7;
-  const float un = ugk_u2f((uint32_t)(hu | (lm ? 0x3f800000 : 0x3f000000)));
-  k = lm ? k : k + 1;
-  hu = lm ? hu : (0x00800000 - hu) >> 2;
-  const float f = k0 ? x : un - 1.0f;
-  k = k0 ? 0 : k;
-  hu = k0 ? 1 : hu;
+  int k = 0, hu = 1;
+  float f = x, c = 0.0f;
+  if (!(hx < 0x3ed413d7 && (hx > 0 || hx <= (int32_t)0xbe95f61fu))) {  // 1 + x = 2^k (1 + f)
+    float u;
+    if (hx < 0x5a000000) {
+      u = 1.0f + x;
+      hu = (int32_t)ugk_f2u(u);
+      k = (hu >> 23) - 127;
+      c = (k > 0) ? 1.0f - (u - x) : x - (u - 1.0f);
+      c = ugk_div_t<kDiv>(c, u);
+    } else {
+      u = x;
+      hu = (int32_t)ugk_f2u(u);
+      k = (hu >> 23) - 127;
+      c = 0.0f;
+    }
+    hu &= 0x007fffff;
+    if (hu < 0x3504f7) {
+      u = ugk_u2f((uint32_t)(hu | 0x3f800000));
+    } else {
+      k += 1;
+      u = ugk_u2f((uint32_t)(hu | 0x3f000000));
+      hu = (0x00800000 - hu) >> 2;
+    }
+    f = u - 1.0f;
+  }
   const float fk = (float)k;
   const float hfsq = 0.5f * f * f;
-  // |f| < 2^-20
-  const float R0 = hfsq * (1.0f - 0.66666666666666666f * f);
-  const float rz = (k == 0) ? 0.0f : fk * ln2_hi + (c + fk * ln2_lo);
-  const float rs = (k == 0) ? f - R0 : fk * ln2_hi - ((R0 - (c + fk * ln2_lo)) - f);
-  const float r_hu0 = (f == 0.0f) ? rz : rs;
-  // general
-  const float s = ugk_div(f, 2.0f + f);
-  const float z = s * s;
-  const float R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
-  const float rg = (k == 0) ? f - (hfsq - s * (hfsq + R))
-                            : fk * ln2_hi - ((hfsq - (s * (hfsq + R) + (c + fk * ln2_lo))) - f);
-  float r = (hu == 0) ? r_hu0 : rg;
-  if (low) {
+  float r;
+  if (hu == 0) {  // |f| < 2^-20
+    const float R0 = hfsq * (1.0f - 0.66666666666666666f * f);
+    const float rz = (k == 0) ? 0.0f : fk * ln2_hi + (c + fk * ln2_lo);
+    const float rs = (k == 0) ? f - R0 : fk * ln2_hi - ((R0 - (c + fk * ln2_lo)) - f);
+    r = (f == 0.0f) ? rz : rs;
+  } else {
+    const float s = ugk_div_t<kDiv>(f, 2.0f + f);
+    const float z = s * s;
+    const float R = z * (Lp1 + z * (Lp2 + z * (Lp3 + z * (Lp4 + z * (Lp5 + z * (Lp6 + z * Lp7))))));
+    r = (k == 0) ? f - (hfsq - s * (hfsq + R))
+                 : fk * ln2_hi - ((hfsq - (s * (hfsq + R) + (c + fk * ln2_lo))) - f);
+  }
+  if (hx < 0x3ed413d7) {
     if (ax < 0x31000000) r = (ax < 0x24800000) ? x : x - x * x * 0.5f;  // |x| < 2^-29
     if (ax >= 0x3f800000) r = (x == -1.0f) ? ugk_u2f(0xff800000u) : ugk_u2f(0x7fc00000u);
   } else if (hx >= 0x7f800000) {
@@ -153,6 +238,10 @@ __device__ __forceinline__ float ugk_dev_log1pf(float x) {
   }
   return r;
 }
+
+__device__ __forceinline__ float ugk_dev_expm1f(float x) { return ugk_dev_expm1f_t<UGK_DIV_STEPS>(x); }
+__device__ __forceinline__ float ugk_dev_tanhf(float x) { return ugk_dev_tanhf_t<UGK_DIV_STEPS>(x); }
+__device__ __forceinline__ float ugk_dev_log1pf(float x) { return ugk_dev_log1pf_t<UGK_DIV_STEPS>(x); }
 
 __device__ __forceinline__ float ugk_dev_softplusf(float x) {
   return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf(x));

@@ -255,12 +255,16 @@ def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
 
 
 MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4}
+# the same functions with division sequence s (0 IEEE, 1-3 reciprocal + corrections)
+MATH_FUNCTIONS.update({f"{name}/div{s}": base + s for name, base in (("tanhf", 10), ("log1pf", 20), ("expm1f", 30))
+                       for s in range(4)})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
     """(mismatches, first) of the kernels' float math against its IEEE restatement over bit patterns."""
     n, first = ctypes.c_ulonglong(0), ctypes.c_uint(0)
-    _check(lib.ugk_diag_math_mismatch(MATH_FUNCTIONS[fn], lo, count, ctypes.byref(n), ctypes.byref(first)))
+    _check(lib.ugk_diag_math_mismatch(MATH_FUNCTIONS[fn], lo, min(count, (1 << 32) - lo), ctypes.byref(n),
+                                      ctypes.byref(first)))
     return int(n.value), int(first.value)
 
 
