@@ -17,11 +17,13 @@
 //                  power of two, linear probing, atomicCAS). Each row gets its
 //                  slot and an arrival rank from atomicAdd on the slot count.
 //                  The same launch also runs the dwpe threads (first chunk).
-//     K2 place   - one workgroup: exclusive scan of the slot counts gives each
-//                  bucket's start; row i goes to start[slot]+rank together
-//                  with its bucket's start, size and token; the table is then
-//                  cleared for the next chunk.
-//     K3 add     - one wavefront per placed position. A bucket of n rows is
+//     K2 scan    - exclusive scan of the slot counts in blocks of 4096 slots
+//                  (the bucket starts within a block, and block totals).
+//     K2 place   - thread per row: bucket start = earlier blocks' totals +
+//                  its start within the block; row i goes to start + rank
+//                  together with its bucket's start, size and token.
+//     K3 add     - (also clears the table for the next chunk or call)
+//                  one wavefront per placed position. A bucket of n rows is
 //                  handled by the wavefront at its first position when
 //                  n <= 64: the n row ids are ranked by comparison (ids are
 //                  distinct) and the rows added in ascending order, 4 channels
@@ -79,11 +81,12 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_scalar(float *out, const int
 struct EncState {
   int *keys;       // [kTableMax] token per slot, kEmpty when free (kept clean between calls)
   int *cnt;        // [kTableMax] rows per slot (kept zero between calls)
-  int *bstart;     // [kTableMax] bucket start of a slot (valid during a call)
+  int *bstart;     // [kTableMax] bucket start of a slot within its scan block (valid during a call)
   int *slot_of;    // [kChunk] slot of row i of the chunk (-1: skipped)
   int *rank_of;    // [kChunk] arrival rank of row i within its slot
   int4 *meta;      // [kChunk] per placed position: {bucket start, bucket size, token, row}
   int *total;      // [1] number of placed rows
+  int *btot;       // [kTableMax / kScanSpan] slot count of each scan block
 };
 
 __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift) {
@@ -163,28 +166,18 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int
   }
 }
 
-// K2: one workgroup of 1024 threads. Exclusive scan of the slot counts over
-// [0, tsize) gives each bucket's start; every row i is placed at
-// start[slot] + rank with its bucket's metadata; the table is then returned
-// to empty for the next chunk or call.
-constexpr int kPlaceThreads = 1024;
-constexpr int kPlaceBatch = 8;
-__global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int n, int tsize) {
-  __shared__ int wsum[kPlaceThreads / kWave];
-  __shared__ int wpre[kPlaceThreads / kWave];
+// K2a: exclusive scan of the slot counts within blocks of kScanSpan slots
+// (1024 threads x 4 slots): bstart[h] = slots before h in its block,
+// btot[b] = the block's total.
+constexpr int kScanThreads = 1024;
+constexpr int kScanSpan = 4 * kScanThreads;
+__global__ __launch_bounds__(kScanThreads) void k_enc_bwd_scan(EncState s, int tsize) {
+  __shared__ int wsum[kScanThreads / kWave];
   const int tid = threadIdx.x;
-  const int per = (tsize + kPlaceThreads - 1) / kPlaceThreads;
-  const int lo = min(tid * per, tsize), hi = min(lo + per, tsize);
-  int local = 0;
-  for (int h0 = lo; h0 < hi; h0 += kPlaceBatch) {
-    int c[kPlaceBatch];
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++) c[q] = (h0 + q < hi) ? s.cnt[h0 + q] : 0;
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++) local += c[q];
-  }
-  // exclusive scan of `local` over the workgroup: wave inclusive scan, then
-  // wave totals
+  const int h0 = blockIdx.x * kScanSpan + tid * 4;
+  int4 c = make_int4(0, 0, 0, 0);
+  if (h0 < tsize) c = *reinterpret_cast<const int4 *>(s.cnt + h0);  // tsize is a multiple of 64
+  const int local = c.x + c.y + c.z + c.w;
   const int lane = tid & (kWave - 1), wave = tid >> 6;
   int inc = local;
 #pragma unroll
@@ -194,50 +187,37 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
   }
   if (lane == kWave - 1) wsum[wave] = inc;
   __syncthreads();
-  if (tid == 0) {
+  int before = 0;
+  for (int w = 0; w < wave; w++) before += wsum[w];
+  if (tid == kScanThreads - 1) s.btot[blockIdx.x] = before + inc;
+  const int e = before + inc - local;
+  if (h0 < tsize)
+    *reinterpret_cast<int4 *>(s.bstart + h0) = make_int4(e, e + c.x, e + c.x + c.y, e + c.x + c.y + c.z);
+}
+
+// K2b: place every row at (start of its bucket) + (its arrival rank), with its
+// bucket's start, size and token. Bucket start = totals of the scan blocks
+// before the slot's block + bstart[slot].
+constexpr int kMaxScanBlocks = kTableMax / kScanSpan;
+__global__ __launch_bounds__(kBlock) void k_enc_bwd_place(EncState s, int n, int nscan) {
+  __shared__ int bpre[kMaxScanBlocks + 1];
+  if (threadIdx.x == 0) {
     int run = 0;
-    for (int w = 0; w < kPlaceThreads / kWave; w++) {
-      wpre[w] = run;
-      run += wsum[w];
+    for (int b = 0; b < nscan; b++) {
+      bpre[b] = run;
+      run += s.btot[b];
     }
-    s.total[0] = run;
+    bpre[nscan] = run;
+    if (blockIdx.x == 0) s.total[0] = run;
   }
   __syncthreads();
-  int start = wpre[wave] + inc - local;
-  for (int h0 = lo; h0 < hi; h0 += kPlaceBatch) {
-    int c[kPlaceBatch];
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++) c[q] = (h0 + q < hi) ? s.cnt[h0 + q] : 0;
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++)
-      if (h0 + q < hi) {
-        s.bstart[h0 + q] = start;
-        start += c[q];
-      }
-  }
-  __syncthreads();
-  for (int i0 = tid * kPlaceBatch; i0 < n; i0 += kPlaceThreads * kPlaceBatch) {
-    int h[kPlaceBatch], rk[kPlaceBatch], st[kPlaceBatch], ct[kPlaceBatch], tk[kPlaceBatch];
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++) {
-      h[q] = (i0 + q < n) ? s.slot_of[i0 + q] : -1;
-      rk[q] = (i0 + q < n) ? s.rank_of[i0 + q] : 0;
-    }
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++) {
-      st[q] = h[q] >= 0 ? s.bstart[h[q]] : 0;
-      ct[q] = h[q] >= 0 ? s.cnt[h[q]] : 0;
-      tk[q] = h[q] >= 0 ? s.keys[h[q]] : 0;
-    }
-#pragma unroll
-    for (int q = 0; q < kPlaceBatch; q++)
-      if (h[q] >= 0) s.meta[st[q] + rk[q]] = make_int4(st[q], ct[q], tk[q], i0 + q);
-  }
-  __syncthreads();
-  for (int h = lo; h < hi; h++) {
-    s.keys[h] = kEmpty;
-    s.cnt[h] = 0;
-  }
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const int h = s.slot_of[i];
+  if (h < 0) return;
+  const int rk = s.rank_of[i];
+  const int st = bpre[h / kScanSpan] + s.bstart[h];
+  s.meta[st + rk] = make_int4(st, s.cnt[h], s.keys[h], i);
 }
 
 // K3: add the buckets, one wavefront per placed position. Dynamic LDS: per
@@ -245,10 +225,15 @@ __global__ __launch_bounds__(kPlaceThreads) void k_enc_bwd_place(EncState s, int
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__restrict__ dwte,
                                                         const float *__restrict__ dout, int n, int C,
-                                                        int words) {
+                                                        int words, int tsize) {
   extern __shared__ unsigned lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
+  // K2b was the table's last reader: return the used slots to empty
+  for (int h = blockIdx.x * kBlock + threadIdx.x; h < tsize; h += gridDim.x * kBlock) {
+    s.keys[h] = kEmpty;
+    s.cnt[h] = 0;
+  }
   const int p = blockIdx.x * kWavesPerBlock + wave;
   if (p >= n || p >= s.total[0]) return;
   const int per_wave = words > kSmall ? words : kSmall;
@@ -343,7 +328,8 @@ __global__ void k_enc_init(EncState s) {
 }
 
 size_t state_bytes() {
-  return ((size_t)3 * kTableMax + (size_t)2 * kChunk + 64) * sizeof(int) + (size_t)kChunk * sizeof(int4);
+  return ((size_t)3 * kTableMax + (size_t)2 * kChunk + 64 + kMaxScanBlocks) * sizeof(int) +
+         (size_t)kChunk * sizeof(int4);
 }
 
 EncState carve(void *base) {
@@ -356,7 +342,8 @@ EncState carve(void *base) {
   s.bstart = p; p += kTableMax;
   s.slot_of = p; p += kChunk;
   s.rank_of = p; p += kChunk;
-  s.total = p;
+  s.total = p; p += 64;
+  s.btot = p;
   return s;
 }
 
@@ -421,16 +408,18 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     else
       hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), s,
                          inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
-    hipLaunchKernelGGL(k_enc_bwd_place, dim3(1), dim3(kPlaceThreads), 0, stream(), s, n, tsize);
+    const int nscan = (tsize + kScanSpan - 1) / kScanSpan;
+    hipLaunchKernelGGL(k_enc_bwd_scan, dim3(nscan), dim3(kScanThreads), 0, stream(), s, tsize);
+    hipLaunchKernelGGL(k_enc_bwd_place, dim3(ins_blocks), dim3(kBlock), 0, stream(), s, n, nscan);
     const int words = (n + 31) / 32;
     const size_t lds = (size_t)kWavesPerBlock * (size_t)(words > kSmall ? words : kSmall) * sizeof(unsigned);
     const float *dchunk = dout + (size_t)c0 * C;
     if (vec)
       hipLaunchKernelGGL(k_enc_bwd_add<true>, dim3(grid_for((size_t)n, kWavesPerBlock)), dim3(kBlock), lds,
-                         stream(), s, dwte, dchunk, n, C, words);
+                         stream(), s, dwte, dchunk, n, C, words, tsize);
     else
       hipLaunchKernelGGL(k_enc_bwd_add<false>, dim3(grid_for((size_t)n, kWavesPerBlock)), dim3(kBlock), lds,
-                         stream(), s, dwte, dchunk, n, C, words);
+                         stream(), s, dwte, dchunk, n, C, words, tsize);
   }
   return check_launch("encoder_backward");
 }

@@ -10,11 +10,10 @@
 // the registers with 64-lane butterfly sums, rstd = 1/sqrtf(var/C + 1e-5)
 // with IEEE division and square root, exactly the CPU formula.
 //
-// Backward: one wavefront per row for dinp (two butterfly sums, two rows in
-// flight per wavefront), and the dweight/dbias column sums are carried in
-// registers across the rows a wavefront visits, then combined in a fixed
-// order: the 16 wavefronts of a workgroup through an LDS tree into one
-// partial row per workgroup (at most 256 workgroups, one per CU), then the
+// Backward: one wavefront per row for dinp (two butterfly sums), and the
+// dweight/dbias column sums are carried in registers across the rows a
+// wavefront visits, then combined in a fixed order: the wavefronts of a workgroup through an LDS tree into one
+// partial row per workgroup (at most 512 workgroups), then the
 // partial rows in index order by a small second kernel that adds the totals
 // into dweight/dbias. No atomics, so the result is identical run to run.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
@@ -113,20 +112,19 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
   }
 }
 
-// Backward, register-resident rows. A workgroup is 16 wavefronts; wavefront w
-// of workgroup g takes the rpw consecutive rows starting at (16 g + w) * rpw,
-// two at a time (both rows' loads are in flight together), writes dinp and
-// carries the dweight/dbias column sums of its rows in registers. The 16
-// wavefronts' sums are then folded pairwise through LDS (8+8, 4+4, 2+2, 1+1,
-// a fixed tree) and wavefront 0 writes the workgroup's partial row:
-// partial[g] = [dweight part (C floats) | dbias part (C floats)].
-constexpr int kBwdWaves = 16;
-template <int V>
-__global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
+// Backward, register-resident rows. A workgroup is W wavefronts; wavefront w
+// of workgroup g takes the rpw consecutive rows starting at (W g + w) * rpw,
+// R at a time (the loads of R rows are in flight together), writes dinp and
+// carries the dweight/dbias column sums of its rows in registers. The W
+// wavefronts' sums are then folded pairwise through LDS (upper half into
+// lower half, a fixed tree) and wavefront 0 writes the workgroup's partial
+// row: partial[g] = [dweight part (C floats) | dbias part (C floats)].
+template <int V, int W, int R>
+__global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpw) {
-  __shared__ float4 red[kBwdWaves / 2][2][V * kWave];
+  __shared__ float4 red[W / 2][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int C4 = C >> 2;
@@ -140,14 +138,14 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
     dg[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     db[v] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const int row0 = (blockIdx.x * kBwdWaves + wave) * rpw;
+  const int row0 = (blockIdx.x * W + wave) * rpw;
   const int row1 = min(row0 + rpw, rows);
-  for (int row = row0; row < row1; row += 2) {
-    const int nr = (row + 1 < row1) ? 2 : 1;
-    float4 x[2][V], dy[2][V], dx[2][V];
-    float m[2], r[2];
+  for (int row = row0; row < row1; row += R) {
+    const int nr = min(R, row1 - row);
+    float4 x[R][V], dy[R][V], dx[R][V];
+    float m[R], r[R];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
+    for (int q = 0; q < R; q++) {
       const int rq = q < nr ? row + q : row;
       const float4 *x4 = reinterpret_cast<const float4 *>(inp + (size_t)rq * C);
       const float4 *dy4 = reinterpret_cast<const float4 *>(dout + (size_t)rq * C);
@@ -166,10 +164,12 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
       m[q] = mean[rq];
       r[q] = rstd[rq];
     }
-    float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
-    float4 xh[2][V], dn[2][V];
+    float s1[R], s2[R];
+    float4 xh[R][V], dn[R][V];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
+    for (int q = 0; q < R; q++) {
+      s1[q] = 0.0f;
+      s2[q] = 0.0f;
 #pragma unroll
       for (int v = 0; v < V; v++) {
         xh[q][v].x = (x[q][v].x - m[q]) * r[q]; dn[q][v].x = dy[q][v].x * w[v].x;
@@ -186,13 +186,14 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
-      s1[0] += __shfl_xor(s1[0], off);
-      s2[0] += __shfl_xor(s2[0], off);
-      s1[1] += __shfl_xor(s1[1], off);
-      s2[1] += __shfl_xor(s2[1], off);
+#pragma unroll
+      for (int q = 0; q < R; q++) {
+        s1[q] += __shfl_xor(s1[q], off);
+        s2[q] += __shfl_xor(s2[q], off);
+      }
     }
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
+    for (int q = 0; q < R; q++) {
       if (q >= nr) break;
       const float dnm = s1[q] / Cf, dnxm = s2[q] / Cf;
       float4 *dx4 = reinterpret_cast<float4 *>(dinp + (size_t)(row + q) * C);
@@ -214,9 +215,9 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void k_ln_bwd_vec(
       }
     }
   }
-  // fold the 16 wavefronts' column sums: upper half adds into lower half
+  // fold the W wavefronts' column sums: upper half adds into lower half
 #pragma unroll
-  for (int half = kBwdWaves / 2; half >= 1; half >>= 1) {
+  for (int half = W / 2; half >= 1; half >>= 1) {
     if (wave >= half && wave < 2 * half) {
 #pragma unroll
       for (int v = 0; v < V; v++) {
@@ -350,12 +351,17 @@ void bwd_shape(int rows, int *nblk, int *rpb) {
   *nblk = (rows + per - 1) / per;
 }
 
-// Vector path: 16 wavefronts per workgroup, rpw rows each, at most 256
-// workgroups (one per CU), so the reduce reads at most 16 rows per group.
-void bwd_shape_vec(int rows, int *nblk, int *rpw) {
-  const int per_wave = (rows + 256 * kBwdWaves - 1) / (256 * kBwdWaves);
+// Vector path: W wavefronts per workgroup (8, or 4 when a lane holds more
+// than 4 float4 of a row, so that the registers fit without spilling), rpw
+// rows each, at most kBwdMaxBlocks workgroups, so the reduce reads at most 32
+// partial rows per group.
+constexpr int kBwdRows = 1;
+constexpr int kBwdMaxBlocks = 512;
+inline int bwd_waves(int V) { return V <= 4 ? 8 : 4; }
+void bwd_shape_vec(int rows, int W, int *nblk, int *rpw) {
+  const int per_wave = (rows + kBwdMaxBlocks * W - 1) / (kBwdMaxBlocks * W);
   *rpw = per_wave < 1 ? 1 : per_wave;
-  *nblk = (rows + kBwdWaves * *rpw - 1) / (kBwdWaves * *rpw);
+  *nblk = (rows + W * *rpw - 1) / (W * *rpw);
 }
 
 }  // namespace
@@ -363,8 +369,10 @@ void bwd_shape_vec(int rows, int *nblk, int *rpw) {
 size_t layernorm_backward_scratch(int rows, int C) {
   int nblk, rpb, nv, rpw;
   bwd_shape(rows, &nblk, &rpb);
-  bwd_shape_vec(rows, &nv, &rpw);
-  if (nv > nblk) nblk = nv;
+  for (int W = 4; W <= 8; W *= 2) {
+    bwd_shape_vec(rows, W, &nv, &rpw);
+    if (nv > nblk) nblk = nv;
+  }
   return (size_t)nblk * 2 * (size_t)C * sizeof(float);
 }
 
@@ -397,12 +405,13 @@ int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const f
   int nblk;
   if (vec_ok(C, {dinp, dout, inp, weight})) {
     int rpw;
-    bwd_shape_vec(rows, &nblk, &rpw);
     const int V = ((C >> 2) + kWave - 1) / kWave;
-    const dim3 grid(nblk), block(kBwdWaves * kWave);
+    const int W = bwd_waves(V);
+    bwd_shape_vec(rows, W, &nblk, &rpw);
+    const dim3 grid(nblk), block(W * kWave);
     switch (V) {
 #define UGK_LN_BWD(v) \
-  case v: hipLaunchKernelGGL(k_ln_bwd_vec<v>, grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw); break;
+  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), kBwdRows>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw); break;
       UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
       UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
 #undef UGK_LN_BWD
