@@ -27,6 +27,7 @@ Printed JSON line (the last line of stdout):
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -61,6 +62,66 @@ def step_bytes(B, T, C, L, n_mat):
     return per, count, sum(per[k] * count[k] for k in per)
 
 
+KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwd>", "gelu_backward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluFwd>", "gelu_forward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::Materialize>", "bayes_materialize"),
+    ("k_map_vec4<ugk::(anonymous namespace)::ResidualBwd>", "residual_backward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::ResidualFwd>", "residual_forward"),
+    ("k_ln_bwd_vec", "layernorm_backward (main)"),
+    ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
+    ("k_ln_fwd_vec", "layernorm_forward"),
+    ("k_enc_fwd_vec", "encoder_forward"),
+    ("k_enc_bwd_insert", "encoder_backward (insert + dwpe)"),
+    ("k_enc_bwd_scan", "encoder_backward (scan)"),
+    ("k_enc_bwd_place", "encoder_backward (place)"),
+    ("k_enc_bwd_add", "encoder_backward (add)"),
+    ("__amd_rocclr_copyBuffer", "calibration copy 1 GiB"),
+]
+PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
+
+
+def short_name(name):
+    for key, short in KERNEL_KEYS:
+        if key in name:
+            return short
+    return None
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Per-kernel HBM bytes per dispatch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE CSVs, each
+    scaled so that the 1 GiB calibration copy reads and writes exactly 1 GiB."""
+    import csv
+    vals = {}
+    for path, counter in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        for r in csv.DictReader(open(path)):
+            k = short_name(r["Kernel_Name"])
+            if k and r["Counter_Name"] == counter:
+                vals.setdefault(k, {}).setdefault(counter, []).append(float(r["Counter_Value"]) * 1024)
+    cal = vals["calibration copy 1 GiB"]
+    f_scale = 2 ** 30 / statistics.mean(cal["FETCH_SIZE"])
+    w_scale = 2 ** 30 / statistics.mean(cal["WRITE_SIZE"])
+    out = {"fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "kernels": {}}
+    for k, d in vals.items():
+        fb = statistics.mean(d.get("FETCH_SIZE", [0])) * f_scale
+        wb = statistics.mean(d.get("WRITE_SIZE", [0])) * w_scale
+        out["kernels"][k] = {"read_bytes": round(fb), "write_bytes": round(wb), "traffic_bytes": round(fb + wb),
+                             "dispatches": len(d.get("FETCH_SIZE", []))}
+    return out
+
+
+def summarize_stats(stats_csv):
+    """Mean/min/max duration per kernel from rocprofv3 --stats (kernel_stats.csv), as text."""
+    import csv
+    lines = [f"{'kernel':34s} {'calls':>6s} {'mean us':>9s} {'min us':>9s} {'max us':>9s}"]
+    for r in csv.DictReader(open(stats_csv)):
+        k = short_name(r["Name"])
+        if k:
+            lines.append(f"{k:34s} {r['Calls']:>6s} {float(r['AverageNs']) / 1e3:9.2f} "
+                         f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f}")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,7 +129,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print per-kernel HBM traffic from two rocprofv3 --pmc runs of this script, and exit")
+    ap.add_argument("--summarize-stats", metavar="STATS_CSV",
+                    help="print per-kernel durations from a rocprofv3 --stats run of this script, and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1, sort_keys=True))
+        return
+    if args.summarize_stats:
+        print(summarize_stats(args.summarize_stats))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
@@ -212,9 +283,14 @@ def main():
     # ---- roofline of the dominant kernel (most algorithmic bytes per step)
     dom = max(per, key=lambda k: per[k] * count[k])
     achieved = per[dom] / (mean_ms[dom] * 1e-3) / 1e9
+    traffic, traffic_src = None, None
+    if os.path.exists(PMC_TRAFFIC):  # recorded by two rocprofv3 --pmc runs of this script
+        rec_k = json.load(open(PMC_TRAFFIC)).get("kernels", {}).get(dom)
+        if rec_k:
+            traffic, traffic_src = rec_k["traffic_bytes"], os.path.relpath(PMC_TRAFFIC, ROOT)
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "launch_ms": round(mean_ms[dom], 5),
-                "bytes_per_launch": per[dom]}
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "launch_ms": round(mean_ms[dom], 5), "bytes_per_launch": per[dom]}
 
     # a plain 1 GiB device-to-device copy (torch's copy kernel): the known-size
     # reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings
