@@ -13,6 +13,9 @@ native step driver of libugk.so (ugk_gpt2_layers_forward/backward).
 Printed JSON line (the last line of stdout):
     value        algorithmic bytes of the step / step time, GB/s
     ms_per_step  layer-kernel milliseconds per step (median-free mean over --steps)
+    configs      the same kernels at the shapes of BASELINE configs 2-4 (LayerNorm
+                 16384x768 and 256x384, GELU/residual over 50,331,648 values,
+                 encoder at B=16 T=1024 with uniform and Zipf(1.1) tokens), cold
     kernels      each kernel at its step shape, cold (launches rotate over buffer
                  sets totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds
                  the operands): mean ms from HIP events, GB/s from algorithmic
@@ -129,6 +132,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other BASELINE configs")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print per-kernel HBM traffic from two rocprofv3 --pmc runs of this script, and exit")
     ap.add_argument("--summarize-stats", metavar="STATS_CSV",
@@ -255,8 +259,7 @@ def main():
         "bayes_materialize": (mk_mat, 16 * n_mat, lambda d: chk(lib.ugk_bayes_materialize(
             P_(d["w"]), P_(d["mu"]), P_(d["rho"]), P_(d["eps"]), n_mat))),
     }
-    kernels, mean_ms = {}, {}
-    for name, (make, set_bytes, fn) in plan.items():
+    def time_cold(make, set_bytes, fn):
         sets = sets_for(make, set_bytes)
         for d in sets:
             fn(d)
@@ -270,15 +273,76 @@ def main():
         e.record()
         e.synchronize()
         ms = s.elapsed_time(e) / (rounds * len(sets))
-        mean_ms[name] = ms
-        gbs = per[name] / (ms * 1e-3) / 1e9
-        kernels[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
-                         "bytes": per[name], "per_step": count[name], "launches_timed": rounds * len(sets),
-                         "buffer_sets": len(sets)}
-        log(f"bench: {name:20s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak"
-            f"  ({rounds * len(sets)} launches over {len(sets)} buffer sets)")
+        n_sets = len(sets)
         del sets
         torch.cuda.empty_cache()
+        return ms, rounds * n_sets, n_sets
+
+    def record(table, name, nbytes, ms, launches, n_sets, extra=None):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        table[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                       "bytes": nbytes, "launches_timed": launches, "buffer_sets": n_sets, **(extra or {})}
+        log(f"bench: {name:34s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak"
+            f"  ({launches} launches over {n_sets} buffer sets)")
+
+    kernels, mean_ms = {}, {}
+    for name, (make, set_bytes, fn) in plan.items():
+        ms, launches, n_sets = time_cold(make, set_bytes, fn)
+        mean_ms[name] = ms
+        record(kernels, name, per[name], ms, launches, n_sets, {"per_step": count[name]})
+
+    # ---- the same kernels at the other BASELINE configurations' shapes (not part of the step)
+    configs = {}
+    if not args.no_configs:
+        import numpy as np
+        B2, T2 = 16, 1024
+        R2, N3 = B2 * T2, 16 * 1024 * 3072
+        for rows_, C_ in ((R2, 768), (256, 384)):
+            def mk_ln2(rows_=rows_, C_=C_):
+                d = {"x": rnd(rows_ * C_), "out": torch.empty(rows_ * C_, device=dev),
+                     "mean": torch.empty(rows_, device=dev), "rstd": torch.empty(rows_, device=dev),
+                     "w": torch.ones(C_, device=dev), "b": torch.zeros(C_, device=dev), "dout": rnd(rows_ * C_),
+                     "dinp": rnd(rows_ * C_), "dw": torch.zeros(C_, device=dev), "db": torch.zeros(C_, device=dev)}
+                ugk.layernorm_forward(d["out"], d["mean"], d["rstd"], d["x"], d["w"], d["b"], 1, rows_, C_)
+                return d
+            tag = f"cfg2 {rows_}x{C_}"
+            ms, l_, k_ = time_cold(mk_ln2, 20 * rows_ * C_, lambda d, rows_=rows_, C_=C_: chk(lib.ugk_layernorm_forward(
+                P_(d["out"]), P_(d["mean"]), P_(d["rstd"]), P_(d["x"]), P_(d["w"]), P_(d["b"]), 1, rows_, C_)))
+            record(configs, f"{tag} layernorm_forward", 8 * rows_ * C_ + 8 * rows_ + 8 * C_, ms, l_, k_)
+            ms, l_, k_ = time_cold(mk_ln2, 20 * rows_ * C_, lambda d, rows_=rows_, C_=C_: chk(lib.ugk_layernorm_backward(
+                P_(d["dinp"]), P_(d["dw"]), P_(d["db"]), P_(d["dout"]), P_(d["x"]), P_(d["w"]), P_(d["mean"]),
+                P_(d["rstd"]), 1, rows_, C_)))
+            record(configs, f"{tag} layernorm_backward", 16 * rows_ * C_ + 8 * rows_ + 20 * C_, ms, l_, k_)
+
+        def mk_big():
+            return {"x": rnd(N3), "y": rnd(N3), "out": torch.empty(N3, device=dev), "dout": rnd(N3)}
+        for nm, nb, fn in (
+                ("gelu_forward", 8, lambda d: chk(lib.ugk_gelu_forward(P_(d["out"]), P_(d["x"]), N3))),
+                ("gelu_backward", 16, lambda d: chk(lib.ugk_gelu_backward(P_(d["y"]), P_(d["x"]), P_(d["dout"]), N3))),
+                ("residual_forward", 12, lambda d: chk(lib.ugk_residual_forward(P_(d["out"]), P_(d["x"]), P_(d["y"]), N3))),
+                ("residual_backward", 20, lambda d: chk(lib.ugk_residual_backward(P_(d["x"]), P_(d["y"]), P_(d["dout"]), N3)))):
+            ms, l_, k_ = time_cold(mk_big, 16 * N3, fn)
+            record(configs, f"cfg3 N={N3} {nm}", nb * N3, ms, l_, k_)
+
+        wcdf = np.cumsum(1.0 / np.arange(1, V + 1, dtype=np.float64) ** 1.1)
+        wcdf /= wcdf[-1]
+        zrng = np.random.Generator(np.random.Philox(key=11))
+        for law in ("uniform", "zipf1.1"):
+            def mk_enc4(law=law):
+                if law == "uniform":
+                    tok = torch.randint(0, V, (R2,), generator=g, device=dev, dtype=torch.int32)
+                else:
+                    tok = torch.from_numpy(np.minimum(np.searchsorted(wcdf, zrng.random(R2)), V - 1)
+                                           .astype(np.int32)).to(dev)
+                return {"out": torch.empty(R2 * C, device=dev), "wte": rnd(V * C) * 0.02, "wpe": rnd(maxT * C) * 0.01,
+                        "dout": rnd(R2 * C), "inp": tok}
+            N4 = R2 * C
+            ms, l_, k_ = time_cold(mk_enc4, 16 * N4, lambda d: chk(lib.ugk_encoder_forward(
+                P_(d["out"]), P_(d["inp"]), P_(d["wte"]), P_(d["wpe"]), B2, T2, C)))
+            record(configs, f"cfg4 {law} encoder_forward", 12 * N4 + 4 * R2, ms, l_, k_)
+            ms, l_, k_ = time_cold(mk_enc4, 16 * N4, lambda d: chk(lib.ugk_encoder_backward(
+                P_(d["wte"]), P_(d["wpe"]), P_(d["dout"]), P_(d["inp"]), B2, T2, C)))
+            record(configs, f"cfg4 {law} encoder_backward", 20 * N4 + 4 * R2, ms, l_, k_)
 
     # ---- roofline of the dominant kernel (most algorithmic bytes per step)
     dom = max(per, key=lambda k: per[k] * count[k])
@@ -311,7 +375,7 @@ def main():
                    "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
                    "param_layout_n": P, "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu,
+        "kernels": kernels, "configs": configs, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
 

@@ -11,29 +11,37 @@
 //   dwpe: thread per (t, 4 channels) adds dout[0,t], dout[1,t], ... in b order.
 //
 //   dwte: the (b,t) rows are bucketed by token, then each bucket is added in
-//   ascending (b,t) order. The tokens are processed in chunks of at most
-//   kChunk rows (chunk k+1 is queued after chunk k, preserving the order):
-//     K1 insert  - open-addressing hash table keyed by token (2x the chunk,
-//                  power of two, linear probing, atomicCAS). Each row gets its
-//                  slot and an arrival rank from atomicAdd on the slot count.
-//                  The same launch also runs the dwpe threads (first chunk).
-//     K2 scan    - exclusive scan of the slot counts in blocks of 4096 slots
-//                  (the bucket starts within a block, and block totals).
-//     K2 place   - thread per row: bucket start = earlier blocks' totals +
-//                  its start within the block; row i goes to start + rank
-//                  together with its bucket's start, size and token.
-//     K3 add     - (also clears the table for the next chunk or call)
-//                  one wavefront per placed position. A bucket of n rows is
-//                  handled by the wavefront at its first position when
-//                  n <= 64: the n row ids are ranked by comparison (ids are
-//                  distinct) and the rows added in ascending order, 4 channels
-//                  per lane. For n > 64 the wavefronts at its first
-//                  ceil(C/64) positions each take 64 channels (one per lane),
-//                  so the long serial chains of a frequent token run 64-wide on
-//                  12 wavefronts at C=768; each builds an LDS bitmap of the
-//                  bucket's row ids and walks it in ascending order.
+//   ascending (b,t) order. Rows are processed in chunks of at most kChunk
+//   (chunk k+1 is queued after chunk k, preserving the order). Two launches
+//   per chunk:
+//     K1 insert  - each workgroup of 256 rows first groups its rows by
+//                  token in an LDS hash table (local count, local rank), then
+//                  one thread per distinct token probes the global open-
+//                  addressing table (2x the chunk, power of two, linear
+//                  probing, atomicCAS) and takes a block of ranks with one
+//                  atomicAdd on the slot count. A frequent token thus costs
+//                  one global atomic per workgroup, not one per row. Every
+//                  row records its slot; ranks below kCap also store the row
+//                  id in the slot's own list. The same launch runs the dwpe
+//                  threads (first chunk).
+//     K2 add     - one wavefront per slot. A bucket of at most kCap rows is
+//                  ranked by comparison (row ids are distinct) and its rows
+//                  added in ascending order, 4 channels per lane, 8 loads in
+//                  flight. A larger bucket's wavefront scans the rows' slots
+//                  in row order and writes the matching row ids, ascending,
+//                  to a list for K3.
+//     K3 large   - workgroups of 16 wavefronts, one per (large bucket, 64
+//                  channels): the wavefronts stage 256 rows at a time into LDS
+//                  (256 loads in flight, the next chunk's loads issued before
+//                  the current chunk is summed) and one wavefront adds them
+//                  in order, one channel per lane. A frequent token's long
+//                  serial chain thus waits on memory once per 256 rows.
+//   The table is double-buffered by chunk parity: K2 of chunk j clears the
+//   half that chunk j-1 used, so no kernel clears what it also reads.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
+#include <mutex>
+
 #include "ugk_internal.h"
 
 namespace ugk {
@@ -42,7 +50,6 @@ namespace {
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kChunk = 65536;            // rows per bucketing pass
 constexpr int kTableMax = 2 * kChunk;    // hash slots (power of two)
-constexpr int kSmall = kWave;            // bucket size handled by one wave
 constexpr int kEmpty = -1;
 
 // ---- forward ---------------------------------------------------------------
@@ -78,15 +85,21 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_scalar(float *out, const int
 
 // ---- backward --------------------------------------------------------------
 
-struct EncState {
-  int *keys;       // [kTableMax] token per slot, kEmpty when free (kept clean between calls)
-  int *cnt;        // [kTableMax] rows per slot (kept zero between calls)
-  int *bstart;     // [kTableMax] bucket start of a slot within its scan block (valid during a call)
-  int *slot_of;    // [kChunk] slot of row i of the chunk (-1: skipped)
-  int *rank_of;    // [kChunk] arrival rank of row i within its slot
-  int4 *meta;      // [kChunk] per placed position: {bucket start, bucket size, token, row}
-  int *total;      // [1] number of placed rows
-  int *btot;       // [kTableMax / kScanSpan] slot count of each scan block
+constexpr int kCap = 32;                 // rows kept in a slot's own list
+constexpr int kMaxLarge = kChunk / (kCap + 1) + 1;
+
+struct EncTable {  // one half of the double-buffered state
+  int *keys;       // [kTableMax] token per slot, kEmpty when free
+  int *cnt;        // [kTableMax] rows per slot
+  int *counters;   // [0] unused, [1] large buckets, [2] sorted-id pool use
+  int *large_j;    // [kTableMax] index of a large slot in the large-bucket list
+};
+
+struct EncShared {
+  int *rows;       // [kTableMax * kCap] row ids by (slot, rank < kCap)
+  int *slot_of;    // [kChunk] slot of each row of the chunk (-1: skipped)
+  int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, 0}
+  int *pool;       // [kChunk] row ids of the large buckets, each bucket ascending
 };
 
 __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift) {
@@ -95,36 +108,63 @@ __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift)
 
 // K1: insert the chunk's rows; blocks past the insert range run dwpe.
 template <bool kVec>
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int *__restrict__ inp, int n,
-                                                           unsigned mask, int shift, int ins_blocks,
-                                                           float *dwpe, const float *dout, int B, int T,
-                                                           int C) {
+__global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShared sh, const int *__restrict__ inp,
+                                                           int n, unsigned mask, int shift, int ins_blocks,
+                                                           float *dwpe, const float *dout, int B, int T, int C) {
   if ((int)blockIdx.x < ins_blocks) {
+    constexpr int kL = 2 * kBlock;  // LDS table slots
+    __shared__ int ltok[kL], lcnt[kL], lslot[kL], lbase[kL];
+    for (int e = threadIdx.x; e < kL; e += kBlock) {
+      ltok[e] = kEmpty;
+      lcnt[e] = 0;
+    }
+    __syncthreads();
     const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
-    const int tok = inp[i];
-    if (tok < 0) {
-      s.slot_of[i] = -1;
-      return;
-    }
-    // At most n distinct tokens occupy 2n or more slots, so a free or matching
-    // slot is always found; the probe count is bounded all the same.
-    unsigned h = hash_slot(tok, mask, shift);
-    bool found = false;
-    for (unsigned probe = 0; probe <= mask; probe++) {
-      const int prev = atomicCAS(&s.keys[h], kEmpty, tok);
-      if (prev == kEmpty || prev == tok) {
-        found = true;
-        break;
+    const int tok = i < n ? inp[i] : -1;
+    int e = -1, lrank = 0;
+    if (tok >= 0) {  // at most 256 distinct tokens in 512 slots: always found
+      e = (int)hash_slot(tok, kL - 1, 32 - 9);
+      for (int probe = 0; probe < kL; probe++) {
+        const int prev = atomicCAS(&ltok[e], kEmpty, tok);
+        if (prev == kEmpty || prev == tok) break;
+        e = (e + 1) & (kL - 1);
       }
-      h = (h + 1) & mask;
+      lrank = atomicAdd(&lcnt[e], 1);
     }
-    if (!found) {
-      s.slot_of[i] = -1;
-      return;
+    __syncthreads();
+    for (int f = threadIdx.x; f < kL; f += kBlock) {
+      const int t = ltok[f];
+      if (t == kEmpty) continue;
+      // At most n distinct tokens occupy 2n or more slots, so a free or
+      // matching slot is always found; the probe count is bounded all the same.
+      unsigned h = hash_slot(t, mask, shift);
+      bool found = false;
+      for (unsigned probe = 0; probe <= mask; probe++) {
+        const int prev = atomicCAS(&tb.keys[h], kEmpty, t);
+        if (prev == kEmpty || prev == t) {
+          found = true;
+          break;
+        }
+        h = (h + 1) & mask;
+      }
+      if (!found) {
+        lslot[f] = -1;
+        continue;
+      }
+      const int c = lcnt[f];
+      const int base = atomicAdd(&tb.cnt[h], c);
+      if (base <= kCap && kCap < base + c) tb.large_j[h] = atomicAdd(&tb.counters[1], 1);
+      lslot[f] = (int)h;
+      lbase[f] = base;
     }
-    s.slot_of[i] = (int)h;
-    s.rank_of[i] = atomicAdd(&s.cnt[h], 1);
+    __syncthreads();
+    if (i >= n) return;
+    const int h = e >= 0 ? lslot[e] : -1;
+    sh.slot_of[i] = h;
+    if (h >= 0) {
+      const int rank = lbase[e] + lrank;
+      if (rank < kCap) sh.rows[(size_t)h * kCap + rank] = i;
+    }
     return;
   }
   // dwpe[t, c] += dout[b, t, c] for b = 0..B-1, in order; 8 rows in flight.
@@ -166,194 +206,210 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncState s, const int
   }
 }
 
-// K2a: exclusive scan of the slot counts within blocks of kScanSpan slots
-// (1024 threads x 4 slots): bstart[h] = slots before h in its block,
-// btot[b] = the block's total.
-constexpr int kScanThreads = 1024;
-constexpr int kScanSpan = 4 * kScanThreads;
-__global__ __launch_bounds__(kScanThreads) void k_enc_bwd_scan(EncState s, int tsize) {
-  __shared__ int wsum[kScanThreads / kWave];
-  const int tid = threadIdx.x;
-  const int h0 = blockIdx.x * kScanSpan + tid * 4;
-  int4 c = make_int4(0, 0, 0, 0);
-  if (h0 < tsize) c = *reinterpret_cast<const int4 *>(s.cnt + h0);  // tsize is a multiple of 64
-  const int local = c.x + c.y + c.z + c.w;
-  const int lane = tid & (kWave - 1), wave = tid >> 6;
-  int inc = local;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(inc, off);
-    if (lane >= off) inc += y;
-  }
-  if (lane == kWave - 1) wsum[wave] = inc;
-  __syncthreads();
-  int before = 0;
-  for (int w = 0; w < wave; w++) before += wsum[w];
-  if (tid == kScanThreads - 1) s.btot[blockIdx.x] = before + inc;
-  const int e = before + inc - local;
-  if (h0 < tsize)
-    *reinterpret_cast<int4 *>(s.bstart + h0) = make_int4(e, e + c.x, e + c.x + c.y, e + c.x + c.y + c.z);
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// K2b: place every row at (start of its bucket) + (its arrival rank), with its
-// bucket's start, size and token. Bucket start = totals of the scan blocks
-// before the slot's block + bstart[slot].
-constexpr int kMaxScanBlocks = kTableMax / kScanSpan;
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_place(EncState s, int n, int nscan) {
-  __shared__ int bpre[kMaxScanBlocks + 1];
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int b = 0; b < nscan; b++) {
-      bpre[b] = run;
-      run += s.btot[b];
-    }
-    bpre[nscan] = run;
-    if (blockIdx.x == 0) s.total[0] = run;
-  }
-  __syncthreads();
-  const int i = blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n) return;
-  const int h = s.slot_of[i];
-  if (h < 0) return;
-  const int rk = s.rank_of[i];
-  const int st = bpre[h / kScanSpan] + s.bstart[h];
-  s.meta[st + rk] = make_int4(st, s.cnt[h], s.keys[h], i);
-}
-
-// K3: add the buckets, one wavefront per placed position. Dynamic LDS: per
-// wave max(kSmall, words) 32-bit words.
+// K2: one wavefront per slot. Also clears `old` (the other half of the
+// table) over [0, old_tsize).
 template <bool kVec>
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncState s, float *__restrict__ dwte,
-                                                        const float *__restrict__ dout, int n, int C,
-                                                        int words, int tsize) {
-  extern __shared__ unsigned lds[];
+__global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable old, EncShared sh,
+                                                        float *__restrict__ dwte, const float *__restrict__ dout,
+                                                        int tsize, int old_tsize, int C, int n) {
+  __shared__ unsigned lds[kWavesPerBlock * kCap];
+  for (int h = blockIdx.x * kBlock + threadIdx.x; h < old_tsize; h += gridDim.x * kBlock) {
+    old.keys[h] = kEmpty;
+    old.cnt[h] = 0;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < 3) old.counters[threadIdx.x] = 0;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
-  // K2b was the table's last reader: return the used slots to empty
-  for (int h = blockIdx.x * kBlock + threadIdx.x; h < tsize; h += gridDim.x * kBlock) {
-    s.keys[h] = kEmpty;
-    s.cnt[h] = 0;
-  }
-  const int p = blockIdx.x * kWavesPerBlock + wave;
-  if (p >= n || p >= s.total[0]) return;
-  const int per_wave = words > kSmall ? words : kSmall;
-  unsigned *mine = lds + (size_t)wave * per_wave;
-  const int4 mt = s.meta[p];
-  const int start = mt.x, cnt = mt.y, tok = mt.z;
-  const int k = p - start;
-  if (cnt <= kSmall) {
-    if (k != 0) return;
-    int nrow = 1;
-    if (cnt == 1) {
-      mine[0] = (unsigned)mt.w;
-    } else {
-      // rank the bucket's row ids; ids are distinct, so ranks are a permutation
-      const int id = lane < cnt ? s.meta[start + lane].w : 0x7fffffff;
-      int rank = 0;
-      for (int j = 0; j < cnt; j++) {
-        const int o = __shfl(id, j);
-        rank += (o < id) ? 1 : 0;
-      }
-      if (lane < cnt) mine[rank] = (unsigned)id;
-      nrow = cnt;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (kVec) {
-      const int C4 = C >> 2;
-      float4 *row = reinterpret_cast<float4 *>(dwte) + (size_t)tok * C4;
-      const float4 *g = reinterpret_cast<const float4 *>(dout);
-      for (int c4 = lane; c4 < C4; c4 += kWave) {
-        float4 acc = row[c4];
-        for (int q = 0; q < nrow; q++) {
-          const float4 d = ld_nt(g + (size_t)mine[q] * C4 + c4);
-          acc.x += d.x; acc.y += d.y; acc.z += d.z; acc.w += d.w;
-        }
-        row[c4] = acc;
-      }
-    } else {
-      float *row = dwte + (size_t)tok * C;
-      for (int c = lane; c < C; c += kWave) {
-        float acc = row[c];
-        for (int q = 0; q < nrow; q++) acc += dout[(size_t)mine[q] * C + c];
-        row[c] = acc;
+  const int w = blockIdx.x * kWavesPerBlock + wave;
+  unsigned *mine = lds + (size_t)wave * kCap;
+  if (w >= tsize) return;
+  const int cnt = tb.cnt[w];
+  if (cnt == 0) return;
+  const int tok = tb.keys[w];
+  if (cnt > kCap) {
+    // large bucket: the rows whose slot is w, in row order, to the pool for K3
+    int base = 0;
+    if (lane == 0) base = atomicAdd(&tb.counters[2], cnt);
+    base = __shfl(base, 0);
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    int off = 0;
+    constexpr int kScanIn = 16;  // loads in flight per lane
+    for (int i0 = 0; i0 < n; i0 += kScanIn * kWave) {
+      int sl[kScanIn];
+#pragma unroll
+      for (int q = 0; q < kScanIn; q++)
+        sl[q] = (i0 + q * kWave + lane < n) ? sh.slot_of[i0 + q * kWave + lane] : -1;
+#pragma unroll
+      for (int q = 0; q < kScanIn; q++) {
+        const unsigned long long m = __ballot(sl[q] == w);
+        if (sl[q] == w) sh.pool[base + off + __popcll(m & below)] = i0 + q * kWave + lane;
+        off += __popcll(m);
       }
     }
+    if (lane == 0) sh.lmeta[tb.large_j[w]] = make_int4(base, cnt, tok, 0);
     return;
   }
-  // large bucket: wave k takes channel slices k, k+cnt, ...
-  const int nslices = (C + kWave - 1) / kWave;
-  if (k >= nslices) return;
-  for (int w = lane; w < words; w += kWave) mine[w] = 0u;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int j = lane; j < cnt; j += kWave) {
-    const int id = s.meta[start + j].w;
-    atomicOr(&mine[id >> 5], 1u << (id & 31));
+  // rank the bucket's row ids; ids are distinct, so ranks are a permutation
+  const int id = lane < cnt ? sh.rows[(size_t)w * kCap + lane] : 0x7fffffff;
+  int rank = 0;
+  for (int j = 0; j < cnt; j++) rank += (__shfl(id, j) < id) ? 1 : 0;
+  if (lane < cnt) mine[rank] = (unsigned)id;
+  wave_lds_sync();
+  // rows in ascending order, kBatch loads in flight before their adds
+  constexpr int kBatch = 8;
+  if (kVec) {
+    const int C4 = C >> 2;
+    float4 *row = reinterpret_cast<float4 *>(dwte) + (size_t)tok * C4;
+    const float4 *g = reinterpret_cast<const float4 *>(dout);
+    for (int c4 = lane; c4 < C4; c4 += kWave) {
+      float4 acc = row[c4];
+      for (int q0 = 0; q0 < cnt; q0 += kBatch) {
+        float4 d[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; q++)
+          if (q0 + q < cnt) d[q] = ld_nt(g + (size_t)mine[q0 + q] * C4 + c4);
+#pragma unroll
+        for (int q = 0; q < kBatch; q++)
+          if (q0 + q < cnt) {
+            acc.x += d[q].x; acc.y += d[q].y; acc.z += d[q].z; acc.w += d[q].w;
+          }
+      }
+      row[c4] = acc;
+    }
+  } else {
+    float *row = dwte + (size_t)tok * C;
+    for (int c = lane; c < C; c += kWave) {
+      float acc = row[c];
+      for (int q0 = 0; q0 < cnt; q0 += kBatch) {
+        float d[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; q++)
+          if (q0 + q < cnt) d[q] = dout[(size_t)mine[q0 + q] * C + c];
+#pragma unroll
+        for (int q = 0; q < kBatch; q++)
+          if (q0 + q < cnt) acc += d[q];
+      }
+      row[c] = acc;
+    }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  for (int sl = k; sl < nslices; sl += cnt) {
-    const int c = sl * kWave + lane;
-    const bool on = c < C;
-    float acc = on ? dwte[(size_t)tok * C + c] : 0.0f;
-    for (int w0 = 0; w0 < words; w0 += kWave) {
-      const unsigned mw = (w0 + lane < words) ? mine[w0 + lane] : 0u;
-      unsigned long long nz = __ballot(mw != 0u);
-      while (nz) {
-        const int j = __builtin_ctzll(nz);
-        nz &= nz - 1;
-        unsigned bits = __shfl(mw, j);
-        const int base = (w0 + j) << 5;
-        while (bits) {
-          const int b = __builtin_ctz(bits);
-          bits &= bits - 1;
-          if (on) acc += dout[(size_t)(base + b) * C + c];
+}
+
+// K3: workgroup (s, g) adds channel slice s (64 channels) of the large
+// buckets g, g + gstride, ... Each round the 16 wavefronts load 32 rows each
+// (512 rows; the row ids with one vector load, read out lane by lane) and
+// stage them in LDS; wavefront 0 adds the staged rows to its running sums in
+// ascending row order while the next round's loads are in flight.
+constexpr int kLargeWaves = 16;
+constexpr int kPerWave = 32;
+constexpr int kStage = kLargeWaves * kPerWave;
+__global__ __launch_bounds__(kLargeWaves * kWave) void k_enc_bwd_large(EncTable tb, EncShared sh,
+                                                                       float *__restrict__ dwte,
+                                                                       const float *__restrict__ dout, int C,
+                                                                       int nslices, int gstride) {
+  __shared__ float stage[kStage][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int sl = blockIdx.x % nslices;
+  const int c = sl * kWave + lane;
+  const bool on = c < C;
+  const int nlarge = tb.counters[1];
+  for (int j = blockIdx.x / nslices; j < nlarge; j += gstride) {
+    const int4 m = sh.lmeta[j];
+    const int *ids = sh.pool + m.x;
+    const int cnt = m.y;
+    float acc = (wave == 0 && on) ? dwte[(size_t)m.z * C + c] : 0.0f;
+    float v[kPerWave];
+    auto load_round = [&](int r0) {
+      const int ri = r0 + wave * kPerWave + (lane & (kPerWave - 1));
+      const int idv = ri < cnt ? ids[ri] : 0;
+#pragma unroll
+      for (int q = 0; q < kPerWave; q++) {
+        const int r = r0 + wave * kPerWave + q;
+        const int id = __builtin_amdgcn_readlane(idv, q);
+        v[q] = (on && r < cnt) ? dout[(size_t)id * C + c] : 0.0f;
+      }
+    };
+    load_round(0);
+    for (int r0 = 0; r0 < cnt; r0 += kStage) {
+#pragma unroll
+      for (int q = 0; q < kPerWave; q++) stage[wave * kPerWave + q][lane] = v[q];
+      __syncthreads();
+      if (r0 + kStage < cnt) load_round(r0 + kStage);
+      if (wave == 0) {
+        const int nr = min(kStage, cnt - r0);
+        for (int r1 = 0; r1 < nr; r1 += 16) {
+          float t[16];
+#pragma unroll
+          for (int q = 0; q < 16; q++) t[q] = stage[r1 + q][lane];  // rows past nr were staged as 0
+#pragma unroll
+          for (int q = 0; q < 16; q++)
+            if (r1 + q < nr) acc += t[q];
         }
       }
+      __syncthreads();
     }
-    if (on) dwte[(size_t)tok * C + c] = acc;
+    if (wave == 0 && on) dwte[(size_t)m.z * C + c] = acc;
   }
 }
 
-__global__ void k_enc_init(EncState s) {
+__global__ void k_enc_init(EncTable a, EncTable b) {
   const int h = blockIdx.x * kBlock + threadIdx.x;
   if (h < kTableMax) {
-    s.keys[h] = kEmpty;
-    s.cnt[h] = 0;
+    a.keys[h] = kEmpty;
+    a.cnt[h] = 0;
+    b.keys[h] = kEmpty;
+    b.cnt[h] = 0;
+  }
+  if (h < 3) {
+    a.counters[h] = 0;
+    b.counters[h] = 0;
   }
 }
 
+size_t table_ints() { return (size_t)3 * kTableMax + 64; }
 size_t state_bytes() {
-  return ((size_t)3 * kTableMax + (size_t)2 * kChunk + 64 + kMaxScanBlocks) * sizeof(int) +
-         (size_t)kChunk * sizeof(int4);
+  return (size_t)kTableMax * kCap * sizeof(int) + (size_t)kChunk * sizeof(int) +
+         (size_t)kMaxLarge * sizeof(int4) + (size_t)kChunk * sizeof(int) + 2 * table_ints() * sizeof(int);
 }
 
-EncState carve(void *base) {
-  int4 *m = static_cast<int4 *>(base);
-  EncState s;
-  s.meta = m;
-  int *p = reinterpret_cast<int *>(m + kChunk);
-  s.keys = p; p += kTableMax;
-  s.cnt = p; p += kTableMax;
-  s.bstart = p; p += kTableMax;
-  s.slot_of = p; p += kChunk;
-  s.rank_of = p; p += kChunk;
-  s.total = p; p += 64;
-  s.btot = p;
-  return s;
-}
-
-// The table must start empty; K2 returns it to empty after each chunk. State
-// is kept per device in the encoder's own allocation (not the shared scratch,
-// which other ops overwrite).
 struct DevState {
   void *mem = nullptr;
+  EncTable half[2];
+  EncShared sh;
+  int parity = 0;
+  int last_tsize[2] = {0, 0};
 };
+
+void carve(DevState &ds) {
+  char *p = static_cast<char *>(ds.mem);
+  ds.sh.rows = reinterpret_cast<int *>(p);
+  p += (size_t)kTableMax * kCap * sizeof(int);
+  ds.sh.slot_of = reinterpret_cast<int *>(p);
+  p += (size_t)kChunk * sizeof(int);
+  ds.sh.lmeta = reinterpret_cast<int4 *>(p);
+  p += (size_t)kMaxLarge * sizeof(int4);
+  ds.sh.pool = reinterpret_cast<int *>(p);
+  p += (size_t)kChunk * sizeof(int);
+  for (int k = 0; k < 2; k++) {
+    int *q = reinterpret_cast<int *>(p);
+    ds.half[k].keys = q; q += kTableMax;
+    ds.half[k].cnt = q; q += kTableMax;
+    ds.half[k].large_j = q; q += kTableMax;
+    ds.half[k].counters = q;
+    p += table_ints() * sizeof(int);
+  }
+}
+
+// Per device. The state lives in the encoder's own allocation (not the shared
+// scratch, which other ops overwrite).
 DevState g_state[64];
+std::mutex g_enc_mu;
 
 }  // namespace
 
@@ -381,6 +437,7 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return set_error(2, "encoder_backward: hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_enc_mu);
   DevState &ds = g_state[dev];
   if (!ds.mem) {
     if (hipMalloc(&ds.mem, state_bytes()) != hipSuccess) {
@@ -388,38 +445,44 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
       (void)hipGetLastError();
       return set_error(3, "encoder_backward: cannot allocate %zu bytes of bucket state", state_bytes());
     }
-    hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(),
-                       carve(ds.mem));
+    carve(ds);
+    hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), ds.half[0],
+                       ds.half[1]);
   }
-  const EncState s = carve(ds.mem);
   const bool vec = (C & 3) == 0 && aligned16(dwte) && aligned16(dwpe) && aligned16(dout);
+  const int nslices = (C + kWave - 1) / kWave;
   for (int c0 = 0; c0 < BT; c0 += kChunk) {
     const int n = BT - c0 < kChunk ? BT - c0 : kChunk;
     int tsize = 64, lg = 6;
     while (tsize < 2 * n) { tsize <<= 1; lg++; }
     const unsigned mask = (unsigned)tsize - 1u;
     const int shift = 32 - lg;
+    const int p = ds.parity;
+    const EncTable tb = ds.half[p], old = ds.half[1 - p];
     const int ins_blocks = (int)grid_for((size_t)n, kBlock);
     int pe_blocks = 0;
     if (c0 == 0) pe_blocks = (int)grid_for((size_t)T * (vec ? C / 4 : C), kBlock);
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_insert<true>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), s,
-                         inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
+      hipLaunchKernelGGL(k_enc_bwd_insert<true>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
+                         ds.sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     else
-      hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), s,
-                         inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
-    const int nscan = (tsize + kScanSpan - 1) / kScanSpan;
-    hipLaunchKernelGGL(k_enc_bwd_scan, dim3(nscan), dim3(kScanThreads), 0, stream(), s, tsize);
-    hipLaunchKernelGGL(k_enc_bwd_place, dim3(ins_blocks), dim3(kBlock), 0, stream(), s, n, nscan);
-    const int words = (n + 31) / 32;
-    const size_t lds = (size_t)kWavesPerBlock * (size_t)(words > kSmall ? words : kSmall) * sizeof(unsigned);
+      hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
+                         ds.sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     const float *dchunk = dout + (size_t)c0 * C;
+    const dim3 g2(grid_for((size_t)tsize, kWavesPerBlock));
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_add<true>, dim3(grid_for((size_t)n, kWavesPerBlock)), dim3(kBlock), lds,
-                         stream(), s, dwte, dchunk, n, C, words, tsize);
+      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk, tsize,
+                         ds.last_tsize[1 - p], C, n);
     else
-      hipLaunchKernelGGL(k_enc_bwd_add<false>, dim3(grid_for((size_t)n, kWavesPerBlock)), dim3(kBlock), lds,
-                         stream(), s, dwte, dchunk, n, C, words, tsize);
+      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk, tsize,
+                         ds.last_tsize[1 - p], C, n);
+    const int max_large = n / (kCap + 1) + 1;
+    const int gstride = max_large < 64 ? max_large : 64;
+    hipLaunchKernelGGL(k_enc_bwd_large, dim3(nslices * gstride), dim3(kLargeWaves * kWave), 0, stream(), tb, ds.sh,
+                       dwte, dchunk, C, nslices, gstride);
+    ds.last_tsize[1 - p] = 0;
+    ds.last_tsize[p] = tsize;
+    ds.parity = 1 - p;
   }
   return check_launch("encoder_backward");
 }

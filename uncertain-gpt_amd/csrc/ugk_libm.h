@@ -34,6 +34,7 @@
 #include <string.h>
 
 #if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
 #define UGK_HD __host__ __device__ __forceinline__
 #else
 #define UGK_HD static inline
