@@ -13,12 +13,12 @@ namespace {
 // math); 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
 // (ugk_div_t<s>), to compare the candidate sequences.
 template <int FN>
-__device__ __forceinline__ float kernel_math(float x) {
-  if (FN == 0) return ugk_expf(x);
+__device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
+  if (FN == 0) return ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
   if (FN == 1) return ugk_dev_log1pf(x);
   if (FN == 2) return ugk_dev_expm1f(x);
   if (FN == 3) return ugk_dev_tanhf(x);
-  if (FN == 4) return ugk_dev_softplusf(x);
+  if (FN == 4) return ugk_dev_softplusf_lds(x, tab);
   if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
   if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
@@ -36,13 +36,16 @@ __device__ __forceinline__ float reference_math(float x) {
 template <int FN>
 __global__ __launch_bounds__(kBlock) void k_math_mismatch(unsigned long long lo, unsigned long long count,
                                                           unsigned long long *nbad, unsigned *first) {
+  __shared__ uint64_t tab[32];
+  ugk_exp2_stage(tab);
+  __syncthreads();
   unsigned long long local = 0;
   unsigned lfirst = 0xffffffffu;
   for (unsigned long long i = (unsigned long long)blockIdx.x * kBlock + threadIdx.x; i < count;
        i += (unsigned long long)gridDim.x * kBlock) {
     const unsigned u = (unsigned)(lo + i);
     const float x = ugk_u2f(u);
-    const float a = kernel_math<FN>(x), b = reference_math<FN>(x);
+    const float a = kernel_math<FN>(x, tab), b = reference_math<FN>(x);
     if (ugk_f2u(a) != ugk_f2u(b) && !(a != a && b != b)) {
       local++;
       lfirst = min(lfirst, u);
@@ -56,8 +59,11 @@ __global__ __launch_bounds__(kBlock) void k_math_mismatch(unsigned long long lo,
 
 template <int FN>
 __global__ __launch_bounds__(kBlock) void k_math_eval(int variant, float *out, const float *in, size_t n) {
+  __shared__ uint64_t tab[32];
+  ugk_exp2_stage(tab);
+  __syncthreads();
   for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock)
-    out[i] = variant == 0 ? kernel_math<FN>(in[i]) : reference_math<FN>(in[i]);
+    out[i] = variant == 0 ? kernel_math<FN>(in[i], tab) : reference_math<FN>(in[i]);
 }
 
 bool fn_ok(int fn) { return (fn >= 0 && fn <= 4) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }

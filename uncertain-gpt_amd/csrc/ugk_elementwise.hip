@@ -29,12 +29,14 @@ constexpr int kUnroll = 2;
 
 struct ResidualFwd {  // train_bnn.c:182-186
   static constexpr int kLoads = 2, kStores = 1;
-  __device__ static void apply(const float *ld, float *st) { st[0] = ld[0] + ld[1]; }
+  static constexpr bool kTable = false;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *) { st[0] = ld[0] + ld[1]; }
 };
 
 struct ResidualBwd {  // train_bnn.c:491-496; loads dout, dx, dy
   static constexpr int kLoads = 3, kStores = 2;
-  __device__ static void apply(const float *ld, float *st) {
+  static constexpr bool kTable = false;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *) {
     st[0] = ld[1] + ld[0];
     st[1] = ld[2] + ld[0];
   }
@@ -43,12 +45,14 @@ struct ResidualBwd {  // train_bnn.c:491-496; loads dout, dx, dy
 // dx and dy are the same buffer: the CPU loop then adds dout twice, in order.
 struct ResidualBwdSame {  // loads dout, dx
   static constexpr int kLoads = 2, kStores = 1;
-  __device__ static void apply(const float *ld, float *st) { st[0] = (ld[1] + ld[0]) + ld[0]; }
+  static constexpr bool kTable = false;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *) { st[0] = (ld[1] + ld[0]) + ld[0]; }
 };
 
 struct GeluFwd {  // train_bnn.c:163-170
   static constexpr int kLoads = 1, kStores = 1;
-  __device__ static void apply(const float *ld, float *st) {
+  static constexpr bool kTable = false;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *) {
     const float k = 0.7978845608f;
     const float x = ld[0];
     const float inner = k * (x + 0.044715f * x * x * x);
@@ -58,7 +62,8 @@ struct GeluFwd {  // train_bnn.c:163-170
 
 struct GeluBwd {  // train_bnn.c:520-533; loads inp, dout, dinp
   static constexpr int kLoads = 3, kStores = 1;
-  __device__ static void apply(const float *ld, float *st) {
+  static constexpr bool kTable = false;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *) {
     const float k = 0.7978845608f;
     const float x = ld[0];
     const float u = k * (x + 0.044715f * x * x * x);
@@ -72,8 +77,9 @@ struct GeluBwd {  // train_bnn.c:520-533; loads inp, dout, dinp
 
 struct Materialize {  // train_bnn.c:831-835; loads mu, rho, eps
   static constexpr int kLoads = 3, kStores = 1;
-  __device__ static void apply(const float *ld, float *st) {
-    st[0] = ld[0] + ugk_dev_softplusf(ld[1]) * ld[2];
+  static constexpr bool kTable = true;  // expf's 2^(i/32) table staged in LDS
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab) {
+    st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * ld[2];
   }
 };
 
@@ -85,6 +91,11 @@ struct Streams {
 
 template <class Op>
 __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
+  __shared__ uint64_t tab[Op::kTable ? 32 : 1];
+  if (Op::kTable) {
+    ugk_exp2_stage(tab);
+    __syncthreads();
+  }
   const size_t base = (size_t)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
   float4 v[kUnroll][Op::kLoads];
 #pragma unroll
@@ -106,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
         in[2][l] = v[u][l].z; in[3][l] = v[u][l].w;
       }
 #pragma unroll
-      for (int e = 0; e < 4; e++) Op::apply(in[e], out[e]);
+      for (int e = 0; e < 4; e++) Op::apply(in[e], out[e], tab);
 #pragma unroll
       for (int o = 0; o < Op::kStores; o++)
         st_nt(reinterpret_cast<float4 *>(s.st[o]) + i, make_float4(out[0][o], out[1][o], out[2][o], out[3][o]));
@@ -116,12 +127,17 @@ __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
 
 template <class Op>
 __global__ __launch_bounds__(kBlock) void k_map_scalar(Streams<Op> s, size_t begin, size_t n) {
+  __shared__ uint64_t tab[Op::kTable ? 32 : 1];
+  if (Op::kTable) {
+    ugk_exp2_stage(tab);
+    __syncthreads();
+  }
   for (size_t i = begin + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n;
        i += (size_t)gridDim.x * kBlock) {
     float in[Op::kLoads], out[Op::kStores];
 #pragma unroll
     for (int l = 0; l < Op::kLoads; l++) in[l] = s.ld[l][i];
-    Op::apply(in, out);
+    Op::apply(in, out, tab);
 #pragma unroll
     for (int o = 0; o < Op::kStores; o++) s.st[o][i] = out[o];
   }

@@ -48,7 +48,7 @@ UGK_HD double ugk_u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
 // 2^(i/32) correctly rounded to binary64, minus (i << 47): adding (k << 47) to
 // entry k%32 gives the bit pattern of 2^(k/32) for any integer k in range.
 // Regenerate with: float(Decimal(2)**(Decimal(i)/32)) at 60 digits.
-UGK_HD double ugk_exp2_tab(uint32_t i, uint64_t ki) {
+UGK_HD uint64_t ugk_exp2_bits(uint32_t i) {
   const uint64_t tab[32] = {
       0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full,
       0x3fef9301d0125b51ull, 0x3fef72b83c7d517bull, 0x3fef54873168b9aaull,
@@ -61,8 +61,14 @@ UGK_HD double ugk_exp2_tab(uint32_t i, uint64_t ki) {
       0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull,
       0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
       0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
-  return ugk_u2d(tab[i] + (ki << 47));
+  return tab[i];
 }
+
+// The table read from the array above (callers may pass their own copy of it,
+// e.g. one staged in GPU local memory).
+struct UgkExp2Table {
+  UGK_HD uint64_t operator()(uint32_t i) const { return ugk_exp2_bits(i); }
+};
 
 // expf. kContract selects how the multiply-adds are rounded, because the x86
 // glibc picks an FMA-compiled copy of this routine at run time on CPUs with
@@ -70,8 +76,8 @@ UGK_HD double ugk_exp2_tab(uint32_t i, uint64_t ki) {
 //   0: every product and sum rounded separately (no FMA);
 //   1: the three polynomial multiply-adds fused;
 //   2: as 1, and also the two uses of InvLn2N*x in the reduction fused.
-template <int kContract>
-UGK_HD float ugk_expf_v(float x) {
+template <int kContract, class Tab>
+UGK_HD float ugk_expf_t(float x, Tab tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
   const double kShift = 0x1.8p+52;
   const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -99,7 +105,7 @@ UGK_HD float ugk_expf_v(float x) {
   } else {
     r = kInvLn2N * xd - kd;
   }
-  const double s = ugk_exp2_tab((uint32_t)(ki % 32), ki);
+  const double s = ugk_u2d(tab((uint32_t)(ki % 32)) + (ki << 47));
   double z, y;
   const double r2 = r * r;
   if (kContract >= 1) {
@@ -113,6 +119,11 @@ UGK_HD float ugk_expf_v(float x) {
   }
   y = y * s;
   return (float)y;
+}
+
+template <int kContract>
+UGK_HD float ugk_expf_v(float x) {
+  return ugk_expf_t<kContract>(x, UgkExp2Table{});
 }
 
 // log1pf, fdlibm.

@@ -246,3 +246,19 @@ __device__ __forceinline__ float ugk_dev_log1pf(float x) { return ugk_dev_log1pf
 __device__ __forceinline__ float ugk_dev_softplusf(float x) {
   return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf(x));
 }
+
+// The expf table of ugk_libm.h, read from a copy in LDS: a per-lane lookup in
+// local memory instead of a dependent global load on every element's path.
+struct UgkExp2Lds {
+  const uint64_t *p;
+  __device__ uint64_t operator()(uint32_t i) const { return p[i]; }
+};
+
+// Fill a 32-entry LDS table; the caller synchronises the workgroup after.
+__device__ __forceinline__ void ugk_exp2_stage(uint64_t *lds_tab) {
+  if (threadIdx.x < 32) lds_tab[threadIdx.x] = ugk_exp2_bits(threadIdx.x);
+}
+
+__device__ __forceinline__ float ugk_dev_softplusf_lds(float x, const uint64_t *lds_tab) {
+  return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{lds_tab}));
+}
