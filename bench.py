@@ -16,6 +16,9 @@ Printed JSON line (the last line of stdout):
     configs      the same kernels at the shapes of BASELINE configs 2-4 (LayerNorm
                  16384x768 and 256x384, GELU/residual over 50,331,648 values,
                  encoder at B=16 T=1024 with uniform and Zipf(1.1) tokens), cold
+    posterior    the ops around the step over the same n parameters, cold:
+                 Philox sample, bayes/KL backward, AdamW, the fused BBB update,
+                 the KL total
     kernels      each kernel at its step shape, cold (launches rotate over buffer
                  sets totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds
                  the operands): mean ms from HIP events, GB/s from algorithmic
@@ -28,6 +31,7 @@ Printed JSON line (the last line of stdout):
                  at the step shapes and composed by launch count
 """
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -133,6 +137,8 @@ def main():
     ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other BASELINE configs")
+    ap.add_argument("--no-posterior", action="store_true",
+                    help="skip the posterior-update ops (Philox sample, bayes/KL backward, AdamW, fused step)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print per-kernel HBM traffic from two rocprofv3 --pmc runs of this script, and exit")
     ap.add_argument("--summarize-stats", metavar="STATS_CSV",
@@ -344,6 +350,42 @@ def main():
                 P_(d["wte"]), P_(d["wpe"]), P_(d["dout"]), P_(d["inp"]), B2, T2, C)))
             record(configs, f"cfg4 {law} encoder_backward", 20 * N4 + 4 * R2, ms, l_, k_)
 
+    # ---- the posterior update around the layer kernels, over the same n (not part of the step)
+    posterior = {}
+    if not args.no_posterior:
+        n = n_mat
+        seed, pstep = 0x5EED, 3
+        bc1, bc2 = 1.0 - 0.9 ** pstep, 1.0 - 0.999 ** pstep
+
+        def mk_post():
+            return {k: rnd(n) * 0.01 for k in ("mu", "dw", "eps", "dmu", "drho", "m_mu", "m_rho")} | \
+                   {"rho": rnd(n) * 0.1 - 5.0, "v_mu": rnd(n).abs_() * 1e-4, "v_rho": rnd(n).abs_() * 1e-4,
+                    "w": torch.empty(n, device=dev)}
+        post_plan = (
+            ("bayes_sample", 12, lambda d: chk(lib.ugk_bayes_sample(
+                P_(d["w"]), None, P_(d["mu"]), P_(d["rho"]), n, seed, pstep))),
+            ("bayes_sample (eps stored)", 16, lambda d: chk(lib.ugk_bayes_sample(
+                P_(d["w"]), P_(d["eps"]), P_(d["mu"]), P_(d["rho"]), n, seed, pstep))),
+            ("bayes_backward", 28, lambda d: chk(lib.ugk_bayes_backward(
+                P_(d["dmu"]), P_(d["drho"]), P_(d["dw"]), P_(d["eps"]), P_(d["rho"]), n))),
+            ("bayes_backward_philox", 24, lambda d: chk(lib.ugk_bayes_backward_philox(
+                P_(d["dmu"]), P_(d["drho"]), P_(d["dw"]), P_(d["rho"]), n, seed, pstep))),
+            ("kl_backward", 24, lambda d: chk(lib.ugk_kl_backward(
+                P_(d["dmu"]), P_(d["drho"]), P_(d["mu"]), P_(d["rho"]), n, 0.1, 1e-6))),
+            ("adamw_update", 28, lambda d: chk(lib.ugk_adamw_update(
+                P_(d["mu"]), P_(d["dw"]), P_(d["m_mu"]), P_(d["v_mu"]), n, pstep, 3e-4, 0.9, 0.999, 1e-8, 0.0))),
+            ("bbb_step_fused", 60, lambda d: chk(lib.ugk_bbb_step_fused(
+                P_(d["mu"]), P_(d["rho"]), P_(d["m_mu"]), P_(d["v_mu"]), P_(d["m_rho"]), P_(d["v_rho"]),
+                P_(d["w"]), P_(d["dw"]), n, seed, pstep, 0.1, 1e-6, bc1, bc2, 3e-4, 0.9, 0.999, 1e-8, 0.0))),
+        )
+        for nm, nb, fn in post_plan:
+            ms, l_, k_ = time_cold(mk_post, 44 * n, fn)
+            record(posterior, nm, nb * n, ms, l_, k_)
+        kl_out = ctypes.c_double(0.0)
+        ms, l_, k_ = time_cold(mk_post, 44 * n, lambda d: chk(lib.ugk_kl_forward(
+            ctypes.byref(kl_out), P_(d["mu"]), P_(d["rho"]), n, 0.1)))
+        record(posterior, "kl_forward (incl. result copy + sync)", 8 * n, ms, l_, k_)
+
     # ---- roofline of the dominant kernel (most algorithmic bytes per step)
     dom = max(per, key=lambda k: per[k] * count[k])
     achieved = per[dom] / (mean_ms[dom] * 1e-3) / 1e9
@@ -375,7 +417,7 @@ def main():
                    "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
                    "param_layout_n": P, "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
-        "kernels": kernels, "configs": configs, "roofline": roofline, "cpu_baseline": cpu,
+        "kernels": kernels, "configs": configs, "posterior": posterior, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
 

@@ -87,6 +87,64 @@ int ugk_residual_backward(float *dx, float *dy, const float *dout, int N);
 int ugk_bayes_materialize(float *w, const float *mu, const float *rho,
                           const float *eps, size_t n);
 
+/* ---- the posterior update around the layer kernels ----------------------
+ * Flat parameter vectors of n floats. The ops that take eps are
+ * bit-identical to train_bnn.c. The *_philox ops draw
+ *     eps_i = philox_normal(seed, step, i)
+ * on the fly (gpt2_kernels.cuh:148-192: Philox4x32-10 with counter
+ * {i low, i high, step, 0} and key {seed low, seed high}, Box-Muller cosine
+ * branch); the integer stream is exact, the transform uses the device
+ * logf/cosf, which differ from glibc's by at most an ulp on a small share of
+ * inputs. Buffers written by one call must not overlap each other. */
+
+/* train_bnn.c:841-845 with the draw of train_bnn_gpu.cu:93-97 (k_bayes_sample):
+ * w = mu + softplus(rho) * eps_i. eps may be NULL (the GPU arms regenerate
+ * it); otherwise eps_i is stored there too. */
+int ugk_bayes_sample(float *w, float *eps, const float *mu, const float *rho,
+                     size_t n, unsigned long long seed, int step);
+
+/* train_bnn.c:855-861. dmu += dw; drho += dw * eps * sigmoid(rho). */
+int ugk_bayes_backward(float *dmu, float *drho, const float *dw,
+                       const float *eps, const float *rho, size_t n);
+
+/* train_bnn_gpu.cu:99-109 (k_bayes_backward): as ugk_bayes_backward with
+ * eps_i regenerated from (seed, step). */
+int ugk_bayes_backward_philox(float *dmu, float *drho, const float *dw,
+                              const float *rho, size_t n,
+                              unsigned long long seed, int step);
+
+/* train_bnn.c:941-957. *kl (a HOST pointer) = sum over i of
+ * log(sp/sigma_i) + (sigma_i^2 + mu_i^2)/(2 sp^2) - 1/2 in double, with
+ * sigma_i = softplus(rho_i) and sp = sigma_prior. Summed in a fixed tree
+ * order (deterministic; within double rounding of the CPU's sequential sum).
+ * Waits for the library stream. */
+int ugk_kl_forward(double *kl, const float *mu, const float *rho, size_t n,
+                   float sigma_prior);
+
+/* train_bnn.c:966-979 / train_bnn_gpu.cu:111-119 (k_kl_backward).
+ * dmu += weight * mu / sp^2; drho += weight * (sigma/sp^2 - 1/sigma) *
+ * sigmoid(rho). */
+int ugk_kl_backward(float *dmu, float *drho, const float *mu, const float *rho,
+                    size_t n, float sigma_prior, float weight);
+
+/* train_bnn.c:699-717 / gpt2_kernels.cuh:973-984 (k_adamw). t >= 1; the bias
+ * corrections 1 - beta^t are computed on the host with powf, as in the
+ * reference. Updates params, m and v in place. */
+int ugk_adamw_update(float *params, const float *grads, float *m, float *v,
+                     size_t n, int t, float lr, float beta1, float beta2,
+                     float eps, float wd);
+
+/* train_bnn_gpu.cu:173-217 (k_bbb_step_fused): one Bayes-by-Backprop update
+ * in one pass. gmu = dw, grho = dw * eps_i(step) * sigmoid(rho), plus the KL
+ * gradient when klw > 0; AdamW on (mu, m_mu, v_mu) and (rho, m_rho, v_rho)
+ * with the caller's bias corrections bc1, bc2; dw cleared to 0; and
+ * w = mu' + softplus(rho') * eps_i(step + 1) for the next step. */
+int ugk_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu,
+                       float *m_rho, float *v_rho, float *w, float *dw,
+                       size_t n, unsigned long long seed, int step, float sp,
+                       float klw, float bc1, float bc2, float lr, float beta1,
+                       float beta2, float aeps, float wd);
+
 /* ---- library control (no counterpart in the reference: its kernels run on
  * the CUDA legacy default stream and abort on error, gpt2_kernels.cuh:88-101) */
 
@@ -118,8 +176,14 @@ int ugk_version(void);
 int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
                            unsigned long long *mismatches, unsigned *first);
 /* out[i] = f(in[i]) on the device; variant 0 = the kernels' math, 1 = the
- * line-by-line restatement. */
+ * line-by-line restatement. fn: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf,
+ * 4 softplus, 5 logf and 6 cosf (the device library's, as the Philox
+ * transform calls them), 7 sqrtf; 10+s, 20+s, 30+s tanhf, log1pf, expm1f
+ * with division sequence s. */
 int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n);
+/* Philox4x32-10 on the device: in holds n tuples of 6 words (counter c0..c3,
+ * key k0, k1), out receives n x 4 output words. */
+int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n);
 
 /* ---- GPT-2 layer-kernel step driver ------------------------------------
  * gpt2_kernels.cuh:634-719 (Config, param_offsets, act_offsets) and the

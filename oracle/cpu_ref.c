@@ -27,6 +27,11 @@
  *     GELU matches float64 tanh within a few ulp and hits gelu(0)=0 and
  *     gelu'(0)=0.5 exactly, materialize hits eps=0 -> w=mu, rho>20 -> mu+rho*eps
  *     and rho<=-104 -> softplus=0.
+ *   - the posterior update (bayes_backward, kl_forward/backward, adamw) against
+ *     the compiled reference, which exports all four; Philox4x32-10 against
+ *     the published Random123 known-answer vectors; philox_normal against a
+ *     float64 Box-Muller of the same words; the fused step against the
+ *     composition of the unfused ops.
  */
 #include "cpu_ref.h"
 
@@ -169,6 +174,156 @@ void oracle_bayes_materialize(float *w, const float *mu, const float *rho,
   for (size_t i = 0; i < n; i++) w[i] = mu[i] + oracle_softplus(rho[i]) * eps[i];
 }
 
+/* ---- the posterior update ------------------------------------------------ */
+
+/* train_bnn.c:820-822 */
+static float oracle_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* train_bnn.c:855-861 */
+void oracle_bayes_backward(float *dmu, float *drho, const float *dw,
+                           const float *eps, const float *rho, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    dmu[i] += dw[i];
+    drho[i] += dw[i] * eps[i] * oracle_sigmoid(rho[i]);
+  }
+}
+
+/* train_bnn.c:941-957 */
+double oracle_kl_forward(const float *mu, const float *rho, size_t n,
+                         float sigma_prior) {
+  float sp2 = sigma_prior * sigma_prior;
+  double kl = 0.0;
+  for (size_t i = 0; i < n; i++) {
+    double sigma = (double)oracle_softplus(rho[i]);
+    double m = (double)mu[i];
+    kl += log((double)sigma_prior / sigma) + (sigma * sigma + m * m) / (2.0 * (double)sp2) - 0.5;
+  }
+  return kl;
+}
+
+/* train_bnn.c:966-979 */
+void oracle_kl_backward(float *dmu, float *drho, const float *mu, const float *rho,
+                        size_t n, float sigma_prior, float weight) {
+  float sp2 = sigma_prior * sigma_prior;
+  for (size_t i = 0; i < n; i++) {
+    float sigma = oracle_softplus(rho[i]);
+    dmu[i] += weight * (mu[i] / sp2);
+    float dsigma = sigma / sp2 - 1.0f / sigma;
+    drho[i] += weight * dsigma * oracle_sigmoid(rho[i]);
+  }
+}
+
+/* train_bnn.c:699-717 */
+void oracle_adamw_update(float *params, const float *grads, float *m, float *v,
+                         size_t n, int t, float lr, float beta1, float beta2,
+                         float eps, float wd) {
+  float bc1 = 1.0f - powf(beta1, (float)t);
+  float bc2 = 1.0f - powf(beta2, (float)t);
+  for (size_t i = 0; i < n; i++) {
+    float g = grads[i];
+    m[i] = beta1 * m[i] + (1.0f - beta1) * g;
+    v[i] = beta2 * v[i] + (1.0f - beta2) * g * g;
+    float m_hat = m[i] / bc1;
+    float v_hat = v[i] / bc2;
+    params[i] -= lr * (m_hat / (sqrtf(v_hat) + eps) + wd * params[i]);
+  }
+}
+
+/* gpt2_kernels.cuh:148-175: Philox4x32-10, ten rounds, the key bumped after
+ * every round. */
+void oracle_philox4x32_10(const unsigned *ctr, const unsigned *key, unsigned *out) {
+  const unsigned M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  const unsigned W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+  unsigned c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+  unsigned k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; r++) {
+    unsigned long long p0 = (unsigned long long)M0 * c0;
+    unsigned long long p1 = (unsigned long long)M1 * c2;
+    unsigned n0 = (unsigned)(p1 >> 32) ^ c1 ^ k0, n1 = (unsigned)p1;
+    unsigned n2 = (unsigned)(p0 >> 32) ^ c3 ^ k1, n3 = (unsigned)p0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    k0 += W0; k1 += W1;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* gpt2_kernels.cuh:177-179 */
+float oracle_u01(unsigned x) { return ((float)x + 0.5f) * 2.3283064365386963e-10f; }
+
+/* gpt2_kernels.cuh:181-192, as the host compiler builds it (glibc logf, cosf,
+ * sqrtf). */
+float oracle_philox_normal(unsigned long long seed, int step, size_t index) {
+  unsigned ctr[4], key[2], out[4];
+  ctr[0] = (unsigned)(index & 0xffffffffu);
+  ctr[1] = (unsigned)((unsigned long long)index >> 32);
+  ctr[2] = (unsigned)step;
+  ctr[3] = 0u;
+  key[0] = (unsigned)(seed & 0xffffffffu);
+  key[1] = (unsigned)(seed >> 32);
+  oracle_philox4x32_10(ctr, key, out);
+  float u1 = oracle_u01(out[0]), u2 = oracle_u01(out[1]);
+  return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+}
+
+/* eps[i] = philox_normal(seed, step, first + i). */
+void oracle_philox_normal_n(float *eps, size_t n, unsigned long long seed, int step,
+                            size_t first) {
+  for (size_t i = 0; i < n; i++) eps[i] = oracle_philox_normal(seed, step, first + i);
+}
+
+/* train_bnn_gpu.cu:93-97 (k_bayes_sample); eps also stored when non-NULL, as
+ * train_bnn.c:841-845 keeps it. */
+void oracle_bayes_sample_philox(float *w, float *eps, const float *mu, const float *rho,
+                                size_t n, unsigned long long seed, int step) {
+  for (size_t i = 0; i < n; i++) {
+    float e = oracle_philox_normal(seed, step, i);
+    w[i] = mu[i] + oracle_softplus(rho[i]) * e;
+    if (eps) eps[i] = e;
+  }
+}
+
+/* train_bnn_gpu.cu:99-109 (k_bayes_backward) */
+void oracle_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho,
+                                  size_t n, unsigned long long seed, int step) {
+  for (size_t i = 0; i < n; i++) {
+    float g = dw[i];
+    float eps = oracle_philox_normal(seed, step, i);
+    dmu[i] += g;
+    drho[i] += g * eps * oracle_sigmoid(rho[i]);
+  }
+}
+
+/* train_bnn_gpu.cu:173-217 (k_bbb_step_fused), statement by statement. */
+void oracle_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m_rho,
+                           float *v_rho, float *w, float *dw, size_t n,
+                           unsigned long long seed, int step, float sp, float klw,
+                           float bc1, float bc2, float lr, float beta1, float beta2,
+                           float aeps, float wd) {
+  for (size_t i = 0; i < n; i++) {
+    float g = dw[i], r = rho[i], mm = mu[i];
+    dw[i] = 0.0f;
+    float sg = oracle_sigmoid(r);
+    float gmu = g;
+    float grho = g * oracle_philox_normal(seed, step, i) * sg;
+    if (klw > 0.0f) {
+      float sp2 = sp * sp, sigma = oracle_softplus(r);
+      gmu += klw * (mm / sp2);
+      grho += klw * (sigma / sp2 - 1.0f / sigma) * sg;
+    }
+    float m1 = beta1 * m_mu[i] + (1.0f - beta1) * gmu;
+    float v1 = beta2 * v_mu[i] + (1.0f - beta2) * gmu * gmu;
+    m_mu[i] = m1; v_mu[i] = v1;
+    float mu_new = mm - lr * ((m1 / bc1) / (sqrtf(v1 / bc2) + aeps) + wd * mm);
+    mu[i] = mu_new;
+    float m2 = beta1 * m_rho[i] + (1.0f - beta1) * grho;
+    float v2 = beta2 * v_rho[i] + (1.0f - beta2) * grho * grho;
+    m_rho[i] = m2; v_rho[i] = v2;
+    float rho_new = r - lr * ((m2 / bc1) / (sqrtf(v2 / bc2) + aeps) + wd * r);
+    rho[i] = rho_new;
+    w[i] = mu_new + oracle_softplus(rho_new) * oracle_philox_normal(seed, step + 1, i);
+  }
+}
+
 /* Elementwise host libm entry points, so tests can compare device math with
  * the very functions the oracle calls. */
 void oracle_expf_n(float *y, const float *x, size_t n) {
@@ -182,6 +337,15 @@ void oracle_tanhf_n(float *y, const float *x, size_t n) {
 }
 void oracle_softplus_n(float *y, const float *x, size_t n) {
   for (size_t i = 0; i < n; i++) y[i] = oracle_softplus(x[i]);
+}
+void oracle_logf_n(float *y, const float *x, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = logf(x[i]);
+}
+void oracle_cosf_n(float *y, const float *x, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = cosf(x[i]);
+}
+void oracle_sqrtf_n(float *y, const float *x, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = sqrtf(x[i]);
 }
 
 /* Bit patterns [lo, lo+n) as floats, the input of an exhaustive sweep. */

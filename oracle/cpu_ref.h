@@ -26,10 +26,37 @@ float oracle_softplus(float x);
 void oracle_bayes_materialize(float *w, const float *mu, const float *rho,
                               const float *eps, size_t n);
 
+void oracle_bayes_backward(float *dmu, float *drho, const float *dw,
+                           const float *eps, const float *rho, size_t n);
+double oracle_kl_forward(const float *mu, const float *rho, size_t n,
+                         float sigma_prior);
+void oracle_kl_backward(float *dmu, float *drho, const float *mu, const float *rho,
+                        size_t n, float sigma_prior, float weight);
+void oracle_adamw_update(float *params, const float *grads, float *m, float *v,
+                         size_t n, int t, float lr, float beta1, float beta2,
+                         float eps, float wd);
+void oracle_philox4x32_10(const unsigned *ctr, const unsigned *key, unsigned *out);
+float oracle_u01(unsigned x);
+float oracle_philox_normal(unsigned long long seed, int step, size_t index);
+void oracle_philox_normal_n(float *eps, size_t n, unsigned long long seed, int step,
+                            size_t first);
+void oracle_bayes_sample_philox(float *w, float *eps, const float *mu, const float *rho,
+                                size_t n, unsigned long long seed, int step);
+void oracle_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho,
+                                  size_t n, unsigned long long seed, int step);
+void oracle_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m_rho,
+                           float *v_rho, float *w, float *dw, size_t n,
+                           unsigned long long seed, int step, float sp, float klw,
+                           float bc1, float bc2, float lr, float beta1, float beta2,
+                           float aeps, float wd);
+
 void oracle_expf_n(float *y, const float *x, size_t n);
 void oracle_log1pf_n(float *y, const float *x, size_t n);
 void oracle_tanhf_n(float *y, const float *x, size_t n);
 void oracle_softplus_n(float *y, const float *x, size_t n);
+void oracle_logf_n(float *y, const float *x, size_t n);
+void oracle_cosf_n(float *y, const float *x, size_t n);
+void oracle_sqrtf_n(float *y, const float *x, size_t n);
 void oracle_float_range(float *x, unsigned lo, size_t n);
 size_t oracle_count_bit_mismatch(const float *a, const float *b, size_t n,
                                  size_t *first);

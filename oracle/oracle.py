@@ -36,6 +36,22 @@ _SIGS = {
     "residual_forward": [_f, _f, _f, _i],
     "residual_backward": [_f, _f, _f, _i],
     "bayes_materialize": [_f, _f, _f, _f, _sz],
+    "bayes_backward": [_f, _f, _f, _f, _f, _sz],
+    "kl_backward": [_f, _f, _f, _f, _sz, ctypes.c_float, ctypes.c_float],
+    "adamw_update": [_f, _f, _f, _f, _sz, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                     ctypes.c_float, ctypes.c_float],
+}
+_u64 = ctypes.c_ulonglong
+_fl = ctypes.c_float
+# Restatement-only entry points (the reference keeps these in CUDA sources).
+_SIGS_RESTATED = {
+    "oracle_philox4x32_10": ([_f, _f, _f], None),
+    "oracle_u01": ([ctypes.c_uint], _fl),
+    "oracle_philox_normal": ([_u64, _i, _sz], _fl),
+    "oracle_philox_normal_n": ([_f, _sz, _u64, _i, _sz], None),
+    "oracle_bayes_sample_philox": ([_f, _f, _f, _f, _sz, _u64, _i], None),
+    "oracle_bayes_backward_philox": ([_f, _f, _f, _f, _sz, _u64, _i], None),
+    "oracle_bbb_step_fused": ([_f] * 8 + [_sz, _u64, _i] + [_fl] * 9, None),
 }
 
 
@@ -61,8 +77,17 @@ class Oracle:
             fn.argtypes = args
             fn.restype = None
             self._fn[name] = fn
+        kl = getattr(self.lib, prefix + "kl_forward")
+        kl.argtypes = [_f, _f, _sz, _fl]
+        kl.restype = ctypes.c_double
+        self._fn["kl_forward"] = kl
         if not reference:
-            for name in ("oracle_expf_n", "oracle_log1pf_n", "oracle_tanhf_n", "oracle_softplus_n"):
+            for name, (args, res) in _SIGS_RESTATED.items():
+                fn = getattr(self.lib, name)
+                fn.argtypes = args
+                fn.restype = res
+            for name in ("oracle_expf_n", "oracle_log1pf_n", "oracle_tanhf_n", "oracle_softplus_n",
+                         "oracle_logf_n", "oracle_cosf_n", "oracle_sqrtf_n"):
                 fn = getattr(self.lib, name)
                 fn.argtypes = [_f, _f, _sz]
                 fn.restype = None
@@ -103,6 +128,50 @@ class Oracle:
     def bayes_materialize(self, w, mu, rho, eps, n):
         self._fn["bayes_materialize"](*(_p(a, np.float32) for a in (w, mu, rho, eps)), n)
 
+    def bayes_backward(self, dmu, drho, dw, eps, rho, n):
+        self._fn["bayes_backward"](*(_p(a, np.float32) for a in (dmu, drho, dw, eps, rho)), n)
+
+    def kl_forward(self, mu, rho, n, sigma_prior) -> float:
+        return float(self._fn["kl_forward"](_p(mu, np.float32), _p(rho, np.float32), n, sigma_prior))
+
+    def kl_backward(self, dmu, drho, mu, rho, n, sigma_prior, weight):
+        self._fn["kl_backward"](*(_p(a, np.float32) for a in (dmu, drho, mu, rho)), n, sigma_prior, weight)
+
+    def adamw_update(self, params, grads, m, v, n, t, lr, beta1, beta2, eps, wd):
+        self._fn["adamw_update"](*(_p(a, np.float32) for a in (params, grads, m, v)), n, t, lr, beta1,
+                                 beta2, eps, wd)
+
+    # ---- Philox and the GPU arms' ops (restatement only) ----------------------
+    def philox4x32_10(self, ctr, key) -> np.ndarray:
+        c = np.ascontiguousarray(ctr, dtype=np.uint32)
+        k = np.ascontiguousarray(key, dtype=np.uint32)
+        out = np.empty(4, np.uint32)
+        self.lib.oracle_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+        return out
+
+    def u01(self, x: int) -> float:
+        return float(self.lib.oracle_u01(x))
+
+    def philox_normal(self, seed: int, step: int, index: int) -> np.float32:
+        return np.float32(self.lib.oracle_philox_normal(seed, step, index))
+
+    def philox_normal_n(self, n: int, seed: int, step: int, first: int = 0) -> np.ndarray:
+        eps = np.empty(n, np.float32)
+        self.lib.oracle_philox_normal_n(eps.ctypes.data, n, seed, step, first)
+        return eps
+
+    def bayes_sample_philox(self, w, eps, mu, rho, n, seed, step):
+        self.lib.oracle_bayes_sample_philox(_p(w, np.float32), None if eps is None else _p(eps, np.float32),
+                                            _p(mu, np.float32), _p(rho, np.float32), n, seed, step)
+
+    def bayes_backward_philox(self, dmu, drho, dw, rho, n, seed, step):
+        self.lib.oracle_bayes_backward_philox(*(_p(a, np.float32) for a in (dmu, drho, dw, rho)), n, seed, step)
+
+    def bbb_step_fused(self, mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw, n, seed, step, sp, klw, bc1, bc2,
+                       lr, beta1, beta2, aeps, wd):
+        self.lib.oracle_bbb_step_fused(*(_p(a, np.float32) for a in (mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw)),
+                                       n, seed, step, sp, klw, bc1, bc2, lr, beta1, beta2, aeps, wd)
+
     # ---- host libm, elementwise (restatement only) ----------------------------
     def _map(self, name, x):
         y = np.empty_like(x)
@@ -120,6 +189,15 @@ class Oracle:
 
     def softplus(self, x):
         return self._map("oracle_softplus_n", x)
+
+    def logf(self, x):
+        return self._map("oracle_logf_n", x)
+
+    def cosf(self, x):
+        return self._map("oracle_cosf_n", x)
+
+    def sqrtf(self, x):
+        return self._map("oracle_sqrtf_n", x)
 
     def float_range(self, lo: int, n: int) -> np.ndarray:
         x = np.empty(n, np.float32)

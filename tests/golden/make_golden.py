@@ -17,6 +17,12 @@ config 1: C=384, V=27, B=4, T=64, and the 256x384 LayerNorm of config 2):
   gelu.npz        GELU fwd + bwd, 65,536 N(0,1) values + special values
   residual.npz    residual fwd + bwd, 65,536 values
   materialize.npz bayes_materialize, 65,536 values + special rho/eps cases
+  posterior.npz   bayes_backward, kl_forward, kl_backward and adamw_update
+                  (t = 1 and t = 7, with weight decay) over 16,384 parameters
+                  drawn like a trained run (rho in [-8, -2], log-uniform
+                  gradients, Adam states with v ~ m^2), plus special values
+
+    python tests/golden/make_golden.py posterior   # write only the named fixtures
 """
 import hashlib
 import json
@@ -38,9 +44,50 @@ def sha(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
 
 
-def main() -> None:
+def posterior(ref) -> dict:
+    g = gen.rng(606)
+    n = 16384
+    mu = gen.normal(g, (n,), 0, 0.02)
+    rho = (g.random(n) * 6.0 - 8.0).astype(np.float32)
+    sp = gen.special_floats()
+    rho = np.concatenate([rho, sp[np.isfinite(sp) & (np.abs(sp) < 100)]]).astype(np.float32)
+    n = rho.size
+    mu = np.concatenate([mu, gen.normal(g, (n - mu.size,), 0, 0.02)]).astype(np.float32)
+    sign = np.where(g.random(n) < 0.5, -1.0, 1.0)
+    dw = (sign * 10.0 ** (g.random(n) * 9.0 - 9.0)).astype(np.float32)
+    eps = gen.normal(g, (n,))
+    dmu0, drho0 = gen.normal(g, (n,), 0, 1e-3), gen.normal(g, (n,), 0, 1e-3)
+    dmu, drho = dmu0.copy(), drho0.copy()
+    ref.bayes_backward(dmu, drho, dw, eps, rho, n)
+    kl = np.float64(ref.kl_forward(mu, rho, n, 0.1))
+    kmu, krho = dmu0.copy(), drho0.copy()
+    ref.kl_backward(kmu, krho, mu, rho, n, 0.1, 1.0 / 300000.0)
+    m0 = (dw * gen.normal(g, (n,), 1.0, 0.3)).astype(np.float32)
+    v0 = (m0.astype(np.float64) ** 2 * (1.0 + g.random(n))).astype(np.float32)
+    adam = {}
+    for t in (1, 7):
+        p_, m_, v_ = mu.copy(), m0.copy(), v0.copy()
+        ref.adamw_update(p_, dw, m_, v_, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01)
+        adam.update({f"p{t}": p_, f"m{t}": m_, f"v{t}": v_})
+    return dict(mu=mu, rho=rho, dw=dw, eps=eps, dmu0=dmu0, drho0=drho0, dmu=dmu, drho=drho, kl=kl,
+                kmu=kmu, krho=krho, m0=m0, v0=v0, **adam)
+
+
+def main(only=None) -> None:
     ref = Oracle(reference=True)
+    meta_path = os.path.join(HERE, "golden.json")
     digests = {}
+    if only:
+        with open(meta_path) as f:
+            digests = json.load(f)["sha256"]
+        for name in only:
+            fx = {"posterior": posterior}[name](ref)
+            np.savez_compressed(os.path.join(HERE, name + ".npz"), **fx)
+            digests[name] = {k: sha(v) for k, v in fx.items() if k not in ("mu", "rho", "dw", "eps", "dmu0",
+                                                                            "drho0", "m0", "v0")}
+        write_meta(meta_path, digests)
+        print("wrote fixtures:", ", ".join(only))
+        return
 
     # ---- encoder ------------------------------------------------------------
     g = gen.rng(101)
@@ -136,15 +183,23 @@ def main() -> None:
     np.savez_compressed(os.path.join(HERE, "materialize.npz"), **ma)
     digests["materialize"] = {"w": sha(w)}
 
+    fx = posterior(ref)
+    np.savez_compressed(os.path.join(HERE, "posterior.npz"), **fx)
+    digests["posterior"] = {k: sha(v) for k, v in fx.items() if k not in ("mu", "rho", "dw", "eps", "dmu0",
+                                                                          "drho0", "m0", "v0")}
+    write_meta(meta_path, digests)
+    print("wrote fixtures:", ", ".join(sorted(digests)))
+
+
+def write_meta(path: str, digests: dict) -> None:
     import platform
     meta = {"generator": "tests/golden/make_golden.py",
             "reference": "train_bnn.c via make -C oracle ref (gcc -O2 -DSKIP_MAIN)",
             "glibc": platform.libc_ver()[1], "machine": platform.machine(),
             "sha256": digests}
-    with open(os.path.join(HERE, "golden.json"), "w") as f:
+    with open(path, "w") as f:
         json.dump(meta, f, indent=1, sort_keys=True)
-    print("wrote fixtures:", ", ".join(sorted(digests)))
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or None)

@@ -29,7 +29,8 @@ def test_header_declares_reference_ops():
     names = set(declared_functions())
     for op in ("encoder_forward", "encoder_backward", "layernorm_forward", "layernorm_backward",
                "gelu_forward", "gelu_backward", "residual_forward", "residual_backward",
-               "bayes_materialize"):
+               "bayes_materialize", "bayes_sample", "bayes_backward", "kl_forward", "kl_backward",
+               "adamw_update", "bbb_step_fused"):
         assert "ugk_" + op in names
 
 
@@ -49,6 +50,29 @@ def test_invalid_arguments_rejected_on_host():
     assert lib.ugk_layernorm_backward(None, None, None, None, None, None, None, None, 0, 5, 7) == 0
     assert lib.ugk_encoder_forward(None, None, None, None, 0, 0, 0) == 0
     assert lib.ugk_last_error() == b""
+
+
+def test_posterior_ops_reject_invalid_arguments_on_host():
+    import ugk
+    lib = ugk.lib
+    assert lib.ugk_bayes_sample(None, None, None, None, 4, 1, 1) == 1
+    assert b"NULL" in lib.ugk_last_error()
+    assert lib.ugk_bayes_sample(16, 16, 32, 48, 4, 1, 1) == 1  # w == eps
+    assert b"distinct" in lib.ugk_last_error()
+    assert lib.ugk_bayes_backward(16, 16, 32, 48, 64, 4) == 1  # dmu == drho
+    assert lib.ugk_bayes_backward_philox(16, 16, 32, 48, 4, 1, 1) == 1
+    assert lib.ugk_kl_backward(16, 16, 32, 48, 4, 0.1, 1.0) == 1
+    assert lib.ugk_adamw_update(16, 32, 48, 64, 4, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0) == 1  # t = 0
+    assert b"t must be >= 1" in lib.ugk_last_error()
+    assert lib.ugk_adamw_update(16, 32, 16, 64, 4, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0) == 1  # params == m
+    assert lib.ugk_bbb_step_fused(*([16] * 8), 4, 1, 1, *([0.1] * 9)) == 1
+    assert lib.ugk_kl_forward(None, 16, 32, 4, 0.1) == 1
+    kl = ctypes.c_double(5.0)
+    assert lib.ugk_kl_forward(ctypes.byref(kl), None, None, 0, 0.1) == 0 and kl.value == 0.0
+    assert lib.ugk_bayes_sample(None, None, None, None, 0, 1, 1) == 0
+    assert lib.ugk_bbb_step_fused(*([None] * 8), 0, 1, 1, *([0.1] * 9)) == 0
+    assert lib.ugk_diag_philox(None, None, 3) == 1
+    assert lib.ugk_last_error() != b""
 
 
 def test_param_layout_counts():

@@ -1,0 +1,271 @@
+"""GPU parity of the posterior-update ops of libugk.so (called through the C-ABI) against the
+CPU oracle: bayes_backward, kl_backward, adamw_update (bit-exact), kl_forward (double, within
+summation-order rounding), and the Philox ops (bayes_sample, bayes_backward_philox,
+bbb_step_fused).
+
+The Philox ops split into an exact part and a float part:
+  * the integer stream (Philox4x32-10 and u01) is bit-exact, checked on the device against the
+    Random123 known-answer vectors and the oracle;
+  * the Box-Muller transform calls the device logf and cosf. Over every u01 value the stream can
+    produce (all 79,691,777 of them) both stay within 2 ulp of the host glibc; eps is then within
+    8 ulp of the oracle's, and everything downstream of eps is bit-exact given the device's eps
+    (each Philox op equals its eps-taking twin fed with the eps the device drew).
+"""
+import ctypes
+import ctypes.util
+
+import numpy as np
+import pytest
+import torch
+
+import gen
+from test_oracle_posterior import PHILOX_KAT, bias_corrections, posterior_inputs, u01_domain
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+CFG5_N = 124_439_808  # GPT-2-124M with a tied head: param_offsets total at C=768 L=12 V=50257
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return bool(((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))).all())
+
+
+def assert_bits(g, c, what):
+    g = np.ascontiguousarray(g, np.float32).ravel()
+    c = np.ascontiguousarray(c, np.float32).ravel()
+    bad = np.nonzero((g.view(np.uint32) != c.view(np.uint32)) & ~(np.isnan(g) & np.isnan(c)))[0]
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {g.size} differ; first at {i}: gpu {g[i]!r} cpu {c[i]!r}")
+
+
+def ordered(a):
+    """float32 bit patterns as integers that increase with the value (ulp distances)."""
+    i = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+
+
+def ulp_dist(a, b):
+    return np.abs(ordered(a) - ordered(b))
+
+
+def assert_eps_close(g, c, what, max_ulp=8):
+    g = np.asarray(g, np.float32)
+    c = np.asarray(c, np.float32)
+    d = ulp_dist(g, c)
+    exact = float((d == 0).mean())
+    print(f"{what}: {exact:.4%} bit-exact, max {int(d.max())} ulp over {d.size}")
+    assert d.max() <= max_ulp, (what, int(d.max()), int(np.argmax(d)))
+    if d.size >= 1000:  # a wrong mapping of the stream would match almost nowhere
+        assert exact > 0.5, (what, exact)
+
+
+# ---- the integer stream ---------------------------------------------------------------
+
+def test_philox_device_known_answers_and_oracle(gpu, oracle):
+    g = gen.rng(901)
+    rand = g.integers(0, 1 << 32, size=(4096, 6), dtype=np.uint64).astype(np.uint32)
+    kat = np.array([list(c) + list(k) for c, k, _ in PHILOX_KAT], np.uint32)
+    tuples = np.concatenate([kat, rand])
+    out = torch.empty(tuples.shape[0] * 4, dtype=torch.int32, device=DEV)
+    gpu.diag_philox(out, dev(tuples.view(np.int32)))
+    got = host(out).view(np.uint32).reshape(-1, 4)
+    for i, (_, _, want) in enumerate(PHILOX_KAT):
+        assert got[i].tolist() == list(want)
+    want = np.array([oracle.philox4x32_10(t[:4], t[4:]) for t in tuples], np.uint32)
+    assert (got == want).all()
+
+
+# ---- the float transform over its whole input domain ------------------------------------
+
+def test_device_logf_cosf_over_the_u01_domain(gpu, oracle):
+    u = u01_domain()
+    theta = np.float32(6.28318530717958647692) * u
+    for fn, x, want in (("logf", u, oracle.logf(u)), ("cosf", theta, oracle.cosf(theta))):
+        tx = dev(x)
+        out = torch.empty_like(tx)
+        gpu.diag_math_eval(fn, out, tx)
+        got = host(out)
+        d = ulp_dist(got, want)
+        print(f"device {fn} vs glibc over {x.size} inputs: {(d == 0).mean():.4%} identical, "
+              f"{int((d == 1).sum())} at 1 ulp, max {int(d.max())} ulp")
+        assert d.max() <= 2, (fn, int(d.max()), float(x[np.argmax(d)]))
+        del tx, out
+
+
+def test_device_sqrtf_is_correctly_rounded_everywhere(gpu, oracle):
+    n, first = gpu.diag_math_mismatch("sqrtf")
+    assert n == 0, hex(first)
+    g = gen.rng(902)
+    x = np.abs(np.concatenate([gen.normal(g, (1 << 20,), 0, 1e3), gen.special_floats()])).astype(np.float32)
+    tx = dev(x)
+    out = torch.empty_like(tx)
+    gpu.diag_math_eval("sqrtf", out, tx)
+    assert_bits(host(out), oracle.sqrtf(x), "sqrtf vs host")
+
+
+# ---- the ops ----------------------------------------------------------------------------
+
+SIZES = [1, 3, 5, 4096 + 3, (1 << 20) + 1]
+
+
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_bayes_backward_kl_backward_adamw(gpu, oracle, n, offset):
+    mu, rho, dw, eps, m, v = posterior_inputs(910 + n, n)
+    rho[: min(n, 3)] = np.array([25.0, -110.0, 0.0], np.float32)[: min(n, 3)]
+    big = lambda a: dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
+    dmu0, drho0 = gen.normal(gen.rng(1), (n,), 0, 1e-3), gen.normal(gen.rng(2), (n,), 0, 1e-3)
+    t_mu, t_rho, t_dw, t_eps = big(mu), big(rho), big(dw), big(eps)
+    t_dmu, t_drho = big(dmu0), big(drho0)
+    gpu.bayes_backward(t_dmu, t_drho, t_dw, t_eps, t_rho, n)
+    dmu, drho = dmu0.copy(), drho0.copy()
+    oracle.bayes_backward(dmu, drho, dw, eps, rho, n)
+    assert_bits(host(t_dmu), dmu, "bayes_backward dmu")
+    assert_bits(host(t_drho), drho, "bayes_backward drho")
+    k_dmu, k_drho = big(dmu0), big(drho0)
+    gpu.kl_backward(k_dmu, k_drho, t_mu, t_rho, n, 0.1, 1.0 / 300000.0)
+    dmu, drho = dmu0.copy(), drho0.copy()
+    oracle.kl_backward(dmu, drho, mu, rho, n, 0.1, 1.0 / 300000.0)
+    assert_bits(host(k_dmu), dmu, "kl_backward dmu")
+    assert_bits(host(k_drho), drho, "kl_backward drho")
+    for t in (1, 7, 1000):
+        tp, tm, tv = big(mu), big(m), big(v)
+        gpu.adamw_update(tp, t_dw, tm, tv, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01)
+        p_, m_, v_ = mu.copy(), m.copy(), v.copy()
+        oracle.adamw_update(p_, dw, m_, v_, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01)
+        assert_bits(host(tp), p_, f"adamw t={t} params")
+        assert_bits(host(tm), m_, f"adamw t={t} m")
+        assert_bits(host(tv), v_, f"adamw t={t} v")
+
+
+def test_golden_posterior_on_gpu(gpu):
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "posterior.npz")
+    with np.load(path, allow_pickle=False) as z:
+        d = {k: z[k] for k in z.files}
+    n = d["mu"].size
+    t_dmu, t_drho = dev(d["dmu0"]), dev(d["drho0"])
+    gpu.bayes_backward(t_dmu, t_drho, dev(d["dw"]), dev(d["eps"]), dev(d["rho"]), n)
+    assert_bits(host(t_dmu), d["dmu"], "golden bayes_backward dmu")
+    assert_bits(host(t_drho), d["drho"], "golden bayes_backward drho")
+    k_dmu, k_drho = dev(d["dmu0"]), dev(d["drho0"])
+    gpu.kl_backward(k_dmu, k_drho, dev(d["mu"]), dev(d["rho"]), n, 0.1, 1.0 / 300000.0)
+    assert_bits(host(k_dmu), d["kmu"], "golden kl_backward dmu")
+    assert_bits(host(k_drho), d["krho"], "golden kl_backward drho")
+    kl = gpu.kl_forward(dev(d["mu"]), dev(d["rho"]), n, 0.1)
+    assert abs(kl - float(d["kl"])) <= 1e-12 * abs(float(d["kl"]))
+    for t in (1, 7):
+        tp, tm, tv = dev(d["mu"]), dev(d["m0"]), dev(d["v0"])
+        gpu.adamw_update(tp, dev(d["dw"]), tm, tv, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01)
+        assert_bits(host(tp), d[f"p{t}"], f"golden adamw t={t}")
+        assert_bits(host(tm), d[f"m{t}"], f"golden adamw m t={t}")
+        assert_bits(host(tv), d[f"v{t}"], f"golden adamw v t={t}")
+
+
+@pytest.mark.parametrize("n", [1, 1000, 5_000_003])
+def test_kl_forward(gpu, oracle, n):
+    mu, rho, _, _, _, _ = posterior_inputs(920 + n, n)
+    want = oracle.kl_forward(mu, rho, n, 0.1)
+    tm, tr = dev(mu), dev(rho)
+    got = gpu.kl_forward(tm, tr, n, 0.1)
+    assert abs(got - want) <= 1e-10 * abs(want), (got, want)
+    assert gpu.kl_forward(tm, tr, n, 0.1) == got  # fixed summation order
+    assert gpu.kl_forward(tm, tr, 0, 0.1) == 0.0
+
+
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("offset", [0, 1])
+def test_bayes_sample_and_backward_philox(gpu, oracle, n, offset):
+    seed, step = 0x1234_5678_9ABC, 17
+    mu, rho, dw, _, _, _ = posterior_inputs(930 + n, n)
+    big = lambda a: dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
+    t_mu, t_rho, t_dw = big(mu), big(rho), big(dw)
+    t_w, t_eps, t_w2 = big(np.zeros(n, np.float32)), big(np.zeros(n, np.float32)), big(np.zeros(n, np.float32))
+    gpu.bayes_sample(t_w, t_eps, t_mu, t_rho, n, seed, step)
+    gpu.bayes_sample(t_w2, None, t_mu, t_rho, n, seed, step)
+    eps_dev = host(t_eps)
+    assert_eps_close(eps_dev, oracle.philox_normal_n(n, seed, step), f"eps n={n}")
+    # downstream of eps: bit-exact
+    w = np.zeros(n, np.float32)
+    oracle.bayes_materialize(w, mu, rho, eps_dev, n)
+    assert_bits(host(t_w), w, "bayes_sample w")
+    assert_bits(host(t_w2), w, "bayes_sample w (no eps output)")
+    dmu0, drho0 = gen.normal(gen.rng(3), (n,), 0, 1e-3), gen.normal(gen.rng(4), (n,), 0, 1e-3)
+    t_dmu, t_drho = big(dmu0), big(drho0)
+    gpu.bayes_backward_philox(t_dmu, t_drho, t_dw, t_rho, n, seed, step)
+    dmu, drho = dmu0.copy(), drho0.copy()
+    oracle.bayes_backward(dmu, drho, dw, eps_dev, rho, n)
+    assert_bits(host(t_dmu), dmu, "bayes_backward_philox dmu")
+    assert_bits(host(t_drho), drho, "bayes_backward_philox drho")
+
+
+@pytest.mark.parametrize("klw", [0.0, 1.0 / 300000.0])
+@pytest.mark.parametrize("n,offset", [(5, 0), (4096 + 3, 1), ((1 << 20) + 1, 0)])
+def test_bbb_step_fused(gpu, oracle, klw, n, offset):
+    seed, step = 77, 12
+    sp, lr, b1, b2, aeps, wd = 0.1, 3e-4, 0.9, 0.999, 1e-8, 0.0
+    mu, rho, dw, _, m, v = posterior_inputs(940 + n, n)
+    state = [mu, rho, m, v, (m * 0.5).astype(np.float32), (v * 0.25).astype(np.float32)]
+    bc1, bc2 = bias_corrections(b1, b2, step)
+    big = lambda a: dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
+    f = [big(a) for a in state]
+    f_w, f_dw = big(np.zeros(n, np.float32)), big(dw)
+    gpu.bbb_step_fused(*f, f_w, f_dw, n, seed, step, sp, klw, float(bc1), float(bc2), lr, b1, b2, aeps, wd)
+    # the device's own unfused ops, fed the same Philox stream: bit-identical
+    c_mu, c_rho, c_m1, c_v1, c_m2, c_v2 = (big(a) for a in state)
+    g_mu, g_rho = big(np.zeros(n, np.float32)), big(np.zeros(n, np.float32))
+    t_dw = big(dw)
+    gpu.bayes_backward_philox(g_mu, g_rho, t_dw, c_rho, n, seed, step)
+    if klw > 0:
+        gpu.kl_backward(g_mu, g_rho, c_mu, c_rho, n, sp, klw)
+    gpu.adamw_update(c_mu, g_mu, c_m1, c_v1, n, step, lr, b1, b2, aeps, wd)
+    gpu.adamw_update(c_rho, g_rho, c_m2, c_v2, n, step, lr, b1, b2, aeps, wd)
+    c_w, c_eps = big(np.zeros(n, np.float32)), big(np.zeros(n, np.float32))
+    gpu.bayes_sample(c_w, c_eps, c_mu, c_rho, n, seed, step + 1)
+    names = ("mu", "rho", "m_mu", "v_mu", "m_rho", "v_rho", "w")
+    for name, a, b in zip(names, f + [f_w], [c_mu, c_rho, c_m1, c_v1, c_m2, c_v2, c_w]):
+        assert_bits(host(a), host(b), f"fused vs unfused {name}")
+    assert (host(f_dw) == 0).all()
+    # and against the oracle's fused step: equal up to the eps of the two draws
+    o = [a.copy() for a in state]
+    o_w, o_dw = np.zeros(n, np.float32), dw.copy()
+    oracle.bbb_step_fused(*o, o_w, o_dw, n, seed, step, sp, klw, bc1, bc2, lr, b1, b2, aeps, wd)
+    got_mu = host(f[0])
+    assert_bits(got_mu, o[0], "fused mu vs oracle")  # the data gradient onto mu carries no eps
+    for name, a, b in zip(("rho", "m_rho", "v_rho"), (f[1], f[4], f[5]), (o[1], o[4], o[5])):
+        assert np.allclose(host(a), b, rtol=1e-5, atol=1e-7 * float(np.abs(b).max())), name
+
+
+def test_full_cfg5_bayes_sample(gpu, oracle):
+    """The sample at GPT-2-124M size: indices up to 124M map to the oracle's stream."""
+    n, seed, step = CFG5_N, 0xC0FFEE, 3
+    g = gen.rng(950)
+    mu = torch.empty(n, device=DEV).normal_(0, 0.02, generator=torch.Generator(DEV).manual_seed(1))
+    rho = torch.empty(n, device=DEV).normal_(-5, 0.1, generator=torch.Generator(DEV).manual_seed(2))
+    w = torch.empty(n, device=DEV)
+    eps = torch.empty(n, device=DEV)
+    gpu.bayes_sample(w, eps, mu, rho, n, seed, step)
+    torch.cuda.synchronize()
+    idx = np.unique(np.concatenate([g.integers(0, n, 200_000), np.arange(n - 1000, n), np.arange(1000)]))
+    ti = torch.from_numpy(idx).to(DEV)
+    e_dev = host(eps[ti])
+    e_ref = np.array([oracle.philox_normal(seed, step, int(i)) for i in idx[:20000]], np.float32)
+    assert_eps_close(e_dev[:20000], e_ref, "cfg5 eps (sampled)")
+    w_ref = np.zeros(idx.size, np.float32)
+    oracle.bayes_materialize(w_ref, host(mu[ti]), host(rho[ti]), e_dev, idx.size)
+    assert_bits(host(w[ti]), w_ref, "cfg5 w (sampled)")
+    mean, var = float(eps.double().mean()), float(eps.double().var())
+    assert abs(mean) < 5.0 / np.sqrt(n) and abs(var - 1.0) < 5.0 * np.sqrt(2.0 / n), (mean, var)

@@ -4,6 +4,7 @@
 // Every entry point validates its arguments on the host before it touches the
 // HIP runtime, so invalid calls are reported (UGK_EINVAL + message) without a
 // GPU, and no kernel is ever launched with a shape it does not expect.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -106,6 +107,15 @@ bool any_null(std::initializer_list<const void *> ps) {
   return false;
 }
 
+// Buffers one call writes must be distinct (the CPU loops would otherwise see
+// each other's stores within an element).
+bool any_same(std::initializer_list<const void *> ps) {
+  for (auto a = ps.begin(); a != ps.end(); ++a)
+    for (auto b = a + 1; b != ps.end(); ++b)
+      if (*a == *b) return true;
+  return false;
+}
+
 }  // namespace
 
 extern "C" {
@@ -194,6 +204,95 @@ int ugk_bayes_materialize(float *w, const float *mu, const float *rho, const flo
   if (n == 0) return ok();
   if (any_null({w, mu, rho, eps})) return bad(fn, "NULL pointer");
   if (int e = launch_bayes_materialize(w, mu, rho, eps, n)) return e;
+  return ok();
+}
+
+int ugk_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
+                     unsigned long long seed, int step) {
+  const char *fn = "ugk_bayes_sample";
+  if (n == 0) return ok();
+  if (any_null({w, mu, rho})) return bad(fn, "NULL pointer");
+  if (eps && w == eps) return bad(fn, "w and eps must be distinct buffers");
+  if (int e = launch_bayes_sample(w, eps, mu, rho, n, seed, step)) return e;
+  return ok();
+}
+
+int ugk_bayes_backward(float *dmu, float *drho, const float *dw, const float *eps, const float *rho,
+                       size_t n) {
+  const char *fn = "ugk_bayes_backward";
+  if (n == 0) return ok();
+  if (any_null({dmu, drho, dw, eps, rho})) return bad(fn, "NULL pointer");
+  if (dmu == drho) return bad(fn, "dmu and drho must be distinct buffers");
+  if (int e = launch_bayes_backward(dmu, drho, dw, eps, rho, n)) return e;
+  return ok();
+}
+
+int ugk_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho, size_t n,
+                              unsigned long long seed, int step) {
+  const char *fn = "ugk_bayes_backward_philox";
+  if (n == 0) return ok();
+  if (any_null({dmu, drho, dw, rho})) return bad(fn, "NULL pointer");
+  if (dmu == drho) return bad(fn, "dmu and drho must be distinct buffers");
+  if (int e = launch_bayes_backward_philox(dmu, drho, dw, rho, n, seed, step)) return e;
+  return ok();
+}
+
+int ugk_kl_forward(double *kl, const float *mu, const float *rho, size_t n, float sigma_prior) {
+  const char *fn = "ugk_kl_forward";
+  if (!kl) return bad(fn, "NULL result pointer");
+  if (n == 0) {
+    *kl = 0.0;
+    return ok();
+  }
+  if (any_null({mu, rho})) return bad(fn, "NULL pointer");
+  double *buf = static_cast<double *>(scratch(kl_forward_scratch()));
+  if (!buf) return UGK_ENOMEM;
+  if (int e = launch_kl_forward(buf, buf + 1, mu, rho, n, sigma_prior)) return e;
+  double h = 0.0;
+  if (hipMemcpyAsync(&h, buf, sizeof h, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+      hipStreamSynchronize(stream()) != hipSuccess) {
+    const hipError_t err = hipGetLastError();
+    return set_error(UGK_EHIP, "%s: %s", fn, hipGetErrorString(err));
+  }
+  *kl = h;
+  return ok();
+}
+
+int ugk_kl_backward(float *dmu, float *drho, const float *mu, const float *rho, size_t n,
+                    float sigma_prior, float weight) {
+  const char *fn = "ugk_kl_backward";
+  if (n == 0) return ok();
+  if (any_null({dmu, drho, mu, rho})) return bad(fn, "NULL pointer");
+  if (dmu == drho) return bad(fn, "dmu and drho must be distinct buffers");
+  if (int e = launch_kl_backward(dmu, drho, mu, rho, n, sigma_prior, weight)) return e;
+  return ok();
+}
+
+int ugk_adamw_update(float *params, const float *grads, float *m, float *v, size_t n, int t, float lr,
+                     float beta1, float beta2, float eps, float wd) {
+  const char *fn = "ugk_adamw_update";
+  if (t < 1) return bad(fn, "t must be >= 1");
+  if (n == 0) return ok();
+  if (any_null({params, grads, m, v})) return bad(fn, "NULL pointer");
+  if (any_same({params, m, v})) return bad(fn, "params, m and v must be distinct buffers");
+  // train_bnn.c:704-705, on the host as there.
+  const float bc1 = 1.0f - powf(beta1, (float)t);
+  const float bc2 = 1.0f - powf(beta2, (float)t);
+  if (int e = launch_adamw(params, grads, m, v, n, lr, beta1, beta2, eps, wd, bc1, bc2)) return e;
+  return ok();
+}
+
+int ugk_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m_rho, float *v_rho,
+                       float *w, float *dw, size_t n, unsigned long long seed, int step, float sp,
+                       float klw, float bc1, float bc2, float lr, float beta1, float beta2, float aeps,
+                       float wd) {
+  const char *fn = "ugk_bbb_step_fused";
+  if (n == 0) return ok();
+  if (any_null({mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw})) return bad(fn, "NULL pointer");
+  if (any_same({mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw})) return bad(fn, "the eight buffers must be distinct");
+  if (int e = launch_bbb_step_fused(mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw, n, seed, step, sp, klw, bc1,
+                                    bc2, lr, beta1, beta2, aeps, wd))
+    return e;
   return ok();
 }
 

@@ -1,0 +1,285 @@
+// ugk_bayes.hip - the O(P) posterior path around the layer kernels: Philox
+// sampling of w, the data-term backward onto (mu, rho), the KL term and its
+// gradient, AdamW, and the fused Bayes-by-Backprop step.
+//
+// All are streams over flat fp32 parameter vectors (ugk_map.h). Arithmetic
+// follows train_bnn.c operation by operation (built with -ffp-contract=off),
+// with expf/log1pf exact to glibc (ugk_libm_dev.h) and IEEE division and
+// square root, so every op that is given its eps is bit-identical to the CPU
+// oracle. The Philox ops draw eps on the fly (ugk_philox.h): their integer
+// stream is exact, their Box-Muller transform uses the device logf/cosf.
+#include "ugk_map.h"
+#include "ugk_philox.h"
+
+namespace ugk {
+namespace {
+
+__device__ __forceinline__ float expf_lds(float x, const uint64_t *tab) {
+  return ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
+}
+
+// train_bnn.c:820-822 (sigmoidf_), gpt2_kernels.cuh:199-201 (d_sigmoid).
+__device__ __forceinline__ float sigmoid_lds(float x, const uint64_t *tab) {
+  return 1.0f / (1.0f + expf_lds(-x, tab));
+}
+
+struct PhiloxParams {
+  unsigned long long seed;
+  int step;
+};
+
+// train_bnn_gpu.cu:93-97 (k_bayes_sample): w = mu + softplus(rho) * eps(seed,
+// step, i). Loads mu, rho.
+struct BayesSample : MapOp {
+  static constexpr int kLoads = 2, kStores = 1;
+  static constexpr bool kTable = true;
+  static constexpr int kUnroll = 1;
+  typedef PhiloxParams Params;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
+    st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * ugk_dev_philox_normal(p.seed, p.step, i);
+  }
+};
+
+// The same draw, also storing eps (train_bnn.c:841-845's bayes_sample keeps eps
+// for the backward). Stores w, eps.
+struct BayesSampleEps : BayesSample {
+  static constexpr int kStores = 2;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
+    const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
+    st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * eps;
+    st[1] = eps;
+  }
+};
+
+// train_bnn.c:855-861: dmu += dw; drho += dw * eps * sigmoid(rho).
+// Loads dw, eps, rho, dmu, drho; stores dmu, drho.
+struct BayesBackward : MapOp {
+  static constexpr int kLoads = 5, kStores = 2;
+  static constexpr bool kTable = true;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t, Params) {
+    st[0] = ld[3] + ld[0];
+    st[1] = ld[4] + ld[0] * ld[1] * sigmoid_lds(ld[2], tab);
+  }
+};
+
+// train_bnn_gpu.cu:99-109 (k_bayes_backward): the same with eps regenerated.
+// Loads dw, rho, dmu, drho; stores dmu, drho.
+struct BayesBackwardPhilox : MapOp {
+  static constexpr int kLoads = 4, kStores = 2;
+  static constexpr bool kTable = true;
+  static constexpr int kUnroll = 1;
+  typedef PhiloxParams Params;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
+    const float g = ld[0];
+    const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
+    st[0] = ld[2] + g;
+    st[1] = ld[3] + g * eps * sigmoid_lds(ld[1], tab);
+  }
+};
+
+// train_bnn.c:966-979: dmu += weight * (mu / sp2);
+// drho += weight * (sigma / sp2 - 1 / sigma) * sigmoid(rho), sigma = softplus(rho).
+// Loads mu, rho, dmu, drho; stores dmu, drho.
+struct KlBackward : MapOp {
+  static constexpr int kLoads = 4, kStores = 2;
+  static constexpr bool kTable = true;
+  struct Params {
+    float sp2, weight;
+  };
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t, const Params &p) {
+    const float r = ld[1];
+    const float sigma = ugk_dev_softplusf_lds(r, tab);
+    st[0] = ld[2] + p.weight * (ld[0] / p.sp2);
+    const float dsigma = sigma / p.sp2 - 1.0f / sigma;
+    st[1] = ld[3] + p.weight * dsigma * sigmoid_lds(r, tab);
+  }
+};
+
+struct AdamParams {
+  float lr, beta1, beta2, eps, wd, bc1, bc2;
+};
+
+// One AdamW update of (param, m, v) by gradient g; train_bnn.c:704-716 and
+// gpt2_kernels.cuh:973-984 evaluate the same expression.
+__device__ __forceinline__ float adamw_one(float param, float g, float &m, float &v, const AdamParams &a) {
+  m = a.beta1 * m + (1.0f - a.beta1) * g;
+  v = a.beta2 * v + (1.0f - a.beta2) * g * g;
+  const float m_hat = m / a.bc1;
+  const float v_hat = v / a.bc2;
+  return param - a.lr * (m_hat / (sqrtf(v_hat) + a.eps) + a.wd * param);
+}
+
+// train_bnn.c:699-717. Loads params, grads, m, v; stores params, m, v.
+struct AdamW : MapOp {
+  static constexpr int kLoads = 4, kStores = 3;
+  typedef AdamParams Params;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, const Params &p) {
+    float m = ld[2], v = ld[3];
+    st[0] = adamw_one(ld[0], ld[1], m, v, p);
+    st[1] = m;
+    st[2] = v;
+  }
+};
+
+// train_bnn_gpu.cu:173-217 (k_bbb_step_fused): bayes_backward with
+// eps(step), kl_backward when klw > 0, AdamW on mu and on rho, dw cleared,
+// and w drawn for step + 1 from the updated parameters.
+// Loads dw, rho, mu, m_mu, v_mu, m_rho, v_rho;
+// stores dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w.
+struct BbbStepFused : MapOp {
+  static constexpr int kLoads = 7, kStores = 8;
+  static constexpr bool kTable = true;
+  static constexpr int kUnroll = 1;
+  struct Params {
+    unsigned long long seed;
+    int step;
+    float sp, klw;
+    AdamParams adam;
+  };
+  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
+    const float g = ld[0], r = ld[1], mm = ld[2];
+    const float sg = sigmoid_lds(r, tab);
+    float gmu = g;
+    float grho = g * ugk_dev_philox_normal(p.seed, p.step, i) * sg;
+    if (p.klw > 0.0f) {
+      const float sp2 = p.sp * p.sp, sigma = ugk_dev_softplusf_lds(r, tab);
+      gmu += p.klw * (mm / sp2);
+      grho += p.klw * (sigma / sp2 - 1.0f / sigma) * sg;
+    }
+    float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
+    const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
+    const float rho_new = adamw_one(r, grho, m2, v2, p.adam);
+    st[0] = 0.0f;
+    st[1] = mu_new;
+    st[2] = rho_new;
+    st[3] = m1;
+    st[4] = v1;
+    st[5] = m2;
+    st[6] = v2;
+    st[7] = mu_new + ugk_dev_softplusf_lds(rho_new, tab) * ugk_dev_philox_normal(p.seed, p.step + 1, i);
+  }
+};
+
+// ---- KL total (train_bnn.c:941-957) -----------------------------------------
+// Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2.
+// Summed in a fixed order: every thread over a fixed stride of float4 slots,
+// then a wavefront butterfly, then the block's waves in order, then one block
+// over the per-block partials. Deterministic for a given n.
+constexpr int kKlBlocks = 2048;
+
+__device__ __forceinline__ double kl_term(float mu, float rho, double sp, double two_sp2, const uint64_t *tab) {
+  const double sigma = (double)ugk_dev_softplusf_lds(rho, tab);
+  const double m = (double)mu;
+  return log(sp / sigma) + (sigma * sigma + m * m) / two_sp2 - 0.5;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ double block_sum_d(double v, double *lds) {
+  v = wave_sum_d(v);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kBlock / kWave; w++) t += lds[w];
+  return t;
+}
+
+__global__ __launch_bounds__(kBlock) void k_kl_partial(double *part, const float *mu, const float *rho,
+                                                       size_t n, float sigma_prior, float sp2) {
+  __shared__ uint64_t tab[32];
+  __shared__ double lds[kBlock / kWave];
+  ugk_exp2_stage(tab);
+  __syncthreads();
+  const double sp = (double)sigma_prior, two_sp2 = 2.0 * (double)sp2;
+  double acc = 0.0;
+  const size_t stride = (size_t)gridDim.x * kBlock;
+  const bool vec = aligned16(mu) && aligned16(rho);
+  const size_t n4 = vec ? n / 4 : 0;
+  for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+    const float4 m = ld_nt(reinterpret_cast<const float4 *>(mu) + i);
+    const float4 r = ld_nt(reinterpret_cast<const float4 *>(rho) + i);
+    acc += kl_term(m.x, r.x, sp, two_sp2, tab);
+    acc += kl_term(m.y, r.y, sp, two_sp2, tab);
+    acc += kl_term(m.z, r.z, sp, two_sp2, tab);
+    acc += kl_term(m.w, r.w, sp, two_sp2, tab);
+  }
+  for (size_t i = 4 * n4 + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    acc += kl_term(mu[i], rho[i], sp, two_sp2, tab);
+  const double t = block_sum_d(acc, lds);
+  if (threadIdx.x == 0) part[blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(kBlock) void k_kl_final(double *out, const double *part, int nparts) {
+  __shared__ double lds[kBlock / kWave];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) acc += part[i];
+  const double t = block_sum_d(acc, lds);
+  if (threadIdx.x == 0) out[0] = t;
+}
+
+}  // namespace
+
+int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
+                        unsigned long long seed, int step) {
+  if (eps) {
+    Streams<BayesSampleEps> s{{mu, rho}, {w, eps}, {seed, step}};
+    return run_map(s, n, "bayes_sample");
+  }
+  Streams<BayesSample> s{{mu, rho}, {w}, {seed, step}};
+  return run_map(s, n, "bayes_sample");
+}
+
+int launch_bayes_backward(float *dmu, float *drho, const float *dw, const float *eps,
+                          const float *rho, size_t n) {
+  Streams<BayesBackward> s{{dw, eps, rho, dmu, drho}, {dmu, drho}, {}};
+  return run_map(s, n, "bayes_backward");
+}
+
+int launch_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho,
+                                 size_t n, unsigned long long seed, int step) {
+  Streams<BayesBackwardPhilox> s{{dw, rho, dmu, drho}, {dmu, drho}, {seed, step}};
+  return run_map(s, n, "bayes_backward_philox");
+}
+
+int launch_kl_backward(float *dmu, float *drho, const float *mu, const float *rho, size_t n,
+                       float sigma_prior, float weight) {
+  Streams<KlBackward> s{{mu, rho, dmu, drho}, {dmu, drho}, {sigma_prior * sigma_prior, weight}};
+  return run_map(s, n, "kl_backward");
+}
+
+int launch_adamw(float *params, const float *grads, float *m, float *v, size_t n, float lr,
+                 float beta1, float beta2, float eps, float wd, float bc1, float bc2) {
+  Streams<AdamW> s{{params, grads, m, v}, {params, m, v}, {lr, beta1, beta2, eps, wd, bc1, bc2}};
+  return run_map(s, n, "adamw_update");
+}
+
+int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m_rho, float *v_rho,
+                          float *w, float *dw, size_t n, unsigned long long seed, int step, float sp,
+                          float klw, float bc1, float bc2, float lr, float beta1, float beta2,
+                          float aeps, float wd) {
+  Streams<BbbStepFused> s{{dw, rho, mu, m_mu, v_mu, m_rho, v_rho},
+                          {dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w},
+                          {seed, step, sp, klw, {lr, beta1, beta2, aeps, wd, bc1, bc2}}};
+  return run_map(s, n, "bbb_step_fused");
+}
+
+size_t kl_forward_scratch() { return (kKlBlocks + 1) * sizeof(double); }
+
+int launch_kl_forward(double *out_dev, double *part, const float *mu, const float *rho, size_t n,
+                      float sigma_prior) {
+  const float sp2 = sigma_prior * sigma_prior;
+  size_t want = (n + 4ull * kBlock - 1) / (4ull * kBlock);
+  const int blocks = (int)(want < 1 ? 1 : (want > (size_t)kKlBlocks ? (size_t)kKlBlocks : want));
+  hipLaunchKernelGGL(k_kl_partial, dim3(blocks), dim3(kBlock), 0, stream(), part, mu, rho, n,
+                     sigma_prior, sp2);
+  hipLaunchKernelGGL(k_kl_final, dim3(1), dim3(kBlock), 0, stream(), out_dev, part, blocks);
+  return check_launch("kl_forward");
+}
+
+}  // namespace ugk

@@ -5,12 +5,16 @@
 #include "../../include/ugk.h"
 #include "ugk_internal.h"
 #include "ugk_libm_dev.h"
+#include "ugk_philox.h"
 
 namespace ugk {
 namespace {
 
 // fn codes: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf, 4 softplus (the kernels'
-// math); 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
+// math); 5 logf, 6 cosf (the device library's, as the Box-Muller transform
+// calls them; evaluation only), 7 sqrtf (its reference: the double square
+// root rounded to float, which is the correctly rounded result);
+// 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
 // (ugk_div_t<s>), to compare the candidate sequences.
 template <int FN>
 __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
@@ -19,6 +23,9 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 2) return ugk_dev_expm1f(x);
   if (FN == 3) return ugk_dev_tanhf(x);
   if (FN == 4) return ugk_dev_softplusf_lds(x, tab);
+  if (FN == 5) return logf(x);
+  if (FN == 6) return cosf(x);
+  if (FN == 7) return sqrtf(x);
   if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
   if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
@@ -30,6 +37,9 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 1 || (FN >= 20 && FN < 24)) return ugk_log1pf(x);
   if (FN == 3 || (FN >= 10 && FN < 14)) return ugk_tanhf(x);
   if (FN == 4) return ugk_softplusf(x);
+  if (FN == 5) return logf(x);
+  if (FN == 6) return cosf(x);
+  if (FN == 7) return (float)sqrt((double)x);
   return ugk_expm1f(x);
 }
 
@@ -66,7 +76,17 @@ __global__ __launch_bounds__(kBlock) void k_math_eval(int variant, float *out, c
     out[i] = variant == 0 ? kernel_math<FN>(in[i], tab) : reference_math<FN>(in[i]);
 }
 
-bool fn_ok(int fn) { return (fn >= 0 && fn <= 4) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
+// Philox4x32-10 of arbitrary (counter, key) tuples: in holds 6 words per
+// tuple (c0..c3, k0, k1), out receives the 4 output words.
+__global__ __launch_bounds__(kBlock) void k_philox(unsigned *out, const unsigned *in, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (size_t)gridDim.x * kBlock) {
+    const unsigned *c = in + 6 * i;
+    const UgkPhilox4 o = ugk_philox4x32_10(c[0], c[1], c[2], c[3], c[4], c[5]);
+    for (int j = 0; j < 4; j++) out[4 * i + j] = o.w[j];
+  }
+}
+
+bool fn_ok(int fn) { return (fn >= 0 && fn <= 7) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
 }  // namespace
@@ -95,7 +115,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
     switch (fn) {
 #define UGK_MM(f) \
   case f: hipLaunchKernelGGL(k_math_mismatch<f>, grid, block, 0, stream(), (unsigned long long)lo, count, &d->n, &d->first); break;
-      UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4)
+      UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4) UGK_MM(5) UGK_MM(6) UGK_MM(7)
       UGK_MM(10) UGK_MM(11) UGK_MM(12) UGK_MM(13) UGK_MM(20) UGK_MM(21) UGK_MM(22) UGK_MM(23)
       UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
 #undef UGK_MM
@@ -120,10 +140,19 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
   switch (fn) {
 #define UGK_EV(f) \
   case f: hipLaunchKernelGGL(k_math_eval<f>, dim3(g), dim3(kBlock), 0, stream(), variant, out, in, n); break;
-    UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4)
+    UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4) UGK_EV(5) UGK_EV(6) UGK_EV(7)
     UGK_EV(10) UGK_EV(11) UGK_EV(12) UGK_EV(13) UGK_EV(20) UGK_EV(21) UGK_EV(22) UGK_EV(23)
     UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");
+}
+
+extern "C" int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n) {
+  if (n == 0) return UGK_OK;
+  if (!out || !in) return set_error(UGK_EINVAL, "ugk_diag_philox: NULL pointer");
+  unsigned g = grid_for(n, kBlock);
+  if (g > 65536u) g = 65536u;
+  hipLaunchKernelGGL(k_philox, dim3(g), dim3(kBlock), 0, stream(), out, in, n);
+  return check_launch("ugk_diag_philox");
 }

@@ -18,7 +18,7 @@ int check_launch(const char *what);
 // with the error already set).
 void *scratch(size_t bytes);
 
-inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+__host__ __device__ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline unsigned grid_for(size_t work, size_t per_block) {
   return (unsigned)((work + per_block - 1) / per_block);
@@ -55,6 +55,23 @@ int launch_gelu_forward(float *out, const float *inp, size_t n);
 int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n);
 int launch_bayes_materialize(float *w, const float *mu, const float *rho,
                              const float *eps, size_t n);
+int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
+                        unsigned long long seed, int step);
+int launch_bayes_backward(float *dmu, float *drho, const float *dw, const float *eps,
+                          const float *rho, size_t n);
+int launch_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho,
+                                 size_t n, unsigned long long seed, int step);
+int launch_kl_backward(float *dmu, float *drho, const float *mu, const float *rho, size_t n,
+                       float sigma_prior, float weight);
+int launch_adamw(float *params, const float *grads, float *m, float *v, size_t n, float lr,
+                 float beta1, float beta2, float eps, float wd, float bc1, float bc2);
+int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m_rho, float *v_rho,
+                          float *w, float *dw, size_t n, unsigned long long seed, int step, float sp,
+                          float klw, float bc1, float bc2, float lr, float beta1, float beta2,
+                          float aeps, float wd);
+// KL total into out_dev[0]; part holds kl_forward_scratch() bytes.
+int launch_kl_forward(double *out_dev, double *part, const float *mu, const float *rho, size_t n,
+                      float sigma_prior);
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
                              const float *weight, const float *bias, int rows, int C);
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias,
@@ -68,5 +85,6 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
 // Scratch sizes, for ugk_reserve.
 size_t layernorm_backward_scratch(int rows, int C);
 size_t encoder_backward_scratch(int rows);
+size_t kl_forward_scratch();
 
 }  // namespace ugk

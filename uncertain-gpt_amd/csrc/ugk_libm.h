@@ -36,8 +36,10 @@
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
 #define UGK_HD __host__ __device__ __forceinline__
+#define UGK_HD_MEMBER __host__ __device__ __forceinline__
 #else
 #define UGK_HD static inline
+#define UGK_HD_MEMBER inline
 #endif
 
 UGK_HD uint32_t ugk_f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -67,7 +69,7 @@ UGK_HD uint64_t ugk_exp2_bits(uint32_t i) {
 // The table read from the array above (callers may pass their own copy of it,
 // e.g. one staged in GPU local memory).
 struct UgkExp2Table {
-  UGK_HD uint64_t operator()(uint32_t i) const { return ugk_exp2_bits(i); }
+  UGK_HD_MEMBER uint64_t operator()(uint32_t i) const { return ugk_exp2_bits(i); }
 };
 
 // expf. kContract selects how the multiply-adds are rounded, because the x86

@@ -1,0 +1,71 @@
+// ugk_philox.h - counter-based normal draws, eps = f(seed, step, index).
+//
+// Philox4x32-10 (Salmon et al., "Parallel random numbers: as easy as 1, 2, 3",
+// SC'11): four 32-bit counter words, a two-word key, ten rounds of two
+// 32x32->64 multiplies (constants 0xD2511F53, 0xCD9E8D57) and a Weyl key
+// schedule (0x9E3779B9, 0xBB67AE85). The stream is the one of
+// gpt2_kernels.cuh:148-192 (philox4x32_10, u01, philox_normal): counter
+// {index low, index high, step, 0}, key {seed low, seed high}, the first two
+// output words mapped to (0,1) as ((float)x + 0.5f) * 2^-32, and one
+// Box-Muller cosine branch per index.
+//
+// The integer part is exact on host and device. The float part uses the
+// device logf and cosf (AMD's device library), which round differently from
+// the host glibc in the last place on a small share of inputs, and a
+// correctly rounded sqrtf.
+#pragma once
+
+#include <stdint.h>
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+#define UGK_PHILOX_HD __host__ __device__ __forceinline__
+#else
+#define UGK_PHILOX_HD static inline
+#endif
+
+struct UgkPhilox4 {
+  uint32_t w[4];
+};
+
+// Ten rounds; each 32x32 product is one 64-bit multiply (one v_mad_u64_u32).
+UGK_PHILOX_HD UgkPhilox4 ugk_philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                           uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return UgkPhilox4{{c0, c1, c2, c3}};
+}
+
+// uint32 -> (0, 1]: the conversion rounds to nearest, the add and the
+// multiply by 2^-32 round separately (no contraction).
+UGK_PHILOX_HD float ugk_u01(uint32_t x) { return ((float)x + 0.5f) * 2.3283064365386963e-10f; }
+
+UGK_PHILOX_HD UgkPhilox4 ugk_philox_words(unsigned long long seed, int step, uint64_t index) {
+  return ugk_philox4x32_10((uint32_t)index, (uint32_t)(index >> 32), (uint32_t)step, 0u,
+                           (uint32_t)seed, (uint32_t)(seed >> 32));
+}
+
+#ifdef __HIPCC__
+// Box-Muller, cosine branch: sqrt(-2 ln u1) * cos(2 pi u2), with 2 pi rounded
+// to float and the product rounded before the cosine.
+__device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
+  const float u1 = ugk_u01(a), u2 = ugk_u01(b);
+  return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+}
+
+__device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {
+  const UgkPhilox4 o = ugk_philox_words(seed, step, index);
+  return ugk_dev_box_muller(o.w[0], o.w[1]);
+}
+#endif

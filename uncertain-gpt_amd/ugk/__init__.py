@@ -41,6 +41,8 @@ lib = ctypes.CDLL(library_path)
 _fp = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
+_u64 = ctypes.c_ulonglong
+_fl = ctypes.c_float
 
 
 class Config(ctypes.Structure):
@@ -70,6 +72,13 @@ _SIGS = {
     "ugk_residual_forward": [_fp, _fp, _fp, _i],
     "ugk_residual_backward": [_fp, _fp, _fp, _i],
     "ugk_bayes_materialize": [_fp, _fp, _fp, _fp, _sz],
+    "ugk_bayes_sample": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
+    "ugk_bayes_backward": [_fp, _fp, _fp, _fp, _fp, _sz],
+    "ugk_bayes_backward_philox": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
+    "ugk_kl_forward": [ctypes.POINTER(ctypes.c_double), _fp, _fp, _sz, _fl],
+    "ugk_kl_backward": [_fp, _fp, _fp, _fp, _sz, _fl, _fl],
+    "ugk_adamw_update": [_fp, _fp, _fp, _fp, _sz, _i, _fl, _fl, _fl, _fl, _fl],
+    "ugk_bbb_step_fused": [_fp] * 8 + [_sz, _u64, _i] + [_fl] * 9,
     "ugk_set_stream": [_fp],
     "ugk_get_stream": [],
     "ugk_reserve": [_i, _i],
@@ -84,6 +93,7 @@ _SIGS = {
     "ugk_diag_math_mismatch": [_i, ctypes.c_uint, ctypes.c_ulonglong, ctypes.POINTER(ctypes.c_ulonglong),
                                ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
+    "ugk_diag_philox": [_fp, _fp, _sz],
 }
 _RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz,
         "ugk_param_count": _sz, "ugk_act_count": _sz}
@@ -199,6 +209,60 @@ def bayes_materialize(w, mu, rho, eps, n: int) -> None:
                                      _ptr(rho, "rho", n, "f32"), _ptr(eps, "eps", n, "f32"), n))
 
 
+def bayes_sample(w, eps, mu, rho, n: int, seed: int, step: int) -> None:
+    """train_bnn.c:841-845 with the Philox draw of train_bnn_gpu.cu:93-97.
+
+    ``w = mu + softplus(rho) * eps_i`` with ``eps_i = philox_normal(seed, step, i)``; ``eps`` may be
+    None, otherwise the draws are stored there too.
+    """
+    _check(lib.ugk_bayes_sample(_ptr(w, "w", n, "f32"), _ptr(eps, "eps", n, "f32"), _ptr(mu, "mu", n, "f32"),
+                                _ptr(rho, "rho", n, "f32"), n, seed, step))
+
+
+def bayes_backward(dmu, drho, dw, eps, rho, n: int) -> None:
+    """train_bnn.c:855-861. ``dmu += dw; drho += dw * eps * sigmoid(rho)``."""
+    _check(lib.ugk_bayes_backward(_ptr(dmu, "dmu", n, "f32"), _ptr(drho, "drho", n, "f32"),
+                                  _ptr(dw, "dw", n, "f32"), _ptr(eps, "eps", n, "f32"),
+                                  _ptr(rho, "rho", n, "f32"), n))
+
+
+def bayes_backward_philox(dmu, drho, dw, rho, n: int, seed: int, step: int) -> None:
+    """train_bnn_gpu.cu:99-109 (k_bayes_backward): ``bayes_backward`` with eps regenerated."""
+    _check(lib.ugk_bayes_backward_philox(_ptr(dmu, "dmu", n, "f32"), _ptr(drho, "drho", n, "f32"),
+                                         _ptr(dw, "dw", n, "f32"), _ptr(rho, "rho", n, "f32"), n, seed, step))
+
+
+def kl_forward(mu, rho, n: int, sigma_prior: float) -> float:
+    """train_bnn.c:941-957. The KL of q(mu, softplus(rho)) against N(0, sigma_prior^2), in double."""
+    out = ctypes.c_double(0.0)
+    _check(lib.ugk_kl_forward(ctypes.byref(out), _ptr(mu, "mu", n, "f32"), _ptr(rho, "rho", n, "f32"), n,
+                              sigma_prior))
+    return float(out.value)
+
+
+def kl_backward(dmu, drho, mu, rho, n: int, sigma_prior: float, weight: float) -> None:
+    """train_bnn.c:966-979. Accumulates the weighted KL gradient onto dmu, drho."""
+    _check(lib.ugk_kl_backward(_ptr(dmu, "dmu", n, "f32"), _ptr(drho, "drho", n, "f32"),
+                               _ptr(mu, "mu", n, "f32"), _ptr(rho, "rho", n, "f32"), n, sigma_prior, weight))
+
+
+def adamw_update(params, grads, m, v, n: int, t: int, lr: float, beta1: float, beta2: float, eps: float,
+                 wd: float) -> None:
+    """train_bnn.c:699-717. AdamW step ``t`` (>= 1) on params, m, v in place."""
+    _check(lib.ugk_adamw_update(_ptr(params, "params", n, "f32"), _ptr(grads, "grads", n, "f32"),
+                                _ptr(m, "m", n, "f32"), _ptr(v, "v", n, "f32"), n, t, lr, beta1, beta2, eps, wd))
+
+
+def bbb_step_fused(mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw, n: int, seed: int, step: int, sp: float,
+                   klw: float, bc1: float, bc2: float, lr: float, beta1: float, beta2: float, aeps: float,
+                   wd: float) -> None:
+    """train_bnn_gpu.cu:173-217 (k_bbb_step_fused): one Bayes-by-Backprop update in one pass."""
+    names = ("mu", "rho", "m_mu", "v_mu", "m_rho", "v_rho", "w", "dw")
+    bufs = (mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw)
+    _check(lib.ugk_bbb_step_fused(*(_ptr(b, nm, n, "f32") for b, nm in zip(bufs, names)), n, seed, step, sp,
+                                  klw, bc1, bc2, lr, beta1, beta2, aeps, wd))
+
+
 def set_stream(stream: Optional[int]) -> None:
     """Queue later calls on ``stream`` (a hipStream_t address, e.g. ``torch.cuda.Stream().cuda_stream``)."""
     _check(lib.ugk_set_stream(stream or None))
@@ -254,7 +318,8 @@ def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
                                         ctypes.byref(ops) if ops is not None else None))
 
 
-MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4}
+MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4, "logf": 5, "cosf": 6,
+                  "sqrtf": 7}
 # the same functions with division sequence s (0 IEEE, 1-3 reciprocal + corrections)
 MATH_FUNCTIONS.update({f"{name}/div{s}": base + s for name, base in (("tanhf", 10), ("log1pf", 20), ("expm1f", 30))
                        for s in range(4)})
@@ -273,3 +338,10 @@ def diag_math_eval(fn: str, out, inp, variant: int = 0) -> None:
     n = inp.numel()
     _check(lib.ugk_diag_math_eval(MATH_FUNCTIONS[fn], variant, _ptr(out, "out", n, "f32"),
                                   _ptr(inp, "inp", n, "f32"), n))
+
+
+def diag_philox(out, tuples) -> None:
+    """Philox4x32-10 on the device: ``tuples`` is an int32 tensor of n x 6 words (counter, key),
+    ``out`` an int32 tensor of n x 4 output words (bit patterns; read them as uint32)."""
+    n = tuples.numel() // 6
+    _check(lib.ugk_diag_philox(_ptr(out, "out", 4 * n, "i32"), _ptr(tuples, "tuples", 6 * n, "i32"), n))
