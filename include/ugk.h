@@ -68,6 +68,28 @@ int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias,
                            const float *weight, const float *mean,
                            const float *rstd, int B, int T, int C);
 
+/* train_bnn.c:182-186 then :81-115 on its output, in one pass: the pair
+ * gpt2_kernels.cuh:793-797 (and :806 -> the next block's :784, :806 -> :813)
+ * launches back to back. res = x + y (bit-identical to residual_forward);
+ * out, mean, rstd = layernorm_forward(res) (identical to calling it on res).
+ * No single counterpart in the reference; ugk_gpt2_layers_forward uses it. */
+int ugk_residual_layernorm_forward(float *res, float *out, float *mean,
+                                   float *rstd, const float *x, const float *y,
+                                   const float *weight, const float *bias,
+                                   int B, int T, int C);
+
+/* train_bnn.c:439-477 then :491-496 with dout = the new dinp, in one pass: the
+ * pairs gpt2_kernels.cuh:870-876 and :888 -> :855 (the next block down), and
+ * :846 -> :855. Identical to ugk_layernorm_backward followed by
+ * ugk_residual_backward(dx, dy, dinp). dinp must differ from dx and dy;
+ * dx == dy adds twice, as residual_backward does. No single counterpart in the
+ * reference; ugk_gpt2_layers_backward uses it. */
+int ugk_layernorm_residual_backward(float *dinp, float *dweight, float *dbias,
+                                    float *dx, float *dy, const float *dout,
+                                    const float *inp, const float *weight,
+                                    const float *mean, const float *rstd,
+                                    int B, int T, int C);
+
 /* train_bnn.c:163-170 / gpt2_kernels.cuh:318-325 (k_gelu_forward). */
 int ugk_gelu_forward(float *out, const float *inp, int N);
 

@@ -75,6 +75,18 @@ def test_posterior_ops_reject_invalid_arguments_on_host():
     assert lib.ugk_last_error() != b""
 
 
+def test_fused_pairs_reject_invalid_arguments_on_host():
+    import ugk
+    lib = ugk.lib
+    assert lib.ugk_residual_layernorm_forward(*([None] * 8), 2, 3, 4) == 1
+    assert lib.ugk_residual_layernorm_forward(*([16] * 8), 2, 3, 0) == 1  # C = 0 with rows
+    assert lib.ugk_layernorm_residual_backward(*([16] * 10), 2, 3, 4) == 1  # dinp == dx
+    assert b"distinct" in lib.ugk_last_error()
+    assert lib.ugk_layernorm_residual_backward(*([None] * 10), -1, 3, 4) == 1
+    assert lib.ugk_residual_layernorm_forward(*([None] * 8), 0, 3, 4) == 0
+    assert lib.ugk_layernorm_residual_backward(*([None] * 10), 2, 3, 0) == 0
+
+
 def test_param_layout_counts():
     """Closed-form sizes of the reference layout (gpt2_kernels.cuh:656-719)."""
     import ugk

@@ -163,6 +163,32 @@ int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias, const floa
   return ok();
 }
 
+int ugk_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
+                                   const float *y, const float *weight, const float *bias, int B, int T,
+                                   int C) {
+  const char *fn = "ugk_residual_layernorm_forward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T == 0) return ok();
+  if (C == 0) return bad(fn, "C must be > 0 when B*T > 0 (mean over an empty row)");
+  if (any_null({res, out, mean, rstd, x, y, weight, bias})) return bad(fn, "NULL pointer");
+  if (int e = launch_residual_layernorm_forward(res, out, mean, rstd, x, y, weight, bias, B * T, C)) return e;
+  return ok();
+}
+
+int ugk_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
+                                    const float *dout, const float *inp, const float *weight,
+                                    const float *mean, const float *rstd, int B, int T, int C) {
+  const char *fn = "ugk_layernorm_residual_backward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T * C == 0) return ok();
+  if (any_null({dinp, dweight, dbias, dx, dy, dout, inp, weight, mean, rstd})) return bad(fn, "NULL pointer");
+  if (dinp == dx || dinp == dy) return bad(fn, "dinp must be distinct from dx and dy");
+  if (int e = launch_layernorm_residual_backward(dinp, dweight, dbias, dx, dy, dout, inp, weight, mean, rstd,
+                                                 B * T, C))
+    return e;
+  return ok();
+}
+
 int ugk_gelu_forward(float *out, const float *inp, int N) {
   const char *fn = "ugk_gelu_forward";
   if (N < 0) return bad(fn, "N must be >= 0");
@@ -439,11 +465,16 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
   const int NBTC = M * C;
   auto A = [&](size_t l, size_t rel) { return acts + a.blk0 + l * a.bstride + rel; };
   auto P = [&](size_t l, size_t rel) { return params + p.blk0 + l * p.bstride + rel; };
+  // Every residual_forward is followed at once by a layernorm_forward of its
+  // output (the next block's LN1, or the final LN): those pairs run as one
+  // pass, ugk_residual_layernorm_forward. Buffers and values are the
+  // reference's.
   UGK_TRY(ugk_encoder_forward(acts + a.enc, inputs, params + p.wte, params + p.wpe, B, T, C));
   const float *stream_in = acts + a.enc;
+  if (cfg.L > 0)
+    UGK_TRY(ugk_layernorm_forward(A(0, a.lno), A(0, a.lnm), A(0, a.lnr), stream_in, P(0, p.lng), P(0, p.lnb),
+                                  B, T, C));
   for (int l = 0; l < cfg.L; l++) {
-    UGK_TRY(ugk_layernorm_forward(A(l, a.lno), A(l, a.lnm), A(l, a.lnr), stream_in, P(l, p.lng),
-                                  P(l, p.lnb), B, T, C));
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.qkv), A(l, a.lno), P(l, p.qw), P(l, p.qb), M, C,
                                         3 * C), "matmul_forward(qkv)"));
@@ -453,9 +484,8 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.apr), A(l, a.atty), P(l, p.pw), P(l, p.pb), M, C, C),
                     "matmul_forward(proj)"));
-    UGK_TRY(ugk_residual_forward(A(l, a.resa), stream_in, A(l, a.apr), NBTC));
-    UGK_TRY(ugk_layernorm_forward(A(l, a.ln2o), A(l, a.ln2m), A(l, a.ln2r), A(l, a.resa), P(l, p.ln2g),
-                                  P(l, p.ln2b), B, T, C));
+    UGK_TRY(ugk_residual_layernorm_forward(A(l, a.resa), A(l, a.ln2o), A(l, a.ln2m), A(l, a.ln2r), stream_in,
+                                           A(l, a.apr), P(l, p.ln2g), P(l, p.ln2b), B, T, C));
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.fch), A(l, a.ln2o), P(l, p.w1), P(l, p.b1), M, C,
                                         4 * C), "matmul_forward(fc)"));
@@ -463,11 +493,19 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.mlpo), A(l, a.gelu), P(l, p.w2), P(l, p.b2), M,
                                         4 * C, C), "matmul_forward(fc2)"));
-    UGK_TRY(ugk_residual_forward(A(l, a.res1), A(l, a.resa), A(l, a.mlpo), NBTC));
+    if (l + 1 < cfg.L)
+      UGK_TRY(ugk_residual_layernorm_forward(A(l, a.res1), A(l + 1, a.lno), A(l + 1, a.lnm), A(l + 1, a.lnr),
+                                             A(l, a.resa), A(l, a.mlpo), P(l + 1, p.lng), P(l + 1, p.lnb), B,
+                                             T, C));
+    else
+      UGK_TRY(ugk_residual_layernorm_forward(A(l, a.res1), acts + a.flo, acts + a.flm, acts + a.flr,
+                                             A(l, a.resa), A(l, a.mlpo), params + p.flng, params + p.flnb, B,
+                                             T, C));
     stream_in = A(l, a.res1);
   }
-  UGK_TRY(ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
-                                params + p.flnb, B, T, C));
+  if (cfg.L == 0)
+    UGK_TRY(ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
+                                  params + p.flnb, B, T, C));
   return ok();
 }
 
@@ -483,13 +521,21 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
   const int NBTC = M * C;
   auto A = [&](size_t l, size_t rel) { return a.blk0 + l * a.bstride + rel; };
   auto P = [&](size_t l, size_t rel) { return p.blk0 + l * p.bstride + rel; };
+  // Every layernorm_backward but the last is followed at once by a
+  // residual_backward whose dout is that LN's dinp (the block's first
+  // residual_backward consumes the LN1 gradient of the block above, or the
+  // final LN's): those pairs run as one pass, ugk_layernorm_residual_backward.
   const size_t last = cfg.L > 0 ? A(cfg.L - 1, a.res1) : a.enc;
-  UGK_TRY(ugk_layernorm_backward(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + a.flo,
-                                 acts + last, params + p.flng, acts + a.flm, acts + a.flr, B, T, C));
+  if (cfg.L > 0)
+    UGK_TRY(ugk_layernorm_residual_backward(grads_acts + last, grads + p.flng, grads + p.flnb,
+                                            grads_acts + A(cfg.L - 1, a.resa), grads_acts + A(cfg.L - 1, a.mlpo),
+                                            grads_acts + a.flo, acts + last, params + p.flng, acts + a.flm,
+                                            acts + a.flr, B, T, C));
+  else
+    UGK_TRY(ugk_layernorm_backward(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + a.flo,
+                                   acts + last, params + p.flng, acts + a.flm, acts + a.flr, B, T, C));
   for (int l = cfg.L - 1; l >= 0; l--) {
     const size_t st = (l == 0) ? a.enc : A(l - 1, a.res1);
-    UGK_TRY(ugk_residual_backward(grads_acts + A(l, a.resa), grads_acts + A(l, a.mlpo),
-                                  grads_acts + A(l, a.res1), NBTC));
     if (ops && ops->matmul_backward)
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.gelu), grads + P(l, p.w2),
                                          grads + P(l, p.b2), acts + A(l, a.gelu), params + P(l, p.w2),
@@ -500,11 +546,11 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.ln2o), grads + P(l, p.w1),
                                          grads + P(l, p.b1), acts + A(l, a.ln2o), params + P(l, p.w1),
                                          grads_acts + A(l, a.fch), M, C, 4 * C), "matmul_backward(fc)"));
-    UGK_TRY(ugk_layernorm_backward(grads_acts + A(l, a.resa), grads + P(l, p.ln2g), grads + P(l, p.ln2b),
-                                   grads_acts + A(l, a.ln2o), acts + A(l, a.resa), params + P(l, p.ln2g),
-                                   acts + A(l, a.ln2m), acts + A(l, a.ln2r), B, T, C));
-    UGK_TRY(ugk_residual_backward(grads_acts + st, grads_acts + A(l, a.apr), grads_acts + A(l, a.resa),
-                                  NBTC));
+    UGK_TRY(ugk_layernorm_residual_backward(grads_acts + A(l, a.resa), grads + P(l, p.ln2g),
+                                            grads + P(l, p.ln2b), grads_acts + st, grads_acts + A(l, a.apr),
+                                            grads_acts + A(l, a.ln2o), acts + A(l, a.resa),
+                                            params + P(l, p.ln2g), acts + A(l, a.ln2m), acts + A(l, a.ln2r), B,
+                                            T, C));
     if (ops && ops->matmul_backward)
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.atty), grads + P(l, p.pw),
                                          grads + P(l, p.pb), acts + A(l, a.atty), params + P(l, p.pw),
@@ -516,9 +562,15 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.lno), grads + P(l, p.qw),
                                          grads + P(l, p.qb), acts + A(l, a.lno), params + P(l, p.qw),
                                          grads_acts + A(l, a.qkv), M, C, 3 * C), "matmul_backward(qkv)"));
-    UGK_TRY(ugk_layernorm_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
-                                   grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
-                                   acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
+    if (l > 0)
+      UGK_TRY(ugk_layernorm_residual_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
+                                              grads_acts + A(l - 1, a.resa), grads_acts + A(l - 1, a.mlpo),
+                                              grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
+                                              acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
+    else
+      UGK_TRY(ugk_layernorm_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
+                                     grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
+                                     acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
   }
   UGK_TRY(ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C));
   return ok();

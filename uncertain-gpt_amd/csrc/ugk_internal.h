@@ -77,6 +77,15 @@ int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias,
                               const float *dout, const float *inp, const float *weight,
                               const float *mean, const float *rstd, int rows, int C);
+// residual_forward then layernorm_forward of its output, in one pass when the
+// float4 path applies (two launches otherwise).
+int launch_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
+                                      const float *y, const float *weight, const float *bias, int rows,
+                                      int C);
+// layernorm_backward then residual_backward(dx, dy, dinp), likewise.
+int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
+                                       const float *dout, const float *inp, const float *weight,
+                                       const float *mean, const float *rstd, int rows, int C);
 int launch_encoder_forward(float *out, const int *inp, const float *wte,
                            const float *wpe, int B, int T, int C);
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,

@@ -26,12 +26,16 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kMaxV = 8;  // float4 per lane held in registers: C <= 2048
 constexpr int kMaxBwdBlocks = 512;
 
-template <int V>
+// kRes: the row is first formed as res = inp + inp2 (residual_forward,
+// train_bnn.c:182-186), stored to res, and normalised from the registers, the
+// pair gpt2_kernels.cuh:793-797 launches back to back.
+template <int V, bool kRes>
 __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, float *__restrict__ mean,
                                                        float *__restrict__ rstd,
                                                        const float *__restrict__ inp,
                                                        const float *__restrict__ weight,
-                                                       const float *__restrict__ bias, int rows, int C) {
+                                                       const float *__restrict__ bias, int rows, int C,
+                                                       float *__restrict__ res, const float *__restrict__ inp2) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -42,6 +46,21 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, 
   for (int v = 0; v < V; v++) {
     const int c4 = lane + v * kWave;
     xv[v] = (c4 < C4) ? ld_nt(x4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (kRes) {
+    const float4 *y4 = reinterpret_cast<const float4 *>(inp2 + (size_t)row * C);
+    float4 *r4 = reinterpret_cast<float4 *>(res + (size_t)row * C);
+    float4 yv[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      const int c4 = lane + v * kWave;
+      yv[v] = (c4 < C4) ? ld_nt(y4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      xv[v] = make_float4(xv[v].x + yv[v].x, xv[v].y + yv[v].y, xv[v].z + yv[v].z, xv[v].w + yv[v].w);
+      if (lane + v * kWave < C4) st_nt(r4 + lane + v * kWave, xv[v]);
+    }
   }
   float s = 0.0f;
 #pragma unroll
@@ -119,11 +138,17 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // wavefronts' sums are then folded pairwise through LDS (upper half into
 // lower half, a fixed tree) and wavefront 0 writes the workgroup's partial
 // row: partial[g] = [dweight part (C floats) | dbias part (C floats)].
-template <int V, int W, int R>
+//
+// kRes: the new dinp row is also added to rdx and rdy (residual_backward with
+// dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
+// gpt2_kernels.cuh:870-876 launches back to back. The rdx/rdy rows are loaded
+// with the others, before any arithmetic.
+template <int V, int W, int R, bool kRes>
 __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
-    const float *__restrict__ rstd, int rows, int C, int rpw) {
+    const float *__restrict__ rstd, int rows, int C, int rpw, float *__restrict__ rdx,
+    float *__restrict__ rdy, int same) {
   __shared__ float4 red[W / 2][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -143,6 +168,7 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
   for (int row = row0; row < row1; row += R) {
     const int nr = min(R, row1 - row);
     float4 x[R][V], dy[R][V], dx[R][V];
+    float4 ra[kRes ? R : 1][kRes ? V : 1], rb[kRes ? R : 1][kRes ? V : 1];
     float m[R], r[R];
 #pragma unroll
     for (int q = 0; q < R; q++) {
@@ -159,6 +185,17 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
           dx[q][v] = ld_nt(dx4 + c4);
         } else {
           x[q][v] = dy[q][v] = dx[q][v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      if (kRes) {
+        const float4 *a4 = reinterpret_cast<const float4 *>(rdx + (size_t)rq * C);
+        const float4 *b4 = reinterpret_cast<const float4 *>(rdy + (size_t)rq * C);
+#pragma unroll
+        for (int v = 0; v < V; v++) {
+          const int c4 = lane + v * kWave;
+          const bool in = c4 < C4 && q < nr;
+          ra[q][v] = in ? ld_nt(a4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+          rb[q][v] = (in && !same) ? ld_nt(b4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
       m[q] = mean[rq];
@@ -207,6 +244,19 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
           o.z = dx[q][v].z + r[q] * (dn[q][v].z - dnm - xh[q][v].z * dnxm);
           o.w = dx[q][v].w + r[q] * (dn[q][v].w - dnm - xh[q][v].w * dnxm);
           st_nt(dx4 + c4, o);
+          if (kRes) {
+            float4 *a4 = reinterpret_cast<float4 *>(rdx + (size_t)(row + q) * C);
+            float4 *b4 = reinterpret_cast<float4 *>(rdy + (size_t)(row + q) * C);
+            float4 a = ra[q][v];
+            a = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+            if (same) {
+              a = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+            } else {
+              const float4 b = rb[q][v];
+              st_nt(b4 + c4, make_float4(b.x + o.x, b.y + o.y, b.z + o.z, b.w + o.w));
+            }
+            st_nt(a4 + c4, a);
+          }
           db[v].x += dy[q][v].x; dg[v].x += dy[q][v].x * xh[q][v].x;
           db[v].y += dy[q][v].y; dg[v].y += dy[q][v].y * xh[q][v].y;
           db[v].z += dy[q][v].z; dg[v].z += dy[q][v].z * xh[q][v].z;
@@ -376,24 +426,84 @@ size_t layernorm_backward_scratch(int rows, int C) {
   return (size_t)nblk * 2 * (size_t)C * sizeof(float);
 }
 
+namespace {
+template <bool kRes>
+void launch_ln_fwd_vec(float *out, float *mean, float *rstd, const float *inp, const float *weight,
+                       const float *bias, int rows, int C, float *res, const float *inp2) {
+  const dim3 grid(grid_for((size_t)rows, kWavesPerBlock)), block(kBlock);
+  const int V = ((C >> 2) + kWave - 1) / kWave;
+  switch (V) {
+#define UGK_LN_FWD(v) \
+  case v: hipLaunchKernelGGL((k_ln_fwd_vec<v, kRes>), grid, block, 0, stream(), out, mean, rstd, inp, weight, bias, rows, C, res, inp2); break;
+    UGK_LN_FWD(1) UGK_LN_FWD(2) UGK_LN_FWD(3) UGK_LN_FWD(4)
+    UGK_LN_FWD(5) UGK_LN_FWD(6) UGK_LN_FWD(7) UGK_LN_FWD(8)
+#undef UGK_LN_FWD
+  }
+}
+}  // namespace
+
+int launch_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
+                                      const float *y, const float *weight, const float *bias, int rows,
+                                      int C) {
+  if (rows == 0) return 0;
+  if (!vec_ok(C, {res, out, x, y, weight, bias})) {
+    if (int e = launch_residual_forward(res, x, y, (size_t)rows * C)) return e;
+    return launch_layernorm_forward(out, mean, rstd, res, weight, bias, rows, C);
+  }
+  launch_ln_fwd_vec<true>(out, mean, rstd, x, weight, bias, rows, C, res, y);
+  return check_launch("residual_layernorm_forward");
+}
+
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
                              const float *weight, const float *bias, int rows, int C) {
   if (rows == 0) return 0;
   const dim3 grid(grid_for((size_t)rows, kWavesPerBlock)), block(kBlock);
   if (vec_ok(C, {out, inp, weight, bias})) {
-    const int V = ((C >> 2) + kWave - 1) / kWave;
-    switch (V) {
-#define UGK_LN_FWD(v) \
-  case v: hipLaunchKernelGGL(k_ln_fwd_vec<v>, grid, block, 0, stream(), out, mean, rstd, inp, weight, bias, rows, C); break;
-      UGK_LN_FWD(1) UGK_LN_FWD(2) UGK_LN_FWD(3) UGK_LN_FWD(4)
-      UGK_LN_FWD(5) UGK_LN_FWD(6) UGK_LN_FWD(7) UGK_LN_FWD(8)
-#undef UGK_LN_FWD
-    }
+    launch_ln_fwd_vec<false>(out, mean, rstd, inp, weight, bias, rows, C, nullptr, nullptr);
   } else {
     hipLaunchKernelGGL(k_ln_fwd_scalar, grid, block, 0, stream(), out, mean, rstd, inp, weight, bias,
                        rows, C);
   }
   return check_launch("layernorm_forward");
+}
+
+namespace {
+template <bool kRes>
+int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const float *inp,
+                      const float *weight, const float *mean, const float *rstd, int rows, int C,
+                      float *rdx, float *rdy) {
+  int nblk, rpw;
+  const int V = ((C >> 2) + kWave - 1) / kWave;
+  const int W = bwd_waves(V);
+  bwd_shape_vec(rows, W, &nblk, &rpw);
+  const dim3 grid(nblk), block(W * kWave);
+  const int same = rdx == rdy ? 1 : 0;
+  switch (V) {
+#define UGK_LN_BWD(v) \
+  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), kBwdRows, kRes>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same); break;
+    UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
+    UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
+#undef UGK_LN_BWD
+  }
+  return nblk;
+}
+}  // namespace
+
+int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
+                                       const float *dout, const float *inp, const float *weight,
+                                       const float *mean, const float *rstd, int rows, int C) {
+  if (rows == 0) return 0;
+  if (!vec_ok(C, {dinp, dout, inp, weight, dx, dy})) {
+    if (int e = launch_layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, rows, C))
+      return e;
+    return launch_residual_backward(dx, dy, dinp, (size_t)rows * C);
+  }
+  float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
+  if (!partial) return 3;
+  const int nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy);
+  hipLaunchKernelGGL(k_ln_bwd_reduce, dim3(grid_for((size_t)2 * C, kWave)), dim3(kWave * kRedGroups), 0,
+                     stream(), dweight, dbias, partial, nblk, C);
+  return check_launch("layernorm_residual_backward");
 }
 
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const float *dout,
@@ -404,18 +514,7 @@ int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const f
   if (!partial) return 3;
   int nblk;
   if (vec_ok(C, {dinp, dout, inp, weight})) {
-    int rpw;
-    const int V = ((C >> 2) + kWave - 1) / kWave;
-    const int W = bwd_waves(V);
-    bwd_shape_vec(rows, W, &nblk, &rpw);
-    const dim3 grid(nblk), block(W * kWave);
-    switch (V) {
-#define UGK_LN_BWD(v) \
-  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), kBwdRows>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw); break;
-      UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
-      UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
-#undef UGK_LN_BWD
-    }
+    nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr);
   } else {
     int rpb;
     bwd_shape(rows, &nblk, &rpb);

@@ -67,6 +67,8 @@ _SIGS = {
     "ugk_encoder_backward": [_fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_forward": [_fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_backward": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_residual_layernorm_forward": [_fp] * 8 + [_i, _i, _i],
+    "ugk_layernorm_residual_backward": [_fp] * 10 + [_i, _i, _i],
     "ugk_gelu_forward": [_fp, _fp, _i],
     "ugk_gelu_backward": [_fp, _fp, _fp, _i],
     "ugk_residual_forward": [_fp, _fp, _fp, _i],
@@ -178,6 +180,26 @@ def layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, B: i
                                       _ptr(dbias, "dbias", C, "f32"), _ptr(dout, "dout", n, "f32"),
                                       _ptr(inp, "inp", n, "f32"), _ptr(weight, "weight", C, "f32"),
                                       _ptr(mean, "mean", r, "f32"), _ptr(rstd, "rstd", r, "f32"), B, T, C))
+
+
+def residual_layernorm_forward(res, out, mean, rstd, x, y, weight, bias, B: int, T: int, C: int) -> None:
+    """``res = x + y`` (residual_forward) then ``layernorm_forward(out, mean, rstd, res, ...)``, one pass."""
+    n, rows = B * T * C, B * T
+    _check(lib.ugk_residual_layernorm_forward(
+        _ptr(res, "res", n, "f32"), _ptr(out, "out", n, "f32"), _ptr(mean, "mean", rows, "f32"),
+        _ptr(rstd, "rstd", rows, "f32"), _ptr(x, "x", n, "f32"), _ptr(y, "y", n, "f32"),
+        _ptr(weight, "weight", C, "f32"), _ptr(bias, "bias", C, "f32"), B, T, C))
+
+
+def layernorm_residual_backward(dinp, dweight, dbias, dx, dy, dout, inp, weight, mean, rstd, B: int, T: int,
+                                C: int) -> None:
+    """``layernorm_backward`` then ``residual_backward(dx, dy, dinp)``, one pass."""
+    n, rows = B * T * C, B * T
+    _check(lib.ugk_layernorm_residual_backward(
+        _ptr(dinp, "dinp", n, "f32"), _ptr(dweight, "dweight", C, "f32"), _ptr(dbias, "dbias", C, "f32"),
+        _ptr(dx, "dx", n, "f32"), _ptr(dy, "dy", n, "f32"), _ptr(dout, "dout", n, "f32"),
+        _ptr(inp, "inp", n, "f32"), _ptr(weight, "weight", C, "f32"), _ptr(mean, "mean", rows, "f32"),
+        _ptr(rstd, "rstd", rows, "f32"), B, T, C))
 
 
 def gelu_forward(out, inp, N: int) -> None:
