@@ -247,7 +247,11 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
 
 /* Backward from the final LayerNorm down to the encoder
  * (gpt2_kernels.cuh:846-894). On entry grads_acts holds d(final LN output)
- * at the reference's flo offset; accumulates into grads and grads_acts. */
+ * at the reference's flo offset; accumulates into grads and grads_acts. The
+ * LayerNorm dweight/dbias column sums are completed by one launch at the end,
+ * and their partial rows live in the library scratch meanwhile, so the dense
+ * callbacks must not call the entry points that use the scratch
+ * (ugk_layernorm_backward, ugk_layernorm_residual_backward, ugk_kl_forward). */
 int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                              const float *params, const int *inputs,
                              ugk_config cfg, const ugk_dense_ops *ops);

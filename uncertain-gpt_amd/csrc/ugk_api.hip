@@ -12,6 +12,7 @@
 #include <atomic>
 #include <climits>
 #include <mutex>
+#include <vector>
 
 #include "../../include/ugk.h"
 #include "ugk_internal.h"
@@ -525,15 +526,33 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
   // residual_backward whose dout is that LN's dinp (the block's first
   // residual_backward consumes the LN1 gradient of the block above, or the
   // final LN's): those pairs run as one pass, ugk_layernorm_residual_backward.
+  // The 2L+1 LayerNorm backwards write their dweight/dbias partial rows to
+  // separate slots of the scratch; one batched launch at the end adds them
+  // (nothing in between reads those gradients), instead of a reduce launch
+  // after each.
+  const size_t slot = (layernorm_backward_scratch(M, C) + 255) / 256 * 256;
+  const int nln = 2 * cfg.L + 1;
+  char *pbase = static_cast<char *>(scratch(slot * (size_t)nln));
+  if (!pbase) return UGK_ENOMEM;
+  std::vector<LnReduceJob> jobs;
+  jobs.reserve((size_t)nln);
+  auto ln_bwd = [&](float *dinp, float *dw, float *db, float *dx, float *dy, const float *dout, const float *inp,
+                    const float *w, const float *mean, const float *rstd) -> int {
+    float *part = reinterpret_cast<float *>(pbase + slot * jobs.size());
+    int nblk = 0;
+    if (int e = launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C, &nblk))
+      return e;
+    jobs.push_back({part, dw, db, nblk});
+    return 0;
+  };
   const size_t last = cfg.L > 0 ? A(cfg.L - 1, a.res1) : a.enc;
   if (cfg.L > 0)
-    UGK_TRY(ugk_layernorm_residual_backward(grads_acts + last, grads + p.flng, grads + p.flnb,
-                                            grads_acts + A(cfg.L - 1, a.resa), grads_acts + A(cfg.L - 1, a.mlpo),
-                                            grads_acts + a.flo, acts + last, params + p.flng, acts + a.flm,
-                                            acts + a.flr, B, T, C));
+    UGK_TRY(ln_bwd(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + A(cfg.L - 1, a.resa),
+                   grads_acts + A(cfg.L - 1, a.mlpo), grads_acts + a.flo, acts + last, params + p.flng,
+                   acts + a.flm, acts + a.flr));
   else
-    UGK_TRY(ugk_layernorm_backward(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + a.flo,
-                                   acts + last, params + p.flng, acts + a.flm, acts + a.flr, B, T, C));
+    UGK_TRY(ln_bwd(grads_acts + last, grads + p.flng, grads + p.flnb, nullptr, nullptr, grads_acts + a.flo,
+                   acts + last, params + p.flng, acts + a.flm, acts + a.flr));
   for (int l = cfg.L - 1; l >= 0; l--) {
     const size_t st = (l == 0) ? a.enc : A(l - 1, a.res1);
     if (ops && ops->matmul_backward)
@@ -546,11 +565,9 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.ln2o), grads + P(l, p.w1),
                                          grads + P(l, p.b1), acts + A(l, a.ln2o), params + P(l, p.w1),
                                          grads_acts + A(l, a.fch), M, C, 4 * C), "matmul_backward(fc)"));
-    UGK_TRY(ugk_layernorm_residual_backward(grads_acts + A(l, a.resa), grads + P(l, p.ln2g),
-                                            grads + P(l, p.ln2b), grads_acts + st, grads_acts + A(l, a.apr),
-                                            grads_acts + A(l, a.ln2o), acts + A(l, a.resa),
-                                            params + P(l, p.ln2g), acts + A(l, a.ln2m), acts + A(l, a.ln2r), B,
-                                            T, C));
+    UGK_TRY(ln_bwd(grads_acts + A(l, a.resa), grads + P(l, p.ln2g), grads + P(l, p.ln2b), grads_acts + st,
+                   grads_acts + A(l, a.apr), grads_acts + A(l, a.ln2o), acts + A(l, a.resa),
+                   params + P(l, p.ln2g), acts + A(l, a.ln2m), acts + A(l, a.ln2r)));
     if (ops && ops->matmul_backward)
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.atty), grads + P(l, p.pw),
                                          grads + P(l, p.pb), acts + A(l, a.atty), params + P(l, p.pw),
@@ -563,15 +580,15 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                                          grads + P(l, p.qb), acts + A(l, a.lno), params + P(l, p.qw),
                                          grads_acts + A(l, a.qkv), M, C, 3 * C), "matmul_backward(qkv)"));
     if (l > 0)
-      UGK_TRY(ugk_layernorm_residual_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
-                                              grads_acts + A(l - 1, a.resa), grads_acts + A(l - 1, a.mlpo),
-                                              grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
-                                              acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
+      UGK_TRY(ln_bwd(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb), grads_acts + A(l - 1, a.resa),
+                     grads_acts + A(l - 1, a.mlpo), grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
+                     acts + A(l, a.lnm), acts + A(l, a.lnr)));
     else
-      UGK_TRY(ugk_layernorm_backward(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb),
-                                     grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng),
-                                     acts + A(l, a.lnm), acts + A(l, a.lnr), B, T, C));
+      UGK_TRY(ln_bwd(grads_acts + st, grads + P(l, p.lng), grads + P(l, p.lnb), nullptr, nullptr,
+                     grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng), acts + A(l, a.lnm),
+                     acts + A(l, a.lnr)));
   }
+  UGK_TRY(launch_layernorm_reduce(jobs.data(), (int)jobs.size(), C));
   UGK_TRY(ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C));
   return ok();
 }

@@ -82,17 +82,31 @@ int launch_layernorm_backward(float *dinp, float *dweight, float *dbias,
 int launch_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
                                       const float *y, const float *weight, const float *bias, int rows,
                                       int C);
-// layernorm_backward then residual_backward(dx, dy, dinp), likewise.
+// layernorm_backward then residual_backward(dx, dy, dinp), likewise (dx, dy
+// null: layernorm_backward alone).
 int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
                                        const float *dout, const float *inp, const float *weight,
                                        const float *mean, const float *rstd, int rows, int C);
+// The LayerNorm backward split in two: the main pass writes dinp (and, with dx
+// non-null, applies residual_backward(dx, dy, dinp)) and *nblk partial rows
+// of the dweight/dbias column sums to `partial`; launch_layernorm_reduce then
+// adds each job's column totals into its dweight/dbias, many jobs per launch.
+struct LnReduceJob {
+  const float *partial;
+  float *dweight, *dbias;
+  int nblk;
+};
+int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
+                                       const float *inp, const float *weight, const float *mean,
+                                       const float *rstd, int rows, int C, int *nblk);
+int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
 int launch_encoder_forward(float *out, const int *inp, const float *wte,
                            const float *wpe, int B, int T, int C);
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
                             const int *inp, int B, int T, int C);
 
 // Scratch sizes, for ugk_reserve.
-size_t layernorm_backward_scratch(int rows, int C);
+size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
 size_t encoder_backward_scratch(int rows);
 size_t kl_forward_scratch();
 

@@ -353,10 +353,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_scalar(float *dinp, float *pa
 // in group order.
 constexpr int kRedGroups = 16;
 constexpr int kRedMaxPer = 32;
-__global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dweight, float *dbias,
-                                                                      const float *partial, int nblk,
-                                                                      int C) {
-  __shared__ float red[kRedGroups][kWave];
+__device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias, const float *partial, int nblk,
+                                                   int C, float (*red)[kWave]) {
   const int cl = threadIdx.x & (kWave - 1);
   const int g = threadIdx.x >> 6;
   const int col = blockIdx.x * kWave + cl;
@@ -381,6 +379,25 @@ __global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dwe
     else
       dbias[col - C] += t;
   }
+}
+
+__global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dweight, float *dbias,
+                                                                      const float *partial, int nblk,
+                                                                      int C) {
+  __shared__ float red[kRedGroups][kWave];
+  ln_bwd_reduce_tile(dweight, dbias, partial, nblk, C, red);
+}
+
+// Several LayerNorm backwards' column totals in one launch (blockIdx.y picks
+// the job); each job is reduced exactly as k_ln_bwd_reduce would.
+constexpr int kMaxReduceJobs = 32;
+struct LnReduceBatch {
+  LnReduceJob job[kMaxReduceJobs];
+};
+__global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce_batch(LnReduceBatch b, int C) {
+  __shared__ float red[kRedGroups][kWave];
+  const LnReduceJob &j = b.job[blockIdx.y];
+  ln_bwd_reduce_tile(j.dweight, j.dbias, j.partial, j.nblk, C, red);
 }
 
 bool vec_ok(int C, std::initializer_list<const void *> ptrs) {
@@ -489,18 +506,48 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
 }
 }  // namespace
 
+int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
+                                       const float *inp, const float *weight, const float *mean,
+                                       const float *rstd, int rows, int C, int *nblk) {
+  *nblk = 0;
+  if (rows == 0) return 0;
+  const bool res = dx != nullptr;
+  if (vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
+    if (res)
+      *nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy);
+    else
+      *nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr);
+    return check_launch("layernorm_backward");
+  }
+  int rpb;
+  bwd_shape(rows, nblk, &rpb);
+  hipLaunchKernelGGL(k_ln_bwd_scalar, dim3(*nblk), dim3(kBlock), 0, stream(), dinp, partial, dout, inp, weight,
+                     mean, rstd, rows, C, rpb);
+  if (int e = check_launch("layernorm_backward")) return e;
+  return res ? launch_residual_backward(dx, dy, dinp, (size_t)rows * C) : 0;
+}
+
+int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C) {
+  for (int j0 = 0; j0 < njobs; j0 += kMaxReduceJobs) {
+    LnReduceBatch b{};
+    const int n = njobs - j0 < kMaxReduceJobs ? njobs - j0 : kMaxReduceJobs;
+    for (int k = 0; k < n; k++) b.job[k] = jobs[j0 + k];
+    hipLaunchKernelGGL(k_ln_bwd_reduce_batch, dim3(grid_for((size_t)2 * C, kWave), n), dim3(kWave * kRedGroups), 0,
+                       stream(), b, C);
+  }
+  return check_launch("layernorm_backward (column sums)");
+}
+
 int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
                                        const float *dout, const float *inp, const float *weight,
                                        const float *mean, const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
-  if (!vec_ok(C, {dinp, dout, inp, weight, dx, dy})) {
-    if (int e = launch_layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, rows, C))
-      return e;
-    return launch_residual_backward(dx, dy, dinp, (size_t)rows * C);
-  }
   float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
   if (!partial) return 3;
-  const int nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy);
+  int nblk;
+  if (int e = launch_layernorm_backward_partials(dinp, partial, dx, dy, dout, inp, weight, mean, rstd, rows, C,
+                                                 &nblk))
+    return e;
   hipLaunchKernelGGL(k_ln_bwd_reduce, dim3(grid_for((size_t)2 * C, kWave)), dim3(kWave * kRedGroups), 0,
                      stream(), dweight, dbias, partial, nblk, C);
   return check_launch("layernorm_residual_backward");
@@ -509,21 +556,8 @@ int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const float *dout,
                               const float *inp, const float *weight, const float *mean,
                               const float *rstd, int rows, int C) {
-  if (rows == 0) return 0;
-  float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
-  if (!partial) return 3;
-  int nblk;
-  if (vec_ok(C, {dinp, dout, inp, weight})) {
-    nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr);
-  } else {
-    int rpb;
-    bwd_shape(rows, &nblk, &rpb);
-    hipLaunchKernelGGL(k_ln_bwd_scalar, dim3(nblk), dim3(kBlock), 0, stream(), dinp, partial, dout, inp, weight,
-                       mean, rstd, rows, C, rpb);
-  }
-  hipLaunchKernelGGL(k_ln_bwd_reduce, dim3(grid_for((size_t)2 * C, kWave)), dim3(kWave * kRedGroups), 0,
-                     stream(), dweight, dbias, partial, nblk, C);
-  return check_launch("layernorm_backward");
+  return launch_layernorm_residual_backward(dinp, dweight, dbias, nullptr, nullptr, dout, inp, weight, mean,
+                                            rstd, rows, C);
 }
 
 }  // namespace ugk
