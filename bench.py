@@ -8,7 +8,12 @@ fp32, L=12 H=12 C=768 V=50257 B=8 T=1024, on the reference's buffer layout:
        12 GELU) -> the layer kernels of gpt2_backward (same, backward).
 The dense ops between them (GEMMs, attention) are not part of the path; their
 output buffers hold synthetic data. A "step" is that sequence, queued by the
-native step driver of libugk.so (ugk_gpt2_layers_forward/backward).
+native step driver of libugk.so (ugk_gpt2_layers_forward/backward), which runs
+each residual -> LayerNorm and LayerNorm -> residual pair as one pass and adds
+the LayerNorm weight/bias gradients of the whole backward in one launch; its
+buffers are bit-identical to the op-by-op sequence. The step's algorithmic
+bytes are still those of the unfused sequence (18.05 GB), so `value` is the
+effective rate of the reference's sequence.
 
 Printed JSON line (the last line of stdout):
     value        algorithmic bytes of the step / step time, GB/s
@@ -16,13 +21,17 @@ Printed JSON line (the last line of stdout):
     configs      the same kernels at the shapes of BASELINE configs 2-4 (LayerNorm
                  16384x768 and 256x384, GELU/residual over 50,331,648 values,
                  encoder at B=16 T=1024 with uniform and Zipf(1.1) tokens), cold
+    head         softmax + cross-entropy forward and backward over B*T rows of
+                 V = 50257 logits, cold
     posterior    the ops around the step over the same n parameters, cold:
                  Philox sample, bayes/KL backward, AdamW, the fused BBB update,
                  the KL total
     kernels      each kernel at its step shape, cold (launches rotate over buffer
                  sets totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds
                  the operands): mean ms from HIP events, GB/s from algorithmic
-                 bytes, fraction of 8 TB/s
+                 bytes, fraction of 8 TB/s; also the two fused pairs the step
+                 driver runs (residual -> LayerNorm forward, LayerNorm ->
+                 residual backward), with the pair's own bytes
     roofline     the dominant kernel (most algorithmic bytes per step: GELU
                  backward), achieved = algorithmic bytes per launch / its mean
                  launch time above
@@ -150,6 +159,8 @@ def main():
     ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other BASELINE configs")
+    ap.add_argument("--no-head", action="store_true",
+                    help="skip softmax + cross-entropy forward/backward at the GPT-2 head shape")
     ap.add_argument("--no-posterior", action="store_true",
                     help="skip the posterior-update ops (Philox sample, bayes/KL backward, AdamW, fused step)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -247,6 +258,11 @@ def main():
         ugk.layernorm_forward(d["out"], d["mean"], d["rstd"], d["x"], d["w"], d["b"], B, T, C)
         return d
 
+    def mk_ln_res():
+        d = mk_ln()
+        d["rx"], d["ry"] = rnd(N), rnd(N)
+        return d
+
     def mk_gelu():
         return {"x": rnd(4 * N), "out": torch.empty(4 * N, device=dev), "dout": rnd(4 * N), "dinp": rnd(4 * N)}
 
@@ -277,6 +293,17 @@ def main():
             P_(d["x"]), P_(d["y"]), P_(d["dout"]), N))),
         "bayes_materialize": (mk_mat, 16 * n_mat, lambda d: chk(lib.ugk_bayes_materialize(
             P_(d["w"]), P_(d["mu"]), P_(d["rho"]), P_(d["eps"]), n_mat))),
+    }
+    # the two fused pairs the step driver runs (not separate entries of `per`:
+    # their bytes are the pair's, 16 and 32 per element, see step_bytes)
+    fused_plan = {
+        "residual_layernorm_forward (fused pair)": (mk_ln, 20 * N, 16 * N + 8 * B * T + 8 * C, lambda d: chk(
+            lib.ugk_residual_layernorm_forward(P_(d["dinp"]), P_(d["out"]), P_(d["mean"]), P_(d["rstd"]),
+                                               P_(d["x"]), P_(d["dout"]), P_(d["w"]), P_(d["b"]), B, T, C))),
+        "layernorm_residual_backward (fused pair)": (mk_ln_res, 28 * N, 32 * N + 8 * B * T + 20 * C, lambda d: chk(
+            lib.ugk_layernorm_residual_backward(P_(d["dinp"]), P_(d["dw"]), P_(d["db"]), P_(d["rx"]), P_(d["ry"]),
+                                                P_(d["dout"]), P_(d["x"]), P_(d["w"]), P_(d["mean"]),
+                                                P_(d["rstd"]), B, T, C))),
     }
     def time_cold(make, set_bytes, fn):
         sets = sets_for(make, set_bytes)
@@ -309,6 +336,9 @@ def main():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
         mean_ms[name] = ms
         record(kernels, name, per[name], ms, launches, n_sets, {"per_step": count[name]})
+    for name, (make, set_bytes, nbytes, fn) in fused_plan.items():
+        ms, launches, n_sets = time_cold(make, set_bytes, fn)
+        record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 2 * L})
 
     # ---- the same kernels at the other BASELINE configurations' shapes (not part of the step)
     configs = {}
@@ -399,6 +429,23 @@ def main():
             ctypes.byref(kl_out), P_(d["mu"]), P_(d["rho"]), n, 0.1)))
         record(posterior, "kl_forward (incl. result copy + sync)", 8 * n, ms, l_, k_)
 
+    # ---- softmax + cross-entropy at the head shape, B*T rows of V logits (not part of the step)
+    head = {}
+    if not args.no_head:
+        rows_h = B * T
+        NV = rows_h * V
+
+        def mk_head():
+            return {"logits": rnd(NV) * 3.0, "probs": torch.empty(NV, device=dev), "dlogits": torch.zeros(NV, device=dev),
+                    "losses": torch.empty(rows_h, device=dev),
+                    "targets": torch.randint(0, V, (rows_h,), generator=g, device=dev, dtype=torch.int32)}
+        ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_softmax_crossentropy(
+            P_(d["losses"]), P_(d["probs"]), P_(d["logits"]), P_(d["targets"]), B, T, V)))
+        record(head, "softmax_crossentropy", 8 * NV + 8 * rows_h, ms, l_, k_)
+        ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_crossentropy_softmax_backward(
+            P_(d["dlogits"]), P_(d["probs"]), P_(d["targets"]), B, T, V)))
+        record(head, "crossentropy_softmax_backward", 12 * NV + 4 * rows_h, ms, l_, k_)
+
     # ---- roofline of the dominant kernel (most algorithmic bytes per step)
     dom = max(per, key=lambda k: per[k] * count[k])
     achieved = per[dom] / (mean_ms[dom] * 1e-3) / 1e9
@@ -430,7 +477,7 @@ def main():
                    "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
                    "param_layout_n": P, "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
-        "kernels": kernels, "configs": configs, "posterior": posterior, "roofline": roofline, "cpu_baseline": cpu,
+        "kernels": kernels, "configs": configs, "posterior": posterior, "head": head, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
 

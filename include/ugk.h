@@ -109,6 +109,22 @@ int ugk_residual_backward(float *dx, float *dy, const float *dout, int N);
 int ugk_bayes_materialize(float *w, const float *mu, const float *rho,
                           const float *eps, size_t n);
 
+/* train_bnn.c:279-304 / gpt2_kernels.cuh:352-374 (k_softmax_crossentropy).
+ * Per (b,t) row of V logits: probs = softmax (max-shifted, glibc-exact expf,
+ * each e divided by the row sum), losses[b,t] = -log(probs[target]). The
+ * exps are the CPU's bit for bit; the row sum is added in a fixed tree order
+ * (deterministic, within float rounding of the CPU's sequential sum), so
+ * probs and losses agree to a few ulp. 0 <= targets[i] < V is the caller's
+ * contract, as in the reference. */
+int ugk_softmax_crossentropy(float *losses, float *probs, const float *logits,
+                             const int *targets, int B, int T, int V);
+
+/* train_bnn.c:358-378 / gpt2_kernels.cuh:376-384
+ * (k_crossentropy_softmax_backward). dlogits += (probs - onehot(target)) *
+ * (1 / (B*T)); bit-identical to the CPU loop. */
+int ugk_crossentropy_softmax_backward(float *dlogits, const float *probs,
+                                      const int *targets, int B, int T, int V);
+
 /* ---- the posterior update around the layer kernels ----------------------
  * Flat parameter vectors of n floats. The ops that take eps are
  * bit-identical to train_bnn.c. The *_philox ops draw

@@ -174,6 +174,45 @@ void oracle_bayes_materialize(float *w, const float *mu, const float *rho,
   for (size_t i = 0; i < n; i++) w[i] = mu[i] + oracle_softplus(rho[i]) * eps[i];
 }
 
+/* train_bnn.c:279-304 */
+void oracle_softmax_crossentropy(float *losses, float *probs, const float *logits,
+                                 const int *targets, int B, int T, int V) {
+  for (int b = 0; b < B; b++) {
+    for (int t = 0; t < T; t++) {
+      const float *logit_bt = logits + (size_t)b * T * V + (size_t)t * V;
+      float *prob_bt = probs + (size_t)b * T * V + (size_t)t * V;
+      float max = -1e30f;
+      for (int v = 0; v < V; v++)
+        if (logit_bt[v] > max) max = logit_bt[v];
+      float sum = 0.0f;
+      for (int v = 0; v < V; v++) {
+        prob_bt[v] = expf(logit_bt[v] - max);
+        sum += prob_bt[v];
+      }
+      for (int v = 0; v < V; v++) prob_bt[v] /= sum;
+      int target_token = targets[b * T + t];
+      losses[b * T + t] = -logf(prob_bt[target_token]);
+    }
+  }
+}
+
+/* train_bnn.c:358-378 */
+void oracle_crossentropy_softmax_backward(float *dlogits, const float *probs,
+                                          const int *targets, int B, int T, int V) {
+  float dloss = 1.0f / (B * T);
+  for (int b = 0; b < B; b++) {
+    for (int t = 0; t < T; t++) {
+      float *dlogit_bt = dlogits + (size_t)b * T * V + (size_t)t * V;
+      const float *prob_bt = probs + (size_t)b * T * V + (size_t)t * V;
+      int target_token = targets[b * T + t];
+      for (int v = 0; v < V; v++) {
+        float indicator = (v == target_token) ? 1.0f : 0.0f;
+        dlogit_bt[v] += (prob_bt[v] - indicator) * dloss;
+      }
+    }
+  }
+}
+
 /* ---- the posterior update ------------------------------------------------ */
 
 /* train_bnn.c:820-822 */

@@ -26,6 +26,10 @@ float oracle_softplus(float x);
 void oracle_bayes_materialize(float *w, const float *mu, const float *rho,
                               const float *eps, size_t n);
 
+void oracle_softmax_crossentropy(float *losses, float *probs, const float *logits,
+                                 const int *targets, int B, int T, int V);
+void oracle_crossentropy_softmax_backward(float *dlogits, const float *probs,
+                                          const int *targets, int B, int T, int V);
 void oracle_bayes_backward(float *dmu, float *drho, const float *dw,
                            const float *eps, const float *rho, size_t n);
 double oracle_kl_forward(const float *mu, const float *rho, size_t n,

@@ -36,6 +36,8 @@ _SIGS = {
     "residual_forward": [_f, _f, _f, _i],
     "residual_backward": [_f, _f, _f, _i],
     "bayes_materialize": [_f, _f, _f, _f, _sz],
+    "softmax_crossentropy": [_f, _f, _f, _f, _i, _i, _i],
+    "crossentropy_softmax_backward": [_f, _f, _f, _i, _i, _i],
     "bayes_backward": [_f, _f, _f, _f, _f, _sz],
     "kl_backward": [_f, _f, _f, _f, _sz, ctypes.c_float, ctypes.c_float],
     "adamw_update": [_f, _f, _f, _f, _sz, _i, ctypes.c_float, ctypes.c_float, ctypes.c_float,
@@ -127,6 +129,14 @@ class Oracle:
 
     def bayes_materialize(self, w, mu, rho, eps, n):
         self._fn["bayes_materialize"](*(_p(a, np.float32) for a in (w, mu, rho, eps)), n)
+
+    def softmax_crossentropy(self, losses, probs, logits, targets, B, T, V):
+        self._fn["softmax_crossentropy"](_p(losses, np.float32), _p(probs, np.float32), _p(logits, np.float32),
+                                         _p(targets, np.int32), B, T, V)
+
+    def crossentropy_softmax_backward(self, dlogits, probs, targets, B, T, V):
+        self._fn["crossentropy_softmax_backward"](_p(dlogits, np.float32), _p(probs, np.float32),
+                                                  _p(targets, np.int32), B, T, V)
 
     def bayes_backward(self, dmu, drho, dw, eps, rho, n):
         self._fn["bayes_backward"](*(_p(a, np.float32) for a in (dmu, drho, dw, eps, rho)), n)

@@ -17,6 +17,8 @@ config 1: C=384, V=27, B=4, T=64, and the 256x384 LayerNorm of config 2):
   gelu.npz        GELU fwd + bwd, 65,536 N(0,1) values + special values
   residual.npz    residual fwd + bwd, 65,536 values
   materialize.npz bayes_materialize, 65,536 values + special rho/eps cases
+  head.npz        softmax_crossentropy + crossentropy_softmax_backward at
+                  B=4 T=64 V=27 (config 1) and B=1 T=2 V=50257
   posterior.npz   bayes_backward, kl_forward, kl_backward and adamw_update
                   (t = 1 and t = 7, with weight decay) over 16,384 parameters
                   drawn like a trained run (rho in [-8, -2], log-uniform
@@ -73,6 +75,27 @@ def posterior(ref) -> dict:
                 kmu=kmu, krho=krho, m0=m0, v0=v0, **adam)
 
 
+def head(ref) -> dict:
+    out = {}
+    for tag, (B, T, V), seed in (("s", (4, 64, 27), 707), ("l", (1, 2, 50257), 708)):
+        g = gen.rng(seed)
+        logits = gen.normal(g, (B, T, V), 0, 3.0)
+        targets = g.integers(0, V, B * T).astype(np.int32)
+        losses, probs = np.zeros(B * T, np.float32), np.zeros_like(logits)
+        ref.softmax_crossentropy(losses, probs, logits, targets, B, T, V)
+        d0 = gen.normal(g, (B, T, V), 0, 1e-3)
+        d = d0.copy()
+        ref.crossentropy_softmax_backward(d, probs, targets, B, T, V)
+        out.update({f"{tag}_shape": np.array([B, T, V], np.int32), f"{tag}_logits": logits,
+                    f"{tag}_targets": targets, f"{tag}_losses": losses, f"{tag}_probs": probs,
+                    f"{tag}_dlogits0": d0, f"{tag}_dlogits": d})
+    return out
+
+
+HASHED = {"posterior": ("dmu", "drho", "kl", "kmu", "krho", "p1", "m1", "v1", "p7", "m7", "v7"),
+          "head": ("s_losses", "s_probs", "s_dlogits", "l_losses", "l_probs", "l_dlogits")}
+
+
 def main(only=None) -> None:
     ref = Oracle(reference=True)
     meta_path = os.path.join(HERE, "golden.json")
@@ -81,10 +104,9 @@ def main(only=None) -> None:
         with open(meta_path) as f:
             digests = json.load(f)["sha256"]
         for name in only:
-            fx = {"posterior": posterior}[name](ref)
+            fx = {"posterior": posterior, "head": head}[name](ref)
             np.savez_compressed(os.path.join(HERE, name + ".npz"), **fx)
-            digests[name] = {k: sha(v) for k, v in fx.items() if k not in ("mu", "rho", "dw", "eps", "dmu0",
-                                                                            "drho0", "m0", "v0")}
+            digests[name] = {k: sha(fx[k]) for k in HASHED[name]}
         write_meta(meta_path, digests)
         print("wrote fixtures:", ", ".join(only))
         return
@@ -183,10 +205,10 @@ def main(only=None) -> None:
     np.savez_compressed(os.path.join(HERE, "materialize.npz"), **ma)
     digests["materialize"] = {"w": sha(w)}
 
-    fx = posterior(ref)
-    np.savez_compressed(os.path.join(HERE, "posterior.npz"), **fx)
-    digests["posterior"] = {k: sha(v) for k, v in fx.items() if k not in ("mu", "rho", "dw", "eps", "dmu0",
-                                                                          "drho0", "m0", "v0")}
+    for name, make in (("posterior", posterior), ("head", head)):
+        fx = make(ref)
+        np.savez_compressed(os.path.join(HERE, name + ".npz"), **fx)
+        digests[name] = {k: sha(fx[k]) for k in HASHED[name]}
     write_meta(meta_path, digests)
     print("wrote fixtures:", ", ".join(sorted(digests)))
 

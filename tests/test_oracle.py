@@ -104,7 +104,7 @@ def test_matches_reference_elementwise(oracle, ref_oracle, N):
 def test_golden_metadata():
     with open(os.path.join(GOLDEN, "golden.json")) as f:
         meta = json.load(f)
-    assert set(meta["sha256"]) == {"encoder", "layernorm", "gelu", "residual", "materialize", "posterior"}
+    assert set(meta["sha256"]) == {"encoder", "layernorm", "gelu", "residual", "materialize", "posterior", "head"}
 
 
 def test_golden_encoder(oracle):

@@ -234,6 +234,28 @@ int ugk_bayes_materialize(float *w, const float *mu, const float *rho, const flo
   return ok();
 }
 
+int ugk_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int B, int T,
+                             int V) {
+  const char *fn = "ugk_softmax_crossentropy";
+  if (int e = check_btc(fn, B, T, V)) return e;
+  if ((long long)B * T == 0) return ok();
+  if (V == 0) return bad(fn, "V must be > 0 when B*T > 0 (the target indexes the row)");
+  if (any_null({losses, probs, logits, targets})) return bad(fn, "NULL pointer");
+  if ((const void *)probs == (const void *)logits) return bad(fn, "probs and logits must be distinct buffers");
+  if (int e = launch_softmax_crossentropy(losses, probs, logits, targets, B * T, V)) return e;
+  return ok();
+}
+
+int ugk_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int B, int T, int V) {
+  const char *fn = "ugk_crossentropy_softmax_backward";
+  if (int e = check_btc(fn, B, T, V)) return e;
+  if ((long long)B * T * V == 0) return ok();
+  if (any_null({dlogits, probs, targets})) return bad(fn, "NULL pointer");
+  const float dloss = 1.0f / (B * T);  // train_bnn.c:360
+  if (int e = launch_crossentropy_softmax_backward(dlogits, probs, targets, B * T, V, dloss)) return e;
+  return ok();
+}
+
 int ugk_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
                      unsigned long long seed, int step) {
   const char *fn = "ugk_bayes_sample";

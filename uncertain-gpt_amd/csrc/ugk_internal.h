@@ -100,6 +100,10 @@ int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, f
                                        const float *inp, const float *weight, const float *mean,
                                        const float *rstd, int rows, int C, int *nblk);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
+int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
+                                int V);
+int launch_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int rows, int V,
+                                         float dloss);
 int launch_encoder_forward(float *out, const int *inp, const float *wte,
                            const float *wpe, int B, int T, int C);
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,

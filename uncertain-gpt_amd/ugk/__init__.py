@@ -23,7 +23,10 @@ __all__ = [
     "UgkError", "lib", "library_path",
     "encoder_forward", "encoder_backward", "layernorm_forward", "layernorm_backward",
     "gelu_forward", "gelu_backward", "residual_forward", "residual_backward",
-    "bayes_materialize", "set_stream", "synchronize", "reserve", "scratch_bytes",
+    "bayes_materialize", "residual_layernorm_forward", "layernorm_residual_backward",
+    "softmax_crossentropy", "crossentropy_softmax_backward", "bayes_sample", "bayes_backward",
+    "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
+    "set_stream", "synchronize", "reserve", "scratch_bytes",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "version",
 ]
@@ -74,6 +77,8 @@ _SIGS = {
     "ugk_residual_forward": [_fp, _fp, _fp, _i],
     "ugk_residual_backward": [_fp, _fp, _fp, _i],
     "ugk_bayes_materialize": [_fp, _fp, _fp, _fp, _sz],
+    "ugk_softmax_crossentropy": [_fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_crossentropy_softmax_backward": [_fp, _fp, _fp, _i, _i, _i],
     "ugk_bayes_sample": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
     "ugk_bayes_backward": [_fp, _fp, _fp, _fp, _fp, _sz],
     "ugk_bayes_backward_philox": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
@@ -147,6 +152,16 @@ def _check_tokens(inp, table, C: int, what: str) -> None:
         lo, hi = int(inp.min()), int(inp.max())
         if lo < 0 or hi >= rows:
             raise ValueError(f"{what}: token ids must lie in [0, {rows}), got [{lo}, {hi}]")
+
+
+def _check_targets(targets, V: int, rows: int, what: str) -> None:
+    """Target ids index a row of V logits (the reference's contract); checked when a tensor."""
+    import torch
+    if isinstance(targets, torch.Tensor) and rows:
+        t = targets.reshape(-1)[:rows]
+        lo, hi = int(t.min()), int(t.max())
+        if lo < 0 or hi >= V:
+            raise ValueError(f"{what}: target ids must lie in [0, {V}), got [{lo}, {hi}]")
 
 
 def encoder_forward(out, inp, wte, wpe, B: int, T: int, C: int) -> None:
@@ -229,6 +244,23 @@ def bayes_materialize(w, mu, rho, eps, n: int) -> None:
     """train_bnn.c:831-835. ``w = mu + softplus(rho) * eps``."""
     _check(lib.ugk_bayes_materialize(_ptr(w, "w", n, "f32"), _ptr(mu, "mu", n, "f32"),
                                      _ptr(rho, "rho", n, "f32"), _ptr(eps, "eps", n, "f32"), n))
+
+
+def softmax_crossentropy(losses, probs, logits, targets, B: int, T: int, V: int) -> None:
+    """train_bnn.c:279-304. ``probs`` = row softmax of ``logits``; ``losses`` = -log probs[target]."""
+    rows, n = B * T, B * T * V
+    _check_targets(targets, V, rows, "softmax_crossentropy")
+    _check(lib.ugk_softmax_crossentropy(_ptr(losses, "losses", rows, "f32"), _ptr(probs, "probs", n, "f32"),
+                                        _ptr(logits, "logits", n, "f32"), _ptr(targets, "targets", rows, "i32"),
+                                        B, T, V))
+
+
+def crossentropy_softmax_backward(dlogits, probs, targets, B: int, T: int, V: int) -> None:
+    """train_bnn.c:358-378. ``dlogits += (probs - onehot(target)) / (B*T)``."""
+    rows, n = B * T, B * T * V
+    _check_targets(targets, V, rows, "crossentropy_softmax_backward")
+    _check(lib.ugk_crossentropy_softmax_backward(_ptr(dlogits, "dlogits", n, "f32"), _ptr(probs, "probs", n, "f32"),
+                                                 _ptr(targets, "targets", rows, "i32"), B, T, V))
 
 
 def bayes_sample(w, eps, mu, rho, n: int, seed: int, step: int) -> None:
