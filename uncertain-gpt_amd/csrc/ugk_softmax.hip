@@ -15,11 +15,15 @@
 //   loss  -log(prob[target]) by the owning thread, from the same register.
 // Rows are V floats long and V is odd for GPT-2, so rows are not 16-byte
 // aligned: loads and stores are dwords, coalesced across the wavefront.
-// Rows longer than kThreads * kMaxPer take a three-pass kernel that re-reads
-// the logits from memory.
+// A row of up to 51,200 logits (GPT-2's 50257) fits in the registers of a
+// 1024-thread workgroup, one row resident per CU. Longer rows take two passes
+// instead: one wavefront per row streams the logits once for the exact max
+// and the sum (kept per lane in double and rescaled as the max grows), then a
+// flat map over all rows forms expf(x - max) / sum, 12 bytes per logit.
 //
-// Backward: dlogits[v] += (probs[v] - (v == target)) * (1 / (B*T)), a map
-// over a (row, column block) grid; bit-identical to the CPU loop.
+// Backward: dlogits[v] += (probs[v] - (v == target)) * (1 / (B*T)), one
+// workgroup per row streaming float4 (dwords for misaligned arrays);
+// bit-identical to the CPU loop.
 #include "ugk_internal.h"
 #include "ugk_libm_dev.h"
 
@@ -108,38 +112,132 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
   }
 }
 
-// Any V: three passes over the row in memory (max; exp and sum, e stored;
-// divide), one workgroup per row.
-constexpr int kLongThreads = 1024;
-__global__ __launch_bounds__(kLongThreads) void k_softmax_xent_long(float *losses, float *probs,
-                                                                    const float *logits, const int *targets,
-                                                                    int V) {
+// Row of flat element i (rows of V elements): a double-precision quotient,
+// then exact integer correction (the estimate is off by at most one).
+__device__ __forceinline__ size_t row_of(size_t i, size_t V, double inv_v) {
+  size_t r = (size_t)((double)i * inv_v);
+  if (r * V > i) r--;
+  else if ((r + 1) * V <= i) r++;
+  return r;
+}
+
+// Long rows, pass 1: one wavefront per row streams its logits once and keeps,
+// per lane, the running max (the CPU's rule, from -1e30) and the sum of
+// exp(x - running max) in double, rescaled when the max grows; the lanes are
+// then combined onto the row max. stats[row] = {max, sum}. The max is exact;
+// the sum is within float rounding of the exact sum of expf(x - max).
+constexpr int kStatsWaves = 4, kStatsUnroll = 8;
+__global__ __launch_bounds__(kStatsWaves * kWave) void k_softmax_stats(float2 *__restrict__ stats,
+                                                                       const float *__restrict__ logits, int rows,
+                                                                       int V) {
   __shared__ uint64_t tab[32];
-  __shared__ float lds[kLongThreads / kWave];
   ugk_exp2_stage(tab);
-  const size_t row = blockIdx.x;
-  const float *lg = logits + row * (size_t)V;
-  float *pr = probs + row * (size_t)V;
-  float m = kNegInit;
-  for (int v = threadIdx.x; v < V; v += kLongThreads) m = max_rule(m, lg[v]);
   __syncthreads();
-  m = block_max<kLongThreads>(m, lds);
-  float s = 0.0f;
-  for (int v = threadIdx.x; v < V; v += kLongThreads) {
-    const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(lg[v] - m, UgkExp2Lds{tab});
-    pr[v] = e;
-    s += e;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kStatsWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *lg = logits + (size_t)row * V;
+  float m = kNegInit;
+  double s = 0.0;
+  for (int v0 = lane; v0 < V; v0 += kWave * kStatsUnroll) {
+    float x[kStatsUnroll];
+#pragma unroll
+    for (int k = 0; k < kStatsUnroll; k++) {
+      const int v = v0 + k * kWave;
+      x[k] = v < V ? ld_nt(lg + v) : kNegInit;
+    }
+    float mb = m;
+#pragma unroll
+    for (int k = 0; k < kStatsUnroll; k++) mb = max_rule(mb, x[k]);
+    if (mb != m) {  // rescale the running sum to the new max
+      s *= (double)ugk_expf_t<UGK_EXPF_CONTRACT>(m - mb, UgkExp2Lds{tab});
+      m = mb;
+    }
+#pragma unroll
+    for (int k = 0; k < kStatsUnroll; k++)
+      if (v0 + k * kWave < V) s += (double)ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
   }
-  s = block_sum<kLongThreads>(s, lds);
-  const int tgt = targets[row];
-  for (int v = threadIdx.x; v < V; v += kLongThreads) {
-    const float p = pr[v] / s;
-    pr[v] = p;
-    if (v == tgt) losses[row] = neg_logf(p);
+  float M = m;
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) M = max_rule(M, __shfl_xor(M, off));
+  s *= (double)ugk_expf_t<UGK_EXPF_CONTRACT>(m - M, UgkExp2Lds{tab});
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) stats[row] = make_float2(M, (float)s);
+}
+
+// Long rows, pass 2: a flat map over all rows x V: p = expf(x - max) / sum,
+// and the thread holding a row's target writes its loss.
+constexpr int kNormUnroll = 4;
+__global__ __launch_bounds__(kBlock) void k_softmax_norm(float *__restrict__ losses, float *__restrict__ probs,
+                                                         const float *__restrict__ logits,
+                                                         const int *__restrict__ targets,
+                                                         const float2 *__restrict__ stats, size_t n, int V,
+                                                         double inv_v) {
+  __shared__ uint64_t tab[32];
+  ugk_exp2_stage(tab);
+  __syncthreads();
+  const size_t i0 = (size_t)blockIdx.x * (kBlock * kNormUnroll) + threadIdx.x;
+  float x[kNormUnroll];
+#pragma unroll
+  for (int k = 0; k < kNormUnroll; k++) {
+    const size_t i = i0 + (size_t)k * kBlock;
+    x[k] = i < n ? ld_nt(logits + i) : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < kNormUnroll; k++) {
+    const size_t i = i0 + (size_t)k * kBlock;
+    if (i < n) {
+      const size_t row = row_of(i, (size_t)V, inv_v);
+      const float2 st = stats[row];
+      const float p = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - st.x, UgkExp2Lds{tab}) / st.y;
+      st_nt(probs + i, p);
+      if ((int)(i - row * (size_t)V) == targets[row]) losses[row] = neg_logf(p);
+    }
   }
 }
 
-constexpr int kBwdThreads = 256, kBwdPer = 4;
+// Backward over the flat rows x V array, float4 at a time when both arrays
+// start 16-byte aligned (their element offsets agree): each float4 spans at
+// most two rows (V >= 4), so it looks up two targets.
+constexpr int kBwdThreads = 256, kBwdUnroll = 2;
+__global__ __launch_bounds__(kBwdThreads) void k_xent_softmax_bwd_flat4(float *__restrict__ dlogits,
+                                                                        const float *__restrict__ probs,
+                                                                        const int *__restrict__ targets, int rows,
+                                                                        int V, float dloss, size_t n4,
+                                                                        double inv_v) {
+  const float4 *p4 = reinterpret_cast<const float4 *>(probs);
+  float4 *d4 = reinterpret_cast<float4 *>(dlogits);
+  const size_t q0 = (size_t)blockIdx.x * (kBwdThreads * kBwdUnroll) + threadIdx.x;
+  float4 p[kBwdUnroll], d[kBwdUnroll];
+#pragma unroll
+  for (int k = 0; k < kBwdUnroll; k++) {
+    const size_t q = q0 + (size_t)k * kBwdThreads;
+    if (q < n4) {
+      p[k] = ld_nt(p4 + q);
+      d[k] = ld_nt(d4 + q);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kBwdUnroll; k++) {
+    const size_t q = q0 + (size_t)k * kBwdThreads;
+    if (q < n4) {
+      const size_t i = 4 * q;
+      const size_t r0 = row_of(i, (size_t)V, inv_v);
+      const size_t t0 = r0 * (size_t)V + (size_t)targets[r0];
+      const size_t t1 = (r0 + 1 < (size_t)rows) ? (r0 + 1) * (size_t)V + (size_t)targets[r0 + 1] : ~(size_t)0;
+      float4 o;
+      o.x = d[k].x + (p[k].x - ((i == t0 || i == t1) ? 1.0f : 0.0f)) * dloss;
+      o.y = d[k].y + (p[k].y - ((i + 1 == t0 || i + 1 == t1) ? 1.0f : 0.0f)) * dloss;
+      o.z = d[k].z + (p[k].z - ((i + 2 == t0 || i + 2 == t1) ? 1.0f : 0.0f)) * dloss;
+      o.w = d[k].w + (p[k].w - ((i + 3 == t0 || i + 3 == t1) ? 1.0f : 0.0f)) * dloss;
+      st_nt(d4 + q, o);
+    }
+  }
+}
+
+// Any alignment: dwords, a (row, column block) grid.
+constexpr int kBwdPer = 4;
 __global__ __launch_bounds__(kBwdThreads) void k_xent_softmax_bwd(float *__restrict__ dlogits,
                                                                   const float *__restrict__ probs,
                                                                   const int *__restrict__ targets, int V,
@@ -181,21 +279,36 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
   if (V <= 64) launch_rows<64, 1>(losses, probs, logits, targets, rows, V);
   else if (V <= 256) launch_rows<64, 4>(losses, probs, logits, targets, rows, V);
   else if (V <= 1024) launch_rows<256, 4>(losses, probs, logits, targets, rows, V);
-  else if (V <= 4096) launch_rows<1024, 4>(losses, probs, logits, targets, rows, V);
+  else if (V <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
   else if (V <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
   else if (V <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
   else if (V <= 51200) launch_rows<1024, 50>(losses, probs, logits, targets, rows, V);
-  else
-    hipLaunchKernelGGL(k_softmax_xent_long, dim3(rows), dim3(kLongThreads), 0, stream(), losses, probs, logits,
-                       targets, V);
+  else {
+    // Rows too long for the registers of one workgroup: a statistics pass
+    // and a flat normalising pass (12 bytes per logit rather than 8).
+    float2 *stats = static_cast<float2 *>(scratch((size_t)rows * sizeof(float2)));
+    if (!stats) return 3;
+    hipLaunchKernelGGL(k_softmax_stats, dim3(grid_for((size_t)rows, kStatsWaves)), dim3(kStatsWaves * kWave), 0,
+                       stream(), stats, logits, rows, V);
+    const size_t n = (size_t)rows * V;
+    hipLaunchKernelGGL(k_softmax_norm, dim3(grid_for(n, (size_t)kBlock * kNormUnroll)), dim3(kBlock), 0, stream(),
+                       losses, probs, logits, targets, stats, n, V, 1.0 / (double)V);
+  }
   return check_launch("softmax_crossentropy");
 }
 
 int launch_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int rows, int V,
                                          float dloss) {
   if (rows == 0 || V == 0) return 0;
-  const dim3 grid(rows, grid_for((size_t)V, (size_t)kBwdThreads * kBwdPer));
-  hipLaunchKernelGGL(k_xent_softmax_bwd, grid, dim3(kBwdThreads), 0, stream(), dlogits, probs, targets, V, dloss);
+  const size_t n = (size_t)rows * V;
+  if (V >= 4 && (n & 3) == 0 && aligned16(dlogits) && aligned16(probs)) {
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(k_xent_softmax_bwd_flat4, dim3(grid_for(n4, (size_t)kBwdThreads * kBwdUnroll)),
+                       dim3(kBwdThreads), 0, stream(), dlogits, probs, targets, rows, V, dloss, n4, 1.0 / (double)V);
+  } else {
+    const dim3 grid(rows, grid_for((size_t)V, (size_t)kBwdThreads * kBwdPer));
+    hipLaunchKernelGGL(k_xent_softmax_bwd, grid, dim3(kBwdThreads), 0, stream(), dlogits, probs, targets, V, dloss);
+  }
   return check_launch("crossentropy_softmax_backward");
 }
 
