@@ -191,6 +191,8 @@ def main():
     n_mat = P - (C * V + V)  # GPT-2-124M with the head tied to wte: 124,439,808
     A = ugk.act_count(cfg)
     per, count, total_bytes = step_bytes(B, T, C, L, n_mat)
+    # the fused pairs of the driver skip 2L LayerNorm input reads and 2L residual dout reads
+    moved_bytes = total_bytes - 2 * (2 * L) * 4 * (B * T * C)
     log(f"bench: params {P} (materialize {n_mat}), acts {A}, algorithmic bytes/step {total_bytes / 1e9:.3f} GB")
 
     g = torch.Generator(device=dev)
@@ -477,14 +479,16 @@ def main():
                    "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
                    "param_layout_n": P, "parallelism": "single GPU"},
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
+        "bytes_per_step_moved": moved_bytes, "GBps_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9, 1),
         "kernels": kernels, "configs": configs, "posterior": posterior, "head": head, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
 
 
 def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
-    """Each CPU op once at the step shape (materialize on a 1/16 slice, scaled),
-    composed by launch count; single-threaded, like train_bnn.c."""
+    """Each CPU op at the step shape, best of 10 runs (materialize on a 1/8 slice,
+    scaled), composed by launch count; single-threaded, like train_bnn.c. About
+    10 s of CPU work in all."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, REF_SO
@@ -502,7 +506,7 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
     wte, wpe = f(V * C) * np.float32(0.02), f(T * C) * np.float32(0.01)
     dwte, dwpe = np.zeros(V * C, np.float32), np.zeros(T * C, np.float32)
     dwl, dbl = np.zeros(C, np.float32), np.zeros(C, np.float32)
-    ns = n_mat // 16
+    ns = n_mat // 8
     mu, rh, ep, wm = f(ns) * np.float32(0.02), f(ns) * np.float32(0.1) - np.float32(5), f(ns), np.zeros(ns, np.float32)
     ops = {
         "encoder_forward": (lambda: o.encoder_forward(out, inp, wte, wpe, B, T, C), 1),
@@ -518,7 +522,7 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
     t_op, t_sample = {}, 0.0
     for name, (fn, scale) in ops.items():
         best = None
-        for _ in range(2):
+        for _ in range(10):
             t0 = time.perf_counter()
             fn()
             dt = time.perf_counter() - t0
@@ -530,8 +534,8 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
     log(f"bench: cpu ({kind}, 1 core) step {step_s * 1e3:.1f} ms -> {gbs:.2f} GB/s; sample {t_sample:.1f} s")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": kind, "ms_per_step": round(step_s * 1e3, 1),
             "per_op_ms": {k: round(v * 1e3, 2) for k, v in t_op.items()},
-            "sample": "each train_bnn.c op once per rep (best of 2) at the config-5 step shape "
-                      "(materialize on a 1/16 slice, scaled), summed by launch count per step; "
+            "sample": "each train_bnn.c op at the config-5 step shape, best of 10 runs "
+                      "(materialize on a 1/8 slice, scaled), summed by launch count per step; "
                       f"{t_sample:.1f} s of CPU work"}
 
 
