@@ -85,6 +85,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualBwd>", "residual_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualFwd>", "residual_forward"),
     ("k_ln_bwd_vec", "layernorm_backward (main)"),
+    ("k_ln_bwd_reduce_batch", "layernorm_backward (batched column sums)"),
     ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
     ("k_ln_fwd_vec", "layernorm_forward"),
     ("k_enc_fwd_vec", "encoder_forward"),
@@ -98,6 +99,10 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_map_vec4<ugk::(anonymous namespace)::KlBackward>", "kl_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::AdamW>", "adamw_update"),
     ("k_map_vec4<ugk::(anonymous namespace)::BbbStepFused>", "bbb_step_fused"),
+    ("k_softmax_xent<", "softmax_crossentropy"),
+    ("k_softmax_stats", "softmax_crossentropy (row statistics)"),
+    ("k_softmax_norm", "softmax_crossentropy (normalise)"),
+    ("k_xent_softmax_bwd", "crossentropy_softmax_backward"),
     ("k_kl_partial", "kl_forward (partial sums)"),
     ("k_kl_final", "kl_forward (final sum)"),
     ("__amd_rocclr_copyBuffer", "calibration copy 1 GiB"),
