@@ -272,6 +272,54 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                              const float *params, const int *inputs,
                              ugk_config cfg, const ugk_dense_ops *ops);
 
+/* ---- file formats of an end-to-end run ----------------------------------
+ * Token files (llm.c's .bin: 256 int32 header with magic 20240520 and the
+ * token count in header[2], then uint16 token ids) and checkpoints (8 int32
+ * header {20240520, n low word, C, L, V, NH, steps, n high word}, then n
+ * floats), as the reference reads and writes them. */
+
+typedef struct ugk_loader ugk_loader;
+
+/* gpt2_kernels.cuh:904-921 (loader_init): read the whole token file into host
+ * memory. *ld is NULL on failure (missing file, short header, bad magic,
+ * short read). */
+int ugk_loader_open(ugk_loader **ld, const char *path);
+
+/* gpt2_kernels.cuh:1318-1331 (loader_count): the token count from the header
+ * alone. */
+int ugk_loader_count(const char *path, long *ntok);
+
+/* gpt2_kernels.cuh:924-929 (loader_next): inputs = tokens[pos, pos+BT),
+ * targets = tokens[pos+1, pos+BT+1) into HOST buffers, pos += BT, restarting
+ * at 0 when the window would pass the end. */
+int ugk_loader_next(ugk_loader *ld, int *h_inp, int *h_tgt, int BT);
+
+/* The same window into DEVICE buffers, widened on the GPU from a uint16 copy
+ * of the tokens kept in device memory (made on the first call; 2 bytes per
+ * token), so no tokens cross PCIe per step. No counterpart in the reference,
+ * which copies each window from the host (train_bnn_gpu.cu:439-441). */
+int ugk_loader_next_device(ugk_loader *ld, int *d_inp, int *d_tgt, int BT);
+
+long ugk_loader_tokens(const ugk_loader *ld);    /* token count, -1 if NULL */
+long ugk_loader_position(const ugk_loader *ld);  /* next window start */
+int ugk_loader_close(ugk_loader *ld);
+
+/* gpt2_kernels.cuh:950-951: "runs/<arm>_C<C>_L<L>_<steps/1000>k_<what>.bin". */
+int ugk_ckpt_path(char *buf, size_t size, const char *arm, const char *what,
+                  ugk_config cfg, int steps);
+
+/* gpt2_kernels.cuh:944-964 (ckpt_save) at an explicit path: the n floats of
+ * the DEVICE buffer d_buf, behind the 8-int header. Waits for the stream. */
+int ugk_ckpt_save(const char *path, const float *d_buf, size_t n,
+                  ugk_config cfg, int steps);
+
+/* gpt2_kernels.cuh:1281-1316 (ckpt_load) at an explicit path: checks the
+ * magic and the header's n, C, L, V, NH against the run's (an error, not a
+ * load, on any mismatch), fills the DEVICE buffer d_buf and returns the
+ * header's step count in *steps (may be NULL). Waits for the stream. */
+int ugk_ckpt_load(const char *path, float *d_buf, size_t n, ugk_config cfg,
+                  int *steps);
+
 #ifdef __cplusplus
 }
 #endif

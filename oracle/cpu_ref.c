@@ -36,6 +36,8 @@
 #include "cpu_ref.h"
 
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* train_bnn.c:41-65 */
@@ -361,6 +363,93 @@ void oracle_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, floa
     rho[i] = rho_new;
     w[i] = mu_new + oracle_softplus(rho_new) * oracle_philox_normal(seed, step + 1, i);
   }
+}
+
+/* ---- file formats ----------------------------------------------------------
+ * gpt2_kernels.cuh:898-930 (Loader), :1318-1331 (loader_count), :944-964
+ * (ckpt_save) and :1281-1316 (ckpt_load), with host buffers in place of the
+ * device copies and a status return in place of the abort. */
+
+/* OracleLoader (cpu_ref.h) mirrors Loader, gpt2_kernels.cuh:903. */
+
+/* gpt2_kernels.cuh:904-921; returns 0, or -1 (missing, bad header, bad magic,
+ * short read) */
+int oracle_loader_init(OracleLoader *ld, const char *path) {
+  FILE *f = fopen(path, "rb");
+  if (!f) return -1;
+  int header[256];
+  if (fread(header, sizeof(int), 256, f) != 256) { fclose(f); return -1; }
+  if (header[0] != 20240520) { fclose(f); return -1; }
+  long ntok = header[2];
+  unsigned short *raw = (unsigned short *)malloc((ntok > 0 ? ntok : 1) * sizeof(unsigned short));
+  if (fread(raw, sizeof(unsigned short), ntok, f) != (size_t)ntok) { free(raw); fclose(f); return -1; }
+  fclose(f);
+  ld->tokens = (int *)malloc((ntok > 0 ? ntok : 1) * sizeof(int));
+  for (long i = 0; i < ntok; i++) ld->tokens[i] = (int)raw[i];
+  free(raw);
+  ld->n = ntok;
+  ld->pos = 0;
+  return 0;
+}
+
+/* gpt2_kernels.cuh:924-929 */
+void oracle_loader_next(OracleLoader *ld, int *h_inp, int *h_tgt, int BT) {
+  if (ld->pos + BT + 1 > ld->n) ld->pos = 0;
+  memcpy(h_inp, ld->tokens + ld->pos, BT * sizeof(int));
+  memcpy(h_tgt, ld->tokens + ld->pos + 1, BT * sizeof(int));
+  ld->pos += BT;
+}
+
+void oracle_loader_free(OracleLoader *ld) { free(ld->tokens); }
+
+/* gpt2_kernels.cuh:1318-1331; -1 on error */
+long oracle_loader_count(const char *path) {
+  FILE *f = fopen(path, "rb");
+  if (!f) return -1;
+  int header[256];
+  if (fread(header, sizeof(int), 256, f) != 256) { fclose(f); return -1; }
+  fclose(f);
+  if (header[0] != 20240520) return -1;
+  return header[2];
+}
+
+/* gpt2_kernels.cuh:950-951 */
+void oracle_ckpt_path(char *buf, size_t size, const char *arm, const char *what,
+                      int C, int L, int steps) {
+  snprintf(buf, size, "runs/%s_C%d_L%d_%dk_%s.bin", arm, C, L, steps / 1000, what);
+}
+
+/* gpt2_kernels.cuh:958-959: the 8-int header */
+void oracle_ckpt_header(int *hdr, size_t n, int C, int L, int V, int NH, int steps) {
+  int h[8] = {20240520, (int)(n & 0xffffffffu), C, L, V, NH, steps, (int)(n >> 32)};
+  memcpy(hdr, h, sizeof h);
+}
+
+/* gpt2_kernels.cuh:944-964 with a host buffer; 0 or -1 */
+int oracle_ckpt_save(const char *path, const float *h, size_t n, int C, int L, int V,
+                     int NH, int steps) {
+  FILE *f = fopen(path, "wb");
+  if (!f) return -1;
+  int hdr[8];
+  oracle_ckpt_header(hdr, n, C, L, V, NH, steps);
+  fwrite(hdr, sizeof(int), 8, f);
+  fwrite(h, sizeof(float), n, f);
+  fclose(f);
+  return 0;
+}
+
+/* gpt2_kernels.cuh:1281-1316 with a host buffer: the header's steps, or -1 */
+int oracle_ckpt_load(const char *path, float *h, size_t n, int C, int L, int V, int NH) {
+  FILE *f = fopen(path, "rb");
+  if (!f) return -1;
+  int hdr[8];
+  if (fread(hdr, sizeof(int), 8, f) != 8) { fclose(f); return -1; }
+  if (hdr[0] != 20240520) { fclose(f); return -1; }
+  size_t got = (size_t)(unsigned int)hdr[1] | ((size_t)(unsigned int)hdr[7] << 32);
+  if (got != n || hdr[2] != C || hdr[3] != L || hdr[4] != V || hdr[5] != NH) { fclose(f); return -1; }
+  if (fread(h, sizeof(float), n, f) != n) { fclose(f); return -1; }
+  fclose(f);
+  return hdr[6];
 }
 
 /* Elementwise host libm entry points, so tests can compare device math with

@@ -54,6 +54,22 @@ void oracle_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, floa
                            float bc1, float bc2, float lr, float beta1, float beta2,
                            float aeps, float wd);
 
+typedef struct {
+  int *tokens;
+  long n;
+  long pos;
+} OracleLoader;
+int oracle_loader_init(OracleLoader *ld, const char *path);
+void oracle_loader_next(OracleLoader *ld, int *h_inp, int *h_tgt, int BT);
+void oracle_loader_free(OracleLoader *ld);
+long oracle_loader_count(const char *path);
+void oracle_ckpt_path(char *buf, size_t size, const char *arm, const char *what,
+                      int C, int L, int steps);
+void oracle_ckpt_header(int *hdr, size_t n, int C, int L, int V, int NH, int steps);
+int oracle_ckpt_save(const char *path, const float *h, size_t n, int C, int L, int V,
+                     int NH, int steps);
+int oracle_ckpt_load(const char *path, float *h, size_t n, int C, int L, int V, int NH);
+
 void oracle_expf_n(float *y, const float *x, size_t n);
 void oracle_log1pf_n(float *y, const float *x, size_t n);
 void oracle_tanhf_n(float *y, const float *x, size_t n);

@@ -182,6 +182,52 @@ class Oracle:
         self.lib.oracle_bbb_step_fused(*(_p(a, np.float32) for a in (mu, rho, m_mu, v_mu, m_rho, v_rho, w, dw)),
                                        n, seed, step, sp, klw, bc1, bc2, lr, beta1, beta2, aeps, wd)
 
+    # ---- file formats (restatement only) --------------------------------------
+    def loader_windows(self, path: str, BT: int, steps: int):
+        """(inputs, targets) of `steps` successive loader_next windows, or None if init fails."""
+        class _L(ctypes.Structure):
+            _fields_ = [("tokens", ctypes.c_void_p), ("n", ctypes.c_long), ("pos", ctypes.c_long)]
+        ld = _L()
+        self.lib.oracle_loader_init.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+        self.lib.oracle_loader_init.restype = ctypes.c_int
+        if self.lib.oracle_loader_init(ctypes.byref(ld), path.encode()) != 0:
+            return None
+        self.lib.oracle_loader_next.argtypes = [ctypes.c_void_p, _f, _f, _i]
+        self.lib.oracle_loader_free.argtypes = [ctypes.c_void_p]
+        inp = np.zeros((steps, BT), np.int32)
+        tgt = np.zeros((steps, BT), np.int32)
+        for k in range(steps):
+            self.lib.oracle_loader_next(ctypes.byref(ld), inp[k].ctypes.data, tgt[k].ctypes.data, BT)
+        self.lib.oracle_loader_free(ctypes.byref(ld))
+        return inp, tgt
+
+    def loader_count(self, path: str) -> int:
+        self.lib.oracle_loader_count.argtypes = [ctypes.c_char_p]
+        self.lib.oracle_loader_count.restype = ctypes.c_long
+        return int(self.lib.oracle_loader_count(path.encode()))
+
+    def ckpt_path(self, arm: str, what: str, C: int, L: int, steps: int) -> str:
+        buf = ctypes.create_string_buffer(512)
+        self.lib.oracle_ckpt_path.argtypes = [ctypes.c_char_p, _sz, ctypes.c_char_p, ctypes.c_char_p, _i, _i, _i]
+        self.lib.oracle_ckpt_path(buf, 512, arm.encode(), what.encode(), C, L, steps)
+        return buf.value.decode()
+
+    def ckpt_header(self, n: int, C: int, L: int, V: int, NH: int, steps: int) -> np.ndarray:
+        hdr = np.zeros(8, np.int32)
+        self.lib.oracle_ckpt_header.argtypes = [_f, _sz, _i, _i, _i, _i, _i]
+        self.lib.oracle_ckpt_header(hdr.ctypes.data, n, C, L, V, NH, steps)
+        return hdr
+
+    def ckpt_save(self, path: str, h: np.ndarray, C: int, L: int, V: int, NH: int, steps: int) -> int:
+        self.lib.oracle_ckpt_save.argtypes = [ctypes.c_char_p, _f, _sz, _i, _i, _i, _i, _i]
+        self.lib.oracle_ckpt_save.restype = ctypes.c_int
+        return int(self.lib.oracle_ckpt_save(path.encode(), _p(h, np.float32), h.size, C, L, V, NH, steps))
+
+    def ckpt_load(self, path: str, h: np.ndarray, C: int, L: int, V: int, NH: int) -> int:
+        self.lib.oracle_ckpt_load.argtypes = [ctypes.c_char_p, _f, _sz, _i, _i, _i, _i]
+        self.lib.oracle_ckpt_load.restype = ctypes.c_int
+        return int(self.lib.oracle_ckpt_load(path.encode(), _p(h, np.float32), h.size, C, L, V, NH))
+
     # ---- host libm, elementwise (restatement only) ----------------------------
     def _map(self, name, x):
         y = np.empty_like(x)

@@ -26,6 +26,7 @@ __all__ = [
     "bayes_materialize", "residual_layernorm_forward", "layernorm_residual_backward",
     "softmax_crossentropy", "crossentropy_softmax_backward", "bayes_sample", "bayes_backward",
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
+    "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "version",
@@ -101,8 +102,19 @@ _SIGS = {
                                ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
     "ugk_diag_philox": [_fp, _fp, _sz],
+    "ugk_loader_open": [ctypes.POINTER(_fp), ctypes.c_char_p],
+    "ugk_loader_count": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_long)],
+    "ugk_loader_next": [_fp, _fp, _fp, _i],
+    "ugk_loader_next_device": [_fp, _fp, _fp, _i],
+    "ugk_loader_tokens": [_fp],
+    "ugk_loader_position": [_fp],
+    "ugk_loader_close": [_fp],
+    "ugk_ckpt_path": [ctypes.c_char_p, _sz, ctypes.c_char_p, ctypes.c_char_p, Config, _i],
+    "ugk_ckpt_save": [ctypes.c_char_p, _fp, _sz, Config, _i],
+    "ugk_ckpt_load": [ctypes.c_char_p, _fp, _sz, Config, ctypes.POINTER(_i)],
 }
 _RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz,
+        "ugk_loader_tokens": ctypes.c_long, "ugk_loader_position": ctypes.c_long,
         "ugk_param_count": _sz, "ugk_act_count": _sz}
 for _name, _args in _SIGS.items():
     _f = getattr(lib, _name)
@@ -399,3 +411,67 @@ def diag_philox(out, tuples) -> None:
     ``out`` an int32 tensor of n x 4 output words (bit patterns; read them as uint32)."""
     n = tuples.numel() // 6
     _check(lib.ugk_diag_philox(_ptr(out, "out", 4 * n, "i32"), _ptr(tuples, "tuples", 6 * n, "i32"), n))
+
+
+# ---- file formats ---------------------------------------------------------------
+
+class Loader:
+    """gpt2_kernels.cuh:898-930 (Loader): llm.c .bin token files. ``next`` fills host int32 arrays
+    (numpy), ``next_device`` device int32 tensors from a copy of the tokens kept in device memory."""
+
+    def __init__(self, path: str):
+        h = _fp()
+        _check(lib.ugk_loader_open(ctypes.byref(h), path.encode()))
+        self._h = h
+
+    @property
+    def tokens(self) -> int:
+        return int(lib.ugk_loader_tokens(self._h))
+
+    @property
+    def position(self) -> int:
+        return int(lib.ugk_loader_position(self._h))
+
+    def next(self, inp, tgt, BT: int) -> None:
+        import numpy as np
+        for a, nm in ((inp, "inp"), (tgt, "tgt")):
+            if not (isinstance(a, np.ndarray) and a.dtype == np.int32 and a.flags.c_contiguous and a.size >= BT):
+                raise ValueError(f"{nm}: expected a contiguous int32 numpy array of at least {BT} elements")
+        _check(lib.ugk_loader_next(self._h, inp.ctypes.data, tgt.ctypes.data, BT))
+
+    def next_device(self, inp, tgt, BT: int) -> None:
+        _check(lib.ugk_loader_next_device(self._h, _ptr(inp, "inp", BT, "i32"), _ptr(tgt, "tgt", BT, "i32"), BT))
+
+    def close(self) -> None:
+        if self._h:
+            h, self._h = self._h, None
+            _check(lib.ugk_loader_close(h))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib.ugk_loader_close(self._h)
+
+
+def loader_count(path: str) -> int:
+    """gpt2_kernels.cuh:1318-1331: the token count from the header alone."""
+    n = ctypes.c_long(0)
+    _check(lib.ugk_loader_count(path.encode(), ctypes.byref(n)))
+    return int(n.value)
+
+
+def ckpt_path(arm: str, what: str, cfg: Config, steps: int) -> str:
+    buf = ctypes.create_string_buffer(512)
+    _check(lib.ugk_ckpt_path(buf, 512, arm.encode(), what.encode(), cfg, steps))
+    return buf.value.decode()
+
+
+def ckpt_save(path: str, buf, n: int, cfg: Config, steps: int) -> None:
+    """gpt2_kernels.cuh:944-964: n floats of a device buffer behind the 8-int header."""
+    _check(lib.ugk_ckpt_save(path.encode(), _ptr(buf, "buf", n, "f32"), n, cfg, steps))
+
+
+def ckpt_load(path: str, buf, n: int, cfg: Config) -> int:
+    """gpt2_kernels.cuh:1281-1316: fill a device buffer, checking the header; returns the step count."""
+    steps = ctypes.c_int(0)
+    _check(lib.ugk_ckpt_load(path.encode(), _ptr(buf, "buf", n, "f32"), n, cfg, ctypes.byref(steps)))
+    return int(steps.value)
