@@ -159,7 +159,10 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   float y = ugk_u2f(ugk_f2u(pre) + ((uint32_t)k << 23));
   y = (lo_k || hi_k) ? y : y - 1.0f;
   y = (k == -1) ? 0.5f * (xr - e2) - 0.5f : y;
-  y = (k == 0) ? ((ha < 0x33000000u) ? a : xr - (xr * e - hxs)) : y;
+  // k == 0. fdlibm returns a itself for |a| < 2^-25; the general formula gives
+  // a there too (a*a/2 is below half an ulp of a, and underflows to 0 for
+  // subnormal a), so that case needs no select of its own.
+  y = (k == 0) ? xr - (xr * e - hxs) : y;
   return y;
 }
 
@@ -175,8 +178,10 @@ __device__ __forceinline__ float ugk_dev_tanhf_t(float x) {
   float z = big ? 1.0f - q : q;
   z = (ix >= 0x41b00000u) ? 1.0f : z;  // |x| >= 22 and +-inf
   float r = ugk_u2f(ugk_f2u(z) ^ (jx & 0x80000000u));
-  r = (ix < 0x24000000u) ? x * (1.0f + x) : r;  // |x| < 2^-55, and +-0
-  r = (ix > 0x7f800000u) ? x + x : r;            // nan
+  // fdlibm's |x| < 2^-55 case, x*(1+x) = x, needs no select either: there
+  // expm1f gives t = -2|x| exactly, 2 - 2|x| rounds to 2, and -t/(t+2) = |x|,
+  // so r = x (also for +-0 and subnormals).
+  r = (ix > 0x7f800000u) ? x + x : r;  // nan
   return r;
 }
 
