@@ -118,7 +118,9 @@ __device__ __forceinline__ float ugk_dev_expm1f_t(float x) {
 
 // expm1f(a) for the arguments tanhf passes: a = 2|x| >= 2 (so k >= 3) when
 // big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3). Arguments
-// beyond 44 (|x| >= 22) and non-finite ones give values tanhf discards.
+// beyond 44 (|x| >= 22) and non-finite ones give values tanhf discards, and
+// for a in (38.8, 44) (k > 56) the value differs from expm1f's but is, like
+// it, above 2^56, which is all tanhf needs.
 template <int kDiv>
 __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
@@ -130,7 +132,7 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   const bool red = ha > 0x3eb17218u;   // |a| > ln2/2
   const bool near = ha < 0x3F851592u;  // |a| < 1.5 ln2 (never when big)
   const float kf = fminf(invln2 * a + (big ? 0.5f : -0.5f), 200.0f);
-  const int k = red ? ((near && !big) ? -1 : (int)kf) : 0;
+  const int k = red ? (near ? -1 : (int)kf) : 0;  // near implies !big (big means a >= 2)
   const float t = (float)k;
   const float hi = a - t * ln2_hi;
   const float lo = t * ln2_lo;
@@ -148,8 +150,11 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   //   k <= -2 or k > 56: base 1 (and 1 is subtracted after scaling);
   //   3 <= k < 23:       base 1 - 2^-k;
   //   23 <= k <= 56:     (xr - (e2 + 2^-k)) + 1 instead.
+  // For tanhf, k > 56 (|x| > 19.4) may take the 23 <= k <= 56 formula: both
+  // give t above 2^56, so 1 - 2/(t+2) rounds to 1 either way, and |x| >= 22
+  // (k up to 63 below that) is set to 1 by the caller.
   const bool lo_k = big && k < 23;
-  const bool hi_k = big && k >= 23 && k <= 56;
+  const bool hi_k = big && k >= 23;
   const int ks = lo_k ? k : 31;
   const float base = ugk_u2f(0x3f800000u - (0x1000000u >> ks));  // 1 - 2^-k, or 1 when ks = 31
   float pre = base - d;
