@@ -15,8 +15,9 @@
 //   loss  -log(prob[target]) by the owning thread, from the same register.
 // Rows are V floats long and V is odd for GPT-2, so rows are not 16-byte
 // aligned: loads and stores are dwords, coalesced across the wavefront.
-// A row of up to 51,200 logits (GPT-2's 50257) fits in the registers of a
-// 1024-thread workgroup, one row resident per CU. Longer rows take two passes
+// A row of up to 51,137 logits (GPT-2's 50257) fits in the registers of a
+// 1024-thread workgroup, one row resident per CU; its elements are laid on the
+// threads from a 256-byte boundary of probs so that stores fill whole lines. Longer rows take two passes
 // instead: one wavefront per row streams the logits once for the exact max
 // and the sum (kept per lane in double and rescaled as the max grows), then a
 // flat map over all rows forms expf(x - max) / sum, 12 bytes per logit.
@@ -80,12 +81,16 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
   const size_t row = blockIdx.x;
   const float *lg = logits + row * (size_t)V;
   float *pr = probs + row * (size_t)V;
+  // Slot u of the row holds element v = u - skew, where skew places u = 0 on a
+  // 256-byte boundary of probs: every wavefront then stores whole 256-byte
+  // spans (a misaligned row's stores would write partial cache lines).
+  const int skew = (int)(((uintptr_t)pr >> 2) & 63);
   const int tid = threadIdx.x;
   float x[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
-    const int v = tid + k * kThreads;
-    x[k] = v < V ? ld_nt(lg + v) : kNegInit;
+    const int v = tid + k * kThreads - skew;
+    x[k] = (v >= 0 && v < V) ? ld_nt(lg + v) : kNegInit;
   }
   float m = kNegInit;
 #pragma unroll
@@ -95,16 +100,16 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
   float s = 0.0f;
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
-    const int v = tid + k * kThreads;
+    const int v = tid + k * kThreads - skew;
     x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
-    if (v < V) s += x[k];
+    if (v >= 0 && v < V) s += x[k];
   }
   s = block_sum<kThreads>(s, lds);
   const int tgt = targets[row];
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
-    const int v = tid + k * kThreads;
-    if (v < V) {
+    const int v = tid + k * kThreads - skew;
+    if (v >= 0 && v < V) {
       const float p = x[k] / s;
       st_nt(pr + v, p);
       if (v == tgt) losses[row] = neg_logf(p);
@@ -276,13 +281,15 @@ void launch_rows(float *losses, float *probs, const float *logits, const int *ta
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V) {
   if (rows == 0 || V == 0) return 0;
-  if (V <= 64) launch_rows<64, 1>(losses, probs, logits, targets, rows, V);
-  else if (V <= 256) launch_rows<64, 4>(losses, probs, logits, targets, rows, V);
-  else if (V <= 1024) launch_rows<256, 4>(losses, probs, logits, targets, rows, V);
-  else if (V <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
-  else if (V <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
-  else if (V <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
-  else if (V <= 51200) launch_rows<1024, 50>(losses, probs, logits, targets, rows, V);
+  // a row takes V + 63 slots at most (the alignment skew)
+  const int W = V + 63;
+  if (W <= 64 * 2) launch_rows<64, 2>(losses, probs, logits, targets, rows, V);
+  else if (W <= 256) launch_rows<64, 4>(losses, probs, logits, targets, rows, V);
+  else if (W <= 1024) launch_rows<256, 4>(losses, probs, logits, targets, rows, V);
+  else if (W <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
+  else if (W <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
+  else if (W <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
+  else if (W <= 51200) launch_rows<1024, 50>(losses, probs, logits, targets, rows, V);
   else {
     // Rows too long for the registers of one workgroup: a statistics pass
     // and a flat normalising pass (12 bytes per logit rather than 8).
