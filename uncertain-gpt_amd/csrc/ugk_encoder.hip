@@ -17,14 +17,18 @@
 //     K1 insert  - each workgroup of 256 rows first groups its rows by
 //                  token in an LDS hash table (local count, local rank), then
 //                  one thread per distinct token probes the global open-
-//                  addressing table (2x the chunk, power of two, linear
-//                  probing, atomicCAS) and takes a block of ranks with one
-//                  atomicAdd on the slot count. A frequent token thus costs
-//                  one global atomic per workgroup, not one per row. Every
-//                  row records its slot; ranks below kCap also store the row
-//                  id in the slot's own list. The same launch runs the dwpe
-//                  threads (first chunk).
-//     K2 add     - one wavefront per slot. A bucket of at most kCap rows is
+//                  addressing table (4x the chunk, power of two, linear
+//                  probing). A slot is one 64-bit word, token and row count:
+//                  a token's first workgroup claims a free slot with its
+//                  count in one atomicCAS, later ones take a block of ranks
+//                  with one atomicAdd. A frequent token thus costs one global
+//                  atomic per workgroup, not one per row. Every row records
+//                  its slot; ranks below kCap also store the row id in the
+//                  slot's own list. The slots a workgroup claims are listed
+//                  in its 256-entry region of the slot list. The same launch
+//                  runs the dwpe threads (first chunk).
+//     K2 add     - one wavefront per slot-list entry (as many as rows, not
+//                  as many as table slots). A bucket of at most kCap rows is
 //                  ranked by comparison (row ids are distinct) and its rows
 //                  added in ascending order, 4 channels per lane, 8 loads in
 //                  flight. A larger bucket's wavefront scans the rows' slots
@@ -92,9 +96,16 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_scalar(float *out, const int
 constexpr int kCap = 32;                 // rows kept in a slot's own list
 constexpr int kMaxLarge = kChunk / (kCap + 1) + 1;
 
+typedef unsigned long long u64;
+// A table slot: token in the high word, row count in the low word (a count
+// never exceeds kChunk, so adding to the word never carries into the token).
+constexpr u64 kFree = 0xffffffff00000000ull;  // token kEmpty, count 0
+__device__ __forceinline__ u64 slot_word(int tok, int cnt) { return ((u64)(unsigned)tok << 32) | (unsigned)cnt; }
+__device__ __forceinline__ int slot_tok(u64 s) { return (int)(s >> 32); }
+__device__ __forceinline__ int slot_cnt(u64 s) { return (int)(unsigned)s; }
+
 struct EncTable {  // one half of the double-buffered state
-  int *keys;       // [kTableMax] token per slot, kEmpty when free
-  int *cnt;        // [kTableMax] rows per slot
+  u64 *slot;       // [kTableMax] token and row count per slot, kFree when free
   int *counters;   // [0] K3 work items taken, [1] large buckets, [2] sorted-id pool use
   int *large_j;    // [kTableMax] index of a large slot in the large-bucket list
 };
@@ -104,6 +115,7 @@ struct EncShared {
   int *slot_of;    // [kChunk] slot of each row of the chunk (-1: skipped)
   int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, 0}
   int *pool;       // [kChunk] row ids of the large buckets, each bucket ascending
+  int *list;       // [kChunk] slots claimed by K1 workgroup b at [256 b, 256 b + k), -1 after
 };
 
 __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift) {
@@ -118,10 +130,12 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
   if ((int)blockIdx.x < ins_blocks) {
     constexpr int kL = 2 * kBlock;  // LDS table slots
     __shared__ int ltok[kL], lcnt[kL], lslot[kL], lbase[kL];
+    __shared__ int lnew[kBlock + 1];  // slots this workgroup claimed; [kBlock] their number
     for (int e = threadIdx.x; e < kL; e += kBlock) {
       ltok[e] = kEmpty;
       lcnt[e] = 0;
     }
+    if (threadIdx.x == 0) lnew[kBlock] = 0;
     __syncthreads();
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const int tok = i < n ? inp[i] : -1;
@@ -141,27 +155,32 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
       if (t == kEmpty) continue;
       // At most n distinct tokens occupy 2n or more slots, so a free or
       // matching slot is always found; the probe count is bounded all the same.
+      const int c = lcnt[f];
       unsigned h = hash_slot(t, mask, shift);
-      bool found = false;
+      int base = -1;
       for (unsigned probe = 0; probe <= mask; probe++) {
-        const int prev = atomicCAS(&tb.keys[h], kEmpty, t);
-        if (prev == kEmpty || prev == t) {
-          found = true;
+        const u64 prev = atomicCAS(&tb.slot[h], kFree, slot_word(t, c));
+        if (prev == kFree) {  // claimed: ranks [0, c) are this workgroup's
+          base = 0;
+          lnew[atomicAdd(&lnew[kBlock], 1)] = (int)h;
+          break;
+        }
+        if (slot_tok(prev) == t) {
+          base = slot_cnt(atomicAdd(&tb.slot[h], (u64)c));
           break;
         }
         h = (h + 1) & mask;
       }
-      if (!found) {
+      if (base < 0) {
         lslot[f] = -1;
         continue;
       }
-      const int c = lcnt[f];
-      const int base = atomicAdd(&tb.cnt[h], c);
       if (base <= kCap && kCap < base + c) tb.large_j[h] = atomicAdd(&tb.counters[1], 1);
       lslot[f] = (int)h;
       lbase[f] = base;
     }
     __syncthreads();
+    sh.list[blockIdx.x * kBlock + threadIdx.x] = (int)threadIdx.x < lnew[kBlock] ? lnew[threadIdx.x] : -1;
     if (i >= n) return;
     const int h = e >= 0 ? lslot[e] : -1;
     sh.slot_of[i] = h;
@@ -216,26 +235,28 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// K2: one wavefront per slot. Also clears `old` (the other half of the
-// table) over [0, old_tsize).
+// K2: one wavefront per slot-list entry (the grid covers K1's regions
+// exactly). Also clears `old` (the other half of the table) over
+// [0, old_tsize).
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable old, EncShared sh,
                                                         float *__restrict__ dwte, const float *__restrict__ dout,
-                                                        int tsize, int old_tsize, int C, int n) {
+                                                        int old_tsize, int C, int n) {
   __shared__ unsigned lds[kWavesPerBlock * kCap];
-  for (int h = blockIdx.x * kBlock + threadIdx.x; h < old_tsize; h += gridDim.x * kBlock) {
-    old.keys[h] = kEmpty;
-    old.cnt[h] = 0;
-  }
+  for (int h = blockIdx.x * kBlock + threadIdx.x; h < old_tsize; h += gridDim.x * kBlock) old.slot[h] = kFree;
   if (blockIdx.x == 0 && threadIdx.x < 3) old.counters[threadIdx.x] = 0;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
-  const int w = blockIdx.x * kWavesPerBlock + wave;
   unsigned *mine = lds + (size_t)wave * kCap;
-  if (w >= tsize) return;
-  const int cnt = tb.cnt[w];
-  if (cnt == 0) return;
-  const int tok = tb.keys[w];
+  const int w = sh.list[blockIdx.x * kWavesPerBlock + wave];  // this wavefront's slot
+  if (w < 0) return;
+  // the slot word and the bucket's first row ids in one round trip (ids past
+  // the count are stale and ignored)
+  const u64 sw = tb.slot[w];
+  const int id_raw = sh.rows[(size_t)w * kCap + (lane & (kCap - 1))];
+  asm volatile("" ::"v"(id_raw));  // keeps the compiler from sinking the ids load below the branch
+  const int cnt = slot_cnt(sw);
+  const int tok = slot_tok(sw);
   if (cnt > kCap) {
     // large bucket: the rows whose slot is w, in row order, to the pool for K3
     int base = 0;
@@ -260,7 +281,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
     return;
   }
   // rank the bucket's row ids; ids are distinct, so ranks are a permutation
-  const int id = lane < cnt ? sh.rows[(size_t)w * kCap + lane] : 0x7fffffff;
+  const int id = lane < cnt ? id_raw : 0x7fffffff;
   int rank = 0;
   for (int j = 0; j < cnt; j++) rank += (__shfl(id, j) < id) ? 1 : 0;
   if (lane < cnt) mine[rank] = (unsigned)id;
@@ -375,10 +396,8 @@ __global__ __launch_bounds__(kLargeWaves * kWave) void k_enc_bwd_large(EncTable 
 __global__ void k_enc_init(EncTable a, EncTable b) {
   const int h = blockIdx.x * kBlock + threadIdx.x;
   if (h < kTableMax) {
-    a.keys[h] = kEmpty;
-    a.cnt[h] = 0;
-    b.keys[h] = kEmpty;
-    b.cnt[h] = 0;
+    a.slot[h] = kFree;
+    b.slot[h] = kFree;
   }
   if (h < 3) {
     a.counters[h] = 0;
@@ -386,10 +405,10 @@ __global__ void k_enc_init(EncTable a, EncTable b) {
   }
 }
 
-size_t table_ints() { return (size_t)3 * kTableMax + 64; }
+size_t table_ints() { return (size_t)3 * kTableMax + 64; }  // slot words (2 ints each), large_j, counters
 size_t state_bytes() {
   return (size_t)kTableMax * kCap * sizeof(int) + (size_t)kChunk * sizeof(int) +
-         (size_t)kMaxLarge * sizeof(int4) + (size_t)kChunk * sizeof(int) + 2 * table_ints() * sizeof(int);
+         (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + 2 * table_ints() * sizeof(int);
 }
 
 struct DevState {
@@ -410,10 +429,11 @@ void carve(DevState &ds) {
   p += (size_t)kMaxLarge * sizeof(int4);
   ds.sh.pool = reinterpret_cast<int *>(p);
   p += (size_t)kChunk * sizeof(int);
-  for (int k = 0; k < 2; k++) {
-    int *q = reinterpret_cast<int *>(p);
-    ds.half[k].keys = q; q += kTableMax;
-    ds.half[k].cnt = q; q += kTableMax;
+  ds.sh.list = reinterpret_cast<int *>(p);
+  p += (size_t)kChunk * sizeof(int);
+  for (int k = 0; k < 2; k++) {  // each half starts 8-byte aligned (every size above is)
+    ds.half[k].slot = reinterpret_cast<u64 *>(p);
+    int *q = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
     ds.half[k].large_j = q; q += kTableMax;
     ds.half[k].counters = q;
     p += table_ints() * sizeof(int);
@@ -483,12 +503,13 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
       hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
                          ds.sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     const float *dchunk = dout + (size_t)c0 * C;
-    const dim3 g2(grid_for((size_t)tsize, kWavesPerBlock));
+    // one wavefront per entry of K1's slot-list regions
+    const dim3 g2((unsigned)ins_blocks * (kBlock / kWavesPerBlock));
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk, tsize,
+      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
                          ds.last_tsize[1 - p], C, n);
     else
-      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk, tsize,
+      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
                          ds.last_tsize[1 - p], C, n);
     // one round of workgroups (one per CU: each stages 128 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
