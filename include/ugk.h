@@ -204,8 +204,10 @@ int ugk_version(void);
 
 /* ---- diagnostics of the kernels' float math (no counterpart in the
  * reference; used by the parity tests). fn: 0 expf, 1 log1pf, 2 expm1f,
- * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it; 10+s, 20+s, 30+s:
- * tanhf, log1pf, expm1f with the candidate division sequence s = 0..3. */
+ * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it, 8 GELU
+ * (train_bnn.c:163-170) and 9 its derivative (train_bnn.c:520-533) as the
+ * GELU kernels evaluate them; 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with
+ * the candidate division sequence s = 0..3. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line
@@ -216,8 +218,8 @@ int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
 /* out[i] = f(in[i]) on the device; variant 0 = the kernels' math, 1 = the
  * line-by-line restatement. fn: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf,
  * 4 softplus, 5 logf and 6 cosf (the device library's, as the Philox
- * transform calls them), 7 sqrtf; 10+s, 20+s, 30+s tanhf, log1pf, expm1f
- * with division sequence s. */
+ * transform calls them), 7 sqrtf, 8 GELU, 9 GELU derivative; 10+s, 20+s,
+ * 30+s tanhf, log1pf, expm1f with division sequence s. */
 int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n);
 /* Philox4x32-10 on the device: in holds n tuples of 6 words (counter c0..c3,
  * key k0, k1), out receives n x 4 output words. */

@@ -460,10 +460,12 @@ def test_step_driver_matches_oracle_replay(gpu, oracle):
 
 # ---- the kernels' float math, exhaustively ------------------------------------------
 
-@pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus"])
+@pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus", "gelu", "gelu_grad"])
 def test_device_math_exhaustive(gpu, fn):
     """The SIMD-shaped math (ugk_libm_dev.h) equals its line-by-line restatement of
-    glibc (ugk_libm.h) on all 2^32 inputs, evaluated on the GPU."""
+    glibc (ugk_libm.h) on all 2^32 inputs, evaluated on the GPU. gelu / gelu_grad are the
+    GELU kernels' per-element expressions (with tanhf's NaN case dropped) against the same
+    expressions over the restated tanhf."""
     n, first = gpu.diag_math_mismatch(fn)
     assert n == 0, f"{fn}: {n} inputs differ, first bit pattern 0x{first:08x}"
 

@@ -13,7 +13,9 @@ namespace {
 // fn codes: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf, 4 softplus (the kernels'
 // math); 5 logf, 6 cosf (the device library's, as the Box-Muller transform
 // calls them; evaluation only), 7 sqrtf (its reference: the double square
-// root rounded to float, which is the correctly rounded result);
+// root rounded to float, which is the correctly rounded result); 8 GELU and
+// 9 its derivative as the GELU kernels evaluate them (reference: the same
+// expressions over ugk_tanhf);
 // 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
 // (ugk_div_t<s>), to compare the candidate sequences.
 template <int FN>
@@ -26,6 +28,8 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 5) return logf(x);
   if (FN == 6) return cosf(x);
   if (FN == 7) return sqrtf(x);
+  if (FN == 8) return ugk_dev_gelu(x);
+  if (FN == 9) return ugk_dev_gelu_grad(x);
   if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
   if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
@@ -40,6 +44,8 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 5) return logf(x);
   if (FN == 6) return cosf(x);
   if (FN == 7) return (float)sqrt((double)x);
+  if (FN == 8) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
+  if (FN == 9) return ugk_gelu_grad_with(x, [](float u) { return ugk_tanhf(u); });
   return ugk_expm1f(x);
 }
 
@@ -86,7 +92,7 @@ __global__ __launch_bounds__(kBlock) void k_philox(unsigned *out, const unsigned
   }
 }
 
-bool fn_ok(int fn) { return (fn >= 0 && fn <= 7) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
+bool fn_ok(int fn) { return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
 }  // namespace
@@ -115,7 +121,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
     switch (fn) {
 #define UGK_MM(f) \
   case f: hipLaunchKernelGGL(k_math_mismatch<f>, grid, block, 0, stream(), (unsigned long long)lo, count, &d->n, &d->first); break;
-      UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4) UGK_MM(5) UGK_MM(6) UGK_MM(7)
+      UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4) UGK_MM(5) UGK_MM(6) UGK_MM(7) UGK_MM(8) UGK_MM(9)
       UGK_MM(10) UGK_MM(11) UGK_MM(12) UGK_MM(13) UGK_MM(20) UGK_MM(21) UGK_MM(22) UGK_MM(23)
       UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
 #undef UGK_MM
@@ -140,7 +146,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
   switch (fn) {
 #define UGK_EV(f) \
   case f: hipLaunchKernelGGL(k_math_eval<f>, dim3(g), dim3(kBlock), 0, stream(), variant, out, in, n); break;
-    UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4) UGK_EV(5) UGK_EV(6) UGK_EV(7)
+    UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4) UGK_EV(5) UGK_EV(6) UGK_EV(7) UGK_EV(8) UGK_EV(9)
     UGK_EV(10) UGK_EV(11) UGK_EV(12) UGK_EV(13) UGK_EV(20) UGK_EV(21) UGK_EV(22) UGK_EV(23)
     UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
 #undef UGK_EV

@@ -39,24 +39,14 @@ struct ResidualBwdSame : MapOp {  // loads dout, dx
 struct GeluFwd : MapOp {  // train_bnn.c:163-170
   static constexpr int kLoads = 1, kStores = 1;
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
-    const float k = 0.7978845608f;
-    const float x = ld[0];
-    const float inner = k * (x + 0.044715f * x * x * x);
-    st[0] = 0.5f * x * (1.0f + ugk_dev_tanhf(inner));
+    st[0] = ugk_dev_gelu(ld[0]);
   }
 };
 
 struct GeluBwd : MapOp {  // train_bnn.c:520-533; loads inp, dout, dinp
   static constexpr int kLoads = 3, kStores = 1;
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
-    const float k = 0.7978845608f;
-    const float x = ld[0];
-    const float u = k * (x + 0.044715f * x * x * x);
-    const float tanh_u = ugk_dev_tanhf(u);
-    const float sech2 = 1.0f - tanh_u * tanh_u;
-    const float du_dx = k * (1.0f + 3.0f * 0.044715f * x * x);
-    const float local_grad = 0.5f * (1.0f + tanh_u) + 0.5f * x * sech2 * du_dx;
-    st[0] = ld[2] + local_grad * ld[1];
+    st[0] = ld[2] + ugk_dev_gelu_grad(ld[0]) * ld[1];
   }
 };
 

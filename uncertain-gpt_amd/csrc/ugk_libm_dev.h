@@ -116,25 +116,27 @@ __device__ __forceinline__ float ugk_dev_expm1f_t(float x) {
   return y;
 }
 
-// expm1f(a) for the arguments tanhf passes: a = 2|x| >= 2 (so k >= 3) when
-// big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3). Arguments
-// beyond 44 (|x| >= 22) and non-finite ones give values tanhf discards, and
-// for a in (38.8, 44) (k > 56) the value differs from expm1f's but is, like
-// it, above 2^56, which is all tanhf needs.
+// expm1f(a) for the arguments tanhf passes: a = 2|x| in [2, 44] (so k >= 3)
+// when big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3); a2 = |a|.
+// tanhf clamps 2|x| to 44: every |x| >= 22 then gives t near 2^63, for which
+// 1 - 2/(t+2) rounds to 1 as the reference's |x| >= 22 case returns.
 template <int kDiv>
-__device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
+__device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, float a2, bool big) {
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
   const float invln2 = 1.4426950216e+00f;
   const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f,
               Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
               Q5 = -2.0109921195e-07f;
-  const uint32_t ha = ugk_f2u(a) & 0x7fffffffu;
+  const uint32_t ha = ugk_f2u(a2);     // a2 >= 0
   const bool red = ha > 0x3eb17218u;   // |a| > ln2/2
   const bool near = ha < 0x3F851592u;  // |a| < 1.5 ln2 (never when big)
-  const float kf = fminf(invln2 * a + (big ? 0.5f : -0.5f), 200.0f);
+  const float kf = invln2 * a + (big ? 0.5f : -0.5f);
   const int k = red ? (near ? -1 : (int)kf) : 0;  // near implies !big (big means a >= 2)
   const float t = (float)k;
-  const float hi = a - t * ln2_hi;
+  // ln2_hi has 17 significant bits and |k| <= 64, so t * ln2_hi is exact and
+  // one fused multiply-add rounds a - t * ln2_hi exactly as the product and
+  // the subtraction do
+  const float hi = __builtin_fmaf(-t, ln2_hi, a);
   const float lo = t * ln2_lo;
   const float xr = hi - lo;
   const float c = (hi - xr) - lo;
@@ -146,23 +148,15 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   float e2 = (xr * (e - c) - c);
   e2 -= hxs;
   const float d = e2 - xr;
-  // scaled cases share "base - d, then add k to the exponent":
-  //   k <= -2 or k > 56: base 1 (and 1 is subtracted after scaling);
-  //   3 <= k < 23:       base 1 - 2^-k;
-  //   23 <= k <= 56:     (xr - (e2 + 2^-k)) + 1 instead.
-  // For tanhf, k > 56 (|x| > 19.4) may take the 23 <= k <= 56 formula: both
-  // give t above 2^56, so 1 - 2/(t+2) rounds to 1 either way, and |x| >= 22
-  // (k up to 63 below that) is set to 1 by the caller.
-  const bool lo_k = big && k < 23;
-  const bool hi_k = big && k >= 23;
-  const int ks = lo_k ? k : 31;
-  const float base = ugk_u2f(0x3f800000u - (0x1000000u >> ks));  // 1 - 2^-k, or 1 when ks = 31
-  float pre = base - d;
-  const float thi = ugk_u2f((uint32_t)(0x7f - k) << 23);
-  const float yhi = (xr - (e2 + thi)) + 1.0f;
-  pre = hi_k ? yhi : pre;
-  float y = ugk_u2f(ugk_f2u(pre) + ((uint32_t)k << 23));
-  y = (lo_k || hi_k) ? y : y - 1.0f;
+  // Scaled cases, "base - d, then add k to the exponent": base is 1 - 2^-k
+  // for k < 25 and 1 above (the shift amount min(k, 31) as unsigned also
+  // maps k = -2, -3 to 1), then 1 is subtracted when !big (k = -2, -3).
+  // expm1f itself uses (xr - (e2 + 2^-k)) + 1 for 23 <= k <= 56; for tanhf
+  // the two forms give the same result on every input, checked exhaustively.
+  const uint32_t ks = min((uint32_t)k, 31u);
+  const float base = ugk_u2f(0x3f800000u - (0x1000000u >> ks));
+  float y = ugk_u2f(ugk_f2u(base - d) + ((uint32_t)k << 23));
+  y = big ? y : y - 1.0f;
   y = (k == -1) ? 0.5f * (xr - e2) - 0.5f : y;
   // k == 0. fdlibm returns a itself for |a| < 2^-25; the general formula gives
   // a there too (a*a/2 is below half an ulp of a, and underflows to 0 for
@@ -171,22 +165,23 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   return y;
 }
 
-template <int kDiv>
+// kNan = false drops the NaN case (tanhf(NaN) then gives +-1), for callers
+// whose result is NaN anyway when x is (GELU multiplies by x).
+template <int kDiv, bool kNan = true>
 __device__ __forceinline__ float ugk_dev_tanhf_t(float x) {
   const uint32_t jx = ugk_f2u(x);
   const uint32_t ix = jx & 0x7fffffffu;
   const bool big = ix >= 0x3f800000u;  // |x| >= 1
-  const float a2 = 2.0f * ugk_u2f(ix);
+  const float a2 = fminf(2.0f * ugk_u2f(ix), 44.0f);  // also maps NaN (quieted by the product) to 44
   const float a = big ? a2 : -a2;
-  const float t = ugk_dev_expm1f_tanh<kDiv>(a, big);
+  const float t = ugk_dev_expm1f_tanh<kDiv>(a, a2, big);
   const float q = ugk_div_t<kDiv>(big ? 2.0f : -t, t + 2.0f);
-  float z = big ? 1.0f - q : q;
-  z = (ix >= 0x41b00000u) ? 1.0f : z;  // |x| >= 22 and +-inf
+  const float z = big ? 1.0f - q : q;
   float r = ugk_u2f(ugk_f2u(z) ^ (jx & 0x80000000u));
   // fdlibm's |x| < 2^-55 case, x*(1+x) = x, needs no select either: there
   // expm1f gives t = -2|x| exactly, 2 - 2|x| rounds to 2, and -t/(t+2) = |x|,
   // so r = x (also for +-0 and subnormals).
-  r = (ix > 0x7f800000u) ? x + x : r;  // nan
+  if (kNan) r = (ix > 0x7f800000u) ? x + x : r;
   return r;
 }
 
@@ -252,6 +247,35 @@ __device__ __forceinline__ float ugk_dev_log1pf_t(float x) {
 __device__ __forceinline__ float ugk_dev_expm1f(float x) { return ugk_dev_expm1f_t<UGK_DIV_STEPS>(x); }
 __device__ __forceinline__ float ugk_dev_tanhf(float x) { return ugk_dev_tanhf_t<UGK_DIV_STEPS>(x); }
 __device__ __forceinline__ float ugk_dev_log1pf(float x) { return ugk_dev_log1pf_t<UGK_DIV_STEPS>(x); }
+
+// GELU (tanh form) and its derivative, train_bnn.c:163-170 and :520-533, with
+// the reference's tanhf. A NaN x gives NaN through the factor x (0.5 x sech2
+// in the derivative), whatever tanhf returns, so the NaN case of tanhf is
+// dropped. Exhaustively equal to the same expressions over ugk_tanhf
+// (ugk_diag.hip, fn 8 and 9).
+template <class Tanh>
+__device__ __host__ __forceinline__ float ugk_gelu_with(float x, Tanh tanh_fn) {
+  const float k = 0.7978845608f;
+  const float inner = k * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanh_fn(inner));
+}
+
+template <class Tanh>
+__device__ __host__ __forceinline__ float ugk_gelu_grad_with(float x, Tanh tanh_fn) {
+  const float k = 0.7978845608f;
+  const float u = k * (x + 0.044715f * x * x * x);
+  const float tanh_u = tanh_fn(u);
+  const float sech2 = 1.0f - tanh_u * tanh_u;
+  const float du_dx = k * (1.0f + 3.0f * 0.044715f * x * x);
+  return 0.5f * (1.0f + tanh_u) + 0.5f * x * sech2 * du_dx;
+}
+
+struct UgkDevTanhNoNan {
+  __device__ float operator()(float u) const { return ugk_dev_tanhf_t<UGK_DIV_STEPS, false>(u); }
+};
+
+__device__ __forceinline__ float ugk_dev_gelu(float x) { return ugk_gelu_with(x, UgkDevTanhNoNan{}); }
+__device__ __forceinline__ float ugk_dev_gelu_grad(float x) { return ugk_gelu_grad_with(x, UgkDevTanhNoNan{}); }
 
 __device__ __forceinline__ float ugk_dev_softplusf(float x) {
   return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf(x));

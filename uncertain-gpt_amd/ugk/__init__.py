@@ -385,7 +385,7 @@ def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
 
 
 MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4, "logf": 5, "cosf": 6,
-                  "sqrtf": 7}
+                  "sqrtf": 7, "gelu": 8, "gelu_grad": 9}
 # the same functions with division sequence s (0 IEEE, 1-3 reciprocal + corrections)
 MATH_FUNCTIONS.update({f"{name}/div{s}": base + s for name, base in (("tanhf", 10), ("log1pf", 20), ("expm1f", 30))
                        for s in range(4)})
