@@ -117,21 +117,22 @@ __device__ __forceinline__ float ugk_dev_expm1f_t(float x) {
 }
 
 // expm1f(a) for the arguments tanhf passes: a = 2|x| in [2, 44] (so k >= 3)
-// when big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3); a2 = |a|.
+// when big, a = -2|x| in (-2, 0] otherwise (so k is 0, -1, -2 or -3).
 // tanhf clamps 2|x| to 44: every |x| >= 22 then gives t near 2^63, for which
 // 1 - 2/(t+2) rounds to 1 as the reference's |x| >= 22 case returns.
 template <int kDiv>
-__device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, float a2, bool big) {
+__device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   const float ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
   const float invln2 = 1.4426950216e+00f;
   const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f,
               Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
               Q5 = -2.0109921195e-07f;
-  const uint32_t ha = ugk_f2u(a2);     // a2 >= 0
-  const bool red = ha > 0x3eb17218u;   // |a| > ln2/2
-  const bool near = ha < 0x3F851592u;  // |a| < 1.5 ln2 (never when big)
+  // fdlibm takes k = 0 for |a| <= ln2/2 and k = -1 for |a| < 1.5 ln2 (a < 0
+  // there); the rounding formula it uses beyond gives the same k over those
+  // ranges too, up to the bit patterns at the two thresholds, where the
+  // exhaustive comparison finds the same tanhf either way.
   const float kf = invln2 * a + (big ? 0.5f : -0.5f);
-  const int k = red ? (near ? -1 : (int)kf) : 0;  // near implies !big (big means a >= 2)
+  const int k = (int)kf;
   const float t = (float)k;
   // ln2_hi has 17 significant bits and |k| <= 64, so t * ln2_hi is exact and
   // one fused multiply-add rounds a - t * ln2_hi exactly as the product and
@@ -171,10 +172,10 @@ template <int kDiv, bool kNan = true>
 __device__ __forceinline__ float ugk_dev_tanhf_t(float x) {
   const uint32_t jx = ugk_f2u(x);
   const uint32_t ix = jx & 0x7fffffffu;
-  const bool big = ix >= 0x3f800000u;  // |x| >= 1
   const float a2 = fminf(2.0f * ugk_u2f(ix), 44.0f);  // also maps NaN (quieted by the product) to 44
+  const bool big = a2 >= 2.0f;                        // |x| >= 1
   const float a = big ? a2 : -a2;
-  const float t = ugk_dev_expm1f_tanh<kDiv>(a, a2, big);
+  const float t = ugk_dev_expm1f_tanh<kDiv>(a, big);
   const float q = ugk_div_t<kDiv>(big ? 2.0f : -t, t + 2.0f);
   const float z = big ? 1.0f - q : q;
   float r = ugk_u2f(ugk_f2u(z) ^ (jx & 0x80000000u));
