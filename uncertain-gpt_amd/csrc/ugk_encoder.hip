@@ -22,7 +22,9 @@
 //                  a token's first workgroup claims a free slot with its
 //                  count in one atomicCAS, later ones take a block of ranks
 //                  with one atomicAdd. A frequent token thus costs one global
-//                  atomic per workgroup, not one per row. Every row records
+//                  atomic per workgroup, not one per row. The workgroup's
+//                  distinct tokens are first listed, one per thread, so all
+//                  their probes are in flight together. Every row records
 //                  its slot; ranks below kCap also store the row id in the
 //                  slot's own list. The slots a workgroup claims are listed
 //                  in its 256-entry region of the slot list. The same launch
@@ -131,11 +133,15 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
     constexpr int kL = 2 * kBlock;  // LDS table slots
     __shared__ int ltok[kL], lcnt[kL], lslot[kL], lbase[kL];
     __shared__ int lnew[kBlock + 1];  // slots this workgroup claimed; [kBlock] their number
+    __shared__ int locc[kBlock + 1];  // occupied LDS slots (at most kBlock); [kBlock] their number
     for (int e = threadIdx.x; e < kL; e += kBlock) {
       ltok[e] = kEmpty;
       lcnt[e] = 0;
     }
-    if (threadIdx.x == 0) lnew[kBlock] = 0;
+    if (threadIdx.x == 0) {
+      lnew[kBlock] = 0;
+      locc[kBlock] = 0;
+    }
     __syncthreads();
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const int tok = i < n ? inp[i] : -1;
@@ -150,9 +156,24 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
       lrank = atomicAdd(&lcnt[e], 1);
     }
     __syncthreads();
-    for (int f = threadIdx.x; f < kL; f += kBlock) {
+    // the occupied LDS slots, listed so that one thread each probes the
+    // global table and all probes are in flight at once
+    {
+      const int lane = threadIdx.x & (kWave - 1);
+      const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+      for (int f = threadIdx.x; f < kL; f += kBlock) {
+        const bool occ = ltok[f] != kEmpty;
+        const unsigned long long mk = __ballot(occ);
+        int at = 0;
+        if (lane == 0 && mk) at = atomicAdd(&locc[kBlock], __popcll(mk));
+        at = __shfl(at, 0);
+        if (occ) locc[at + __popcll(mk & below)] = f;
+      }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < locc[kBlock]) {
+      const int f = locc[threadIdx.x];
       const int t = ltok[f];
-      if (t == kEmpty) continue;
       // At most n distinct tokens occupy 2n or more slots, so a free or
       // matching slot is always found; the probe count is bounded all the same.
       const int c = lcnt[f];
@@ -173,11 +194,11 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
       }
       if (base < 0) {
         lslot[f] = -1;
-        continue;
+      } else {
+        if (base <= kCap && kCap < base + c) tb.large_j[h] = atomicAdd(&tb.counters[1], 1);
+        lslot[f] = (int)h;
+        lbase[f] = base;
       }
-      if (base <= kCap && kCap < base + c) tb.large_j[h] = atomicAdd(&tb.counters[1], 1);
-      lslot[f] = (int)h;
-      lbase[f] = base;
     }
     __syncthreads();
     sh.list[blockIdx.x * kBlock + threadIdx.x] = (int)threadIdx.x < lnew[kBlock] ? lnew[threadIdx.x] : -1;
