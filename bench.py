@@ -313,6 +313,8 @@ def main():
                                                 P_(d["rstd"]), B, T, C))),
     }
     def time_cold(make, set_bytes, fn):
+        """Mean time of one call, cycling over enough buffer sets (1.5 GB) that no input is
+        cache resident (MI355X's 256 MB last-level cache would otherwise hold small ones)."""
         sets = sets_for(make, set_bytes)
         for d in sets:
             fn(d)
@@ -346,6 +348,34 @@ def main():
     for name, (make, set_bytes, nbytes, fn) in fused_plan.items():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
         record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 2 * L})
+
+    # ---- the practical HBM ceiling of each kernel's load/store mix: a pure
+    # stream (ugk_diag_stream) with the same number of input and output
+    # tensors of the same size, timed cold the same way
+    pattern = {  # kernel: (tensors read, tensors written, floats per tensor)
+        "encoder_forward": (2, 1, N), "encoder_backward": (3, 2, N),
+        "layernorm_forward": (1, 1, N), "layernorm_backward": (3, 1, N),
+        "gelu_forward": (1, 1, 4 * N), "gelu_backward": (3, 1, 4 * N),
+        "residual_forward": (2, 1, N), "residual_backward": (3, 2, N),
+        "bayes_materialize": (3, 1, n_mat),
+        "residual_layernorm_forward (fused pair)": (2, 2, N),
+        "layernorm_residual_backward (fused pair)": (5, 3, N),
+    }
+    ceil_cache = {}
+    for name, (nr, nw, n) in pattern.items():
+        if (nr, nw, n) not in ceil_cache:
+            best = 0.0
+            for u, bs in ((1, 256), (2, 256), (3, 256), (1, 512), (2, 512)):  # the best of a few shapes
+                ms, _, _ = time_cold(lambda: torch.empty((nr + nw) * n, device=dev), 4 * (nr + nw) * n,
+                                     lambda b: chk(lib.ugk_diag_stream(P_(b), n, nr, nw, u, bs)))
+                best = max(best, 4 * (nr + nw) * n / (ms * 1e-3) / 1e9)
+            ceil_cache[(nr, nw, n)] = best
+        ceil = ceil_cache[(nr, nw, n)]
+        k = kernels[name]
+        k["stream_ceiling_GBps"] = round(ceil, 1)
+        k["frac_of_ceiling"] = round(k["GBps"] / ceil, 4)
+        log(f"bench: ceiling {name:34s} {nr}R{nw}W stream {ceil:8.1f} GB/s ({100 * ceil / PEAK_GBS:4.1f}% of peak);"
+            f" kernel at {100 * k['GBps'] / ceil:5.1f}% of it")
 
     # ---- the same kernels at the other BASELINE configurations' shapes (not part of the step)
     configs = {}

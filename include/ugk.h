@@ -51,7 +51,11 @@ int ugk_encoder_forward(float *out, const int *inp, const float *wte,
  * dwte[inp[b,t],:] += dout[b,t,:];  dwpe[t,:] += dout[b,t,:].
  * Each row's contributions are added in ascending (b,t) order, the order of
  * the CPU loop, so the result is deterministic and bit-identical to it. Rows
- * with a negative token are skipped. */
+ * with a negative token are skipped. Its bucket table (per device) is
+ * double-buffered and the host picks the half each call uses, alternating:
+ * a HIP graph that captures these calls must hold an even number of them
+ * per 65,536-row chunk, all of one shape, and the calls made after capture
+ * must be replays or made before the next capture. */
 int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout,
                          const int *inp, int B, int T, int C);
 
@@ -224,6 +228,14 @@ int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t 
 /* Philox4x32-10 on the device: in holds n tuples of 6 words (counter c0..c3,
  * key k0, k1), out receives n x 4 output words. */
 int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n);
+/* The practical HBM ceiling of a load/store mix: a pure stream over nr input
+ * and nw output tensors of n floats each, consecutive in buf (16-byte
+ * aligned, n a multiple of 4, 1 <= nr <= 5, 1 <= nw <= 3). out_w[i] =
+ * sum_r in_r[i] + w, non-temporal, per_thread (1-3) float4 per thread in
+ * workgroups of block (256 or 512) threads. The benchmark times it at each
+ * kernel's size, takes the best shape, and reports how close the kernel comes
+ * to what its access pattern allows. Asynchronous. */
+int ugk_diag_stream(float *buf, size_t n, int nr, int nw, int per_thread, int block);
 
 /* ---- GPT-2 layer-kernel step driver ------------------------------------
  * gpt2_kernels.cuh:634-719 (Config, param_offsets, act_offsets) and the

@@ -73,6 +73,10 @@ def test_posterior_ops_reject_invalid_arguments_on_host():
     assert lib.ugk_bbb_step_fused(*([None] * 8), 0, 1, 1, *([0.1] * 9)) == 0
     assert lib.ugk_diag_philox(None, None, 3) == 1
     assert lib.ugk_last_error() != b""
+    assert lib.ugk_diag_stream(16, 8, 0, 1, 2, 256) == 1 and b"nr" in lib.ugk_last_error()  # nr out of range
+    assert lib.ugk_diag_stream(16, 8, 2, 4, 2, 256) == 1  # nw out of range
+    assert lib.ugk_diag_stream(16, 6, 2, 1, 2, 256) == 1 and b"multiple of 4" in lib.ugk_last_error()
+    assert lib.ugk_diag_stream(None, 0, 2, 1, 2, 256) == 0
 
 
 def test_fused_pairs_reject_invalid_arguments_on_host():

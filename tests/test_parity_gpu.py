@@ -470,6 +470,22 @@ def test_device_math_exhaustive(gpu, fn):
     assert n == 0, f"{fn}: {n} inputs differ, first bit pattern 0x{first:08x}"
 
 
+@pytest.mark.parametrize("nr,nw,per_thread,block", [(1, 1, 1, 256), (3, 2, 2, 256), (5, 3, 3, 512), (2, 1, 1, 512)])
+def test_diag_stream(gpu, nr, nw, per_thread, block):
+    """The stream-ceiling probe writes out_w = sum of its inputs + w (so its traffic is real)."""
+    n = 4 * 1000 + 8
+    g = gen.rng(nr * 10 + nw)
+    ins = [gen.normal(g, (n,)) for _ in range(nr)]
+    buf = dev(np.concatenate(ins + [np.zeros(n * nw, np.float32)]))
+    gpu.diag_stream(buf, n, nr, nw, per_thread, block)
+    got = host(buf)
+    s = ins[0].copy()
+    for x in ins[1:]:
+        s = s + x
+    for w in range(nw):
+        assert_bits(got[(nr + w) * n:(nr + w + 1) * n], s + np.float32(w), f"stream out {w}")
+
+
 def test_device_math_matches_host_libm(gpu, oracle):
     """Both device variants against the host glibc on every 4093rd bit pattern."""
     x = (np.arange(0, 1 << 32, 4093, dtype=np.uint64).astype(np.uint32)).view(np.float32)

@@ -92,6 +92,46 @@ __global__ __launch_bounds__(kBlock) void k_philox(unsigned *out, const unsigned
   }
 }
 
+// A pure stream with the load/store mix of a kernel: element group i reads
+// float4 i of each of NR input tensors and writes float4 i of NW output
+// tensors (their sum, plus w for output w), non-temporal, U float4 per thread
+// in BS-thread workgroups. Tensors are consecutive in buf, n floats each.
+template <int NR, int NW, int U, int BS>
+__global__ __launch_bounds__(BS) void k_stream(float4 *buf, size_t n4) {
+  const size_t base = (size_t)blockIdx.x * (BS * U) + threadIdx.x;
+  float4 a[U][NR];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const size_t i = base + (size_t)u * BS;
+#pragma unroll
+    for (int r = 0; r < NR; r++) a[u][r] = i < n4 ? ld_nt(buf + (size_t)r * n4 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const size_t i = base + (size_t)u * BS;
+    if (i >= n4) continue;
+    float4 s = a[u][0];
+#pragma unroll
+    for (int r = 1; r < NR; r++) s = make_float4(s.x + a[u][r].x, s.y + a[u][r].y, s.z + a[u][r].z, s.w + a[u][r].w);
+#pragma unroll
+    for (int w = 0; w < NW; w++)
+      st_nt(buf + (size_t)(NR + w) * n4 + i, make_float4(s.x + w, s.y + w, s.z + w, s.w + w));
+  }
+}
+
+template <int NR, int NW>
+int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
+  const int key = per_thread * 10000 + block;
+  switch (key) {
+#define UGK_SH(u, bs) \
+  case u * 10000 + bs: hipLaunchKernelGGL((k_stream<NR, NW, u, bs>), dim3(grid_for(n4, (size_t)u * bs)), dim3(bs), 0, stream(), b, n4); break;
+    UGK_SH(1, 256) UGK_SH(2, 256) UGK_SH(3, 256) UGK_SH(1, 512) UGK_SH(2, 512) UGK_SH(3, 512)
+#undef UGK_SH
+    default: return set_error(UGK_EINVAL, "ugk_diag_stream: per_thread must be 1-3 and block 256 or 512");
+  }
+  return UGK_OK;
+}
+
 bool fn_ok(int fn) { return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
@@ -152,6 +192,23 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");
+}
+
+extern "C" int ugk_diag_stream(float *buf, size_t n, int nr, int nw, int per_thread, int block) {
+  if (nr < 1 || nr > 5 || nw < 1 || nw > 3) return set_error(UGK_EINVAL, "ugk_diag_stream: need 1 <= nr <= 5, 1 <= nw <= 3");
+  if (n == 0) return UGK_OK;
+  if (!buf || (n & 3) || !aligned16(buf)) return set_error(UGK_EINVAL, "ugk_diag_stream: buf must be 16-byte aligned and n a multiple of 4");
+  const size_t n4 = n / 4;
+  float4 *b = reinterpret_cast<float4 *>(buf);
+  int rc = UGK_OK;
+  switch (nr * 10 + nw) {
+#define UGK_ST(r, w) \
+  case r * 10 + w: rc = launch_stream<r, w>(b, n4, per_thread, block); break;
+    UGK_ST(1, 1) UGK_ST(1, 2) UGK_ST(1, 3) UGK_ST(2, 1) UGK_ST(2, 2) UGK_ST(2, 3) UGK_ST(3, 1) UGK_ST(3, 2)
+    UGK_ST(3, 3) UGK_ST(4, 1) UGK_ST(4, 2) UGK_ST(4, 3) UGK_ST(5, 1) UGK_ST(5, 2) UGK_ST(5, 3)
+#undef UGK_ST
+  }
+  return rc != UGK_OK ? rc : check_launch("ugk_diag_stream");
 }
 
 extern "C" int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n) {

@@ -19,11 +19,13 @@ namespace {
 
 struct ResidualFwd : MapOp {  // train_bnn.c:182-186
   static constexpr int kLoads = 2, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) { st[0] = ld[0] + ld[1]; }
 };
 
 struct ResidualBwd : MapOp {  // train_bnn.c:491-496; loads dout, dx, dy
   static constexpr int kLoads = 3, kStores = 2;
+  static constexpr int kUnroll = 1, kThreads = 512;
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
     st[0] = ld[1] + ld[0];
     st[1] = ld[2] + ld[0];
@@ -33,6 +35,7 @@ struct ResidualBwd : MapOp {  // train_bnn.c:491-496; loads dout, dx, dy
 // dx and dy are the same buffer: the CPU loop then adds dout twice, in order.
 struct ResidualBwdSame : MapOp {  // loads dout, dx
   static constexpr int kLoads = 2, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) { st[0] = (ld[1] + ld[0]) + ld[0]; }
 };
 
@@ -45,6 +48,7 @@ struct GeluFwd : MapOp {  // train_bnn.c:163-170
 
 struct GeluBwd : MapOp {  // train_bnn.c:520-533; loads inp, dout, dinp
   static constexpr int kLoads = 3, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
     st[0] = ld[2] + ugk_dev_gelu_grad(ld[0]) * ld[1];
   }

@@ -5,16 +5,17 @@
 // workgroup size, so every load and store instruction of a wavefront covers
 // one contiguous 1 KiB span, all of a thread's loads are issued before its
 // first arithmetic instruction, and every access is non-temporal (each byte
-// is touched once). A launch-shape sweep on MI355X (unroll 1-8, 256-1024
-// threads, flat or grid-stride, with and without nt) put unroll 1-2 of 256
-// threads with nt loads and stores on top for the pure streams.
+// is touched once). Launch-shape sweeps on MI355X over inputs too large for
+// the last-level cache (unroll 1-8, 256-1024 threads, flat or grid-stride,
+// with and without nt) put nt loads and stores with unroll 1-2 and 256-512
+// threads on top; each operator picks its own (the spread is a few percent).
 // Arrays whose pointers are not all 16-byte aligned, and the n % 4 tail, take
 // a scalar grid-stride path with identical arithmetic.
 //
 // An operator is a struct with
 //   kLoads, kStores          stream counts;
 //   kTable                   stage expf's 2^(i/32) table in LDS (tab != null);
-//   kUnroll                  float4 slots per thread;
+//   kUnroll, kThreads        float4 slots per thread, threads per workgroup;
 //   Params                   per-launch scalars passed by value;
 //   apply(ld, st, tab, i, p) the per-element body; i is the element index.
 #pragma once
@@ -29,6 +30,7 @@ struct MapOp {
   struct Params {};
   static constexpr bool kTable = false;
   static constexpr int kUnroll = 2;
+  static constexpr int kThreads = kBlock;
 };
 
 template <class Op>
@@ -39,18 +41,18 @@ struct Streams {
 };
 
 template <class Op>
-__global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
+__global__ __launch_bounds__(Op::kThreads) void k_map_vec4(Streams<Op> s, size_t n4) {
   __shared__ uint64_t tab[Op::kTable ? 32 : 1];
   if (Op::kTable) {
     ugk_exp2_stage(tab);
     __syncthreads();
   }
-  constexpr int kU = Op::kUnroll;
-  const size_t base = (size_t)blockIdx.x * (kBlock * kU) + threadIdx.x;
+  constexpr int kU = Op::kUnroll, kT = Op::kThreads;
+  const size_t base = (size_t)blockIdx.x * (kT * kU) + threadIdx.x;
   float4 v[kU][Op::kLoads];
 #pragma unroll
   for (int u = 0; u < kU; u++) {
-    const size_t i = base + (size_t)u * kBlock;
+    const size_t i = base + (size_t)u * kT;
     if (i < n4) {
 #pragma unroll
       for (int l = 0; l < Op::kLoads; l++) v[u][l] = ld_nt(reinterpret_cast<const float4 *>(s.ld[l]) + i);
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(kBlock) void k_map_vec4(Streams<Op> s, size_t n4) {
   }
 #pragma unroll
   for (int u = 0; u < kU; u++) {
-    const size_t i = base + (size_t)u * kBlock;
+    const size_t i = base + (size_t)u * kT;
     if (i < n4) {
       float in[4][Op::kLoads], out[4][Op::kStores];
 #pragma unroll
@@ -102,8 +104,8 @@ int run_map(const Streams<Op> &s, size_t n, const char *name) {
   size_t done = 0;
   if (vec && n >= 4) {
     const size_t n4 = n / 4;
-    hipLaunchKernelGGL(k_map_vec4<Op>, dim3(grid_for(n4, (size_t)kBlock * Op::kUnroll)),
-                       dim3(kBlock), 0, stream(), s, n4);
+    hipLaunchKernelGGL(k_map_vec4<Op>, dim3(grid_for(n4, (size_t)Op::kThreads * Op::kUnroll)),
+                       dim3(Op::kThreads), 0, stream(), s, n4);
     done = n4 * 4;
   }
   if (done < n) {

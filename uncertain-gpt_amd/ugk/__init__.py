@@ -102,6 +102,7 @@ _SIGS = {
                                ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
     "ugk_diag_philox": [_fp, _fp, _sz],
+    "ugk_diag_stream": [_fp, _sz, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
     "ugk_loader_open": [ctypes.POINTER(_fp), ctypes.c_char_p],
     "ugk_loader_count": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_long)],
     "ugk_loader_next": [_fp, _fp, _fp, _i],
@@ -411,6 +412,14 @@ def diag_philox(out, tuples) -> None:
     ``out`` an int32 tensor of n x 4 output words (bit patterns; read them as uint32)."""
     n = tuples.numel() // 6
     _check(lib.ugk_diag_philox(_ptr(out, "out", 4 * n, "i32"), _ptr(tuples, "tuples", 6 * n, "i32"), n))
+
+
+def diag_stream(buf, n: int, nr: int, nw: int, per_thread: int = 2, block: int = 256) -> None:
+    """A pure stream with nr input and nw output tensors of n floats each, laid out one after
+    another in ``buf`` (a float32 tensor of at least (nr + nw) * n elements): out_w = sum of the
+    inputs + w, ``per_thread`` float4 per thread in ``block``-thread workgroups. Times the HBM
+    ceiling of a kernel's load/store mix."""
+    _check(lib.ugk_diag_stream(_ptr(buf, "buf", (nr + nw) * n, "f32"), n, nr, nw, per_thread, block))
 
 
 # ---- file formats ---------------------------------------------------------------
