@@ -106,6 +106,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_kl_partial", "kl_forward (partial sums)"),
     ("k_kl_final", "kl_forward (final sum)"),
     ("__amd_rocclr_copyBuffer", "calibration copy 1 GiB"),
+    ("k_stream<", "stream ceiling probe"),
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 
