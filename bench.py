@@ -114,7 +114,7 @@ PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 def short_name(name):
     for key, short in KERNEL_KEYS:
         if key in name:
-            if key.startswith("k_ln_") and "<" in name:  # one line per row-width instantiation
+            if (key.startswith("k_ln_") or key == "k_stream<") and "<" in name:  # one line per instantiation
                 short += " " + name[name.index("<"):name.index(">") + 1]
             return short
     return None
