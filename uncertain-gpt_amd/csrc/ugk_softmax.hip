@@ -15,9 +15,12 @@
 //   loss  -log(prob[target]) by the owning thread, from the same register.
 // Rows are V floats long and V is odd for GPT-2, so rows are not 16-byte
 // aligned: loads and stores are dwords, coalesced across the wavefront.
-// A row of up to 51,137 logits (GPT-2's 50257) fits in the registers of a
-// 1024-thread workgroup, one row resident per CU; its elements are laid on the
-// threads from a 256-byte boundary of probs so that stores fill whole lines. Longer rows take two passes
+// A row's elements are laid on the threads from a 256-byte boundary of probs
+// so that stores fill whole lines. Rows of up to 32,705 logits fit in the
+// registers of one workgroup; rows of up to 51,393 (GPT-2's 50257) keep 42
+// slots per thread in registers and 25 in LDS (768 threads), two rows resident
+// per CU so that one row's loads overlap the other's arithmetic and stores
+// (k_softmax_xent_split). Longer rows take two passes
 // instead: one wavefront per row streams the logits once for the exact max
 // and the sum (kept per lane in double and rescaled as the max grows), then a
 // flat map over all rows forms expf(x - max) / sum, 12 bytes per logit.
@@ -111,6 +114,91 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
     const int v = tid + k * kThreads - skew;
     if (v >= 0 && v < V) {
       const float p = x[k] / s;
+      st_nt(pr + v, p);
+      if (v == tgt) losses[row] = neg_logf(p);
+    }
+  }
+}
+
+// The same row computation for rows of up to 51,393 logits, with two rows
+// resident per CU: each thread keeps kReg slots in registers (the bound of 8
+// wavefronts per SIMD caps it at 64 VGPRs, so two 1024-thread workgroups fit a
+// CU) and kLds slots in LDS, which
+// global_load_lds fills straight from memory without passing through
+// registers. Slots are visited in the same order (registers, then LDS), so
+// every value, the sums included, is bit-identical to k_softmax_xent's with
+// the same thread count.
+template <int kThreads, int kReg, int kLds>
+__global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_xent_split(
+    float *__restrict__ losses, float *__restrict__ probs, const float *__restrict__ logits,
+    const int *__restrict__ targets, int V) {
+  __shared__ uint64_t tab[32];
+  __shared__ float lds[kThreads / kWave];
+  __shared__ float part[kLds * kThreads];
+  ugk_exp2_stage(tab);
+  const size_t row = blockIdx.x;
+  const float *lg = logits + row * (size_t)V;
+  float *pr = probs + row * (size_t)V;
+  const int skew = (int)(((uintptr_t)pr >> 2) & 63);  // as in k_softmax_xent
+  const int tid = threadIdx.x, wave = tid / kWave;
+  const int v0 = tid - skew;  // element of slot tid; slot tid + k * kThreads holds v0 + k * kThreads
+  // Slots outside the row hold -inf: the max rule skips it and expf gives +0,
+  // which leaves the sum's bits unchanged, so only the loads and stores test
+  // for the row's bounds (registers stay within the 2-rows-per-CU budget).
+  const float kNegInf = -__builtin_huge_valf();
+#pragma unroll 1
+  for (int k = 0; k < kLds; k++) {
+    const int v = v0 + (kReg + k) * kThreads;
+    if ((unsigned)v < (unsigned)V)  // lane i of the wavefront lands at part[base + i]; nt as the other loads
+      __builtin_amdgcn_global_load_lds(lg + v, part + k * kThreads + wave * kWave, 4, 0, 2);
+    else
+      part[k * kThreads + tid] = kNegInf;
+  }
+  float x[kReg];
+#pragma unroll
+  for (int k = 0; k < kReg; k++) {
+    const int v = v0 + k * kThreads;
+    x[k] = (unsigned)v < (unsigned)V ? ld_nt(lg + v) : kNegInf;
+  }
+  float m = kNegInit;
+#pragma unroll
+  for (int k = 0; k < kReg; k++) m = max_rule(m, x[k]);
+  __syncthreads();  // tab staged, LDS slots filled
+#pragma unroll 1
+  for (int k = 0; k < kLds; k++) m = max_rule(m, part[k * kThreads + tid]);
+  m = block_max<kThreads>(m, lds);
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kReg; k++) {
+    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
+    s += x[k];
+  }
+#pragma unroll 1
+  for (int k = 0; k < kLds; k++) {
+    const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(part[k * kThreads + tid] - m, UgkExp2Lds{tab});
+    part[k * kThreads + tid] = e;
+    s += e;
+  }
+  s = block_sum<kThreads>(s, lds);
+  const int tgt = targets[row];
+  // a fresh copy of v0: the compiler would otherwise keep every slot's index
+  // (and bounds test) alive from the loads to the stores, past the budget
+  int vs = v0;
+  asm volatile("" : "+v"(vs));
+#pragma unroll
+  for (int k = 0; k < kReg; k++) {
+    const int v = vs + k * kThreads;
+    if ((unsigned)v < (unsigned)V) {
+      const float p = x[k] / s;
+      st_nt(pr + v, p);
+      if (v == tgt) losses[row] = neg_logf(p);
+    }
+  }
+#pragma unroll 1
+  for (int k = 0; k < kLds; k++) {
+    const int v = vs + (kReg + k) * kThreads;
+    if ((unsigned)v < (unsigned)V) {
+      const float p = part[k * kThreads + tid] / s;
       st_nt(pr + v, p);
       if (v == tgt) losses[row] = neg_logf(p);
     }
@@ -289,7 +377,9 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
   else if (W <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
-  else if (W <= 51200) launch_rows<1024, 50>(losses, probs, logits, targets, rows, V);
+  else if (W <= 768 * (42 + 25))  // 42 slots per thread in registers, 25 in LDS: two rows per CU
+    hipLaunchKernelGGL((k_softmax_xent_split<768, 42, 25>), dim3(rows), dim3(768), 0, stream(), losses, probs,
+                       logits, targets, V);
   else {
     // Rows too long for the registers of one workgroup: a statistics pass
     // and a flat normalising pass (12 bytes per logit rather than 8).
