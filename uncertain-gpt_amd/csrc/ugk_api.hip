@@ -57,8 +57,9 @@ void *scratch(size_t bytes) {
   Scratch &s = g_scratch[dev];
   if (s.bytes >= bytes && s.ptr) return s.ptr;
   if (s.ptr) {
-    // queued kernels may still read the old buffer
-    (void)hipStreamSynchronize(stream());
+    // kernels queued earlier, on this or another stream, may still use the
+    // old buffer
+    (void)hipDeviceSynchronize();
     (void)hipFree(s.ptr);
     s.ptr = nullptr;
     s.bytes = 0;
