@@ -34,14 +34,14 @@
 //                  ranked by comparison (row ids are distinct) and its rows
 //                  added in ascending order, 4 channels per lane, 8 loads in
 //                  flight. A larger bucket's wavefront scans the rows' slots
-//                  in row order and writes the matching row ids, ascending,
-//                  to a list for K3.
+//                  in row order (four per lane per load, 2048 per round) and
+//                  writes the matching row ids, ascending, to a list for K3.
 //     K3 large   - workgroups of 16 wavefronts, one per (large bucket, 64
-//                  channels): the wavefronts stage 256 rows at a time into LDS
-//                  (256 loads in flight, the next chunk's loads issued before
+//                  channels): the wavefronts stage 512 rows at a time into LDS
+//                  (512 loads in flight, the next chunk's loads issued before
 //                  the current chunk is summed) and one wavefront adds them
 //                  in order, one channel per lane. A frequent token's long
-//                  serial chain thus waits on memory once per 256 rows.
+//                  serial chain thus waits on memory once per 512 rows.
 //   The table is double-buffered by chunk parity: K2 of chunk j clears the
 //   half that chunk j-1 used, so no kernel clears what it also reads.
 //   The arrival order inside a bucket depends on scheduling, but it is
@@ -269,7 +269,12 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   unsigned *mine = lds + (size_t)wave * kCap;
-  const int w = sh.list[blockIdx.x * kWavesPerBlock + wave];  // this wavefront's slot
+  // Wavefront g takes entry g / R of region g % R (R regions of kBlock
+  // entries): the entries of one region (one K1 workgroup's tokens, where a
+  // skewed batch puts its frequent tokens early) spread over all workgroups.
+  const int R = (int)(gridDim.x * kWavesPerBlock / kBlock);
+  const int gw = blockIdx.x * kWavesPerBlock + wave;
+  const int w = sh.list[(gw % R) * kBlock + gw / R];  // this wavefront's slot
   if (w < 0) return;
   // the slot word and the bucket's first row ids in one round trip (ids past
   // the count are stale and ignored)
@@ -279,23 +284,40 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
   const int cnt = slot_cnt(sw);
   const int tok = slot_tok(sw);
   if (cnt > kCap) {
-    // large bucket: the rows whose slot is w, in row order, to the pool for K3
+    // large bucket: the rows whose slot is w, in row order, to the pool for
+    // K3; 2048 slot_of entries per round, four consecutive per lane
     int base = 0;
     if (lane == 0) base = atomicAdd(&tb.counters[2], cnt);
     base = __shfl(base, 0);
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
     int off = 0;
-    constexpr int kScanIn = 16;  // loads in flight per lane
-    for (int i0 = 0; i0 < n; i0 += kScanIn * kWave) {
-      int sl[kScanIn];
+    constexpr int kScanQ = 8;  // int4 loads in flight per lane (more would raise the kernel's VGPR count)
+    for (int i0 = 0; i0 < n; i0 += kScanQ * kWave * 4) {
+      int4 sl[kScanQ];
 #pragma unroll
-      for (int q = 0; q < kScanIn; q++)
-        sl[q] = (i0 + q * kWave + lane < n) ? sh.slot_of[i0 + q * kWave + lane] : -1;
+      for (int q = 0; q < kScanQ; q++) {
+        const int e = i0 + (q * kWave + lane) * 4;
+        if (e + 3 < n) {
+          sl[q] = *reinterpret_cast<const int4 *>(sh.slot_of + e);
+        } else {
+          sl[q].x = e < n ? sh.slot_of[e] : -1;
+          sl[q].y = e + 1 < n ? sh.slot_of[e + 1] : -1;
+          sl[q].z = e + 2 < n ? sh.slot_of[e + 2] : -1;
+          sl[q].w = -1;
+        }
+      }
 #pragma unroll
-      for (int q = 0; q < kScanIn; q++) {
-        const unsigned long long m = __ballot(sl[q] == w);
-        if (sl[q] == w) sh.pool[base + off + __popcll(m & below)] = i0 + q * kWave + lane;
-        off += __popcll(m);
+      for (int q = 0; q < kScanQ; q++) {
+        const int e = i0 + (q * kWave + lane) * 4;
+        const bool f0 = sl[q].x == w, f1 = sl[q].y == w, f2 = sl[q].z == w, f3 = sl[q].w == w;
+        const unsigned long long m0 = __ballot(f0), m1 = __ballot(f1), m2 = __ballot(f2), m3 = __ballot(f3);
+        int o = base + off + __popcll(m0 & below) + __popcll(m1 & below) + __popcll(m2 & below) +
+                __popcll(m3 & below);
+        if (f0) sh.pool[o++] = e;
+        if (f1) sh.pool[o++] = e + 1;
+        if (f2) sh.pool[o++] = e + 2;
+        if (f3) sh.pool[o] = e + 3;
+        off += __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
       }
     }
     if (lane == 0) sh.lmeta[tb.large_j[w]] = make_int4(base, cnt, tok, 0);
