@@ -211,7 +211,10 @@ int ugk_version(void);
  * 3 tanhf, 4 softplus as train_bnn.c:814-816 writes it, 8 GELU
  * (train_bnn.c:163-170) and 9 its derivative (train_bnn.c:520-533) as the
  * GELU kernels evaluate them; 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with
- * the candidate division sequence s = 0..3. */
+ * the candidate division sequence s = 0..3; 40+j: x / b for eight fixed
+ * divisors b (1, 3, 50257, 2 - 2^-23, 65536 - 2^-8, 1 + 2^-23, 12345.678,
+ * 21504) by the softmax's reciprocal-and-correction quotient, against the
+ * IEEE quotient. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

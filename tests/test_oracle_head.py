@@ -114,3 +114,33 @@ def test_math_softmax_special_rows(oracle):
     assert probs[3][V // 2] == 1.0 and (np.delete(probs[3], V // 2) == 0).all() and losses[3] == 0.0
     # every logit below the CPU's -1e30 start: max stays -1e30, exp underflows, 0/0 = nan
     assert np.isnan(probs[4]).all()
+
+
+def test_shared_divisor_quotient_is_correctly_rounded(tmp_path):
+    """The device softmax divides every e of a row by the row's sum s as q = e * y,
+    r = fma(-s, q, e), fma(r, y, q) with y = 1 / s (Markstein's correction). On the CPU, with
+    IEEE fmaf: equal to e / s for every e in [2^-86, 1] (the kernel's domain for this form; e
+    below it takes the division), for divisors with all-ones and near-one significands and
+    random ones in [1, 2^16)."""
+    import shutil
+    import subprocess
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "div_recip_check.c")
+    exe = str(tmp_path / "div_recip_check")
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    for flags in (["-mfma", "-fopenmp"], ["-fopenmp"], []):
+        if subprocess.run([gcc, "-O2", "-ffp-contract=off", *flags, src, "-o", exe, "-lm"],
+                          capture_output=True).returncode == 0:
+            break
+    else:
+        pytest.fail("div_recip_check.c does not build")
+    f2u = lambda f: int(np.float32(f).view(np.uint32))
+    bs = [1.0, 3.0, 50257.0, 21504.0, 12345.678]
+    bs += [float(np.uint32((127 + e) << 23 | m).view(np.float32)) for e in (0, 1, 7, 15)
+           for m in (0x7FFFFF, 0x7FFFFE, 0x000001, 0x400001)]
+    g = np.random.default_rng(1)
+    bs += [float(np.uint32((127 + int(e)) << 23 | int(m)).view(np.float32))
+           for e, m in zip(g.integers(0, 16, 12), g.integers(0, 1 << 23, 12))]
+    out = subprocess.run([exe] + [hex(f2u(b)) for b in bs], capture_output=True, text=True, check=True).stdout
+    assert out.strip().splitlines()[-1] == "0", out

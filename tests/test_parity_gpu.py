@@ -460,12 +460,15 @@ def test_step_driver_matches_oracle_replay(gpu, oracle):
 
 # ---- the kernels' float math, exhaustively ------------------------------------------
 
-@pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus", "gelu", "gelu_grad"])
+@pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus", "gelu", "gelu_grad"] +
+                         [f"div_recip{j}" for j in range(8)])
 def test_device_math_exhaustive(gpu, fn):
     """The SIMD-shaped math (ugk_libm_dev.h) equals its line-by-line restatement of
     glibc (ugk_libm.h) on all 2^32 inputs, evaluated on the GPU. gelu / gelu_grad are the
     GELU kernels' per-element expressions (with tanhf's NaN case dropped) against the same
-    expressions over the restated tanhf."""
+    expressions over the restated tanhf. div_recip<j> is the softmax's quotient by a shared
+    divisor (reciprocal, then one fma correction) against IEEE division, for eight divisors
+    including significands of all ones and 1 + 2^-23."""
     n, first = gpu.diag_math_mismatch(fn)
     assert n == 0, f"{fn}: {n} inputs differ, first bit pattern 0x{first:08x}"
 

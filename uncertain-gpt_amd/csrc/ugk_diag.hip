@@ -17,7 +17,19 @@ namespace {
 // 9 its derivative as the GELU kernels evaluate them (reference: the same
 // expressions over ugk_tanhf);
 // 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
-// (ugk_div_t<s>), to compare the candidate sequences.
+// (ugk_div_t<s>), to compare the candidate sequences; 40+j: x / b for the
+// divisor kDivisors[j] by ugk_div_recip on its domain (IEEE division outside
+// it; reference: x / b).
+__constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
+                                   0x1.5p14f};
+
+__device__ __forceinline__ float div_by(float x, int j) {
+  const float b = kDivisors[j], y = 1.0f / b;
+  const float ax = fabsf(x);
+  const bool dom = ugk_f2u(x) == 0u || x != x || (ax >= 0x1p-86f && ax <= 0x1p100f);
+  return dom ? ugk_div_recip(x, b, y) : x / b;
+}
+
 template <int FN>
 __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 0) return ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
@@ -32,6 +44,7 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 9) return ugk_dev_gelu_grad(x);
   if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
   if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
+  if (FN >= 40 && FN < 48) return div_by(x, FN - 40);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
@@ -46,6 +59,7 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 7) return (float)sqrt((double)x);
   if (FN == 8) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
   if (FN == 9) return ugk_gelu_grad_with(x, [](float u) { return ugk_tanhf(u); });
+  if (FN >= 40 && FN < 48) return x / kDivisors[FN - 40];
   return ugk_expm1f(x);
 }
 
@@ -132,7 +146,10 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
   return UGK_OK;
 }
 
-bool fn_ok(int fn) { return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34); }
+bool fn_ok(int fn) {
+  return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
+         (fn >= 40 && fn < 48);
+}
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
 }  // namespace
@@ -164,6 +181,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(0) UGK_MM(1) UGK_MM(2) UGK_MM(3) UGK_MM(4) UGK_MM(5) UGK_MM(6) UGK_MM(7) UGK_MM(8) UGK_MM(9)
       UGK_MM(10) UGK_MM(11) UGK_MM(12) UGK_MM(13) UGK_MM(20) UGK_MM(21) UGK_MM(22) UGK_MM(23)
       UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
+      UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -189,6 +207,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(0) UGK_EV(1) UGK_EV(2) UGK_EV(3) UGK_EV(4) UGK_EV(5) UGK_EV(6) UGK_EV(7) UGK_EV(8) UGK_EV(9)
     UGK_EV(10) UGK_EV(11) UGK_EV(12) UGK_EV(13) UGK_EV(20) UGK_EV(21) UGK_EV(22) UGK_EV(23)
     UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
+    UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

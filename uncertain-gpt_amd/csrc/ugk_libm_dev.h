@@ -50,6 +50,30 @@ __device__ __forceinline__ float ugk_div_t(float a, float b) {
 #define UGK_DIV_STEPS 1
 #endif
 
+// a / b, correctly rounded, from y = 1.0f / b (itself correctly rounded), for
+// a divisor shared by many quotients: q = a*y is within one ulp of a/b, so the
+// remainder a - b*q is exact in one fma, and q + r*y rounds to the correctly
+// rounded quotient (Markstein, "Computation of elementary functions on the
+// IBM RISC System/6000 processor", IBM J. Res. Develop. 34(1), 1990). Three
+// operations instead of the dozen of a general division. Domain:
+// 1 <= b <= 2^16, and a == +0, NaN, or 2^-86 <= |a| <= 2^100 (-0 would come
+// out +0). There the quotient is at least 2^-102, so the exact remainder is a
+// multiple of 2^-149 and stays representable where it is subnormal, and
+// nothing overflows.
+// Checked against a / b on every a for a set of b (ugk_diag.hip fn 40-47)
+// and on the CPU (tests/div_recip_check.c).
+__device__ __forceinline__ float ugk_div_recip(float a, float b, float y) {
+  const float q = a * y;
+  const float r = __builtin_fmaf(-b, q, a);
+  return __builtin_fmaf(r, y, q);
+}
+
+// The domain test of ugk_div_recip for a in [0, 1] or NaN, folded over many
+// a with a running unsigned minimum: lo = min(lo, ugk_div_recip_key(a)) stays
+// >= kUgkDivRecipKeyMin exactly when every a was +0, NaN or in [2^-86, 1].
+__device__ __forceinline__ uint32_t ugk_div_recip_key(float a) { return ugk_f2u(a) - 1u; }
+constexpr uint32_t kUgkDivRecipKeyMin = 0x14800000u - 1u;  // bits of 2^-86, minus 1
+
 __device__ __forceinline__ float ugk_div(float a, float b) { return ugk_div_t<UGK_DIV_STEPS>(a, b); }
 
 // expm1f for any input, branch-free (used by the exhaustive diagnostic and as

@@ -11,8 +11,11 @@
 //   sum   thread-local in v order, wavefront butterfly, wavefronts in order
 //         (a fixed tree: deterministic, within float rounding of the CPU's
 //         sequential sum);
-//   prob  e / sum with IEEE division, stored non-temporally;
-//   loss  -log(prob[target]) by the owning thread, from the same register.
+//   prob  e / sum correctly rounded, from the reciprocal of the sum and one
+//         fma correction (ugk_div_recip; a wavefront holding an e below
+//         2^-86 divides instead), stored non-temporally;
+//   loss  -log(prob[target]) by the thread holding the target, which
+//         recomputes that probability from the logit.
 // Rows are V floats long and V is odd for GPT-2, so rows are not 16-byte
 // aligned: loads and stores are dwords, coalesced across the wavefront.
 // A row's elements are laid on the threads from a 256-byte boundary of probs
@@ -28,6 +31,8 @@
 // Backward: dlogits[v] += (probs[v] - (v == target)) * (1 / (B*T)), one
 // workgroup per row streaming float4 (dwords for misaligned arrays);
 // bit-identical to the CPU loop.
+#include <type_traits>
+
 #include "ugk_internal.h"
 #include "ugk_libm_dev.h"
 
@@ -74,6 +79,16 @@ __device__ __forceinline__ float block_sum(float v, float *lds) {
 // 99.8% of inputs).
 __device__ __forceinline__ float neg_logf(float p) { return -(float)log((double)p); }
 
+// The loss of a row held in slots (element v in slot v + skew, slot u on
+// thread u % threads): the thread holding the target recomputes its
+// probability from the logit, with the same expf and the correctly rounded
+// quotient the stores hold, and writes -log of it.
+__device__ __forceinline__ void store_loss(float *losses, size_t row, const float *lg, int tgt, int skew, float m,
+                                           float s, const uint64_t *tab, int threads) {
+  if ((int)threadIdx.x == (tgt + skew) % threads)
+    losses[row] = neg_logf(ugk_expf_t<UGK_EXPF_CONTRACT>(lg[tgt] - m, UgkExp2Lds{tab}) / s);
+}
+
 template <int kThreads, int kPer>
 __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ losses, float *__restrict__ probs,
                                                            const float *__restrict__ logits,
@@ -101,23 +116,26 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
   __syncthreads();  // tab staged
   m = block_max<kThreads>(m, lds);
   float s = 0.0f;
+  uint32_t lo = 0xffffffffu;
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const int v = tid + k * kThreads - skew;
     x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
+    lo = min(lo, ugk_div_recip_key(x[k]));
     if (v >= 0 && v < V) s += x[k];
   }
   s = block_sum<kThreads>(s, lds);
-  const int tgt = targets[row];
+  const float y = 1.0f / s;
+  auto store = [&](auto recip) {
 #pragma unroll
-  for (int k = 0; k < kPer; k++) {
-    const int v = tid + k * kThreads - skew;
-    if (v >= 0 && v < V) {
-      const float p = x[k] / s;
-      st_nt(pr + v, p);
-      if (v == tgt) losses[row] = neg_logf(p);
+    for (int k = 0; k < kPer; k++) {
+      const int v = tid + k * kThreads - skew;
+      if (v >= 0 && v < V) st_nt(pr + v, decltype(recip)::value ? ugk_div_recip(x[k], s, y) : x[k] / s);
     }
-  }
+  };
+  if (__all(lo >= kUgkDivRecipKeyMin)) store(std::true_type{});
+  else store(std::false_type{});
+  store_loss(losses, row, lg, targets[row], skew, m, s, tab, kThreads);
 }
 
 // The same row computation for rows of up to 51,393 logits, with two rows
@@ -154,11 +172,13 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
     else
       part[k * kThreads + tid] = kNegInf;
   }
+  // Rows are longer than the register slots (V >= kReg * kThreads, checked at
+  // launch), so only slot 0 can fall outside the row, below its start.
   float x[kReg];
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
     const int v = v0 + k * kThreads;
-    x[k] = (unsigned)v < (unsigned)V ? ld_nt(lg + v) : kNegInf;
+    x[k] = (k > 0 || v >= 0) ? ld_nt(lg + v) : kNegInf;
   }
   float m = kNegInit;
 #pragma unroll
@@ -168,41 +188,42 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
   for (int k = 0; k < kLds; k++) m = max_rule(m, part[k * kThreads + tid]);
   m = block_max<kThreads>(m, lds);
   float s = 0.0f;
+  uint32_t lo = 0xffffffffu;
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
     x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
     s += x[k];
+    lo = min(lo, ugk_div_recip_key(x[k]));
   }
 #pragma unroll 1
   for (int k = 0; k < kLds; k++) {
     const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(part[k * kThreads + tid] - m, UgkExp2Lds{tab});
     part[k * kThreads + tid] = e;
     s += e;
+    lo = min(lo, ugk_div_recip_key(e));
   }
   s = block_sum<kThreads>(s, lds);
-  const int tgt = targets[row];
+  const float y = 1.0f / s;
   // a fresh copy of v0: the compiler would otherwise keep every slot's index
   // (and bounds test) alive from the loads to the stores, past the budget
   int vs = v0;
   asm volatile("" : "+v"(vs));
+  auto store = [&](auto recip) {
+    auto div = [&](float e) { return decltype(recip)::value ? ugk_div_recip(e, s, y) : e / s; };
 #pragma unroll
-  for (int k = 0; k < kReg; k++) {
-    const int v = vs + k * kThreads;
-    if ((unsigned)v < (unsigned)V) {
-      const float p = x[k] / s;
-      st_nt(pr + v, p);
-      if (v == tgt) losses[row] = neg_logf(p);
+    for (int k = 0; k < kReg; k++) {
+      const int v = vs + k * kThreads;
+      if (k > 0 || v >= 0) st_nt(pr + v, div(x[k]));
     }
-  }
 #pragma unroll 1
-  for (int k = 0; k < kLds; k++) {
-    const int v = vs + (kReg + k) * kThreads;
-    if ((unsigned)v < (unsigned)V) {
-      const float p = part[k * kThreads + tid] / s;
-      st_nt(pr + v, p);
-      if (v == tgt) losses[row] = neg_logf(p);
+    for (int k = 0; k < kLds; k++) {
+      const int v = vs + (kReg + k) * kThreads;
+      if ((unsigned)v < (unsigned)V) st_nt(pr + v, div(part[k * kThreads + tid]));
     }
-  }
+  };
+  if (__all(lo >= kUgkDivRecipKeyMin)) store(std::true_type{});
+  else store(std::false_type{});
+  store_loss(losses, row, lg, targets[row], skew, m, s, tab, kThreads);
 }
 
 // Row of flat element i (rows of V elements): a double-precision quotient,
@@ -377,10 +398,11 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
   else if (W <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
-  else if (W <= 768 * (42 + 25))  // 42 slots per thread in registers, 25 in LDS: two rows per CU
+  else if (W <= 768 * (42 + 25)) {  // 42 slots per thread in registers, 25 in LDS: two rows per CU
+    static_assert(32768 - 63 >= 768 * 42, "the split kernel's register slots must lie inside every row it takes");
     hipLaunchKernelGGL((k_softmax_xent_split<768, 42, 25>), dim3(rows), dim3(768), 0, stream(), losses, probs,
                        logits, targets, V);
-  else {
+  } else {
     // Rows too long for the registers of one workgroup: a statistics pass
     // and a flat normalising pass (12 bytes per logit rather than 8).
     float2 *stats = static_cast<float2 *>(scratch((size_t)rows * sizeof(float2)));

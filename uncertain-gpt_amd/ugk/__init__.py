@@ -390,6 +390,8 @@ MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4
 # the same functions with division sequence s (0 IEEE, 1-3 reciprocal + corrections)
 MATH_FUNCTIONS.update({f"{name}/div{s}": base + s for name, base in (("tanhf", 10), ("log1pf", 20), ("expm1f", 30))
                        for s in range(4)})
+# x / b for the eight divisors of the softmax quotient check
+MATH_FUNCTIONS.update({f"div_recip{j}": 40 + j for j in range(8)})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
