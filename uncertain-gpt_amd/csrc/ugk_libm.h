@@ -46,6 +46,15 @@ UGK_HD uint32_t ugk_f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 UGK_HD float ugk_u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 UGK_HD uint64_t ugk_d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
 UGK_HD double ugk_u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+// The double with high word hi and low word lo (on the GPU, a register pair
+// filled without 64-bit integer arithmetic).
+UGK_HD double ugk_hilo2d(uint32_t hi, uint32_t lo) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __hiloint2double((int)hi, (int)lo);
+#else
+  return ugk_u2d(((uint64_t)hi << 32) | lo);
+#endif
+}
 
 // 2^(i/32) correctly rounded to binary64, minus (i << 47): adding (k << 47) to
 // entry k%32 gives the bit pattern of 2^(k/32) for any integer k in range.
@@ -78,12 +87,21 @@ struct UgkExp2Table {
 //   0: every product and sum rounded separately (no FMA);
 //   1: the three polynomial multiply-adds fused;
 //   2: as 1, and also the two uses of InvLn2N*x in the reduction fused.
+// The two constants that enter expf only as addends. Callers may pass copies
+// held in registers (GPU code, where an instruction takes one scalar operand
+// and a constant addend would otherwise be copied into a vector register
+// before every call); the values are always these.
+struct UgkExpfAddends {
+  double shift = 0x1.8p+52;
+  double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+};
+
 template <int kContract, class Tab>
-UGK_HD float ugk_expf_t(float x, Tab tab) {
+UGK_HD float ugk_expf_t(float x, Tab tab, UgkExpfAddends add = UgkExpfAddends{}) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
-  const double kShift = 0x1.8p+52;
+  const double kShift = add.shift;
   const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
-  const double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double kC1 = add.c1;
   const double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
   const uint32_t ux = ugk_f2u(x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -107,7 +125,10 @@ UGK_HD float ugk_expf_t(float x, Tab tab) {
   } else {
     r = kInvLn2N * xd - kd;
   }
-  const double s = ugk_u2d(tab((uint32_t)(ki % 32)) + (ki << 47));
+  // 2^(k/32) = table entry k % 32 plus (k << 47) as a 64-bit integer; the
+  // addend's low word is zero, so only the high words are added.
+  const uint64_t tb = tab((uint32_t)(ki % 32));
+  const double s = ugk_hilo2d((uint32_t)(tb >> 32) + ((uint32_t)ki << 15), (uint32_t)tb);
   double z, y;
   const double r2 = r * r;
   if (kContract >= 1) {

@@ -313,6 +313,15 @@ struct UgkExp2Lds {
   __device__ uint64_t operator()(uint32_t i) const { return p[i]; }
 };
 
+// expf's addend constants in vector registers, for a loop of expf calls: the
+// empty asm statement hides their values, so the compiler keeps the one copy
+// rather than rebuilding both for every call.
+__device__ __forceinline__ UgkExpfAddends ugk_expf_addends_vgpr() {
+  UgkExpfAddends a;
+  asm volatile("" : "+v"(a.shift), "+v"(a.c1));
+  return a;
+}
+
 // Fill a 32-entry LDS table; the caller synchronises the workgroup after.
 __device__ __forceinline__ void ugk_exp2_stage(uint64_t *lds_tab) {
   if (threadIdx.x < 32) lds_tab[threadIdx.x] = ugk_exp2_bits(threadIdx.x);

@@ -117,10 +117,11 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
   m = block_max<kThreads>(m, lds);
   float s = 0.0f;
   uint32_t lo = 0xffffffffu;
+  const UgkExpfAddends add = ugk_expf_addends_vgpr();
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const int v = tid + k * kThreads - skew;
-    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
+    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab}, add);
     lo = min(lo, ugk_div_recip_key(x[k]));
     if (v >= 0 && v < V) s += x[k];
   }
@@ -150,9 +151,15 @@ template <int kThreads, int kReg, int kLds>
 __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_xent_split(
     float *__restrict__ losses, float *__restrict__ probs, const float *__restrict__ logits,
     const int *__restrict__ targets, int V) {
-  __shared__ uint64_t tab[32];
-  __shared__ float lds[kThreads / kWave];
-  __shared__ float part[kLds * kThreads];
+  // one LDS block with the expf table first, so that its address fits the
+  // offset field of the table reads
+  __shared__ struct {
+    uint64_t tab[32];
+    float lds[kThreads / kWave];
+    float part[kLds * kThreads];
+  } sh;
+  uint64_t *tab = sh.tab;
+  float *lds = sh.lds, *part = sh.part;
   ugk_exp2_stage(tab);
   const size_t row = blockIdx.x;
   const float *lg = logits + row * (size_t)V;
@@ -189,15 +196,16 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
   m = block_max<kThreads>(m, lds);
   float s = 0.0f;
   uint32_t lo = 0xffffffffu;
+  const UgkExpfAddends add = ugk_expf_addends_vgpr();
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
-    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab});
+    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab}, add);
     s += x[k];
     lo = min(lo, ugk_div_recip_key(x[k]));
   }
 #pragma unroll 1
   for (int k = 0; k < kLds; k++) {
-    const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(part[k * kThreads + tid] - m, UgkExp2Lds{tab});
+    const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(part[k * kThreads + tid] - m, UgkExp2Lds{tab}, add);
     part[k * kThreads + tid] = e;
     s += e;
     lo = min(lo, ugk_div_recip_key(e));
