@@ -214,7 +214,10 @@ int ugk_version(void);
  * the candidate division sequence s = 0..3; 40+j: x / b for eight fixed
  * divisors b (1, 3, 50257, 2 - 2^-23, 65536 - 2^-8, 1 + 2^-23, 12345.678,
  * 21504) by the softmax's reciprocal-and-correction quotient, against the
- * IEEE quotient. */
+ * IEEE quotient; 48 the square root of the Box-Muller transform (inputs
+ * >= 2^-96) against the correctly rounded one; 49+s: 1 / x for x >= 1 by the
+ * division sequence s = 0..3 against the IEEE quotient; 53 the sigmoid's
+ * 1 / x for x >= 1 against the IEEE quotient. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

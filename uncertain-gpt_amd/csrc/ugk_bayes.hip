@@ -20,7 +20,7 @@ __device__ __forceinline__ float expf_lds(float x, const uint64_t *tab) {
 
 // train_bnn.c:820-822 (sigmoidf_), gpt2_kernels.cuh:199-201 (d_sigmoid).
 __device__ __forceinline__ float sigmoid_lds(float x, const uint64_t *tab) {
-  return 1.0f / (1.0f + expf_lds(-x, tab));
+  return ugk_dev_recip_ge1(1.0f + expf_lds(-x, tab));
 }
 
 struct PhiloxParams {

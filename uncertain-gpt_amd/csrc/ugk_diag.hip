@@ -19,7 +19,11 @@ namespace {
 // 10+s, 20+s, 30+s: tanhf, log1pf, expm1f with division sequence s
 // (ugk_div_t<s>), to compare the candidate sequences; 40+j: x / b for the
 // divisor kDivisors[j] by ugk_div_recip on its domain (IEEE division outside
-// it; reference: x / b).
+// it; reference: x / b); 48: ugk_dev_sqrtf_large on its domain (sqrtf
+// outside; reference as fn 7); 49+s: 1 / x by ugk_div_t<s> for x >= 1, +inf
+// and NaN (1.0f / x elsewhere; reference 1.0f / x), the candidate sequences
+// for the sigmoid's quotient; 53: ugk_dev_recip_ge1, the one it uses, on the
+// same domain.
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -45,6 +49,9 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN >= 10 && FN < 14) return ugk_dev_tanhf_t<FN - 10>(x);
   if (FN >= 20 && FN < 24) return ugk_dev_log1pf_t<FN - 20>(x);
   if (FN >= 40 && FN < 48) return div_by(x, FN - 40);
+  if (FN == 48) return (fabsf(x) >= 0x1p-96f || x == 0.0f || x != x) ? ugk_dev_sqrtf_large(x) : sqrtf(x);
+  if (FN >= 49 && FN < 53) return (x >= 1.0f || x != x) ? ugk_div_t<FN - 49>(1.0f, x) : 1.0f / x;
+  if (FN == 53) return (x >= 1.0f || x != x) ? ugk_dev_recip_ge1(x) : 1.0f / x;
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
@@ -60,6 +67,8 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 8) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
   if (FN == 9) return ugk_gelu_grad_with(x, [](float u) { return ugk_tanhf(u); });
   if (FN >= 40 && FN < 48) return x / kDivisors[FN - 40];
+  if (FN == 48) return (float)sqrt((double)x);
+  if (FN >= 49 && FN < 54) return 1.0f / x;
   return ugk_expm1f(x);
 }
 
@@ -148,7 +157,7 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 48);
+         (fn >= 40 && fn < 54);
 }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
@@ -182,6 +191,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(10) UGK_MM(11) UGK_MM(12) UGK_MM(13) UGK_MM(20) UGK_MM(21) UGK_MM(22) UGK_MM(23)
       UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
+      UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -208,6 +218,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(10) UGK_EV(11) UGK_EV(12) UGK_EV(13) UGK_EV(20) UGK_EV(21) UGK_EV(22) UGK_EV(23)
     UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
+    UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

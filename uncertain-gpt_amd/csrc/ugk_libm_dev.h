@@ -76,6 +76,31 @@ constexpr uint32_t kUgkDivRecipKeyMin = 0x14800000u - 1u;  // bits of 2^-86, min
 
 __device__ __forceinline__ float ugk_div(float a, float b) { return ugk_div_t<UGK_DIV_STEPS>(a, b); }
 
+// 1 / b for b >= 1 or NaN, correctly rounded (the sigmoid's quotient): the
+// reciprocal seed with one correction (ugk_div_t<1>) is the IEEE quotient for
+// every b in [1, 2^126] (ugk_diag.hip fn 50 finds it wrong only above, where
+// the quotient is subnormal or 0), and the rare larger b divide.
+__device__ __forceinline__ float ugk_dev_recip_ge1(float b) {
+  float q = ugk_div_t<1>(1.0f, b);
+  if (__builtin_expect(b > 0x1p126f, 0)) q = 1.0f / b;
+  return q;
+}
+
+// sqrtf, correctly rounded, for x >= 2^-96 and for +-0, +inf and NaN: the
+// hardware square root s is within one ulp, and its neighbour below (above)
+// replaces it when the remainder x - neighbour * s shows that neighbour to be
+// the nearer one. This is the device library's sequence without the rescaling
+// it applies first to inputs below 2^-96 and its +-0/inf/NaN selects, which the
+// sequence already gets right. Checked on every input of the domain
+// (ugk_diag.hip fn 48).
+__device__ __forceinline__ float ugk_dev_sqrtf_large(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float dn = ugk_u2f(ugk_f2u(s) - 1u), up = ugk_u2f(ugk_f2u(s) + 1u);
+  float t = __builtin_fmaf(-dn, s, x) <= 0.0f ? dn : s;
+  t = __builtin_fmaf(-up, s, x) > 0.0f ? up : t;
+  return t;
+}
+
 // expm1f for any input, branch-free (used by the exhaustive diagnostic and as
 // the general form of the specialised copy inside tanhf).
 template <int kDiv>

@@ -12,13 +12,15 @@
 // The integer part is exact on host and device. The float part uses the
 // device logf and cosf (AMD's device library), which round differently from
 // the host glibc in the last place on a small share of inputs, and a
-// correctly rounded sqrtf.
+// correctly rounded square root.
 #pragma once
 
 #include <stdint.h>
 
 #ifdef __HIPCC__
 #include <hip/hip_runtime.h>
+
+#include "ugk_libm_dev.h"
 #define UGK_PHILOX_HD __host__ __device__ __forceinline__
 #else
 #define UGK_PHILOX_HD static inline
@@ -58,10 +60,12 @@ UGK_PHILOX_HD UgkPhilox4 ugk_philox_words(unsigned long long seed, int step, uin
 
 #ifdef __HIPCC__
 // Box-Muller, cosine branch: sqrt(-2 ln u1) * cos(2 pi u2), with 2 pi rounded
-// to float and the product rounded before the cosine.
+// to float and the product rounded before the cosine. u1 in [2^-33, 1] puts
+// -2 ln u1 at -0 or in [1.1e-7, 46]: inside the domain of the correctly
+// rounded square root without rescaling.
 __device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
   const float u1 = ugk_u01(a), u2 = ugk_u01(b);
-  return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+  return ugk_dev_sqrtf_large(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
 }
 
 __device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {

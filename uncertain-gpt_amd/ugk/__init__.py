@@ -392,6 +392,10 @@ MATH_FUNCTIONS.update({f"{name}/div{s}": base + s for name, base in (("tanhf", 1
                        for s in range(4)})
 # x / b for the eight divisors of the softmax quotient check
 MATH_FUNCTIONS.update({f"div_recip{j}": 40 + j for j in range(8)})
+# sqrtf for inputs >= 2^-96 (the Box-Muller transform's); 1 / x for x >= 1 (the sigmoid's)
+MATH_FUNCTIONS.update({"sqrtf_large": 48})
+MATH_FUNCTIONS.update({f"recip/div{s}": 49 + s for s in range(4)})
+MATH_FUNCTIONS.update({"recip_ge1": 53})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
