@@ -59,6 +59,37 @@ UGK_PHILOX_HD UgkPhilox4 ugk_philox_words(unsigned long long seed, int step, uin
 }
 
 #ifdef __HIPCC__
+// a ^ b ^ k in one v_bitop3_b32 (truth table 0x96), k in a scalar register.
+// Only for a k that is the same in every lane of the wavefront.
+__device__ __forceinline__ uint32_t ugk_xor3_uniform(uint32_t a, uint32_t b, uint32_t k) {
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+}
+
+// ugk_philox_words for a (seed, step) shared by the whole wavefront (the
+// kernels draw eps(seed, step, i) for their own i): the same rounds, with each
+// round's two three-way xors as one instruction each, the round key scalar.
+__device__ __forceinline__ UgkPhilox4 ugk_dev_philox_words_uniform(unsigned long long seed, int step,
+                                                                  uint64_t index) {
+  uint32_t c0 = (uint32_t)index, c1 = (uint32_t)(index >> 32), c2 = (uint32_t)step, c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = ugk_xor3_uniform((uint32_t)(p1 >> 32), c1, k0);
+    const uint32_t n2 = ugk_xor3_uniform((uint32_t)(p0 >> 32), c3, k1);
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return UgkPhilox4{{c0, c1, c2, c3}};
+}
+
 // Box-Muller, cosine branch: sqrt(-2 ln u1) * cos(2 pi u2), with 2 pi rounded
 // to float and the product rounded before the cosine. u1 in [2^-33, 1] puts
 // -2 ln u1 at -0 or in [1.1e-7, 46]: inside the domain of the correctly
@@ -68,8 +99,9 @@ __device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
   return ugk_dev_sqrtf_large(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
 }
 
+// eps(seed, step, index); seed and step must be the same across the wavefront.
 __device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {
-  const UgkPhilox4 o = ugk_philox_words(seed, step, index);
+  const UgkPhilox4 o = ugk_dev_philox_words_uniform(seed, step, index);
   return ugk_dev_box_muller(o.w[0], o.w[1]);
 }
 #endif
