@@ -186,6 +186,25 @@ def test_kl_forward(gpu, oracle, n):
     assert gpu.kl_forward(tm, tr, 0, 0.1) == 0.0
 
 
+def test_kl_forward_terms(gpu, oracle):
+    """Single KL terms across the range of sigma = softplus(rho): subnormal and zero sigma
+    (rho below -87 and -103), the x > 20 shortcut, every cell of the logarithm's table
+    (sigma with all 128 leading fraction patterns), against the oracle's double terms."""
+    rho = [-200.0, -104.0, -100.0, -90.0, -88.0, -50.0, -5.0, -1.0, 0.0, 0.5, 5.0, 20.0, 20.5, 100.0, 1e30]
+    g = gen.rng(77)
+    rho += list(np.log(np.expm1(np.float64(1.0) + (np.arange(128) + g.random(128)) / 128.0)).astype(np.float32))
+    rho += list(gen.normal(g, (64,), -5.0, 3.0))
+    mu = gen.normal(g, (len(rho),), 0, 0.05)
+    rho = np.array(rho, np.float32)
+    for k in range(len(rho)):
+        want = oracle.kl_forward(mu[k:k + 1], rho[k:k + 1], 1, 0.1)
+        got = gpu.kl_forward(dev(mu[k:k + 1]), dev(rho[k:k + 1]), 1, 0.1)
+        if np.isinf(want):
+            assert got == want, (k, rho[k], got, want)
+        else:
+            assert abs(got - want) <= 1e-14 * max(1.0, abs(want)), (k, rho[k], got, want)
+
+
 @pytest.mark.parametrize("n", SIZES)
 @pytest.mark.parametrize("offset", [0, 1])
 def test_bayes_sample_and_backward_philox(gpu, oracle, n, offset):

@@ -161,16 +161,60 @@ struct BbbStepFused : MapOp {
 };
 
 // ---- KL total (train_bnn.c:941-957) -----------------------------------------
-// Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2.
-// Summed in a fixed order: every thread over a fixed stride of float4 slots,
-// then a wavefront butterfly, then the block's waves in order, then one block
-// over the per-block partials. Deterministic for a given n.
+// Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2,
+// evaluated as (log sp - log sigma) + (sigma^2 + mu^2) * (1 / (2 sp^2)) - 1/2
+// with the logarithm below: the same value to within a few units of 2^-53
+// relative per term. Summed in a fixed order: every thread over a fixed
+// stride of float4 slots, then a wavefront butterfly, then the block's waves
+// in order, then one block over the per-block partials. Deterministic for a
+// given n.
 constexpr int kKlBlocks = 2048;
+constexpr int kKlLogCells = 128;
 
-__device__ __forceinline__ double kl_term(float mu, float rho, double sp, double two_sp2, const uint64_t *tab) {
-  const double sigma = (double)ugk_dev_softplusf_lds(rho, tab);
-  const double m = (double)mu;
-  return log(sp / sigma) + (sigma * sigma + m * m) / two_sp2 - 0.5;
+// log of a float argument, in double. x = 2^e m with m in [1, 2); c is the
+// centre of m's cell (the top seven fraction bits i: c = 1 + (i + 1/2)/128),
+// and log x = e ln2 + log c + log1p(r), r = (m - c)/c in [-2^-8, 2^-8], with
+// log1p by its series to r^6 (the remainder is below 2^-56 |r|). m - c is
+// formed exactly from the bits below the cell's; r carries the rounding of
+// 1/c. Per-cell log c and 1/c come from the device library, once per
+// workgroup. 0 gives -inf, +inf and NaN themselves.
+struct KlLogTable {
+  double logc[kKlLogCells];
+  double invc[kKlLogCells];
+};
+
+__device__ __forceinline__ void kl_log_stage(KlLogTable *t) {
+  for (int i = threadIdx.x; i < kKlLogCells; i += blockDim.x) {
+    const double c = 1.0 + (i + 0.5) / kKlLogCells;
+    t->logc[i] = log(c);
+    t->invc[i] = 1.0 / c;
+  }
+}
+
+__device__ __forceinline__ double kl_log(float x, const KlLogTable *t) {
+  const uint64_t u = ugk_d2u((double)x);
+  const uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
+  const int e = (int)(hi >> 20) - 1023;
+  const uint32_t i = (hi >> 13) & (kKlLogCells - 1);
+  // 1 + (the fraction bits below the cell's), minus the cell's half-width
+  const double d = ugk_hilo2d((hi & 0x1fffu) | 0x3ff00000u, lo) - (1.0 + 0.5 / kKlLogCells);
+  const double r = d * t->invc[i];
+  double p = -1.0 / 6;
+  p = __builtin_fma(p, r, 1.0 / 5);
+  p = __builtin_fma(p, r, -1.0 / 4);
+  p = __builtin_fma(p, r, 1.0 / 3);
+  p = __builtin_fma(p, r, -1.0 / 2);
+  p = p * r;
+  const double res = __builtin_fma((double)e, 0.69314718055994530942, t->logc[i] + __builtin_fma(p, r, r));
+  const bool finite_pos = x > 0.0f && x < __builtin_huge_valf();
+  return finite_pos ? res : (x == 0.0f ? -__builtin_huge_val() : (double)x);
+}
+
+__device__ __forceinline__ double kl_term(float mu, float rho, double log_sp, double inv_two_sp2,
+                                          const uint64_t *tab, const KlLogTable *lt) {
+  const float sigma_f = ugk_dev_softplusf_lds(rho, tab);
+  const double sigma = (double)sigma_f, m = (double)mu;
+  return (log_sp - kl_log(sigma_f, lt)) + (sigma * sigma + m * m) * inv_two_sp2 - 0.5;
 }
 
 __device__ __forceinline__ double wave_sum_d(double v) {
@@ -194,9 +238,11 @@ __global__ __launch_bounds__(kBlock) void k_kl_partial(double *part, const float
                                                        size_t n, float sigma_prior, float sp2) {
   __shared__ uint64_t tab[32];
   __shared__ double lds[kBlock / kWave];
+  __shared__ KlLogTable lt;
   ugk_exp2_stage(tab);
+  kl_log_stage(&lt);
   __syncthreads();
-  const double sp = (double)sigma_prior, two_sp2 = 2.0 * (double)sp2;
+  const double log_sp = log((double)sigma_prior), inv_two_sp2 = 1.0 / (2.0 * (double)sp2);
   double acc = 0.0;
   const size_t stride = (size_t)gridDim.x * kBlock;
   const bool vec = aligned16(mu) && aligned16(rho);
@@ -204,13 +250,13 @@ __global__ __launch_bounds__(kBlock) void k_kl_partial(double *part, const float
   for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
     const float4 m = ld_nt(reinterpret_cast<const float4 *>(mu) + i);
     const float4 r = ld_nt(reinterpret_cast<const float4 *>(rho) + i);
-    acc += kl_term(m.x, r.x, sp, two_sp2, tab);
-    acc += kl_term(m.y, r.y, sp, two_sp2, tab);
-    acc += kl_term(m.z, r.z, sp, two_sp2, tab);
-    acc += kl_term(m.w, r.w, sp, two_sp2, tab);
+    acc += kl_term(m.x, r.x, log_sp, inv_two_sp2, tab, &lt);
+    acc += kl_term(m.y, r.y, log_sp, inv_two_sp2, tab, &lt);
+    acc += kl_term(m.z, r.z, log_sp, inv_two_sp2, tab, &lt);
+    acc += kl_term(m.w, r.w, log_sp, inv_two_sp2, tab, &lt);
   }
   for (size_t i = 4 * n4 + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-    acc += kl_term(mu[i], rho[i], sp, two_sp2, tab);
+    acc += kl_term(mu[i], rho[i], log_sp, inv_two_sp2, tab, &lt);
   const double t = block_sum_d(acc, lds);
   if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
