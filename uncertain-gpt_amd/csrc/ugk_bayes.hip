@@ -80,33 +80,46 @@ struct BayesBackwardPhilox : MapOp {
 // train_bnn.c:966-979: dmu += weight * (mu / sp2);
 // drho += weight * (sigma / sp2 - 1 / sigma) * sigmoid(rho), sigma = softplus(rho).
 // Loads mu, rho, dmu, drho; stores dmu, drho.
+// A launch-wide divisor with its reciprocal (1.0f / b, correctly rounded) and
+// whether the reciprocal form of the quotient applies to it.
+struct SharedDivisor {
+  float b, y;
+  bool ok;
+  static SharedDivisor of(float b) { return SharedDivisor{b, 1.0f / b, ugk_div_shared_ok(b)}; }
+};
+
+__device__ __forceinline__ float div_by(float a, const SharedDivisor &d) { return ugk_div_shared(a, d.b, d.y, d.ok); }
+
 struct KlBackward : MapOp {
   static constexpr int kLoads = 4, kStores = 2;
   static constexpr bool kTable = true;
   struct Params {
-    float sp2, weight;
+    SharedDivisor sp2;
+    float weight;
   };
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t, const Params &p) {
     const float r = ld[1];
     const float sigma = ugk_dev_softplusf_lds(r, tab);
-    st[0] = ld[2] + p.weight * (ld[0] / p.sp2);
-    const float dsigma = sigma / p.sp2 - 1.0f / sigma;
+    st[0] = ld[2] + p.weight * div_by(ld[0], p.sp2);
+    const float dsigma = div_by(sigma, p.sp2) - 1.0f / sigma;
     st[1] = ld[3] + p.weight * dsigma * sigmoid_lds(r, tab);
   }
 };
 
 struct AdamParams {
-  float lr, beta1, beta2, eps, wd, bc1, bc2;
+  float lr, beta1, beta2, eps, wd;
+  SharedDivisor bc1, bc2;
 };
 
 // One AdamW update of (param, m, v) by gradient g; train_bnn.c:704-716 and
-// gpt2_kernels.cuh:973-984 evaluate the same expression.
+// gpt2_kernels.cuh:973-984 evaluate the same expression (the quotients by
+// the bias corrections and the square root are the correctly rounded ones).
 __device__ __forceinline__ float adamw_one(float param, float g, float &m, float &v, const AdamParams &a) {
   m = a.beta1 * m + (1.0f - a.beta1) * g;
   v = a.beta2 * v + (1.0f - a.beta2) * g * g;
-  const float m_hat = m / a.bc1;
-  const float v_hat = v / a.bc2;
-  return param - a.lr * (m_hat / (sqrtf(v_hat) + a.eps) + a.wd * param);
+  const float m_hat = div_by(m, a.bc1);
+  const float v_hat = div_by(v, a.bc2);
+  return param - a.lr * (m_hat / (ugk_dev_sqrtf(v_hat) + a.eps) + a.wd * param);
 }
 
 // train_bnn.c:699-717. Loads params, grads, m, v; stores params, m, v.
@@ -133,7 +146,8 @@ struct BbbStepFused : MapOp {
   struct Params {
     unsigned long long seed;
     int step;
-    float sp, klw;
+    SharedDivisor sp2;  // the prior variance sp * sp
+    float klw;
     AdamParams adam;
   };
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
@@ -142,9 +156,9 @@ struct BbbStepFused : MapOp {
     float gmu = g;
     float grho = g * ugk_dev_philox_normal(p.seed, p.step, i) * sg;
     if (p.klw > 0.0f) {
-      const float sp2 = p.sp * p.sp, sigma = ugk_dev_softplusf_lds(r, tab);
-      gmu += p.klw * (mm / sp2);
-      grho += p.klw * (sigma / sp2 - 1.0f / sigma) * sg;
+      const float sigma = ugk_dev_softplusf_lds(r, tab);
+      gmu += p.klw * div_by(mm, p.sp2);
+      grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
     }
     float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
     const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
@@ -295,13 +309,15 @@ int launch_bayes_backward_philox(float *dmu, float *drho, const float *dw, const
 
 int launch_kl_backward(float *dmu, float *drho, const float *mu, const float *rho, size_t n,
                        float sigma_prior, float weight) {
-  Streams<KlBackward> s{{mu, rho, dmu, drho}, {dmu, drho}, {sigma_prior * sigma_prior, weight}};
+  Streams<KlBackward> s{{mu, rho, dmu, drho}, {dmu, drho}, {SharedDivisor::of(sigma_prior * sigma_prior), weight}};
   return run_map(s, n, "kl_backward");
 }
 
 int launch_adamw(float *params, const float *grads, float *m, float *v, size_t n, float lr,
                  float beta1, float beta2, float eps, float wd, float bc1, float bc2) {
-  Streams<AdamW> s{{params, grads, m, v}, {params, m, v}, {lr, beta1, beta2, eps, wd, bc1, bc2}};
+  Streams<AdamW> s{{params, grads, m, v},
+                   {params, m, v},
+                   {lr, beta1, beta2, eps, wd, SharedDivisor::of(bc1), SharedDivisor::of(bc2)}};
   return run_map(s, n, "adamw_update");
 }
 
@@ -311,7 +327,8 @@ int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float
                           float aeps, float wd) {
   Streams<BbbStepFused> s{{dw, rho, mu, m_mu, v_mu, m_rho, v_rho},
                           {dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w},
-                          {seed, step, sp, klw, {lr, beta1, beta2, aeps, wd, bc1, bc2}}};
+                          {seed, step, SharedDivisor::of(sp * sp), klw,
+                           {lr, beta1, beta2, aeps, wd, SharedDivisor::of(bc1), SharedDivisor::of(bc2)}}};
   return run_map(s, n, "bbb_step_fused");
 }
 

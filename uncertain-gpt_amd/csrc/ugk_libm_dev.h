@@ -68,6 +68,24 @@ __device__ __forceinline__ float ugk_div_recip(float a, float b, float y) {
   return __builtin_fmaf(r, y, q);
 }
 
+// a / b for a divisor shared by a whole launch (a per-launch scalar), given
+// y = 1.0f / b: ugk_div_recip where it is exact, IEEE division elsewhere (a
+// rare branch). Exact for b in [2^-24, 2^24] (b_ok, decided by the caller)
+// and a == +0 or 2^-102 <= |a| <= 2^100: then a/b >= 2^-126 is normal, and
+// the exponents of b and of the quotient sum to at least -103, so the exact
+// remainder is a multiple of 2^-149 (ugk_diag.hip fn 54-61 check eight
+// divisors on every a).
+__device__ __forceinline__ float ugk_div_shared(float a, float b, float y, bool b_ok) {
+  float q = ugk_div_recip(a, b, y);
+  const float aa = fabsf(a);
+  const bool ok = b_ok && ((aa >= 0x1p-102f && aa <= 0x1p100f) || ugk_f2u(a) == 0u);
+  if (__builtin_expect(!ok, 0)) q = a / b;
+  return q;
+}
+
+// Whether b may take ugk_div_shared's reciprocal form.
+__host__ __device__ inline bool ugk_div_shared_ok(float b) { return b >= 0x1p-24f && b <= 0x1p24f; }
+
 // The domain test of ugk_div_recip for a in [0, 1] or NaN, folded over many
 // a with a running unsigned minimum: lo = min(lo, ugk_div_recip_key(a)) stays
 // >= kUgkDivRecipKeyMin exactly when every a was +0, NaN or in [2^-86, 1].
@@ -99,6 +117,14 @@ __device__ __forceinline__ float ugk_dev_sqrtf_large(float x) {
   float t = __builtin_fmaf(-dn, s, x) <= 0.0f ? dn : s;
   t = __builtin_fmaf(-up, s, x) > 0.0f ? up : t;
   return t;
+}
+
+// sqrtf for any input: ugk_dev_sqrtf_large on its domain, the library's
+// sqrtf (which rescales) for the rare tiny or negative inputs (fn 62).
+__device__ __forceinline__ float ugk_dev_sqrtf(float x) {
+  float r = ugk_dev_sqrtf_large(x);
+  if (__builtin_expect(x < 0x1p-96f && x != 0.0f, 0)) r = sqrtf(x);
+  return r;
 }
 
 // expm1f for any input, branch-free (used by the exhaustive diagnostic and as

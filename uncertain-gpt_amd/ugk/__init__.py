@@ -396,6 +396,9 @@ MATH_FUNCTIONS.update({f"div_recip{j}": 40 + j for j in range(8)})
 MATH_FUNCTIONS.update({"sqrtf_large": 48})
 MATH_FUNCTIONS.update({f"recip/div{s}": 49 + s for s in range(4)})
 MATH_FUNCTIONS.update({"recip_ge1": 53})
+# x / b for the launch-wide divisors of the posterior ops; sqrtf for any input
+MATH_FUNCTIONS.update({f"div_shared{j}": 54 + j for j in range(8)})
+MATH_FUNCTIONS.update({"sqrtf_any": 62})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
