@@ -40,11 +40,31 @@ __device__ __forceinline__ void st_nt(float4 *p, float4 v) {
 __device__ __forceinline__ float ld_nt(const float *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_nt(float *p, float v) { __builtin_nontemporal_store(v, p); }
 
-// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+// v from lane dpp(i) of the same row of 16 (kCtrl: a DPP lane pattern).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_lane(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kDppQuadSwap1 = 0xb1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4e;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror: lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;     // row_mirror: lane i <-> 15 - i within 16
+
+// Sum over the 64 lanes of a wavefront, all lanes active; every lane gets the
+// same bits. Within each row of 16 lanes, four DPP steps each add the value
+// of a partner lane (partners then hold the same two operands, so the same
+// sum); the four row sums are read into scalar registers and added as
+// (r0 + r1) + (r2 + r3). No LDS round trips, unlike a shuffle butterfly.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v += dpp_lane<kDppQuadSwap1>(v);
+  v += dpp_lane<kDppQuadSwap2>(v);
+  v += dpp_lane<kDppHalfMirror>(v);
+  v += dpp_lane<kDppMirror>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Launchers, one per kernel family. Each validates nothing (ugk_api.hip does)

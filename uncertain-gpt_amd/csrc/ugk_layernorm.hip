@@ -222,12 +222,9 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
       }
     }
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-#pragma unroll
-      for (int q = 0; q < R; q++) {
-        s1[q] += __shfl_xor(s1[q], off);
-        s2[q] += __shfl_xor(s2[q], off);
-      }
+    for (int q = 0; q < R; q++) {
+      s1[q] = wave_sum(s1[q]);
+      s2[q] = wave_sum(s2[q]);
     }
 #pragma unroll
     for (int q = 0; q < R; q++) {
