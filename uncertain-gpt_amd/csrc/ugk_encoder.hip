@@ -36,12 +36,13 @@
 //                  flight. A larger bucket's wavefront scans the rows' slots
 //                  in row order (four per lane per load, 2048 per round) and
 //                  writes the matching row ids, ascending, to a list for K3.
-//     K3 large   - workgroups of 16 wavefronts, one per (large bucket, 64
-//                  channels): the wavefronts stage 512 rows at a time into LDS
-//                  (512 loads in flight, the next chunk's loads issued before
-//                  the current chunk is summed) and one wavefront adds them
-//                  in order, one channel per lane. A frequent token's long
-//                  serial chain thus waits on memory once per 512 rows.
+//     K3 large   - workgroups of 9 wavefronts, one per (large bucket, 64
+//                  channels): one wavefront only adds staged rows in order,
+//                  one channel per lane, from one half of a double-buffered
+//                  LDS stage, while eight loader wavefronts stage the next
+//                  256 rows into the other half with two rounds of loads in
+//                  flight. A frequent token's serial chain of adds thus runs
+//                  without waiting for its loads.
 //   The table is double-buffered by chunk parity: K2 of chunk j clears the
 //   half that chunk j-1 used, so no kernel clears what it also reads.
 //   The arrival order inside a bucket depends on scheduling, but it is
@@ -369,24 +370,37 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
 }
 
 // K3: workgroups take (large bucket, 64-channel slice) work items from a
-// counter until none are left. Each round the 16 wavefronts load 32 rows each
-// (512 rows; the row ids with one vector load, read out lane by lane) and
-// stage them in LDS; wavefront 0 adds the staged rows to its running sums in
-// ascending row order while the next round's loads are in flight.
-constexpr int kLargeWaves = 16;
+// counter until none are left. A bucket's rows must be added in ascending row
+// order, one dependent add per row and channel, so one wavefront (the adder,
+// wavefront 0) does nothing else: it adds a round of 256 staged rows from one
+// half of a double-buffered LDS stage while eight loader wavefronts stage the
+// next round into the other half. Each loader holds 32 rows of two rounds in
+// registers (rounds alternate between its two sets), so a row's load is
+// issued two rounds before it is staged; row ids are loaded with one vector
+// load per round, two rounds ahead of the rows, and read out lane by lane.
+// Rows past the bucket are staged as -0.0f, which leaves every sum unchanged
+// (x + -0.0f == x for every x, -0.0f included), so the adds test nothing.
+constexpr int kLoaders = 8;
 constexpr int kPerWave = 32;
-constexpr int kStage = kLargeWaves * kPerWave;
+constexpr int kRound = kLoaders * kPerWave;  // rows per round
+constexpr int kLargeThreads = (kLoaders + 1) * kWave;
 constexpr int kLargeGrid = 256;
-__global__ __launch_bounds__(kLargeWaves * kWave) void k_enc_bwd_large(EncTable tb, EncShared sh,
-                                                                       float *__restrict__ dwte,
-                                                                       const float *__restrict__ dout, int C,
-                                                                       int nslices) {
-  __shared__ float stage[kStage][kWave];
+
+__global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, EncShared sh,
+                                                                 float *__restrict__ dwte,
+                                                                 const float *__restrict__ dout, int C,
+                                                                 int nslices) {
+  // stage[h][channel][row]: a lane's rows are consecutive, so both sides
+  // move four rows per LDS instruction; the row stride of kRound + 4 floats
+  // puts the 16 lanes of each 16-byte access on distinct banks
+  __shared__ float4 stage[2][kWave][kRound / 4 + 1];
   __shared__ int next_item;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int total = tb.counters[1] * nslices;
   if (total == 0) return;  // the common case: no bucket beyond kCap rows
+  const bool adder = wave == 0;
+  const int mine = (wave - 1) * kPerWave + (lane & (kPerWave - 1));  // loader: row of this lane's id
   for (;;) {
     // the next (bucket, slice) work item, taken from a counter so that
     // workgroups with short buckets go on to others
@@ -398,41 +412,95 @@ __global__ __launch_bounds__(kLargeWaves * kWave) void k_enc_bwd_large(EncTable 
     const int j = wi / nslices;
     const int c = (wi % nslices) * kWave + lane;
     const bool on = c < C;
+    const int cc = on ? c : 0;  // a valid column for the lanes past C
     const int4 m = sh.lmeta[j];
     const int *ids = sh.pool + m.x;
     const int cnt = m.y;
-    float acc = (wave == 0 && on) ? dwte[(size_t)m.z * C + c] : 0.0f;
-    float v[kPerWave];
-    auto load_round = [&](int r0) {
-      const int ri = r0 + wave * kPerWave + (lane & (kPerWave - 1));
-      const int idv = ri < cnt ? ids[ri] : 0;
+    const int nrounds = (cnt + kRound - 1) / kRound;
+    float acc = (adder && on) ? dwte[(size_t)m.z * C + c] : 0.0f;
+    // loader state: the row ids and rows of two rounds, in sets a and b
+    float va[kPerWave], vb[kPerWave];
+    auto load_ids = [&](int r) {
+      return (!adder && r < nrounds && r * kRound + mine < cnt) ? ids[r * kRound + mine] : 0;
+    };
+#define UGK_LOAD_ROWS(v, idv)                                                                \
+  _Pragma("unroll") for (int q = 0; q < kPerWave; q++) v[q] =                                \
+      dout[(size_t)__builtin_amdgcn_readlane(idv, q) * C + cc];
+#define UGK_STAGE_ROWS(v, r)                                                                 \
+  {                                                                                          \
+    float4 *dst = &stage[(r) & 1][lane][(wave - 1) * kPerWave / 4];                          \
+    const int lim = on ? cnt - (r) * kRound - (wave - 1) * kPerWave : 0;                     \
+    _Pragma("unroll") for (int q = 0; q < kPerWave; q += 4) dst[q / 4] =                     \
+        make_float4(q < lim ? v[q] : -0.0f, q + 1 < lim ? v[q + 1] : -0.0f,                  \
+                    q + 2 < lim ? v[q + 2] : -0.0f, q + 3 < lim ? v[q + 3] : -0.0f);         \
+  }
+    auto add_round = [&](int r) {
+      // 16 staged rows at a time (whole batches: rows past the bucket hold
+      // -0.0f), the next batches read from LDS while this one is added
+      const float4 *src = stage[r & 1][lane];
+      const int nb = (min(kRound, cnt - r * kRound) + 15) / 16;
+      float4 t[4], u[4];
 #pragma unroll
-      for (int q = 0; q < kPerWave; q++) {
-        const int r = r0 + wave * kPerWave + q;
-        const int id = __builtin_amdgcn_readlane(idv, q);
-        v[q] = (on && r < cnt) ? dout[(size_t)id * C + c] : 0.0f;
+      for (int q = 0; q < 4; q++) t[q] = src[q];
+      for (int b = 0; b < nb; b += 2) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) u[q] = src[(b + 1 < kRound / 16 ? 4 * (b + 1) : 0) + q];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          acc += t[q].x;
+          acc += t[q].y;
+          acc += t[q].z;
+          acc += t[q].w;
+        }
+        if (b + 1 >= nb) break;
+#pragma unroll
+        for (int q = 0; q < 4; q++) t[q] = src[(b + 2 < kRound / 16 ? 4 * (b + 2) : 0) + q];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          acc += u[q].x;
+          acc += u[q].y;
+          acc += u[q].z;
+          acc += u[q].w;
+        }
       }
     };
-    load_round(0);
-    for (int r0 = 0; r0 < cnt; r0 += kStage) {
-#pragma unroll
-      for (int q = 0; q < kPerWave; q++) stage[wave * kPerWave + q][lane] = v[q];
+    int ida = 0, idb = 0;
+    if (!adder) {
+      ida = load_ids(0);
+      idb = load_ids(1);
+      UGK_LOAD_ROWS(va, ida)
+      ida = load_ids(2);
+      if (nrounds > 1) { UGK_LOAD_ROWS(vb, idb) }
+      idb = load_ids(3);
+      UGK_STAGE_ROWS(va, 0)
+      if (nrounds > 2) { UGK_LOAD_ROWS(va, ida) }
+      ida = load_ids(4);
+    }
+    __syncthreads();
+    // round k is in stage[k & 1]; rounds k + 1 and k + 2 are in the loaders'
+    // registers (set b and set a for even k)
+    for (int k = 0; k < nrounds; k += 2) {
+      if (adder) {
+        add_round(k);
+      } else if (k + 1 < nrounds) {
+        UGK_STAGE_ROWS(vb, k + 1)
+        if (k + 3 < nrounds) { UGK_LOAD_ROWS(vb, idb) }
+        idb = load_ids(k + 5);
+      }
       __syncthreads();
-      if (r0 + kStage < cnt) load_round(r0 + kStage);
-      if (wave == 0) {
-        const int nr = min(kStage, cnt - r0);
-        for (int r1 = 0; r1 < nr; r1 += 16) {
-          float t[16];
-#pragma unroll
-          for (int q = 0; q < 16; q++) t[q] = stage[r1 + q][lane];  // rows past nr were staged as 0
-#pragma unroll
-          for (int q = 0; q < 16; q++)
-            if (r1 + q < nr) acc += t[q];
-        }
+      if (k + 1 >= nrounds) break;
+      if (adder) {
+        add_round(k + 1);
+      } else if (k + 2 < nrounds) {
+        UGK_STAGE_ROWS(va, k + 2)
+        if (k + 4 < nrounds) { UGK_LOAD_ROWS(va, ida) }
+        ida = load_ids(k + 6);
       }
       __syncthreads();
     }
-    if (wave == 0 && on) dwte[(size_t)m.z * C + c] = acc;
+#undef UGK_LOAD_ROWS
+#undef UGK_STAGE_ROWS
+    if (adder && on) dwte[(size_t)m.z * C + c] = acc;
   }
 }
 
@@ -554,12 +622,12 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     else
       hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
                          ds.last_tsize[1 - p], C, n);
-    // one round of workgroups (one per CU: each stages 128 KB in LDS) takes
+    // one round of workgroups (one per CU: each stages 130 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
     // every workgroup exits at once
     const int max_items = (n / (kCap + 1) + 1) * nslices;
     hipLaunchKernelGGL(k_enc_bwd_large, dim3(max_items < kLargeGrid ? max_items : kLargeGrid),
-                       dim3(kLargeWaves * kWave), 0, stream(), tb, ds.sh, dwte, dchunk, C, nslices);
+                       dim3(kLargeThreads), 0, stream(), tb, ds.sh, dwte, dchunk, C, nslices);
     ds.last_tsize[1 - p] = 0;
     ds.last_tsize[p] = tsize;
     ds.parity = 1 - p;
