@@ -259,6 +259,30 @@ def test_encoder_one_token(gpu, oracle):
     enc_case(gpu, oracle, B, T, C, V, np.full(B * T, 3, np.int32), 2)
 
 
+def test_encoder_large_bucket_boundaries(gpu, oracle):
+    """Buckets of 33..1000 rows, sized around the large-bucket kernel's 16-row batches and
+    256-row rounds, at C = 100 (a partial 64-channel slice) and C = 6 (scalar path), with signed
+    zeros in dwte and dout: the -0.0f padding of partial rounds must leave every sum unchanged."""
+    sizes = [33, 47, 255, 256, 257, 511, 512, 513, 1000]
+    inp = np.concatenate([np.full(k, j, np.int32) for j, k in enumerate(sizes)])
+    inp = inp[gen.rng(21).permutation(inp.size)]
+    for C in (100, 6):
+        B, T, V = 1, inp.size, len(sizes) + 1
+        g = gen.rng(C)
+        wte, wpe = gen.normal(g, (V, C), 0, 0.02), gen.normal(g, (T, C), 0, 0.01)
+        dout = gen.normal(g, (B, T, C))
+        dout[:, ::3, :] = np.float32(-0.0)
+        dout[:, 1::7, :] = np.float32(0.0)
+        dwte0, dwpe0 = gen.normal(g, (V, C)), gen.normal(g, (T, C))
+        dwte0[::2] = np.float32(-0.0)
+        dwte, dwpe = dwte0.copy(), dwpe0.copy()
+        oracle.encoder_backward(dwte, dwpe, dout, inp, B, T, C)
+        tdwte, tdwpe = dev(dwte0), dev(dwpe0)
+        gpu.encoder_backward(tdwte, tdwpe, dev(dout), dev(inp), B, T, C)
+        assert_bits(host(tdwte), dwte, f"encoder_backward dwte C={C}")
+        assert_bits(host(tdwpe), dwpe, f"encoder_backward dwpe C={C}")
+
+
 def test_encoder_zipf_cfg4_shape(gpu, oracle):
     B, T, C, V = 16, 1024, 768, 50257
     enc_case(gpu, oracle, B, T, C, V, gen.tokens_zipf(gen.rng(11), B * T, V), 3, reps=2)
