@@ -183,7 +183,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "the layer kernels shard by rows with no exchange, see DESIGN.md", file=sys.stderr)
+              "the layer kernels shard by rows with no exchange, so per-GPU throughput is the one-GPU figure",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
