@@ -372,18 +372,22 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
 // K3: workgroups take (large bucket, 64-channel slice) work items from a
 // counter until none are left. A bucket's rows must be added in ascending row
 // order, one dependent add per row and channel, so one wavefront (the adder,
-// wavefront 0) does nothing else: it adds a round of 256 staged rows from one
-// half of a double-buffered LDS stage while eight loader wavefronts stage the
-// next round into the other half. Each loader holds 32 rows of two rounds in
-// registers (rounds alternate between its two sets), so a row's load is
-// issued two rounds before it is staged; row ids are loaded with one vector
-// load per round, two rounds ahead of the rows, and read out lane by lane.
-// Rows past the bucket are staged as -0.0f, which leaves every sum unchanged
-// (x + -0.0f == x for every x, -0.0f included), so the adds test nothing.
-constexpr int kLoaders = 8;
-constexpr int kPerWave = 32;
-constexpr int kRound = kLoaders * kPerWave;  // rows per round
-constexpr int kLargeThreads = (kLoaders + 1) * kWave;
+// wavefront 0) does nothing else: it adds a round of 240 staged rows from one
+// half of a double-buffered LDS stage while loader wavefronts stage the next
+// round into the other half. The loaders form three groups of five; group
+// g holds rounds g, g + 3, g + 6, ... (48 rows per wavefront), stages its
+// round the iteration before the adder needs it and then loads its next
+// one, so every row is loaded three rounds ahead and each loader has only
+// its own round's loads in flight when it waits for them. Row ids come with
+// one vector load per round, issued with the previous round's rows, and are
+// read out lane by lane. Rows past the bucket are staged as -0.0f, which
+// leaves every sum unchanged (x + -0.0f == x for every x, -0.0f included),
+// so the adds test nothing.
+constexpr int kGroups = 3;
+constexpr int kGroupWaves = 5;
+constexpr int kPerWave = 48;
+constexpr int kRound = kGroupWaves * kPerWave;  // rows per round
+constexpr int kLargeThreads = (kGroups * kGroupWaves + 1) * kWave;
 constexpr int kLargeGrid = 256;
 
 __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, EncShared sh,
@@ -400,7 +404,9 @@ __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, En
   const int total = tb.counters[1] * nslices;
   if (total == 0) return;  // the common case: no bucket beyond kCap rows
   const bool adder = wave == 0;
-  const int mine = (wave - 1) * kPerWave + (lane & (kPerWave - 1));  // loader: row of this lane's id
+  const int group = adder ? -1 : (wave - 1) / kGroupWaves;
+  const int slot = adder ? 0 : (wave - 1) % kGroupWaves;  // this loader's share of a round
+  const int mine = slot * kPerWave + (lane < kPerWave ? lane : 0);  // loader: row of this lane's id
   for (;;) {
     // the next (bucket, slice) work item, taken from a counter so that
     // workgroups with short buckets go on to others
@@ -418,22 +424,22 @@ __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, En
     const int cnt = m.y;
     const int nrounds = (cnt + kRound - 1) / kRound;
     float acc = (adder && on) ? dwte[(size_t)m.z * C + c] : 0.0f;
-    // loader state: the row ids and rows of two rounds, in sets a and b
-    float va[kPerWave], vb[kPerWave];
-    auto load_ids = [&](int r) {
-      return (!adder && r < nrounds && r * kRound + mine < cnt) ? ids[r * kRound + mine] : 0;
+    // a loader's round: the ids of its rows, then the rows
+    float v[kPerWave];
+    int idv = 0;
+    auto load_ids = [&](int r) { return (r < nrounds && r * kRound + mine < cnt) ? ids[r * kRound + mine] : 0; };
+    auto load_rows = [&]() {
+#pragma unroll
+      for (int q = 0; q < kPerWave; q++) v[q] = dout[(size_t)__builtin_amdgcn_readlane(idv, q) * C + cc];
     };
-#define UGK_LOAD_ROWS(v, idv)                                                                \
-  _Pragma("unroll") for (int q = 0; q < kPerWave; q++) v[q] =                                \
-      dout[(size_t)__builtin_amdgcn_readlane(idv, q) * C + cc];
-#define UGK_STAGE_ROWS(v, r)                                                                 \
-  {                                                                                          \
-    float4 *dst = &stage[(r) & 1][lane][(wave - 1) * kPerWave / 4];                          \
-    const int lim = on ? cnt - (r) * kRound - (wave - 1) * kPerWave : 0;                     \
-    _Pragma("unroll") for (int q = 0; q < kPerWave; q += 4) dst[q / 4] =                     \
-        make_float4(q < lim ? v[q] : -0.0f, q + 1 < lim ? v[q + 1] : -0.0f,                  \
-                    q + 2 < lim ? v[q + 2] : -0.0f, q + 3 < lim ? v[q + 3] : -0.0f);         \
-  }
+    auto stage_rows = [&](int r) {
+      float4 *dst = &stage[r & 1][lane][slot * kPerWave / 4];
+      const int lim = on ? cnt - r * kRound - slot * kPerWave : 0;
+#pragma unroll
+      for (int q = 0; q < kPerWave; q += 4)
+        dst[q / 4] = make_float4(q < lim ? v[q] : -0.0f, q + 1 < lim ? v[q + 1] : -0.0f,
+                                 q + 2 < lim ? v[q + 2] : -0.0f, q + 3 < lim ? v[q + 3] : -0.0f);
+    };
     auto add_round = [&](int r) {
       // 16 staged rows at a time (whole batches: rows past the bucket hold
       // -0.0f), the next batches read from LDS while this one is added
@@ -464,42 +470,31 @@ __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, En
         }
       }
     };
-    int ida = 0, idb = 0;
-    if (!adder) {
-      ida = load_ids(0);
-      idb = load_ids(1);
-      UGK_LOAD_ROWS(va, ida)
-      ida = load_ids(2);
-      if (nrounds > 1) { UGK_LOAD_ROWS(vb, idb) }
-      idb = load_ids(3);
-      UGK_STAGE_ROWS(va, 0)
-      if (nrounds > 2) { UGK_LOAD_ROWS(va, ida) }
-      ida = load_ids(4);
+    // group g starts with round g; group 0 stages it at once and goes on to
+    // round 3
+    if (!adder && group < nrounds) {
+      idv = load_ids(group);
+      load_rows();
+      idv = load_ids(group + kGroups);
+      if (group == 0) {
+        stage_rows(0);
+        if (kGroups < nrounds) load_rows();
+        idv = load_ids(2 * kGroups);
+      }
     }
     __syncthreads();
-    // round k is in stage[k & 1]; rounds k + 1 and k + 2 are in the loaders'
-    // registers (set b and set a for even k)
-    for (int k = 0; k < nrounds; k += 2) {
+    for (int k = 0; k < nrounds; k++) {
+      // round k is in stage[k & 1]; the group holding round k + 1 stages it
+      // into the other half and then loads its round k + 4
       if (adder) {
         add_round(k);
-      } else if (k + 1 < nrounds) {
-        UGK_STAGE_ROWS(vb, k + 1)
-        if (k + 3 < nrounds) { UGK_LOAD_ROWS(vb, idb) }
-        idb = load_ids(k + 5);
-      }
-      __syncthreads();
-      if (k + 1 >= nrounds) break;
-      if (adder) {
-        add_round(k + 1);
-      } else if (k + 2 < nrounds) {
-        UGK_STAGE_ROWS(va, k + 2)
-        if (k + 4 < nrounds) { UGK_LOAD_ROWS(va, ida) }
-        ida = load_ids(k + 6);
+      } else if (group == (k + 1) % kGroups && k + 1 < nrounds) {
+        stage_rows(k + 1);
+        if (k + 1 + kGroups < nrounds) load_rows();
+        idv = load_ids(k + 1 + 2 * kGroups);
       }
       __syncthreads();
     }
-#undef UGK_LOAD_ROWS
-#undef UGK_STAGE_ROWS
     if (adder && on) dwte[(size_t)m.z * C + c] = acc;
   }
 }
@@ -622,7 +617,7 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     else
       hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
                          ds.last_tsize[1 - p], C, n);
-    // one round of workgroups (one per CU: each stages 130 KB in LDS) takes
+    // one round of workgroups (one per CU: each stages 122 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
     // every workgroup exits at once
     const int max_items = (n / (kCap + 1) + 1) * nslices;
