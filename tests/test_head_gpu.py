@@ -105,6 +105,25 @@ def test_softmax_special_rows(gpu, oracle, V):
     check_forward(gp, host(tlo), cp, cl, logits, targets)
 
 
+@pytest.mark.parametrize("V", [961, 32706, 50257, 51393])
+def test_softmax_loss_at_row_edges(gpu, oracle, V):
+    """Targets at the first and last logit of rows with every start offset mod 64 (the kernels
+    lay a row on the threads from a 256-byte boundary of probs, so the thread holding the
+    target depends on the row's offset): the loss is -log of the stored probability."""
+    rows = 66
+    logits, _ = head_inputs(V + 7, 1, rows, V)
+    logits = logits.reshape(rows, V)
+    targets = np.where(np.arange(rows) % 2 == 0, 0, V - 1).astype(np.int32)
+    tp, tlo = torch.empty(rows * V, device=DEV), torch.empty(rows, device=DEV)
+    gpu.softmax_crossentropy(tlo, tp, dev(logits), dev(targets), 1, rows, V)
+    gp, gl = host(tp).reshape(rows, V), host(tlo)
+    pt = gp[np.arange(rows), targets].astype(np.float64)
+    assert bits_equal(gl, (-np.log(pt)).astype(np.float32))
+    cp, cl = np.zeros_like(logits), np.zeros(rows, np.float32)
+    oracle.softmax_crossentropy(cl, cp, logits, targets, 1, rows, V)
+    check_forward(gp, gl, cp, cl, logits, targets)
+
+
 def test_softmax_ragged_and_empty(gpu):
     t = torch.zeros(8, device=DEV)
     gpu.softmax_crossentropy(t, t, t, torch.zeros(4, dtype=torch.int32, device=DEV), 0, 4, 2)  # B = 0
