@@ -10,12 +10,13 @@
 // the registers with 64-lane butterfly sums, rstd = 1/sqrtf(var/C + 1e-5)
 // with IEEE division and square root, exactly the CPU formula.
 //
-// Backward: one wavefront per row for dinp (two butterfly sums), and the
-// dweight/dbias column sums are carried in registers across the rows a
-// wavefront visits, then combined in a fixed order: the wavefronts of a workgroup through an LDS tree into one
-// partial row per workgroup (at most 512 workgroups), then the
-// partial rows in index order by a small second kernel that adds the totals
-// into dweight/dbias. No atomics, so the result is identical run to run.
+// Backward: one wavefront per row for dinp (two wavefront sums), and the
+// dweight/dbias column sums are accumulated per wavefront (in LDS) across the
+// rows it visits, then combined in a fixed order: the wavefronts of a
+// workgroup through an LDS tree into one partial row per workgroup (at most
+// 512 workgroups), then the partial rows in index order by a small second
+// kernel that adds the totals into dweight/dbias. No atomics, so the result
+// is identical run to run.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
 #include "ugk_internal.h"
 
@@ -134,10 +135,10 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // Backward, register-resident rows. A workgroup is W wavefronts; wavefront w
 // of workgroup g takes the rpw consecutive rows starting at (W g + w) * rpw,
 // R at a time (the loads of R rows are in flight together), writes dinp and
-// carries the dweight/dbias column sums of its rows in registers. The W
-// wavefronts' sums are then folded pairwise through LDS (upper half into
-// lower half, a fixed tree) and wavefront 0 writes the workgroup's partial
-// row: partial[g] = [dweight part (C floats) | dbias part (C floats)].
+// adds the dweight/dbias terms of its rows, in row order, into its own column
+// sums in LDS. The W wavefronts' sums are then folded pairwise (upper half
+// into lower half, a fixed tree) and wavefront 0 writes the workgroup's
+// partial row: partial[g] = [dweight part (C floats) | dbias part (C floats)].
 //
 // kRes: the new dinp row is also added to rdx and rdy (residual_backward with
 // dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
@@ -149,20 +150,23 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpw, float *__restrict__ rdx,
     float *__restrict__ rdy, int same) {
-  __shared__ float4 red[W / 2][2][V * kWave];
+  // the weight row, and each wavefront's dweight/dbias column sums, live in
+  // LDS rather than registers, which leaves the registers to the rows in
+  // flight and lets two workgroups share a CU
+  __shared__ float4 w4s[V * kWave];
+  __shared__ float4 acc[W][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int C4 = C >> 2;
   const float Cf = (float)C;
   const float4 *w4 = reinterpret_cast<const float4 *>(weight);
-  float4 w[V], dg[V], db[V];
+  for (int e = threadIdx.x; e < V * kWave; e += W * kWave) w4s[e] = e < C4 ? w4[e] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int v = 0; v < V; v++) {
-    const int c4 = lane + v * kWave;
-    w[v] = (c4 < C4) ? w4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    dg[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    db[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    acc[wave][0][v * kWave + lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+    acc[wave][1][v * kWave + lane] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  __syncthreads();
   const int row0 = (blockIdx.x * W + wave) * rpw;
   const int row1 = min(row0 + rpw, rows);
   for (int row = row0; row < row1; row += R) {
@@ -202,22 +206,23 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
       r[q] = rstd[rq];
     }
     float s1[R], s2[R];
-    float4 xh[R][V], dn[R][V];
 #pragma unroll
     for (int q = 0; q < R; q++) {
       s1[q] = 0.0f;
       s2[q] = 0.0f;
 #pragma unroll
       for (int v = 0; v < V; v++) {
-        xh[q][v].x = (x[q][v].x - m[q]) * r[q]; dn[q][v].x = dy[q][v].x * w[v].x;
-        xh[q][v].y = (x[q][v].y - m[q]) * r[q]; dn[q][v].y = dy[q][v].y * w[v].y;
-        xh[q][v].z = (x[q][v].z - m[q]) * r[q]; dn[q][v].z = dy[q][v].z * w[v].z;
-        xh[q][v].w = (x[q][v].w - m[q]) * r[q]; dn[q][v].w = dy[q][v].w * w[v].w;
+        const float4 w = w4s[v * kWave + lane];
+        float4 xh, dn;
+        xh.x = (x[q][v].x - m[q]) * r[q]; dn.x = dy[q][v].x * w.x;
+        xh.y = (x[q][v].y - m[q]) * r[q]; dn.y = dy[q][v].y * w.y;
+        xh.z = (x[q][v].z - m[q]) * r[q]; dn.z = dy[q][v].z * w.z;
+        xh.w = (x[q][v].w - m[q]) * r[q]; dn.w = dy[q][v].w * w.w;
         if (lane + v * kWave < C4) {
-          s1[q] += dn[q][v].x; s2[q] += dn[q][v].x * xh[q][v].x;
-          s1[q] += dn[q][v].y; s2[q] += dn[q][v].y * xh[q][v].y;
-          s1[q] += dn[q][v].z; s2[q] += dn[q][v].z * xh[q][v].z;
-          s1[q] += dn[q][v].w; s2[q] += dn[q][v].w * xh[q][v].w;
+          s1[q] += dn.x; s2[q] += dn.x * xh.x;
+          s1[q] += dn.y; s2[q] += dn.y * xh.y;
+          s1[q] += dn.z; s2[q] += dn.z * xh.z;
+          s1[q] += dn.w; s2[q] += dn.w * xh.w;
         }
       }
     }
@@ -235,11 +240,17 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
       for (int v = 0; v < V; v++) {
         const int c4 = lane + v * kWave;
         if (c4 < C4) {
+          const float4 w = w4s[c4];
+          float4 xh, dn;
+          xh.x = (x[q][v].x - m[q]) * r[q]; dn.x = dy[q][v].x * w.x;
+          xh.y = (x[q][v].y - m[q]) * r[q]; dn.y = dy[q][v].y * w.y;
+          xh.z = (x[q][v].z - m[q]) * r[q]; dn.z = dy[q][v].z * w.z;
+          xh.w = (x[q][v].w - m[q]) * r[q]; dn.w = dy[q][v].w * w.w;
           float4 o;
-          o.x = dx[q][v].x + r[q] * (dn[q][v].x - dnm - xh[q][v].x * dnxm);
-          o.y = dx[q][v].y + r[q] * (dn[q][v].y - dnm - xh[q][v].y * dnxm);
-          o.z = dx[q][v].z + r[q] * (dn[q][v].z - dnm - xh[q][v].z * dnxm);
-          o.w = dx[q][v].w + r[q] * (dn[q][v].w - dnm - xh[q][v].w * dnxm);
+          o.x = dx[q][v].x + r[q] * (dn.x - dnm - xh.x * dnxm);
+          o.y = dx[q][v].y + r[q] * (dn.y - dnm - xh.y * dnxm);
+          o.z = dx[q][v].z + r[q] * (dn.z - dnm - xh.z * dnxm);
+          o.w = dx[q][v].w + r[q] * (dn.w - dnm - xh.w * dnxm);
           st_nt(dx4 + c4, o);
           if (kRes) {
             float4 *a4 = reinterpret_cast<float4 *>(rdx + (size_t)(row + q) * C);
@@ -254,10 +265,13 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
             }
             st_nt(a4 + c4, a);
           }
-          db[v].x += dy[q][v].x; dg[v].x += dy[q][v].x * xh[q][v].x;
-          db[v].y += dy[q][v].y; dg[v].y += dy[q][v].y * xh[q][v].y;
-          db[v].z += dy[q][v].z; dg[v].z += dy[q][v].z * xh[q][v].z;
-          db[v].w += dy[q][v].w; dg[v].w += dy[q][v].w * xh[q][v].w;
+          float4 g = acc[wave][0][c4], bb = acc[wave][1][c4];
+          bb.x += dy[q][v].x; g.x += dy[q][v].x * xh.x;
+          bb.y += dy[q][v].y; g.y += dy[q][v].y * xh.y;
+          bb.z += dy[q][v].z; g.z += dy[q][v].z * xh.z;
+          bb.w += dy[q][v].w; g.w += dy[q][v].w * xh.w;
+          acc[wave][0][c4] = g;
+          acc[wave][1][c4] = bb;
         }
       }
     }
@@ -265,23 +279,19 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
   // fold the W wavefronts' column sums: upper half adds into lower half
 #pragma unroll
   for (int half = W / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
-#pragma unroll
-      for (int v = 0; v < V; v++) {
-        red[wave - half][0][v * kWave + lane] = dg[v];
-        red[wave - half][1][v * kWave + lane] = db[v];
-      }
-    }
     __syncthreads();
     if (wave < half) {
 #pragma unroll
       for (int v = 0; v < V; v++) {
-        const float4 g = red[wave][0][v * kWave + lane], b = red[wave][1][v * kWave + lane];
-        dg[v].x += g.x; dg[v].y += g.y; dg[v].z += g.z; dg[v].w += g.w;
-        db[v].x += b.x; db[v].y += b.y; db[v].z += b.z; db[v].w += b.w;
+        const int e = v * kWave + lane;
+        const float4 g = acc[wave + half][0][e], b = acc[wave + half][1][e];
+        float4 dg = acc[wave][0][e], db = acc[wave][1][e];
+        dg.x += g.x; dg.y += g.y; dg.z += g.z; dg.w += g.w;
+        db.x += b.x; db.y += b.y; db.z += b.z; db.w += b.w;
+        acc[wave][0][e] = dg;
+        acc[wave][1][e] = db;
       }
     }
-    __syncthreads();
   }
   if (wave == 0) {
     float4 *pg = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C);
@@ -290,8 +300,8 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     for (int v = 0; v < V; v++) {
       const int c4 = lane + v * kWave;
       if (c4 < C4) {
-        pg[c4] = dg[v];
-        pb[c4] = db[v];
+        pg[c4] = acc[0][0][c4];
+        pb[c4] = acc[0][1][c4];
       }
     }
   }
@@ -415,11 +425,14 @@ void bwd_shape(int rows, int *nblk, int *rpb) {
   *nblk = (rows + per - 1) / per;
 }
 
+// Rows whose loads a wavefront issues together: two while that fits the
+// registers (C <= 768; measured 43.9 -> 41.7 us for the fused pair at config
+// 5, where each wavefront then takes its two rows in one pass), else one.
+constexpr int bwd_rows(int V) { return V <= 3 ? 2 : 1; }
 // Vector path: W wavefronts per workgroup (8, or 4 when a lane holds more
 // than 4 float4 of a row, so that the registers fit without spilling), rpw
 // rows each, at most kBwdMaxBlocks workgroups, so the reduce reads at most 32
 // partial rows per group.
-constexpr int kBwdRows = 1;
 constexpr int kBwdMaxBlocks = 512;
 inline int bwd_waves(int V) { return V <= 4 ? 8 : 4; }
 void bwd_shape_vec(int rows, int W, int *nblk, int *rpw) {
@@ -494,7 +507,7 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
   const int same = rdx == rdy ? 1 : 0;
   switch (V) {
 #define UGK_LN_BWD(v) \
-  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), kBwdRows, kRes>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same); break;
+  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), bwd_rows(v), kRes>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same); break;
     UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
     UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
 #undef UGK_LN_BWD
