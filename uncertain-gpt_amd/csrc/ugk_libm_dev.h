@@ -157,9 +157,11 @@ __device__ __forceinline__ float ugk_dev_expm1f_t(float x) {
   const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
   const float tt = 3.0f - r1 * hfx;
   const float e = hxs * ugk_div_t<kDiv>(r1 - tt, 6.0f - xr * tt);
-  const float y0 = xr - (xr * e - hxs);  // k == 0
   float e2 = (xr * (e - c) - c);
   e2 -= hxs;
+  // k == 0: fdlibm's xr - (xr*e - hxs); there t = 0 gives c = +0, so e2 rounds
+  // exactly as xr*e - hxs
+  const float y0 = xr - e2;
   const float ym1 = 0.5f * (xr - e2) - 0.5f;  // k == -1
   const float yp1 = (xr < -0.25f) ? -2.0f * (e2 - (xr + 0.5f)) : 1.0f + 2.0f * (xr - e2);  // k == 1
   const uint32_t kbits = (uint32_t)k << 23;
@@ -234,10 +236,12 @@ __device__ __forceinline__ float ugk_dev_expm1f_tanh(float a, bool big) {
   float y = ugk_u2f(ugk_f2u(base - d) + ((uint32_t)k << 23));
   y = big ? y : y - 1.0f;
   y = (k == -1) ? 0.5f * (xr - e2) - 0.5f : y;
-  // k == 0. fdlibm returns a itself for |a| < 2^-25; the general formula gives
-  // a there too (a*a/2 is below half an ulp of a, and underflows to 0 for
-  // subnormal a), so that case needs no select of its own.
-  y = (k == 0) ? xr - (xr * e - hxs) : y;
+  // k == 0: fdlibm's xr - (xr*e - hxs). There t = 0 makes hi = xr = a and
+  // lo = c = +0, so e2 = xr*(e - c) - c - hxs rounds exactly as xr*e - hxs
+  // and xr - e2 is that result. fdlibm returns a itself for |a| < 2^-25; the
+  // general formula gives a there too (a*a/2 is below half an ulp of a, and
+  // underflows to 0 for subnormal a), so that case needs no select of its own.
+  y = (k == 0) ? xr - e2 : y;
   return y;
 }
 
