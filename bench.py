@@ -157,6 +157,22 @@ def summarize_stats(stats_csv):
     return "\n".join(lines)
 
 
+def summarize_trace(trace_csv):
+    """Mean/min/max duration per kernel and grid size from a rocprofv3 --kernel-trace CSV, as
+    text: the per-shape split of summarize_stats (one kernel serves several configurations)."""
+    import csv
+    groups = {}
+    for r in csv.DictReader(open(trace_csv)):
+        k = short_name(r["Kernel_Name"])
+        if k:
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            groups.setdefault((k, int(r["Grid_Size_X"])), []).append(d)
+    lines = [f"{'kernel':34s} {'grid':>10s} {'calls':>6s} {'mean us':>9s} {'min us':>9s} {'max us':>9s}"]
+    for (k, grid), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{k:34s} {grid:10d} {len(ds):6d} {statistics.mean(ds):9.2f} {min(ds):9.2f} {max(ds):9.2f}")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,12 +189,18 @@ def main():
                     help="print per-kernel HBM traffic from two rocprofv3 --pmc runs of this script, and exit")
     ap.add_argument("--summarize-stats", metavar="STATS_CSV",
                     help="print per-kernel durations from a rocprofv3 --stats run of this script, and exit")
+    ap.add_argument("--summarize-trace", metavar="TRACE_CSV",
+                    help="print per-kernel, per-grid durations from a rocprofv3 --kernel-trace run of this "
+                         "script, and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1, sort_keys=True))
         return
     if args.summarize_stats:
         print(summarize_stats(args.summarize_stats))
+        return
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
