@@ -7,8 +7,9 @@
 // Forward: one wavefront per row. Each lane holds V float4 of the row in
 // registers (V = ceil(C/256); C = 768 -> 3), so the row is read from HBM once
 // and written once (8 bytes per element). Mean and variance are two-pass over
-// the registers with 64-lane butterfly sums, rstd = 1/sqrtf(var/C + 1e-5)
-// with IEEE division and square root, exactly the CPU formula.
+// the registers with wavefront sums (DPP within rows of 16 lanes, the four
+// row sums added in scalar registers), rstd = 1/sqrtf(var/C + 1e-5) with IEEE
+// division and square root, exactly the CPU formula.
 //
 // Backward: one wavefront per row for dinp (two wavefront sums), and the
 // dweight/dbias column sums are accumulated per wavefront (in LDS) across the

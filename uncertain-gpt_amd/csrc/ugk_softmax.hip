@@ -8,7 +8,7 @@
 //   max   thread-local `x > m ? x : m` from -1e30 (the CPU loop's rule), then
 //         a wavefront butterfly and the block's wavefronts through LDS;
 //   exp   e = expf(x - max) with the glibc-exact expf (the CPU's values);
-//   sum   thread-local in v order, wavefront butterfly, wavefronts in order
+//   sum   thread-local in v order, a wavefront sum (DPP), wavefronts in order
 //         (a fixed tree: deterministic, within float rounding of the CPU's
 //         sequential sum);
 //   prob  e / sum correctly rounded, from the reciprocal of the sum and one
