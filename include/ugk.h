@@ -23,9 +23,12 @@
  * order.
  *
  * The library never allocates inside a kernel. It owns one scratch buffer per
- * device (LayerNorm-backward partial sums, the encoder-backward bucket table),
- * allocated on the first call that needs it and grown only when a larger
- * shape arrives; ugk_reserve() allocates it up front.
+ * device (LayerNorm-backward partial sums, the KL partial sums), allocated on
+ * the first call that needs it and grown only when a larger shape arrives
+ * (ugk_reserve() allocates it up front), and the encoder backward's bucket
+ * state, a fixed allocation made on its first call on a device. Both are
+ * used in stream order: ugk_set_stream waits for the work already queued on
+ * the previous stream, so calls on two streams never share them at once.
  */
 #ifndef UGK_H
 #define UGK_H
@@ -193,7 +196,8 @@ int ugk_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu,
 /* Text of the last failure on this thread ("" if none). */
 const char *ugk_last_error(void);
 /* Stream for subsequent calls from any thread (a hipStream_t; NULL = the
- * null stream). */
+ * null stream). When the stream changes, first waits for the work queued on
+ * the previous one (it may still use the library's scratch). */
 int ugk_set_stream(void *stream);
 void *ugk_get_stream(void);
 /* Allocate the current device's scratch for shapes up to (rows = B*T, C)

@@ -221,6 +221,41 @@ def test_layernorm_misaligned(gpu, oracle):
     ln_case(gpu, oracle, 2, 8, 384, seed=9, offset=1)
 
 
+def test_layernorm_backward_across_a_stream_switch(gpu):
+    """Two LayerNorm backwards, whose partial column sums live in the library's one scratch
+    buffer, queued on two different streams one after the other: the same bits as the two
+    calls on one stream, because switching the stream waits for the first call's kernels.
+    Config-5 rows, so the first call is still running when the second is queued."""
+    B, T, C = 8, 1024, 768
+    n = B * T * C
+    g = gen.rng(31)
+    calls = []
+    for _ in range(2):
+        x, w, b = dev(gen.normal(g, (n,))), dev(gen.normal(g, (C,), 1, 0.1)), dev(gen.normal(g, (C,), 0, 0.1))
+        m, r = torch.empty(B * T, device=DEV), torch.empty(B * T, device=DEV)
+        gpu.layernorm_forward(torch.empty(n, device=DEV), m, r, x, w, b, B, T, C)
+        calls.append((dev(gen.normal(g, (n,))), x, w, m, r))
+    zero = lambda: (torch.zeros(n, device=DEV), torch.zeros(C, device=DEV), torch.zeros(C, device=DEV))
+    want = []
+    for do, x, w, m, r in calls:  # one stream
+        di, dw, db = zero()
+        gpu.layernorm_backward(di, dw, db, do, x, w, m, r, B, T, C)
+        want.append((host(di), host(dw), host(db)))
+    got = [zero() for _ in calls]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    try:
+        for (do, x, w, m, r), (di, dw, db), s in zip(calls, got, streams):
+            gpu.set_stream(s.cuda_stream)
+            gpu.layernorm_backward(di, dw, db, do, x, w, m, r, B, T, C)
+    finally:
+        gpu.set_stream(None)
+    torch.cuda.synchronize()
+    for k in range(2):
+        for a, e, what in zip(got[k], want[k], ("dinp", "dweight", "dbias")):
+            assert_bits(host(a), e, f"call {k} {what}")
+
+
 # ---- encoder ------------------------------------------------------------------------
 
 def enc_case(gpu, oracle, B, T, C, V, inp, seed, reps=1):

@@ -349,7 +349,14 @@ int ugk_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m
 const char *ugk_last_error(void) { return g_err; }
 
 int ugk_set_stream(void *s) {
-  g_stream.store(static_cast<hipStream_t>(s));
+  const hipStream_t next = static_cast<hipStream_t>(s);
+  const hipStream_t prev = g_stream.exchange(next);
+  // kernels still queued on the previous stream may use the scratch and the
+  // encoder's bucket state, which the new stream's work would then share
+  if (prev != next && hipStreamSynchronize(prev) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_EHIP, "ugk_set_stream: waiting for the previous stream failed");
+  }
   return ok();
 }
 

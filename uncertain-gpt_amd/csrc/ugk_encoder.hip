@@ -12,7 +12,7 @@
 //
 //   dwte: the (b,t) rows are bucketed by token, then each bucket is added in
 //   ascending (b,t) order. Rows are processed in chunks of at most kChunk
-//   (chunk k+1 is queued after chunk k, preserving the order). Two launches
+//   (chunk k+1 is queued after chunk k, preserving the order). Three launches
 //   per chunk:
 //     K1 insert  - each workgroup of 256 rows first groups its rows by
 //                  token in an LDS hash table (local count, local rank), then
@@ -36,13 +36,15 @@
 //                  flight. A larger bucket's wavefront scans the rows' slots
 //                  in row order (four per lane per load, 2048 per round) and
 //                  writes the matching row ids, ascending, to a list for K3.
-//     K3 large   - workgroups of 9 wavefronts, one per (large bucket, 64
+//     K3 large   - workgroups of 16 wavefronts, one per (large bucket, 64
 //                  channels): one wavefront only adds staged rows in order,
 //                  one channel per lane, from one half of a double-buffered
-//                  LDS stage, while eight loader wavefronts stage the next
-//                  256 rows into the other half with two rounds of loads in
-//                  flight. A frequent token's serial chain of adds thus runs
-//                  without waiting for its loads.
+//                  LDS stage, while three groups of five loader wavefronts
+//                  take turns staging the next round of 240 rows into the
+//                  other half, each group loading its round three rounds
+//                  ahead (one round of loads in flight per wavefront, so its
+//                  waits are exact). A frequent token's serial chain of adds
+//                  thus runs without waiting for its loads.
 //   The table is double-buffered by chunk parity: K2 of chunk j clears the
 //   half that chunk j-1 used, so no kernel clears what it also reads.
 //   The arrival order inside a bucket depends on scheduling, but it is
