@@ -100,6 +100,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_map_vec4<ugk::(anonymous namespace)::AdamW>", "adamw_update"),
     ("k_map_vec4<ugk::(anonymous namespace)::BbbStepFused>", "bbb_step_fused"),
     ("k_softmax_xent<", "softmax_crossentropy"),
+    ("k_softmax_xent_split<", "softmax_crossentropy"),
     ("k_softmax_stats", "softmax_crossentropy (row statistics)"),
     ("k_softmax_norm", "softmax_crossentropy (normalise)"),
     ("k_xent_softmax_bwd", "crossentropy_softmax_backward"),

@@ -24,7 +24,9 @@ namespace {
 // and NaN (1.0f / x elsewhere; reference 1.0f / x), the candidate sequences
 // for the sigmoid's quotient; 53: ugk_dev_recip_ge1, the one it uses, on the
 // same domain; 54+j: x / b for the launch-wide divisor kSharedDivisors[j] by
-// ugk_div_shared (reference x / b); 62: ugk_dev_sqrtf (reference as fn 7).
+// ugk_div_shared (reference x / b); 62: ugk_dev_sqrtf (reference as fn 7);
+// 63: ugk_dev_expf_nonpos on its domain, x <= 0 or NaN (ugk_expf_t
+// elsewhere; reference ugk_expf).
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -62,12 +64,15 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 53) return (x >= 1.0f || x != x) ? ugk_dev_recip_ge1(x) : 1.0f / x;
   if (FN >= 54 && FN < 62) return div_shared_by(x, FN - 54);
   if (FN == 62) return ugk_dev_sqrtf(x);
+  if (FN == 63)
+    return (ugk_f2u(x) >> 31 || x != x) ? ugk_dev_expf_nonpos(x, UgkExp2Lds{tab}, UgkExpfAddends{})
+                                        : ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
 template <int FN>
 __device__ __forceinline__ float reference_math(float x) {
-  if (FN == 0) return ugk_expf(x);
+  if (FN == 0 || FN == 63) return ugk_expf(x);
   if (FN == 1 || (FN >= 20 && FN < 24)) return ugk_log1pf(x);
   if (FN == 3 || (FN >= 10 && FN < 14)) return ugk_tanhf(x);
   if (FN == 4) return ugk_softplusf(x);
@@ -169,7 +174,7 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 63);
+         (fn >= 40 && fn < 64);
 }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
@@ -204,7 +209,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(30) UGK_MM(31) UGK_MM(32) UGK_MM(33)
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
       UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
-      UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62)
+      UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62) UGK_MM(63)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -232,7 +237,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(30) UGK_EV(31) UGK_EV(32) UGK_EV(33)
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
     UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
-    UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62)
+    UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62) UGK_EV(63)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

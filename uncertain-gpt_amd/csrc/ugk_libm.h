@@ -96,21 +96,15 @@ struct UgkExpfAddends {
   double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
 };
 
+// expf's formula without its special cases: correct for |x| < 88, and for
+// x in [-0x1.9fe368p6, -88] too, where the routine falls through to it.
 template <int kContract, class Tab>
-UGK_HD float ugk_expf_t(float x, Tab tab, UgkExpfAddends add = UgkExpfAddends{}) {
+UGK_HD float ugk_expf_core(float x, Tab tab, UgkExpfAddends add = UgkExpfAddends{}) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32;
   const double kShift = add.shift;
   const double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
   const double kC1 = add.c1;
   const double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
-  const uint32_t ux = ugk_f2u(x);
-  const uint32_t abstop = (ux >> 20) & 0x7ff;
-  if (abstop >= 0x42b) {                        // |x| >= 88 or nan
-    if (ux == 0xff800000u) return 0.0f;         // -inf
-    if (abstop >= 0x7f8) return x + x;          // +inf, nan
-    if (x > 0x1.62e42ep6f) return ugk_u2f(0x7f800000u);  // overflow
-    if (x < -0x1.9fe368p6f) return 0.0f;        // underflow
-  }
   const double xd = (double)x;
   double kd, r;
   if (kContract == 2) {
@@ -142,6 +136,19 @@ UGK_HD float ugk_expf_t(float x, Tab tab, UgkExpfAddends add = UgkExpfAddends{})
   }
   y = y * s;
   return (float)y;
+}
+
+template <int kContract, class Tab>
+UGK_HD float ugk_expf_t(float x, Tab tab, UgkExpfAddends add = UgkExpfAddends{}) {
+  const uint32_t ux = ugk_f2u(x);
+  const uint32_t abstop = (ux >> 20) & 0x7ff;
+  if (abstop >= 0x42b) {                        // |x| >= 88 or nan
+    if (ux == 0xff800000u) return 0.0f;         // -inf
+    if (abstop >= 0x7f8) return x + x;          // +inf, nan
+    if (x > 0x1.62e42ep6f) return ugk_u2f(0x7f800000u);  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;        // underflow
+  }
+  return ugk_expf_core<kContract>(x, tab, add);
 }
 
 template <int kContract>

@@ -377,6 +377,18 @@ __device__ __forceinline__ UgkExpfAddends ugk_expf_addends_vgpr() {
   return a;
 }
 
+// expf(x) for x <= 0 (-0 and -inf included) or NaN, the softmax's x - max,
+// without branches: expf's formula for every x, then its underflow case.
+// Where that case does not apply (x >= -0x1.9fe368p6) the routine itself
+// takes the formula; for -inf it returns +0 as the underflow case does; for
+// NaN the formula gives a NaN. Checked against ugk_expf on every input of the
+// domain (ugk_diag.hip fn 63).
+template <class Tab>
+__device__ __forceinline__ float ugk_dev_expf_nonpos(float x, Tab tab, UgkExpfAddends add) {
+  const float y = ugk_expf_core<UGK_EXPF_CONTRACT>(x, tab, add);
+  return x < -0x1.9fe368p6f ? 0.0f : y;
+}
+
 // Fill a 32-entry LDS table; the caller synchronises the workgroup after.
 __device__ __forceinline__ void ugk_exp2_stage(uint64_t *lds_tab) {
   if (threadIdx.x < 32) lds_tab[threadIdx.x] = ugk_exp2_bits(threadIdx.x);

@@ -7,7 +7,8 @@
 // from HBM once and the probabilities written once (8 bytes per logit):
 //   max   thread-local `x > m ? x : m` from -1e30 (the CPU loop's rule), then
 //         a wavefront butterfly and the block's wavefronts through LDS;
-//   exp   e = expf(x - max) with the glibc-exact expf (the CPU's values);
+//   exp   e = expf(x - max) with the glibc-exact expf (the CPU's values),
+//         in its branch-free form for arguments <= 0;
 //   sum   thread-local in v order, a wavefront sum (DPP), wavefronts in order
 //         (a fixed tree: deterministic, within float rounding of the CPU's
 //         sequential sum);
@@ -86,7 +87,7 @@ __device__ __forceinline__ float neg_logf(float p) { return -(float)log((double)
 __device__ __forceinline__ void store_loss(float *losses, size_t row, const float *lg, int tgt, int skew, float m,
                                            float s, const uint64_t *tab, int threads) {
   if ((int)threadIdx.x == (tgt + skew) % threads)
-    losses[row] = neg_logf(ugk_expf_t<UGK_EXPF_CONTRACT>(lg[tgt] - m, UgkExp2Lds{tab}) / s);
+    losses[row] = neg_logf(ugk_dev_expf_nonpos(lg[tgt] - m, UgkExp2Lds{tab}, UgkExpfAddends{}) / s);
 }
 
 template <int kThreads, int kPer>
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const int v = tid + k * kThreads - skew;
-    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab}, add);
+    x[k] = ugk_dev_expf_nonpos(x[k] - m, UgkExp2Lds{tab}, add);
     lo = min(lo, ugk_div_recip_key(x[k]));
     if (v >= 0 && v < V) s += x[k];
   }
@@ -180,13 +181,18 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
       part[k * kThreads + tid] = kNegInf;
   }
   // Rows are longer than the register slots (V >= kReg * kThreads, checked at
-  // launch), so only slot 0 can fall outside the row, below its start.
+  // launch), so only slot 0 can fall outside the row, below its start. Its
+  // load reads element 0 there instead and the value is replaced afterwards:
+  // a load under a branch would make the wait for it, at the branch's end,
+  // wait for every load issued before it as well, and the other register
+  // slots would then be loaded only after the LDS slots had arrived.
   float x[kReg];
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
     const int v = v0 + k * kThreads;
-    x[k] = (k > 0 || v >= 0) ? ld_nt(lg + v) : kNegInf;
+    x[k] = ld_nt(lg + (k > 0 ? v : max(v, 0)));
   }
+  if (v0 < 0) x[0] = kNegInf;
   float m = kNegInit;
 #pragma unroll
   for (int k = 0; k < kReg; k++) m = max_rule(m, x[k]);
@@ -199,13 +205,13 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
   const UgkExpfAddends add = ugk_expf_addends_vgpr();
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
-    x[k] = ugk_expf_t<UGK_EXPF_CONTRACT>(x[k] - m, UgkExp2Lds{tab}, add);
+    x[k] = ugk_dev_expf_nonpos(x[k] - m, UgkExp2Lds{tab}, add);
     s += x[k];
     lo = min(lo, ugk_div_recip_key(x[k]));
   }
 #pragma unroll 1
   for (int k = 0; k < kLds; k++) {
-    const float e = ugk_expf_t<UGK_EXPF_CONTRACT>(part[k * kThreads + tid] - m, UgkExp2Lds{tab}, add);
+    const float e = ugk_dev_expf_nonpos(part[k * kThreads + tid] - m, UgkExp2Lds{tab}, add);
     part[k * kThreads + tid] = e;
     s += e;
     lo = min(lo, ugk_div_recip_key(e));
