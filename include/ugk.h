@@ -224,8 +224,9 @@ int ugk_version(void);
  * 1 / x for x >= 1 against the IEEE quotient; 54+j: x / b for eight
  * launch-wide divisors b (0.01, 0.1, 1e-3, 0.19, 2^-24, 1e-7, 0.999, 2^24) as
  * AdamW and the KL gradient divide, against the IEEE quotient; 62 the square
- * root AdamW takes, against the correctly rounded one; 63 the softmax's
- * branch-free expf for x <= 0 and NaN, against expf. */
+ * root AdamW takes, against the correctly rounded one; 63 the branch-free
+ * expf of the softmax and softplus, for x <= 88.72 (finite results) and NaN,
+ * against expf. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

@@ -520,7 +520,7 @@ def test_step_driver_matches_oracle_replay(gpu, oracle):
 # ---- the kernels' float math, exhaustively ------------------------------------------
 
 @pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus", "gelu", "gelu_grad", "sqrtf_large",
-                                "recip_ge1", "sqrtf_any", "expf_nonpos"] + [f"div_recip{j}" for j in range(8)] +
+                                "recip_ge1", "sqrtf_any", "expf_nooverflow"] + [f"div_recip{j}" for j in range(8)] +
                          [f"div_shared{j}" for j in range(8)])
 def test_device_math_exhaustive(gpu, fn):
     """The SIMD-shaped math (ugk_libm_dev.h) equals its line-by-line restatement of
@@ -534,7 +534,8 @@ def test_device_math_exhaustive(gpu, fn):
     with the library's operation outside them. div_shared<j> is AdamW's and the KL gradient's
     quotient by a launch-wide divisor (bias corrections, prior variance) and sqrtf_any AdamW's
     square root, against IEEE division and the correctly rounded root on every input.
-    expf_nonpos is the softmax's branch-free expf for x <= 0 and NaN, against expf."""
+    expf_nooverflow is the branch-free expf of the softmax and softplus, for x <= 88.72 and
+    NaN, against expf."""
     n, first = gpu.diag_math_mismatch(fn)
     assert n == 0, f"{fn}: {n} inputs differ, first bit pattern 0x{first:08x}"
 

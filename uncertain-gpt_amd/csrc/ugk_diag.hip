@@ -25,8 +25,8 @@ namespace {
 // for the sigmoid's quotient; 53: ugk_dev_recip_ge1, the one it uses, on the
 // same domain; 54+j: x / b for the launch-wide divisor kSharedDivisors[j] by
 // ugk_div_shared (reference x / b); 62: ugk_dev_sqrtf (reference as fn 7);
-// 63: ugk_dev_expf_nonpos on its domain, x <= 0 or NaN (ugk_expf_t
-// elsewhere; reference ugk_expf).
+// 63: ugk_dev_expf_nooverflow on its domain, x <= 0x1.62e42ep6 or NaN
+// (ugk_expf_t elsewhere; reference ugk_expf).
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -65,8 +65,8 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN >= 54 && FN < 62) return div_shared_by(x, FN - 54);
   if (FN == 62) return ugk_dev_sqrtf(x);
   if (FN == 63)
-    return (ugk_f2u(x) >> 31 || x != x) ? ugk_dev_expf_nonpos(x, UgkExp2Lds{tab}, UgkExpfAddends{})
-                                        : ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
+    return (x <= 0x1.62e42ep6f || x != x) ? ugk_dev_expf_nooverflow(x, UgkExp2Lds{tab}, UgkExpfAddends{})
+                                          : ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 

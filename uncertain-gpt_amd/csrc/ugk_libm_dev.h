@@ -377,14 +377,16 @@ __device__ __forceinline__ UgkExpfAddends ugk_expf_addends_vgpr() {
   return a;
 }
 
-// expf(x) for x <= 0 (-0 and -inf included) or NaN, the softmax's x - max,
-// without branches: expf's formula for every x, then its underflow case.
+// expf(x) without branches for x <= 0x1.62e42ep6 (the largest x whose expf
+// is finite; -inf included) or NaN: the softmax's x - max and softplus's
+// arguments up to 20. expf's formula for every x, then its underflow case.
 // Where that case does not apply (x >= -0x1.9fe368p6) the routine itself
 // takes the formula; for -inf it returns +0 as the underflow case does; for
-// NaN the formula gives a NaN. Checked against ugk_expf on every input of the
-// domain (ugk_diag.hip fn 63).
+// NaN the formula gives a NaN. Outside the domain the value is meaningless
+// (the table index stays in range). Checked against ugk_expf on every input
+// of the domain (ugk_diag.hip fn 63).
 template <class Tab>
-__device__ __forceinline__ float ugk_dev_expf_nonpos(float x, Tab tab, UgkExpfAddends add) {
+__device__ __forceinline__ float ugk_dev_expf_nooverflow(float x, Tab tab, UgkExpfAddends add) {
   const float y = ugk_expf_core<UGK_EXPF_CONTRACT>(x, tab, add);
   return x < -0x1.9fe368p6f ? 0.0f : y;
 }
@@ -395,5 +397,7 @@ __device__ __forceinline__ void ugk_exp2_stage(uint64_t *lds_tab) {
 }
 
 __device__ __forceinline__ float ugk_dev_softplusf_lds(float x, const uint64_t *lds_tab) {
-  return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{lds_tab}));
+  // expf is taken only for x <= 20, inside the branch-free form's domain
+  const float e = ugk_dev_expf_nooverflow(x, UgkExp2Lds{lds_tab}, UgkExpfAddends{});
+  return x > 20.0f ? x : ugk_dev_log1pf(e);
 }

@@ -87,7 +87,7 @@ __device__ __forceinline__ float neg_logf(float p) { return -(float)log((double)
 __device__ __forceinline__ void store_loss(float *losses, size_t row, const float *lg, int tgt, int skew, float m,
                                            float s, const uint64_t *tab, int threads) {
   if ((int)threadIdx.x == (tgt + skew) % threads)
-    losses[row] = neg_logf(ugk_dev_expf_nonpos(lg[tgt] - m, UgkExp2Lds{tab}, UgkExpfAddends{}) / s);
+    losses[row] = neg_logf(ugk_dev_expf_nooverflow(lg[tgt] - m, UgkExp2Lds{tab}, UgkExpfAddends{}) / s);
 }
 
 template <int kThreads, int kPer>
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void k_softmax_xent(float *__restrict__ l
 #pragma unroll
   for (int k = 0; k < kPer; k++) {
     const int v = tid + k * kThreads - skew;
-    x[k] = ugk_dev_expf_nonpos(x[k] - m, UgkExp2Lds{tab}, add);
+    x[k] = ugk_dev_expf_nooverflow(x[k] - m, UgkExp2Lds{tab}, add);
     lo = min(lo, ugk_div_recip_key(x[k]));
     if (v >= 0 && v < V) s += x[k];
   }
@@ -205,13 +205,13 @@ __global__ __launch_bounds__(kThreads, 2 * kThreads / kWave / 4) void k_softmax_
   const UgkExpfAddends add = ugk_expf_addends_vgpr();
 #pragma unroll
   for (int k = 0; k < kReg; k++) {
-    x[k] = ugk_dev_expf_nonpos(x[k] - m, UgkExp2Lds{tab}, add);
+    x[k] = ugk_dev_expf_nooverflow(x[k] - m, UgkExp2Lds{tab}, add);
     s += x[k];
     lo = min(lo, ugk_div_recip_key(x[k]));
   }
 #pragma unroll 1
   for (int k = 0; k < kLds; k++) {
-    const float e = ugk_dev_expf_nonpos(part[k * kThreads + tid] - m, UgkExp2Lds{tab}, add);
+    const float e = ugk_dev_expf_nooverflow(part[k * kThreads + tid] - m, UgkExp2Lds{tab}, add);
     part[k * kThreads + tid] = e;
     s += e;
     lo = min(lo, ugk_div_recip_key(e));

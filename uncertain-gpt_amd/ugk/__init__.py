@@ -399,8 +399,8 @@ MATH_FUNCTIONS.update({"recip_ge1": 53})
 # x / b for the launch-wide divisors of the posterior ops; sqrtf for any input
 MATH_FUNCTIONS.update({f"div_shared{j}": 54 + j for j in range(8)})
 MATH_FUNCTIONS.update({"sqrtf_any": 62})
-# expf for x <= 0 and NaN without branches (the softmax's)
-MATH_FUNCTIONS.update({"expf_nonpos": 63})
+# expf without branches for x <= 88.72 and NaN (the softmax's and softplus's)
+MATH_FUNCTIONS.update({"expf_nooverflow": 63})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
