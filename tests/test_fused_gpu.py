@@ -73,10 +73,14 @@ def test_fused_backward_rejects_aliased_dinp(gpu):
         gpu.layernorm_residual_backward(t, t, t, t, torch.zeros(64, device=DEV), t, t, t, t, t, 1, 4, 16)
 
 
-def test_step_driver_equals_per_op_replay_on_gpu(gpu):
+@pytest.mark.parametrize("B,T,L", [(2, 32, 3), (4, 128, 1)])
+def test_step_driver_equals_per_op_replay_on_gpu(gpu, B, T, L):
     """ugk_gpt2_layers_forward/backward (fused pairs) == the reference launch sequence issued op by
-    op through the same library, bit for bit, on every activation, gradient and parameter gradient."""
-    B, T, C, V, NH, maxT, L = 2, 32, 768, 50, 12, 64, 3
+    op through the same library, bit for bit, on every activation, gradient and parameter gradient.
+    The driver reduces all LayerNorms' partial rows in one batched launch, the per-op path each
+    in its own: the same additions in the same order (8 and 64 partial rows, 1 and 4 per group)."""
+    C, V, NH = 768, 50, 12
+    maxT = max(T, 64)
     cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=maxT, L=L)
     p, prel, a, arel = ref_offsets(B, T, C, V, maxT, L)
     g = gen.rng(67)
