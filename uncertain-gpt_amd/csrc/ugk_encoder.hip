@@ -578,14 +578,14 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
   if (BT == 0 || C == 0) return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return set_error(2, "encoder_backward: hipGetDevice failed");
+    return set_error(UGK_EHIP, "encoder_backward: hipGetDevice failed");
   std::lock_guard<std::mutex> lock(g_enc_mu);
   DevState &ds = g_state[dev];
   if (!ds.mem) {
     if (hipMalloc(&ds.mem, state_bytes()) != hipSuccess) {
       ds.mem = nullptr;
       (void)hipGetLastError();
-      return set_error(3, "encoder_backward: cannot allocate %zu bytes of bucket state", state_bytes());
+      return set_error(UGK_ENOMEM, "encoder_backward: cannot allocate %zu bytes of bucket state", state_bytes());
     }
     carve(ds);
     hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), ds.half[0],

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "ugk.h"  // status codes
+
 namespace ugk {
 
 constexpr int kWave = 64;      // CDNA wavefront width

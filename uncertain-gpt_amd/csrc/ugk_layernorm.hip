@@ -554,7 +554,7 @@ int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias
                                        const float *mean, const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
   float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
-  if (!partial) return 3;
+  if (!partial) return UGK_ENOMEM;
   int nblk;
   if (int e = launch_layernorm_backward_partials(dinp, partial, dx, dy, dout, inp, weight, mean, rstd, rows, C,
                                                  &nblk))

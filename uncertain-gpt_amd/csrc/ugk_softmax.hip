@@ -420,7 +420,7 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
     // Rows too long for the registers of one workgroup: a statistics pass
     // and a flat normalising pass (12 bytes per logit rather than 8).
     float2 *stats = static_cast<float2 *>(scratch((size_t)rows * sizeof(float2)));
-    if (!stats) return 3;
+    if (!stats) return UGK_ENOMEM;
     hipLaunchKernelGGL(k_softmax_stats, dim3(grid_for((size_t)rows, kStatsWaves)), dim3(kStatsWaves * kWave), 0,
                        stream(), stats, logits, rows, V);
     const size_t n = (size_t)rows * V;
