@@ -28,6 +28,16 @@
 // Whether each function equals the host glibc on ALL 2^32 inputs is checked
 // exhaustively by oracle/libm_exhaustive.cpp (CPU) and on the GPU by
 // tests/test_parity_gpu.py.
+//
+// Attribution. log1pf, expm1f and tanhf restate fdlibm, whose notice reads:
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
+// expf restates ARM optimized-routines' expf (Copyright (c) 2017-2018 Arm
+// Limited; MIT OR Apache-2.0 WITH LLVM-exception). The LICENSE file at the
+// repository root repeats both notices.
 #pragma once
 
 #include <stdint.h>
