@@ -11,33 +11,32 @@ output buffers hold synthetic data. A "step" is that sequence, queued by the
 native step driver of libugk.so (ugk_gpt2_layers_forward/backward), which runs
 each residual -> LayerNorm and LayerNorm -> residual pair as one pass and adds
 the LayerNorm weight/bias gradients of the whole backward in one launch; its
-buffers are bit-identical to the op-by-op sequence. The step's algorithmic
-bytes are still those of the unfused sequence (18.05 GB), so `value` is the
-effective rate of the reference's sequence.
+buffers are bit-identical to the op-by-op sequence.
 
 Printed JSON line (the last line of stdout):
-    value        algorithmic bytes of the step / step time, GB/s
-    ms_per_step  layer-kernel milliseconds per step (median-free mean over --steps)
-    configs      the same kernels at the shapes of BASELINE configs 2-4 (LayerNorm
-                 16384x768 and 256x384, GELU/residual over 50,331,648 values,
-                 encoder at B=16 T=1024 with uniform and Zipf(1.1) tokens), cold
-    head         softmax + cross-entropy forward and backward over B*T rows of
-                 V = 50257 logits, cold
-    posterior    the ops around the step over the same n parameters, cold:
-                 Philox sample, bayes/KL backward, AdamW, the fused BBB update,
-                 the KL total
-    kernels      each kernel at its step shape, cold (launches rotate over buffer
-                 sets totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds
-                 the operands): mean ms from HIP events, GB/s from algorithmic
-                 bytes, fraction of 8 TB/s; also the two fused pairs the step
-                 driver runs (residual -> LayerNorm forward, LayerNorm ->
-                 residual backward), with the pair's own bytes
-    roofline     the dominant kernel (most algorithmic bytes per step: GELU
-                 backward), achieved = algorithmic bytes per launch / its mean
-                 launch time above
-    cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this
-                 repo's bit-identical restatement) on one host core, timed per op
-                 at the step shapes and composed by launch count
+    value        the reference sequence's algorithmic bytes (18.05 GB, unfused) / step
+                 time: the effective rate of the reference's work; GBps_moved divides the
+                 bytes the fused sequence must move (16.84 GB) instead
+    ms_per_step  mean over --steps steps (events on the kernels' stream; median, p25, p75
+                 of the per-step times beside it)
+    in_step      each op of the step, timed inside the step with a HIP event pair that
+                 its kernel's dispatch records (the library's op timer), over --op-steps
+                 further steps: launches per step, mean us, us per step, algorithmic GB/s
+    roofline     the op with the most microseconds per step (the fused LayerNorm ->
+                 residual backward), achieved = its algorithmic bytes per launch / its mean
+                 in-step duration; traffic = HBM bytes per launch from rocprofv3 --pmc
+                 FETCH_SIZE and WRITE_SIZE runs (profiles/pmc_traffic_cfg5.json)
+    kernels      each kernel at its step shape, cold (launches rotate over buffer sets
+                 totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds the operands):
+                 median of 5 batches of back-to-back launches (p25, p75), GB/s from
+                 algorithmic bytes, fraction of 8 TB/s, and the stream ceiling of its mix
+    configs      the same kernels at BASELINE configs 2-4, cold
+    head         softmax + cross-entropy forward and backward over B*T rows of V = 50257
+    posterior    the ops around the step over the same n parameters, cold
+    cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this repo's
+                 bit-identical restatement) on one pinned host core: median of 5 runs per
+                 op at the config-5 step shapes (composed by launch count) and at configs
+                 2-4, with nproc, the CPU model and the glibc version
 """
 import argparse
 import ctypes
@@ -110,6 +109,11 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_stream<", "stream ceiling probe"),
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
+# in-step op name -> the prefix of its kernel's short name in the PMC summary
+PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main) <3, 8, 2, true",
+           "layernorm_backward (main)": "layernorm_backward (main) <3, 8, 2, false",
+           "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
+           "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 
 
 def short_name(name):
@@ -179,7 +183,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--reps", type=int, default=40, help="cold launches timed per kernel (at least one per buffer set)")
+    ap.add_argument("--reps", type=int, default=40,
+                    help="cold launches per timed batch of a kernel (at least one per buffer set); 5 batches")
+    ap.add_argument("--op-steps", type=int, default=3, help="steps timed op by op with the library's op timer")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other BASELINE configs")
     ap.add_argument("--no-head", action="store_true",
@@ -255,24 +261,66 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
+    ev[0].record()
+    for k in range(args.steps):
         step()
-    e1.record()
+        ev[k + 1].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
-    ms_step = e0.elapsed_time(e1) / args.steps
+    ms_step = ev[0].elapsed_time(ev[-1]) / args.steps
+    per_step = sorted(ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps))
+    q = lambda xs, f: xs[min(len(xs) - 1, int(f * (len(xs) - 1) + 0.5))]
+    step_stats = {"median": round(q(per_step, 0.5), 4), "p25": round(q(per_step, 0.25), 4),
+                  "p75": round(q(per_step, 0.75), 4)}
     value = total_bytes / (ms_step * 1e-3) / 1e9
-    log(f"bench: step {ms_step:.4f} ms (host wall {wall:.4f} ms) -> {value:.1f} GB/s algorithmic")
+    log(f"bench: step {ms_step:.4f} ms (median {step_stats['median']}, host wall {wall:.4f} ms) -> {value:.1f} GB/s "
+        f"on the reference's bytes, {moved_bytes / (ms_step * 1e-3) / 1e9:.1f} GB/s moved")
+
+    # ---- each op inside the step: a HIP event pair recorded by the dispatch of
+    # every kernel the step driver issues (ugk_op_timer; the three-kernel
+    # encoder backward is bracketed by two event records instead), over
+    # --op-steps further steps; materialize is bracketed here by two records
+    N = B * T * C
+    op_bytes = {  # algorithmic bytes per launch at the step shape
+        "encoder_forward": per["encoder_forward"], "layernorm_forward": per["layernorm_forward"],
+        "residual_layernorm_forward": 16 * N + 8 * B * T + 8 * C, "gelu_forward": per["gelu_forward"],
+        "layernorm_backward (main)": 16 * N + 8 * B * T + 4 * C,
+        "layernorm_residual_backward (main)": 32 * N + 8 * B * T + 4 * C,
+        "gelu_backward": per["gelu_backward"], "layernorm column sums (batched)": (2 * L + 1) * 16 * C,
+        "encoder_backward": per["encoder_backward"], "bayes_materialize": per["bayes_materialize"]}
+    m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    agg, mat_ms = {}, []
+    for _ in range(args.op_steps):
+        ugk.op_timer_start(1024)
+        m0.record()
+        chk(lib.ugk_bayes_materialize(wp, mup, rhop, epsp, n_mat))
+        m1.record()
+        chk(lib.ugk_gpt2_layers_forward(ap_, wp, ip, cfg, None))
+        chk(lib.ugk_gpt2_layers_backward(gp, gap, ap_, wp, ip, cfg, None))
+        for name, ms in ugk.op_timer_read(1024):
+            agg.setdefault(name, []).append(ms)
+        mat_ms.append(m0.elapsed_time(m1))
+    agg["bayes_materialize"] = mat_ms
+    in_step = {}
+    for name, ms_list in agg.items():
+        mean_ms = statistics.mean(ms_list)
+        per_launch = op_bytes[name]
+        gbs = per_launch / (mean_ms * 1e-3) / 1e9
+        in_step[name] = {"launches_per_step": len(ms_list) / args.op_steps, "mean_us": round(mean_ms * 1e3, 2),
+                         "us_per_step": round(sum(ms_list) * 1e3 / args.op_steps, 1), "bytes": per_launch,
+                         "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    for name, r in sorted(in_step.items(), key=lambda kv: -kv[1]["us_per_step"]):
+        log(f"bench: in-step {name:38s} x{r['launches_per_step']:4.0f} {r['mean_us']:8.2f} us "
+            f"{r['us_per_step']:8.1f} us/step {r['GBps']:8.1f} GB/s {100 * r['frac']:5.1f}%")
 
     # ---- each kernel alone at its step shape, cold ----------------------------
     # Each kernel cycles through k private buffer sets whose total exceeds
     # 1.5 GiB, so every launch finds its operands outside the L2 and the 256 MB
-    # MALL; R*k back-to-back launches sit between two HIP events on the stream
-    # the kernels run on, and the mean launch time is (t1 - t0) / (R*k).
-    N = B * T * C
+    # MALL; a batch of R*k back-to-back launches sits between two HIP events on
+    # the stream the kernels run on; the launch time is the median over 5
+    # batches of (t1 - t0) / (R*k).
     rnd = lambda n: torch.randn(n, generator=g, device=dev)
 
     def sets_for(make, set_bytes):
@@ -346,24 +394,31 @@ def main():
         torch.cuda.synchronize()
         rounds = max(1, args.reps // len(sets))
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(rounds):
-            for d in sets:
-                fn(d)
-        e.record()
-        e.synchronize()
-        ms = s.elapsed_time(e) / (rounds * len(sets))
+        batches = []
+        for _ in range(5):
+            s.record()
+            for _ in range(rounds):
+                for d in sets:
+                    fn(d)
+            e.record()
+            e.synchronize()
+            batches.append(s.elapsed_time(e) / (rounds * len(sets)))
+        batches.sort()
         n_sets = len(sets)
         del sets
         torch.cuda.empty_cache()
-        return ms, rounds * n_sets, n_sets
+        time_cold.spread = (batches[1], batches[3])
+        return batches[2], 5 * rounds * n_sets, n_sets
 
     def record(table, name, nbytes, ms, launches, n_sets, extra=None):
         gbs = nbytes / (ms * 1e-3) / 1e9
-        table[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
-                       "bytes": nbytes, "launches_timed": launches, "buffer_sets": n_sets, **(extra or {})}
+        p25, p75 = time_cold.spread
+        table[name] = {"ms": round(ms, 5), "ms_p25": round(p25, 5), "ms_p75": round(p75, 5), "GBps": round(gbs, 1),
+                       "frac": round(gbs / PEAK_GBS, 4), "bytes": nbytes, "launches_timed": launches,
+                       "buffer_sets": n_sets, **(extra or {})}
         log(f"bench: {name:34s} {ms * 1e3:9.2f} us  {gbs:8.1f} GB/s  {100 * gbs / PEAK_GBS:5.1f}% of peak"
-            f"  ({launches} launches over {n_sets} buffer sets)")
+            f"  (median of 5 batches, p25-p75 {p25 * 1e3:.2f}-{p75 * 1e3:.2f} us; {launches} launches over "
+            f"{n_sets} buffer sets)")
 
     kernels, mean_ms = {}, {}
     for name, (make, set_bytes, fn) in plan.items():
@@ -373,6 +428,13 @@ def main():
     for name, (make, set_bytes, nbytes, fn) in fused_plan.items():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
         record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 2 * L})
+    # materialize over the reference's own untied layout at this shape (it stores
+    # the head weight and bias, gpt2_kernels.cuh:681-683): all P parameters
+    ms, launches, n_sets = time_cold(lambda: {"mu": rnd(P) * 0.02, "rho": rnd(P) * 0.1 - 5.0, "eps": rnd(P),
+                                              "w": torch.empty(P, device=dev)}, 16 * P,
+                                     lambda d: chk(lib.ugk_bayes_materialize(P_(d["w"]), P_(d["mu"]), P_(d["rho"]),
+                                                                             P_(d["eps"]), P)))
+    record(kernels, f"bayes_materialize (untied layout, n={P})", 16 * P, ms, launches, n_sets, {"per_step": 0})
 
     # ---- the practical HBM ceiling of each kernel's load/store mix: a pure
     # stream (ugk_diag_stream) with the same number of input and output
@@ -448,9 +510,17 @@ def main():
                 return {"out": torch.empty(R2 * C, device=dev), "wte": rnd(V * C) * 0.02, "wpe": rnd(maxT * C) * 0.01,
                         "dout": rnd(R2 * C), "inp": tok}
             N4 = R2 * C
+            # the distinct wte rows a call gathers (the repeats of a Zipf batch come from cache), wpe's T
+            # rows, the output and the ids: the bytes that must cross HBM
+            probe = mk_enc4()
+            distinct = int(torch.unique(probe["inp"]).numel())
+            del probe
             ms, l_, k_ = time_cold(mk_enc4, 16 * N4, lambda d: chk(lib.ugk_encoder_forward(
                 P_(d["out"]), P_(d["inp"]), P_(d["wte"]), P_(d["wpe"]), B2, T2, C)))
-            record(configs, f"cfg4 {law} encoder_forward", 12 * N4 + 4 * R2, ms, l_, k_)
+            dbytes = 4 * C * (distinct + T2) + 4 * N4 + 4 * R2
+            record(configs, f"cfg4 {law} encoder_forward", 12 * N4 + 4 * R2, ms, l_, k_,
+                   {"distinct_tokens": distinct, "bytes_distinct_rows": dbytes,
+                    "frac_distinct_rows": round(dbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)})
             ms, l_, k_ = time_cold(mk_enc4, 16 * N4, lambda d: chk(lib.ugk_encoder_backward(
                 P_(d["wte"]), P_(d["wpe"]), P_(d["dout"]), P_(d["inp"]), B2, T2, C)))
             record(configs, f"cfg4 {law} encoder_backward", 20 * N4 + 4 * R2, ms, l_, k_)
@@ -508,17 +578,23 @@ def main():
             P_(d["dlogits"]), P_(d["probs"]), P_(d["targets"]), B, T, V)))
         record(head, "crossentropy_softmax_backward", 12 * NV + 4 * rows_h, ms, l_, k_)
 
-    # ---- roofline of the dominant kernel (most algorithmic bytes per step)
-    dom = max(per, key=lambda k: per[k] * count[k])
-    achieved = per[dom] / (mean_ms[dom] * 1e-3) / 1e9
+    # ---- roofline of the op with the most microseconds per step, from its in-step
+    # launches (a HIP event pair around each, on the library stream)
+    dom = max(in_step, key=lambda k: in_step[k]["us_per_step"])
+    d = in_step[dom]
+    achieved = d["bytes"] / (d["mean_us"] * 1e-6) / 1e9
     traffic, traffic_src = None, None
     if os.path.exists(PMC_TRAFFIC):  # recorded by two rocprofv3 --pmc runs of this script
-        rec_k = json.load(open(PMC_TRAFFIC)).get("kernels", {}).get(dom)
-        if rec_k:
-            traffic, traffic_src = rec_k["traffic_bytes"], os.path.relpath(PMC_TRAFFIC, ROOT)
+        pmc = json.load(open(PMC_TRAFFIC)).get("kernels", {})
+        key = next((k for k in pmc if k.startswith(PMC_KEY.get(dom, dom))), None)
+        if key:
+            traffic, traffic_src = pmc[key]["traffic_bytes"], f"{os.path.relpath(PMC_TRAFFIC, ROOT)}: {key}"
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                "launch_ms": round(mean_ms[dom], 5), "bytes_per_launch": per[dom]}
+                "launch_ms": round(d["mean_us"] * 1e-3, 5), "bytes_per_launch": d["bytes"],
+                "launches_per_step": d["launches_per_step"], "us_per_step": d["us_per_step"],
+                "measured": f"in-step: a HIP event pair recorded by each of its dispatches (ugk op timer, "
+                            f"hipExtLaunchKernelGGL), {args.op_steps} steps"}
 
     # a plain 1 GiB device-to-device copy (torch's copy kernel): the known-size
     # reference that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings
@@ -528,7 +604,7 @@ def main():
     torch.cuda.synchronize()
     del calib
 
-    cpu = None if args.no_cpu else cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes)
+    cpu = None if args.no_cpu else cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes)
 
     rec = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -538,64 +614,141 @@ def main():
                                "(materialize + encoder/LN/GELU/residual fwd+bwd)",
                    "L": L, "H": NH, "C": C, "V": V, "B": B, "T": T, "materialize_n": n_mat,
                    "param_layout_n": P, "parallelism": "single GPU"},
+        "ms_per_step_stats": step_stats, "value_basis": "reference sequence's algorithmic bytes (unfused) / step time",
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
         "bytes_per_step_moved": moved_bytes, "GBps_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "frac_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4), "in_step": in_step,
         "kernels": kernels, "configs": configs, "posterior": posterior, "head": head, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
 
 
-def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes):
-    """Each CPU op at the step shape, best of 10 runs (materialize on a 1/8 slice,
-    scaled), composed by launch count; single-threaded, like train_bnn.c. About
-    10 s of CPU work in all."""
+def host_facts():
+    """nproc, the CPU model and the C library of the host the baseline runs on."""
+    import platform
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = " ".join(platform.libc_ver())
+    return {"nproc": os.cpu_count(), "cpus_allowed": len(os.sched_getaffinity(0)), "cpu_model": model,
+            "libc": libc}
+
+
+def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes):
+    """The reference's CPU ops (train_bnn.c, single-threaded) on one pinned core: the median of
+    5 runs of each op at the config-5 step shapes, composed by launch count into a step, and at
+    the shapes of configs 2-4 (GELU/residual over 50.3M values on a 1/8 slice, scaled;
+    materialize on a 1/8 slice, scaled). About 10-20 s of CPU work in all."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, REF_SO
     kind = "reference" if os.path.exists(REF_SO) else "port"
     o = Oracle(reference=(kind == "reference"))
-    rng = np.random.Generator(np.random.Philox(key=7))
-    N = B * T * C
-    f = lambda n: rng.standard_normal(n, dtype=np.float32)
-    x, y, d = f(N), f(N), f(N)
-    h, hd = f(4 * N), f(4 * N)
-    wv, bv = np.ones(C, np.float32), np.zeros(C, np.float32)
-    mean, rstd = np.zeros(B * T, np.float32), np.zeros(B * T, np.float32)
-    out, out4 = np.zeros(N, np.float32), np.zeros(4 * N, np.float32)
-    inp = rng.integers(0, V, B * T, dtype=np.int32)
-    wte, wpe = f(V * C) * np.float32(0.02), f(T * C) * np.float32(0.01)
-    dwte, dwpe = np.zeros(V * C, np.float32), np.zeros(T * C, np.float32)
-    dwl, dbl = np.zeros(C, np.float32), np.zeros(C, np.float32)
-    ns = n_mat // 8
-    mu, rh, ep, wm = f(ns) * np.float32(0.02), f(ns) * np.float32(0.1) - np.float32(5), f(ns), np.zeros(ns, np.float32)
-    ops = {
-        "encoder_forward": (lambda: o.encoder_forward(out, inp, wte, wpe, B, T, C), 1),
-        "encoder_backward": (lambda: o.encoder_backward(dwte, dwpe, d, inp, B, T, C), 1),
-        "layernorm_forward": (lambda: o.layernorm_forward(out, mean, rstd, x, wv, bv, B, T, C), 1),
-        "layernorm_backward": (lambda: o.layernorm_backward(y, dwl, dbl, d, x, wv, mean, rstd, B, T, C), 1),
-        "gelu_forward": (lambda: o.gelu_forward(out4, h, 4 * N), 1),
-        "gelu_backward": (lambda: o.gelu_backward(hd, h, out4, 4 * N), 1),
-        "residual_forward": (lambda: o.residual_forward(out, x, y, N), 1),
-        "residual_backward": (lambda: o.residual_backward(y, out, d, N), 1),
-        "bayes_materialize": (lambda: o.bayes_materialize(wm, mu, rh, ep, ns), n_mat / ns),
-    }
-    t_op, t_sample = {}, 0.0
-    for name, (fn, scale) in ops.items():
-        best = None
-        for _ in range(10):
-            t0 = time.perf_counter()
-            fn()
-            dt = time.perf_counter() - t0
-            t_sample += dt
-            best = dt if best is None else min(best, dt)
-        t_op[name] = best * scale
-    step_s = sum(t_op[k] * count[k] for k in t_op)
-    gbs = total_bytes / step_s / 1e9
-    log(f"bench: cpu ({kind}, 1 core) step {step_s * 1e3:.1f} ms -> {gbs:.2f} GB/s; sample {t_sample:.1f} s")
+    facts = host_facts()
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[len(allowed) // 2]
+    os.sched_setaffinity(0, {core})
+    try:
+        rng = np.random.Generator(np.random.Philox(key=7))
+        f = lambda n: rng.standard_normal(n, dtype=np.float32)
+        reps = 5
+        t_sample = 0.0
+
+        def med(fn, scale=1.0):
+            nonlocal t_sample
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            t_sample += sum(ts)
+            ts.sort()
+            return ts[reps // 2] * scale, ts[1] * scale, ts[3] * scale
+
+        # config 5, the step's shapes
+        N = B * T * C
+        x, y, d = f(N), f(N), f(N)
+        h, hd = f(4 * N), f(4 * N)
+        wv, bv = np.ones(C, np.float32), np.zeros(C, np.float32)
+        mean, rstd = np.zeros(B * T, np.float32), np.zeros(B * T, np.float32)
+        out, out4 = np.zeros(N, np.float32), np.zeros(4 * N, np.float32)
+        inp = rng.integers(0, V, B * T, dtype=np.int32)
+        wte, wpe = f(V * C) * np.float32(0.02), f(T * C) * np.float32(0.01)
+        dwte, dwpe = np.zeros(V * C, np.float32), np.zeros(T * C, np.float32)
+        dwl, dbl = np.zeros(C, np.float32), np.zeros(C, np.float32)
+        ns = n_mat // 8
+        mu, rh, ep, wm = f(ns) * np.float32(0.02), f(ns) * np.float32(0.1) - np.float32(5), f(ns), np.zeros(ns, np.float32)
+        ops = {
+            "encoder_forward": (lambda: o.encoder_forward(out, inp, wte, wpe, B, T, C), 1),
+            "encoder_backward": (lambda: o.encoder_backward(dwte, dwpe, d, inp, B, T, C), 1),
+            "layernorm_forward": (lambda: o.layernorm_forward(out, mean, rstd, x, wv, bv, B, T, C), 1),
+            "layernorm_backward": (lambda: o.layernorm_backward(y, dwl, dbl, d, x, wv, mean, rstd, B, T, C), 1),
+            "gelu_forward": (lambda: o.gelu_forward(out4, h, 4 * N), 1),
+            "gelu_backward": (lambda: o.gelu_backward(hd, h, out4, 4 * N), 1),
+            "residual_forward": (lambda: o.residual_forward(out, x, y, N), 1),
+            "residual_backward": (lambda: o.residual_backward(y, out, d, N), 1),
+            "bayes_materialize": (lambda: o.bayes_materialize(wm, mu, rh, ep, ns), n_mat / ns),
+        }
+        t_op, spread = {}, {}
+        for name, (fn, scale) in ops.items():
+            t_op[name], lo, hi = med(fn, scale)
+            spread[name] = (lo, hi)
+        del x, y, d, h, hd, out, out4, wte, dwte, mu, rh, ep, wm
+        step_s = sum(t_op[k] * count[k] for k in t_op)
+        gbs = total_bytes / step_s / 1e9
+        # configs 2-4
+        cfgs = {}
+        for rows, Cc in ((256, 384), (16384, 768)):
+            n2 = rows * Cc
+            x2, d2, y2 = f(n2), f(n2), f(n2)
+            w2, b2 = np.ones(Cc, np.float32), np.zeros(Cc, np.float32)
+            m2, r2, o2 = np.zeros(rows, np.float32), np.zeros(rows, np.float32), np.zeros(n2, np.float32)
+            g2, bb2 = np.zeros(Cc, np.float32), np.zeros(Cc, np.float32)
+            t, _, _ = med(lambda: o.layernorm_forward(o2, m2, r2, x2, w2, b2, 1, rows, Cc))
+            cfgs[f"cfg2 {rows}x{Cc} layernorm_forward"] = t
+            t, _, _ = med(lambda: o.layernorm_backward(y2, g2, bb2, d2, x2, w2, m2, r2, 1, rows, Cc))
+            cfgs[f"cfg2 {rows}x{Cc} layernorm_backward"] = t
+        n3 = 16 * 1024 * 3072
+        s3 = n3 // 8
+        a3, b3, c3, e3 = f(s3), f(s3), f(s3), np.zeros(s3, np.float32)
+        for nm, fn in (("gelu_forward", lambda: o.gelu_forward(e3, a3, s3)),
+                       ("gelu_backward", lambda: o.gelu_backward(c3, a3, b3, s3)),
+                       ("residual_forward", lambda: o.residual_forward(e3, a3, b3, s3)),
+                       ("residual_backward", lambda: o.residual_backward(c3, e3, b3, s3))):
+            cfgs[f"cfg3 N={n3} {nm}"] = med(fn, 8.0)[0]
+        del a3, b3, c3, e3
+        B4, T4 = 16, 1024
+        n4 = B4 * T4 * C
+        d4, o4 = f(n4), np.zeros(n4, np.float32)
+        wte4, wpe4 = f(V * C) * np.float32(0.02), f(T4 * C) * np.float32(0.01)
+        dwte4, dwpe4 = np.zeros(V * C, np.float32), np.zeros(T4 * C, np.float32)
+        wcdf = np.cumsum(1.0 / np.arange(1, V + 1, dtype=np.float64) ** 1.1)
+        wcdf /= wcdf[-1]
+        for law in ("uniform", "zipf1.1"):
+            tok = (rng.integers(0, V, B4 * T4, dtype=np.int32) if law == "uniform" else
+                   np.minimum(np.searchsorted(wcdf, rng.random(B4 * T4)), V - 1).astype(np.int32))
+            cfgs[f"cfg4 {law} encoder_forward"] = med(lambda: o.encoder_forward(o4, tok, wte4, wpe4, B4, T4, C))[0]
+            cfgs[f"cfg4 {law} encoder_backward"] = med(lambda: o.encoder_backward(dwte4, dwpe4, d4, tok, B4, T4, C))[0]
+    finally:
+        os.sched_setaffinity(0, set(allowed))
+    log(f"bench: cpu ({kind}, 1 core: cpu {core}) step {step_s * 1e3:.1f} ms -> {gbs:.2f} GB/s; "
+        f"sample {t_sample:.1f} s; {facts}")
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": kind, "ms_per_step": round(step_s * 1e3, 1),
+            "GBps_moved_equivalent": round(moved_bytes / step_s / 1e9, 3), "pinned_cpu": core, **facts,
             "per_op_ms": {k: round(v * 1e3, 2) for k, v in t_op.items()},
-            "sample": "each train_bnn.c op at the config-5 step shape, best of 10 runs "
-                      "(materialize on a 1/8 slice, scaled), summed by launch count per step; "
+            "per_op_ms_p25_p75": {k: [round(a * 1e3, 2), round(b * 1e3, 2)] for k, (a, b) in spread.items()},
+            "configs_ms": {k: round(v * 1e3, 3) for k, v in cfgs.items()},
+            "sample": "train_bnn.c's ops on one pinned core, median of 5 runs each: at the config-5 step "
+                      "shapes (materialize on a 1/8 slice, scaled) composed by launch count per step, and at the "
+                      "config 2-4 shapes (config-3 ops on a 1/8 slice, scaled); "
                       f"{t_sample:.1f} s of CPU work"}
 
 

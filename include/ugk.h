@@ -16,19 +16,28 @@
  *     and a call returns before the GPU has finished.
  * Semantics are the reference's: backward outputs ACCUMULATE (+=) into the
  * caller's buffers, and the caller zeroes them when it wants plain gradients.
- * Results: encoder fwd/bwd, residual fwd/bwd, GELU fwd/bwd and
- * bayes_materialize are bit-identical to train_bnn.c on a host with glibc 2.35
- * and FMA; LayerNorm row statistics and dinp are within fp32 rounding of it,
- * and LayerNorm dweight/dbias are reduced in a fixed, run-to-run deterministic
- * order.
+ * Results: encoder fwd/bwd, residual fwd/bwd and bayes_materialize are
+ * bit-identical to train_bnn.c on a host with glibc 2.35 and FMA; GELU fwd/bwd
+ * are within 1e-5 relative / 1e-6 absolute of it on every input, and
+ * bit-identical after ugk_set_gelu_exact(1); LayerNorm row statistics and dinp
+ * are within fp32 rounding of it, and LayerNorm dweight/dbias are reduced in a
+ * fixed, run-to-run deterministic order.
  *
- * The library never allocates inside a kernel. It owns one scratch buffer per
- * device (LayerNorm-backward partial sums, the KL partial sums), allocated on
- * the first call that needs it and grown only when a larger shape arrives
- * (ugk_reserve() allocates it up front), and the encoder backward's bucket
- * state, a fixed allocation made on its first call on a device. Both are
- * used in stream order: ugk_set_stream waits for the work already queued on
- * the previous stream, so calls on two streams never share them at once.
+ * The library never allocates inside a kernel. A few entry points need device
+ * workspace beyond their arguments: the LayerNorm backward's partial column
+ * sums (one slot per call, 2L+1 for the step driver), the encoder backward's
+ * bucket state, the KL total's partial sums and the long-row softmax's row
+ * statistics, each in a region of its own. By default the library allocates
+ * a region on the first call that needs it and grows it, after waiting for
+ * the device, when a larger shape arrives; ugk_reserve / ugk_reserve_config
+ * allocate everything up front, after which calls at those shapes neither
+ * allocate nor wait. A caller that owns all device memory (as the reference's
+ * arms do) sizes a workspace with ugk_workspace_bytes and hands it over with
+ * ugk_set_workspace; the library then never allocates. The workspace is used
+ * in stream order: ugk_set_stream waits for the work already queued on the
+ * previous stream, so calls on two streams never share it at once. The
+ * library's state is per device and meant for one host thread per device at a
+ * time, as the reference's one host thread and one stream.
  */
 #ifndef UGK_H
 #define UGK_H
@@ -54,11 +63,9 @@ int ugk_encoder_forward(float *out, const int *inp, const float *wte,
  * dwte[inp[b,t],:] += dout[b,t,:];  dwpe[t,:] += dout[b,t,:].
  * Each row's contributions are added in ascending (b,t) order, the order of
  * the CPU loop, so the result is deterministic and bit-identical to it. Rows
- * with a negative token are skipped. Its bucket table (per device) is
- * double-buffered and the host picks the half each call uses, alternating:
- * a HIP graph that captures these calls must hold an even number of them
- * per 65,536-row chunk, all of one shape, and the calls made after capture
- * must be replays or made before the next capture. */
+ * with a negative token are skipped. Its bucket table lives in the workspace
+ * and every call leaves it cleared, on the device, so the calls may be
+ * captured in a HIP graph and replayed any number of times. */
 int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout,
                          const int *inp, int B, int T, int C);
 
@@ -97,12 +104,23 @@ int ugk_layernorm_residual_backward(float *dinp, float *dweight, float *dbias,
                                     const float *mean, const float *rstd,
                                     int B, int T, int C);
 
-/* train_bnn.c:163-170 / gpt2_kernels.cuh:318-325 (k_gelu_forward). */
+/* train_bnn.c:163-170 / gpt2_kernels.cuh:318-325 (k_gelu_forward).
+ * By default GELU is evaluated as x / (1 + e^{-2u}), the same function
+ * through the hardware exponential and reciprocal: within 1e-5 relative /
+ * 1e-6 absolute of train_bnn.c on every float input, not bit-identical to it.
+ * After ugk_set_gelu_exact(1) both GELU entry points (and the step driver)
+ * use a restatement of glibc's tanhf and equal train_bnn.c bit for bit. */
 int ugk_gelu_forward(float *out, const float *inp, int N);
 
 /* train_bnn.c:520-533 / gpt2_kernels.cuh:327-338 (k_gelu_backward).
- * dinp += gelu'(inp) * dout. */
+ * dinp += gelu'(inp) * dout; the form follows ugk_set_gelu_exact. */
 int ugk_gelu_backward(float *dinp, const float *inp, const float *dout, int N);
+
+/* GELU form for later calls from any thread: 0 (the default) the logistic
+ * form above, nonzero the glibc-exact tanhf. No counterpart in the reference,
+ * whose CPU and GPU builds each use their own tanhf. */
+int ugk_set_gelu_exact(int exact);
+int ugk_get_gelu_exact(void);
 
 /* train_bnn.c:182-186 / gpt2_kernels.cuh:340-344 (k_residual_forward). */
 int ugk_residual_forward(float *out, const float *x, const float *y, int N);
@@ -200,10 +218,10 @@ const char *ugk_last_error(void);
  * the previous one (it may still use the library's scratch). */
 int ugk_set_stream(void *stream);
 void *ugk_get_stream(void);
-/* Allocate the current device's scratch for shapes up to (rows = B*T, C)
- * now instead of on first use. */
+/* Allocate the current device's workspace for the per-op entry points at
+ * shapes up to (rows = B*T, C) now instead of on first use. */
 int ugk_reserve(int rows, int C);
-/* Bytes of scratch currently held on the current device. */
+/* Bytes of workspace held on the current device (the caller's, if set). */
 size_t ugk_scratch_bytes(void);
 /* Wait for all work queued on the library's stream. */
 int ugk_synchronize(void);
@@ -226,7 +244,9 @@ int ugk_version(void);
  * AdamW and the KL gradient divide, against the IEEE quotient; 62 the square
  * root AdamW takes, against the correctly rounded one; 63 the branch-free
  * expf of the softmax and softplus, for x <= 88.72 (finite results) and NaN,
- * against expf. */
+ * against expf; 64 and 65 the default GELU and its derivative (logistic
+ * form) against fn 8 and 9's glibc-exact expressions, counting results
+ * outside |a - b| <= 1e-6 + 1e-5 |b|. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line
@@ -285,6 +305,46 @@ typedef struct {
 size_t ugk_param_count(ugk_config cfg);
 size_t ugk_act_count(ugk_config cfg);
 
+/* ---- workspace (no counterpart in the reference: its kernels need none
+ * beyond their arguments, and the caller owns every buffer, _C.cu:239-244) */
+
+/* Bytes of device workspace every entry point needs at shapes up to cfg:
+ * rows B*T of C channels, the step driver's L blocks, V logits per row. */
+size_t ugk_workspace_bytes(ugk_config cfg);
+/* Allocate the current device's workspace for shapes up to cfg now (library
+ * owned, like ugk_reserve, but also covering the step driver). */
+int ugk_reserve_config(ugk_config cfg);
+/* Hand the current device a caller-owned workspace of `bytes` device bytes
+ * (256-byte aligned, at least ugk_workspace_bytes(cfg)) for shapes up to cfg.
+ * The library frees its own regions (after waiting for the device) and from
+ * then on allocates nothing on this device; a call whose shape needs more
+ * than cfg provides fails with UGK_ENOMEM. The memory must stay valid and be
+ * left to the library until the next ugk_set_workspace on this device; NULL
+ * returns to library-owned regions. Waits for the library stream. */
+int ugk_set_workspace(void *ptr, size_t bytes, ugk_config cfg);
+
+/* ---- per-op timing of the step driver (no counterpart in the reference,
+ * which times single launches with cudaEvents in its dev/ harnesses). While
+ * started, ugk_gpt2_layers_forward/backward time each library op they issue
+ * (at most `capacity`) with a pair of HIP events: an op of one kernel has
+ * them recorded by its dispatch (hipExtLaunchKernelGGL), so they measure the
+ * kernel itself; the encoder backward (three kernels) is bracketed by two
+ * event records on the library stream. ugk_op_timer_read waits for the last
+ * event, writes each op's duration in milliseconds and its kind (UGK_OP_*)
+ * in issue order, sets *count, and stops the timer. The events are created by
+ * ugk_op_timer_start. */
+#define UGK_OP_ENCODER_FORWARD 1
+#define UGK_OP_LAYERNORM_FORWARD 2
+#define UGK_OP_RESIDUAL_LAYERNORM_FORWARD 3
+#define UGK_OP_GELU_FORWARD 4
+#define UGK_OP_LAYERNORM_BACKWARD_MAIN 5          /* dinp + partial column sums */
+#define UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN 6 /* the same, fused with residual_backward */
+#define UGK_OP_GELU_BACKWARD 7
+#define UGK_OP_LAYERNORM_COLUMN_SUMS 8            /* all LayerNorms' dweight/dbias, batched */
+#define UGK_OP_ENCODER_BACKWARD 9
+int ugk_op_timer_start(int capacity);
+int ugk_op_timer_read(float *ms, int *ops, int capacity, int *count);
+
 /* Forward from the encoder to the final LayerNorm (gpt2_kernels.cuh:775-813).
  * The head GEMM and softmax/cross-entropy are not part of it. */
 int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
@@ -294,9 +354,9 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
  * (gpt2_kernels.cuh:846-894). On entry grads_acts holds d(final LN output)
  * at the reference's flo offset; accumulates into grads and grads_acts. The
  * LayerNorm dweight/dbias column sums are completed by one launch at the end,
- * and their partial rows live in the library scratch meanwhile, so the dense
- * callbacks must not call the entry points that use the scratch
- * (ugk_layernorm_backward, ugk_layernorm_residual_backward, ugk_kl_forward). */
+ * and their partial rows live in the workspace's LayerNorm region meanwhile,
+ * so the dense callbacks must not call ugk_layernorm_backward or
+ * ugk_layernorm_residual_backward (the other entry points use other regions). */
 int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                              const float *params, const int *inputs,
                              ugk_config cfg, const ugk_dense_ops *ops);

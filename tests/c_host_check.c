@@ -6,9 +6,10 @@
  * infrastructure) on the same seeded inputs, at config 1's shapes (B=4, T=64,
  * C=384, V=27) and a materialize over 100,003 parameters.
  *
- * Bars: bit-exact for the encoder, GELU, residual and materialize; 1e-5
- * relative + 1e-6 absolute for LayerNorm (2e-5 absolute for its column
- * sums). Also checks the error channel: a NULL pointer returns UGK_EINVAL with
+ * Bars: bit-exact for the encoder, residual, materialize and GELU in its
+ * glibc-exact mode; 1e-5 relative + 1e-6 absolute for LayerNorm (2e-5
+ * absolute for its column sums) and the default GELU (1e-5 absolute for its
+ * accumulated backward, whose upstream gradients are of order 1). Also checks the error channel: a NULL pointer returns UGK_EINVAL with
  * a message, and zero-size work returns UGK_OK.
  *
  * Prints one line per check and "c host check: <n> failures"; the exit status
@@ -147,12 +148,22 @@ int main(void) {
   float *d_h = to_device(h, N4 * 4), *d_hout = to_device(hout, N4 * 4);
   call_ok(ugk_gelu_forward(d_hout, d_h, (int)N4), "ugk_gelu_forward");
   oracle_gelu_forward(hout, h, (int)N4);
-  check("gelu_forward out", d_hout, hout, N4, 0, 0);
+  check("gelu_forward out", d_hout, hout, N4, 1e-5, 1e-6);
   float *hd = host_normal(N4, 0.0f, 1.0f), *hdin = host_normal(N4, 0.0f, 1.0f);
+  float *hdin0 = malloc(N4 * 4);
+  memcpy(hdin0, hdin, N4 * 4);
   float *d_hd = to_device(hd, N4 * 4), *d_hdin = to_device(hdin, N4 * 4);
   call_ok(ugk_gelu_backward(d_hdin, d_h, d_hd, (int)N4), "ugk_gelu_backward");
   oracle_gelu_backward(hdin, h, hd, (int)N4);
-  check("gelu_backward dinp", d_hdin, hdin, N4, 0, 0);
+  check("gelu_backward dinp", d_hdin, hdin, N4, 1e-5, 1e-5);
+  /* the glibc-exact mode: bit for bit */
+  call_ok(ugk_set_gelu_exact(1), "ugk_set_gelu_exact");
+  call_ok(ugk_gelu_forward(d_hout, d_h, (int)N4), "ugk_gelu_forward (exact)");
+  check("gelu_forward out (exact)", d_hout, hout, N4, 0, 0);
+  float *d_hdin0 = to_device(hdin0, N4 * 4);
+  call_ok(ugk_gelu_backward(d_hdin0, d_h, d_hd, (int)N4), "ugk_gelu_backward (exact)");
+  check("gelu_backward dinp (exact)", d_hdin0, hdin, N4, 0, 0);
+  call_ok(ugk_set_gelu_exact(0), "ugk_set_gelu_exact");
 
   /* residual */
   float *y = host_normal(NB, 0.0f, 1.0f);

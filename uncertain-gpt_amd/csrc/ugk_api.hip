@@ -24,14 +24,87 @@ thread_local char g_err[512] = "";
 std::atomic<hipStream_t> g_stream{nullptr};
 std::mutex g_mu;
 constexpr int kMaxDevices = 64;
-struct Scratch {
-  void *ptr = nullptr;
-  size_t bytes = 0;
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+const char *const kRegionName[kNumRegions] = {"LayerNorm partial rows", "encoder bucket state", "KL partial sums",
+                                              "softmax row statistics"};
+
+// Per device: the library's own region allocations, or the caller's workspace
+// and the offset and capacity of each region in it.
+struct DevWorkspace {
+  void *own[kNumRegions] = {};
+  size_t own_bytes[kNumRegions] = {};
+  char *user = nullptr;
+  size_t user_bytes = 0;
+  size_t off[kNumRegions] = {}, cap[kNumRegions] = {};
+  bool fresh[kNumRegions] = {true, true, true, true};
 };
-Scratch g_scratch[kMaxDevices];
+DevWorkspace g_ws[kMaxDevices];
+
+int current_device(const char *what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  (void)what;
+  return dev;
+}
+
+// Region sizes for every entry point at shapes up to cfg: the step driver's
+// 2L+1 LayerNorm slots (at least the one slot of a per-op call), the encoder
+// state, the KL partial sums and the softmax statistics of B*T rows.
+void region_sizes(const ugk_config &cfg, size_t out[kNumRegions]) {
+  const int rows = cfg.B * cfg.T;
+  const size_t slot = align_up(layernorm_backward_scratch(rows, cfg.C));
+  out[kRegLn] = slot * (size_t)(2 * (cfg.L > 0 ? cfg.L : 0) + 1);
+  out[kRegEncoder] = encoder_backward_scratch();
+  out[kRegKl] = kl_forward_scratch();
+  out[kRegSoftmax] = softmax_scratch(rows, cfg.V);
+}
+
+// Grow the library-owned region r of device dev to `bytes` (lock held).
+void *own_region(DevWorkspace &w, Region r, size_t bytes) {
+  if (w.own[r] && w.own_bytes[r] >= bytes) return w.own[r];
+  if (w.own[r]) {
+    // kernels queued earlier, on this or another stream, may still use the old buffer
+    (void)hipDeviceSynchronize();
+    (void)hipFree(w.own[r]);
+    w.own[r] = nullptr;
+    w.own_bytes[r] = 0;
+  }
+  const size_t want = align_up(bytes < ((size_t)1 << 16) ? ((size_t)1 << 16) : bytes);
+  if (hipMalloc(&w.own[r], want) != hipSuccess) {
+    (void)hipGetLastError();
+    w.own[r] = nullptr;
+    set_error(UGK_ENOMEM, "workspace: cannot allocate %zu bytes for the %s", want, kRegionName[r]);
+    return nullptr;
+  }
+  w.own_bytes[r] = want;
+  w.fresh[r] = true;
+  return w.own[r];
+}
+
+void free_own(DevWorkspace &w) {
+  bool any = false;
+  for (int r = 0; r < kNumRegions; r++) any = any || w.own[r];
+  if (!any) return;
+  (void)hipDeviceSynchronize();
+  for (int r = 0; r < kNumRegions; r++) {
+    if (w.own[r]) (void)hipFree(w.own[r]);
+    w.own[r] = nullptr;
+    w.own_bytes[r] = 0;
+    w.fresh[r] = true;
+  }
+}
 }  // namespace
 
 hipStream_t stream() { return g_stream.load(std::memory_order_relaxed); }
+
+LaunchEvents *&armed_events() {
+  thread_local LaunchEvents *armed = nullptr;
+  return armed;
+}
 
 int set_error(int code, const char *fmt, ...) {
   va_list ap;
@@ -47,39 +120,44 @@ int check_launch(const char *what) {
   return UGK_OK;
 }
 
-void *scratch(size_t bytes) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    set_error(UGK_EHIP, "scratch: hipGetDevice failed");
+void *workspace(Region r, size_t bytes, bool *fresh) {
+  const int dev = current_device("workspace");
+  if (dev < 0) {
+    set_error(UGK_EHIP, "workspace: hipGetDevice failed");
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_mu);
-  Scratch &s = g_scratch[dev];
-  if (s.bytes >= bytes && s.ptr) return s.ptr;
-  if (s.ptr) {
-    // kernels queued earlier, on this or another stream, may still use the
-    // old buffer
-    (void)hipDeviceSynchronize();
-    (void)hipFree(s.ptr);
-    s.ptr = nullptr;
-    s.bytes = 0;
+  DevWorkspace &w = g_ws[dev];
+  void *p;
+  if (w.user) {
+    if (bytes > w.cap[r]) {
+      set_error(UGK_ENOMEM,
+                "workspace: the %s need %zu bytes, the caller's workspace holds %zu for them (size it with "
+                "ugk_workspace_bytes for the largest shape)",
+                kRegionName[r], bytes, w.cap[r]);
+      return nullptr;
+    }
+    p = w.user + w.off[r];
+  } else {
+    p = own_region(w, r, bytes);
+    if (!p) return nullptr;
   }
-  size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-  if (hipMalloc(&s.ptr, want) != hipSuccess) {
-    (void)hipGetLastError();
-    s.ptr = nullptr;
-    set_error(UGK_ENOMEM, "scratch: cannot allocate %zu bytes", want);
-    return nullptr;
+  if (fresh) {  // the fresh mark is for the region's user, not for ugk_reserve*
+    *fresh = w.fresh[r];
+    w.fresh[r] = false;
   }
-  s.bytes = want;
-  return s.ptr;
+  return p;
 }
 
-size_t scratch_bytes_current() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+size_t workspace_bytes_current() {
+  const int dev = current_device("ugk_scratch_bytes");
+  if (dev < 0) return 0;
   std::lock_guard<std::mutex> lock(g_mu);
-  return g_scratch[dev].bytes;
+  const DevWorkspace &w = g_ws[dev];
+  if (w.user) return w.user_bytes;
+  size_t t = 0;
+  for (int r = 0; r < kNumRegions; r++) t += w.own_bytes[r];
+  return t;
 }
 
 }  // namespace ugk
@@ -295,7 +373,7 @@ int ugk_kl_forward(double *kl, const float *mu, const float *rho, size_t n, floa
     return ok();
   }
   if (any_null({mu, rho})) return bad(fn, "NULL pointer");
-  double *buf = static_cast<double *>(scratch(kl_forward_scratch()));
+  double *buf = static_cast<double *>(workspace(kRegKl, kl_forward_scratch()));
   if (!buf) return UGK_ENOMEM;
   if (int e = launch_kl_forward(buf, buf + 1, mu, rho, n, sigma_prior)) return e;
   double h = 0.0;
@@ -346,13 +424,20 @@ int ugk_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float *m
   return ok();
 }
 
+int ugk_set_gelu_exact(int exact) {
+  set_gelu_exact(exact);
+  return ok();
+}
+
+int ugk_get_gelu_exact(void) { return gelu_exact(); }
+
 const char *ugk_last_error(void) { return g_err; }
 
 int ugk_set_stream(void *s) {
   const hipStream_t next = static_cast<hipStream_t>(s);
   const hipStream_t prev = g_stream.exchange(next);
-  // kernels still queued on the previous stream may use the scratch and the
-  // encoder's bucket state, which the new stream's work would then share
+  // kernels still queued on the previous stream may use the workspace, which
+  // the new stream's work would then share
   if (prev != next && hipStreamSynchronize(prev) != hipSuccess) {
     (void)hipGetLastError();
     return set_error(UGK_EHIP, "ugk_set_stream: waiting for the previous stream failed");
@@ -364,12 +449,65 @@ void *ugk_get_stream(void) { return g_stream.load(); }
 
 int ugk_reserve(int rows, int C) {
   if (rows < 0 || C < 0) return bad("ugk_reserve", "rows and C must be >= 0");
-  size_t need = layernorm_backward_scratch(rows, C);
-  if (!scratch(need)) return UGK_ENOMEM;
+  ugk_config cfg{1, rows, C, 1, 1, rows, 0};
+  return ugk_reserve_config(cfg);
+}
+
+size_t ugk_workspace_bytes(ugk_config cfg) {
+  if (cfg.B < 0 || cfg.T < 0 || cfg.C < 0 || cfg.V < 0 || cfg.L < 0 || (long long)cfg.B * cfg.T > INT_MAX) return 0;
+  size_t sz[kNumRegions];
+  region_sizes(cfg, sz);
+  size_t t = 0;
+  for (int r = 0; r < kNumRegions; r++) t += align_up(sz[r]);
+  return t;
+}
+
+int ugk_reserve_config(ugk_config cfg) {
+  const char *fn = "ugk_reserve_config";
+  if (cfg.B < 0 || cfg.T < 0 || cfg.C < 0 || cfg.V < 0 || cfg.L < 0) return bad(fn, "negative size in config");
+  if ((long long)cfg.B * cfg.T > INT_MAX) return bad(fn, "B*T exceeds INT_MAX");
+  size_t sz[kNumRegions];
+  region_sizes(cfg, sz);
+  for (int r = 0; r < kNumRegions; r++)
+    if (!workspace(static_cast<Region>(r), sz[r])) return UGK_ENOMEM;
   return ok();
 }
 
-size_t ugk_scratch_bytes(void) { return scratch_bytes_current(); }
+int ugk_set_workspace(void *ptr, size_t bytes, ugk_config cfg) {
+  const char *fn = "ugk_set_workspace";
+  if (ptr && ((uintptr_t)ptr % kAlign) != 0) return bad(fn, "the workspace must be 256-byte aligned");
+  size_t sz[kNumRegions];
+  if (ptr) {
+    if (cfg.B < 0 || cfg.T < 0 || cfg.C < 0 || cfg.V < 0 || cfg.L < 0 || (long long)cfg.B * cfg.T > INT_MAX)
+      return bad(fn, "invalid config");
+    region_sizes(cfg, sz);
+    size_t need = 0;
+    for (int r = 0; r < kNumRegions; r++) need += align_up(sz[r]);
+    if (bytes < need) return set_error(UGK_EINVAL, "%s: %zu bytes given, the config needs %zu", fn, bytes, need);
+  }
+  const int dev = current_device(fn);
+  if (dev < 0) return set_error(UGK_EHIP, "%s: hipGetDevice failed", fn);
+  // work queued on the library stream may still use the current workspace
+  if (hipStreamSynchronize(stream()) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_EHIP, "%s: waiting for the stream failed", fn);
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  DevWorkspace &w = g_ws[dev];
+  free_own(w);
+  w.user = static_cast<char *>(ptr);
+  w.user_bytes = ptr ? bytes : 0;
+  size_t o = 0;
+  for (int r = 0; r < kNumRegions; r++) {
+    w.off[r] = o;
+    w.cap[r] = ptr ? align_up(sz[r]) : 0;
+    o += w.cap[r];
+    w.fresh[r] = true;
+  }
+  return ok();
+}
+
+size_t ugk_scratch_bytes(void) { return workspace_bytes_current(); }
 
 int ugk_synchronize(void) {
   const hipError_t e = hipStreamSynchronize(stream());
@@ -477,6 +615,40 @@ int dense(int rc, const char *what) {
   return rc ? set_error(rc, "dense op callback %s returned %d", what, rc) : UGK_OK;
 }
 
+// Per-op timer of the step driver. An op of one kernel gets its event pair
+// recorded by the dispatch itself (the kernel's own duration); the encoder
+// backward, three kernels, is bracketed by two event records on the stream.
+struct OpTimer {
+  std::vector<hipEvent_t> ev;
+  std::vector<LaunchEvents> pair;
+  std::vector<int> op;
+  int n = 0;
+  bool on = false;
+};
+OpTimer g_timer;
+
+template <class F>
+int timed(int op, F &&f) {
+  OpTimer &t = g_timer;
+  if (!t.on || t.n >= (int)t.op.size()) return f();
+  const int i = t.n++;
+  t.op[i] = op;
+  if (op == UGK_OP_ENCODER_BACKWARD) {
+    if (hipEventRecord(t.ev[2 * i], stream()) != hipSuccess) return check_launch("op timer");
+    const int rc = f();
+    if (hipEventRecord(t.ev[2 * i + 1], stream()) != hipSuccess) return check_launch("op timer");
+    return rc;
+  }
+  t.pair[i] = {t.ev[2 * i], t.ev[2 * i + 1]};
+  armed_events() = &t.pair[i];
+  const int rc = f();
+  if (armed_events()) {  // nothing was launched (an empty op): no record
+    armed_events() = nullptr;
+    t.n--;
+  }
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -500,11 +672,14 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
   // output (the next block's LN1, or the final LN): those pairs run as one
   // pass, ugk_residual_layernorm_forward. Buffers and values are the
   // reference's.
-  UGK_TRY(ugk_encoder_forward(acts + a.enc, inputs, params + p.wte, params + p.wpe, B, T, C));
+  UGK_TRY(timed(UGK_OP_ENCODER_FORWARD,
+                [&] { return ugk_encoder_forward(acts + a.enc, inputs, params + p.wte, params + p.wpe, B, T, C); }));
   const float *stream_in = acts + a.enc;
   if (cfg.L > 0)
-    UGK_TRY(ugk_layernorm_forward(A(0, a.lno), A(0, a.lnm), A(0, a.lnr), stream_in, P(0, p.lng), P(0, p.lnb),
-                                  B, T, C));
+    UGK_TRY(timed(UGK_OP_LAYERNORM_FORWARD, [&] {
+      return ugk_layernorm_forward(A(0, a.lno), A(0, a.lnm), A(0, a.lnr), stream_in, P(0, p.lng), P(0, p.lnb), B,
+                                   T, C);
+    }));
   for (int l = 0; l < cfg.L; l++) {
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.qkv), A(l, a.lno), P(l, p.qw), P(l, p.qb), M, C,
@@ -515,28 +690,36 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.apr), A(l, a.atty), P(l, p.pw), P(l, p.pb), M, C, C),
                     "matmul_forward(proj)"));
-    UGK_TRY(ugk_residual_layernorm_forward(A(l, a.resa), A(l, a.ln2o), A(l, a.ln2m), A(l, a.ln2r), stream_in,
-                                           A(l, a.apr), P(l, p.ln2g), P(l, p.ln2b), B, T, C));
+    UGK_TRY(timed(UGK_OP_RESIDUAL_LAYERNORM_FORWARD, [&] {
+      return ugk_residual_layernorm_forward(A(l, a.resa), A(l, a.ln2o), A(l, a.ln2m), A(l, a.ln2r), stream_in,
+                                            A(l, a.apr), P(l, p.ln2g), P(l, p.ln2b), B, T, C);
+    }));
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.fch), A(l, a.ln2o), P(l, p.w1), P(l, p.b1), M, C,
                                         4 * C), "matmul_forward(fc)"));
-    UGK_TRY(ugk_gelu_forward(A(l, a.gelu), A(l, a.fch), NBTC * 4));
+    UGK_TRY(timed(UGK_OP_GELU_FORWARD, [&] { return ugk_gelu_forward(A(l, a.gelu), A(l, a.fch), NBTC * 4); }));
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.mlpo), A(l, a.gelu), P(l, p.w2), P(l, p.b2), M,
                                         4 * C, C), "matmul_forward(fc2)"));
     if (l + 1 < cfg.L)
-      UGK_TRY(ugk_residual_layernorm_forward(A(l, a.res1), A(l + 1, a.lno), A(l + 1, a.lnm), A(l + 1, a.lnr),
-                                             A(l, a.resa), A(l, a.mlpo), P(l + 1, p.lng), P(l + 1, p.lnb), B,
-                                             T, C));
+      UGK_TRY(timed(UGK_OP_RESIDUAL_LAYERNORM_FORWARD, [&] {
+        return ugk_residual_layernorm_forward(A(l, a.res1), A(l + 1, a.lno), A(l + 1, a.lnm), A(l + 1, a.lnr),
+                                              A(l, a.resa), A(l, a.mlpo), P(l + 1, p.lng), P(l + 1, p.lnb), B, T,
+                                              C);
+      }));
     else
-      UGK_TRY(ugk_residual_layernorm_forward(A(l, a.res1), acts + a.flo, acts + a.flm, acts + a.flr,
-                                             A(l, a.resa), A(l, a.mlpo), params + p.flng, params + p.flnb, B,
-                                             T, C));
+      UGK_TRY(timed(UGK_OP_RESIDUAL_LAYERNORM_FORWARD, [&] {
+        return ugk_residual_layernorm_forward(A(l, a.res1), acts + a.flo, acts + a.flm, acts + a.flr,
+                                              A(l, a.resa), A(l, a.mlpo), params + p.flng, params + p.flnb, B, T,
+                                              C);
+      }));
     stream_in = A(l, a.res1);
   }
   if (cfg.L == 0)
-    UGK_TRY(ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
-                                  params + p.flnb, B, T, C));
+    UGK_TRY(timed(UGK_OP_LAYERNORM_FORWARD, [&] {
+      return ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
+                                   params + p.flnb, B, T, C);
+    }));
   return ok();
 }
 
@@ -557,12 +740,12 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
   // residual_backward consumes the LN1 gradient of the block above, or the
   // final LN's): those pairs run as one pass, ugk_layernorm_residual_backward.
   // The 2L+1 LayerNorm backwards write their dweight/dbias partial rows to
-  // separate slots of the scratch; one batched launch at the end adds them
+  // separate slots of the workspace; one batched launch at the end adds them
   // (nothing in between reads those gradients), instead of a reduce launch
   // after each.
-  const size_t slot = (layernorm_backward_scratch(M, C) + 255) / 256 * 256;
+  const size_t slot = align_up(layernorm_backward_scratch(M, C));
   const int nln = 2 * cfg.L + 1;
-  char *pbase = static_cast<char *>(scratch(slot * (size_t)nln));
+  char *pbase = static_cast<char *>(workspace(kRegLn, slot * (size_t)nln));
   if (!pbase) return UGK_ENOMEM;
   std::vector<LnReduceJob> jobs;
   jobs.reserve((size_t)nln);
@@ -570,7 +753,10 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                     const float *w, const float *mean, const float *rstd) -> int {
     float *part = reinterpret_cast<float *>(pbase + slot * jobs.size());
     int nblk = 0;
-    if (int e = launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C, &nblk))
+    if (int e = timed(dx ? UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN : UGK_OP_LAYERNORM_BACKWARD_MAIN, [&] {
+          return launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C,
+                                                    kMaxPartialRows, &nblk);
+        }))
       return e;
     jobs.push_back({part, dw, db, nblk});
     return 0;
@@ -589,8 +775,9 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.gelu), grads + P(l, p.w2),
                                          grads + P(l, p.b2), acts + A(l, a.gelu), params + P(l, p.w2),
                                          grads_acts + A(l, a.mlpo), M, 4 * C, C), "matmul_backward(fc2)"));
-    UGK_TRY(ugk_gelu_backward(grads_acts + A(l, a.fch), acts + A(l, a.fch), grads_acts + A(l, a.gelu),
-                              NBTC * 4));
+    UGK_TRY(timed(UGK_OP_GELU_BACKWARD, [&] {
+      return ugk_gelu_backward(grads_acts + A(l, a.fch), acts + A(l, a.fch), grads_acts + A(l, a.gelu), NBTC * 4);
+    }));
     if (ops && ops->matmul_backward)
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.ln2o), grads + P(l, p.w1),
                                          grads + P(l, p.b1), acts + A(l, a.ln2o), params + P(l, p.w1),
@@ -618,8 +805,53 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                      grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng), acts + A(l, a.lnm),
                      acts + A(l, a.lnr)));
   }
-  UGK_TRY(launch_layernorm_reduce(jobs.data(), (int)jobs.size(), C));
-  UGK_TRY(ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C));
+  UGK_TRY(timed(UGK_OP_LAYERNORM_COLUMN_SUMS, [&] { return launch_layernorm_reduce(jobs.data(), (int)jobs.size(), C); }));
+  UGK_TRY(timed(UGK_OP_ENCODER_BACKWARD, [&] {
+    return ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C);
+  }));
+  return ok();
+}
+
+int ugk_op_timer_start(int capacity) {
+  const char *fn = "ugk_op_timer_start";
+  if (capacity < 0) return bad(fn, "capacity must be >= 0");
+  OpTimer &t = g_timer;
+  for (hipEvent_t e : t.ev) (void)hipEventDestroy(e);
+  t.ev.assign(2 * (size_t)capacity, nullptr);
+  t.pair.assign((size_t)capacity, LaunchEvents{nullptr, nullptr});
+  t.op.assign((size_t)capacity, 0);
+  t.n = 0;
+  t.on = false;
+  for (auto &e : t.ev)
+    if (hipEventCreate(&e) != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(UGK_EHIP, "%s: hipEventCreate failed", fn);
+    }
+  t.on = true;
+  return ok();
+}
+
+int ugk_op_timer_read(float *ms, int *ops, int capacity, int *count) {
+  const char *fn = "ugk_op_timer_read";
+  if (!count || (capacity > 0 && (!ms || !ops))) return bad(fn, "NULL pointer");
+  OpTimer &t = g_timer;
+  t.on = false;
+  const int n = t.n < capacity ? t.n : capacity;
+  if (t.n > 0 && hipEventSynchronize(t.ev[2 * (t.n - 1) + 1]) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_EHIP, "%s: waiting for the events failed", fn);
+  }
+  for (int i = 0; i < n; i++) {
+    float v = 0.0f;
+    if (hipEventElapsedTime(&v, t.ev[2 * i], t.ev[2 * i + 1]) != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(UGK_EHIP, "%s: hipEventElapsedTime failed", fn);
+    }
+    ms[i] = v;
+    ops[i] = t.op[i];
+  }
+  *count = n;
+  t.n = 0;
   return ok();
 }
 

@@ -26,7 +26,10 @@ namespace {
 // same domain; 54+j: x / b for the launch-wide divisor kSharedDivisors[j] by
 // ugk_div_shared (reference x / b); 62: ugk_dev_sqrtf (reference as fn 7);
 // 63: ugk_dev_expf_nooverflow on its domain, x <= 0x1.62e42ep6 or NaN
-// (ugk_expf_t elsewhere; reference ugk_expf).
+// (ugk_expf_t elsewhere; reference ugk_expf); 64 and 65: the default GELU
+// and its derivative (the logistic form, ugk_fast_gelu*) against the
+// glibc-exact expressions of fn 8 and 9, where a "mismatch" is a result
+// outside |a - b| <= 1e-6 + 1e-5 |b| (equal bits and NaN against NaN pass).
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -67,6 +70,8 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 63)
     return (x <= 0x1.62e42ep6f || x != x) ? ugk_dev_expf_nooverflow(x, UgkExp2Lds{tab}, UgkExpfAddends{})
                                           : ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
+  if (FN == 64) return ugk_fast_gelu(x);
+  if (FN == 65) return ugk_fast_gelu_grad(x);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
@@ -79,8 +84,8 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 5) return logf(x);
   if (FN == 6) return cosf(x);
   if (FN == 7) return (float)sqrt((double)x);
-  if (FN == 8) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
-  if (FN == 9) return ugk_gelu_grad_with(x, [](float u) { return ugk_tanhf(u); });
+  if (FN == 8 || FN == 64) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
+  if (FN == 9 || FN == 65) return ugk_gelu_grad_with(x, [](float u) { return ugk_tanhf(u); });
   if (FN >= 40 && FN < 48) return x / kDivisors[FN - 40];
   if (FN == 48) return (float)sqrt((double)x);
   if (FN >= 49 && FN < 54) return 1.0f / x;
@@ -102,7 +107,9 @@ __global__ __launch_bounds__(kBlock) void k_math_mismatch(unsigned long long lo,
     const unsigned u = (unsigned)(lo + i);
     const float x = ugk_u2f(u);
     const float a = kernel_math<FN>(x, tab), b = reference_math<FN>(x);
-    if (ugk_f2u(a) != ugk_f2u(b) && !(a != a && b != b)) {
+    // fn 64/65: the literal bar; the others: the same bits
+    const bool within = FN >= 64 && fabsf(a - b) <= 1e-6f + 1e-5f * fabsf(b);
+    if (ugk_f2u(a) != ugk_f2u(b) && !(a != a && b != b) && !within) {
       local++;
       lfirst = min(lfirst, u);
     }
@@ -174,7 +181,7 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 64);
+         (fn >= 40 && fn < 66);
 }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
@@ -210,6 +217,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
       UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
       UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62) UGK_MM(63)
+      UGK_MM(64) UGK_MM(65)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -238,6 +246,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
     UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
     UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62) UGK_EV(63)
+    UGK_EV(64) UGK_EV(65)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

@@ -7,7 +7,13 @@
 // Arithmetic follows train_bnn.c operation by operation (the library is built
 // with -ffp-contract=off) and the transcendental functions come from
 // ugk_libm_dev.h, which equals the host glibc on every input, so every result
-// is bit-identical to the CPU oracle.
+// is bit-identical to the CPU oracle -- except GELU's default form, which
+// evaluates the same function through the hardware exponential and
+// reciprocal (ugk_fast_gelu*: within 1e-5 relative / 1e-6 absolute of the CPU
+// on every input, and memory-bound where the glibc-exact tanhf made the
+// forward VALU-bound); ugk_set_gelu_exact(1) selects the bit-exact kernels.
+#include <atomic>
+
 #include "ugk_map.h"
 
 namespace ugk {
@@ -46,6 +52,21 @@ struct GeluFwd : MapOp {  // train_bnn.c:163-170
   }
 };
 
+struct GeluFwdFast : MapOp {  // train_bnn.c:163-170, logistic form
+  static constexpr int kLoads = 1, kStores = 1;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
+    st[0] = ugk_fast_gelu(ld[0]);
+  }
+};
+
+struct GeluBwdFast : MapOp {  // train_bnn.c:520-533, logistic form; loads inp, dout, dinp
+  static constexpr int kLoads = 3, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
+    st[0] = ld[2] + ugk_fast_gelu_grad(ld[0]) * ld[1];
+  }
+};
+
 struct GeluBwd : MapOp {  // train_bnn.c:520-533; loads inp, dout, dinp
   static constexpr int kLoads = 3, kStores = 1;
   static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
@@ -78,13 +99,28 @@ int launch_residual_backward(float *dx, float *dy, const float *dout, size_t n) 
   return run_map(s, n, "residual_backward");
 }
 
+namespace {
+std::atomic<int> g_gelu_exact{0};
+}  // namespace
+
+void set_gelu_exact(int exact) { g_gelu_exact.store(exact ? 1 : 0); }
+int gelu_exact() { return g_gelu_exact.load(); }
+
 int launch_gelu_forward(float *out, const float *inp, size_t n) {
-  Streams<GeluFwd> s{{inp}, {out}, {}};
+  if (gelu_exact()) {
+    Streams<GeluFwd> s{{inp}, {out}, {}};
+    return run_map(s, n, "gelu_forward");
+  }
+  Streams<GeluFwdFast> s{{inp}, {out}, {}};
   return run_map(s, n, "gelu_forward");
 }
 
 int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n) {
-  Streams<GeluBwd> s{{inp, dout, dinp}, {dinp}, {}};
+  if (gelu_exact()) {
+    Streams<GeluBwd> s{{inp, dout, dinp}, {dinp}, {}};
+    return run_map(s, n, "gelu_backward");
+  }
+  Streams<GeluBwdFast> s{{inp, dout, dinp}, {dinp}, {}};
   return run_map(s, n, "gelu_backward");
 }
 

@@ -45,12 +45,13 @@
 //                  ahead (one round of loads in flight per wavefront, so its
 //                  waits are exact). A frequent token's serial chain of adds
 //                  thus runs without waiting for its loads.
-//   The table is double-buffered by chunk parity: K2 of chunk j clears the
-//   half that chunk j-1 used, so no kernel clears what it also reads.
+//   The table and its counters return to their cleared state within each
+//   chunk, on the device: K2's wavefront for a slot frees the slot once it has
+//   read it (every claimed slot has exactly one), and the last K3 workgroup to
+//   finish zeroes the counters. No state stays on the host between calls, so a
+//   captured HIP graph may replay any number of calls.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
-#include <mutex>
-
 #include "ugk_internal.h"
 
 namespace ugk {
@@ -109,9 +110,9 @@ __device__ __forceinline__ u64 slot_word(int tok, int cnt) { return ((u64)(unsig
 __device__ __forceinline__ int slot_tok(u64 s) { return (int)(s >> 32); }
 __device__ __forceinline__ int slot_cnt(u64 s) { return (int)(unsigned)s; }
 
-struct EncTable {  // one half of the double-buffered state
+struct EncTable {
   u64 *slot;       // [kTableMax] token and row count per slot, kFree when free
-  int *counters;   // [0] K3 work items taken, [1] large buckets, [2] sorted-id pool use
+  int *counters;   // [0] K3 work items taken, [1] large buckets, [2] sorted-id pool use, [3] K3 workgroups done
   int *large_j;    // [kTableMax] index of a large slot in the large-bucket list
 };
 
@@ -260,15 +261,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // K2: one wavefront per slot-list entry (the grid covers K1's regions
-// exactly). Also clears `old` (the other half of the table) over
-// [0, old_tsize).
+// exactly). Each frees its slot once it has read it.
 template <bool kVec>
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable old, EncShared sh,
-                                                        float *__restrict__ dwte, const float *__restrict__ dout,
-                                                        int old_tsize, int C, int n) {
+__global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncShared sh, float *__restrict__ dwte,
+                                                        const float *__restrict__ dout, int C, int n) {
   __shared__ unsigned lds[kWavesPerBlock * kCap];
-  for (int h = blockIdx.x * kBlock + threadIdx.x; h < old_tsize; h += gridDim.x * kBlock) old.slot[h] = kFree;
-  if (blockIdx.x == 0 && threadIdx.x < 3) old.counters[threadIdx.x] = 0;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   unsigned *mine = lds + (size_t)wave * kCap;
@@ -286,6 +283,8 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncTable ol
   asm volatile("" ::"v"(id_raw));  // keeps the compiler from sinking the ids load below the branch
   const int cnt = slot_cnt(sw);
   const int tok = slot_tok(sw);
+  // the slot's only reader has read it: free it for the next chunk's K1
+  if (lane == 0) tb.slot[w] = kFree;
   if (cnt > kCap) {
     // large bucket: the rows whose slot is w, in row order, to the pool for
     // K3; 2048 slot_of entries per round, four consecutive per lane
@@ -392,19 +391,14 @@ constexpr int kRound = kGroupWaves * kPerWave;  // rows per round
 constexpr int kLargeThreads = (kGroups * kGroupWaves + 1) * kWave;
 constexpr int kLargeGrid = 256;
 
-__global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, EncShared sh,
-                                                                 float *__restrict__ dwte,
-                                                                 const float *__restrict__ dout, int C,
-                                                                 int nslices) {
-  // stage[h][channel][row]: a lane's rows are consecutive, so both sides
-  // move four rows per LDS instruction; the row stride of kRound + 4 floats
-  // puts the 16 lanes of each 16-byte access on distinct banks
-  __shared__ float4 stage[2][kWave][kRound / 4 + 1];
-  __shared__ int next_item;
+// The (bucket, slice) work items of one workgroup, until the counter passes
+// `total`.
+__device__ __forceinline__ void large_items(EncTable tb, EncShared sh, float *__restrict__ dwte,
+                                            const float *__restrict__ dout, int C, int nslices, int total,
+                                            float4 (*stage)[kWave][kRound / 4 + 1], int *next_item_p) {
+  int &next_item = *next_item_p;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
-  const int total = tb.counters[1] * nslices;
-  if (total == 0) return;  // the common case: no bucket beyond kCap rows
   const bool adder = wave == 0;
   const int group = adder ? -1 : (wave - 1) / kGroupWaves;
   const int slot = adder ? 0 : (wave - 1) % kGroupWaves;  // this loader's share of a round
@@ -501,61 +495,66 @@ __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, En
   }
 }
 
-__global__ void k_enc_init(EncTable a, EncTable b) {
+__global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, EncShared sh,
+                                                                 float *__restrict__ dwte,
+                                                                 const float *__restrict__ dout, int C,
+                                                                 int nslices) {
+  // stage[h][channel][row]: a lane's rows are consecutive, so both sides
+  // move four rows per LDS instruction; the row stride of kRound + 4 floats
+  // puts the 16 lanes of each 16-byte access on distinct banks
+  __shared__ float4 stage[2][kWave][kRound / 4 + 1];
+  __shared__ int next_item;
+  // The common case, no bucket beyond kCap rows: every counter is still zero
+  // (K1 counts large buckets, K2 takes pool space for them), nothing to reset.
+  // Otherwise every workgroup reads the same count: the counters are reset
+  // only after the last workgroup has arrived below, past all its reads.
+  const int total = tb.counters[1] * nslices;
+  if (total == 0) return;
+  large_items(tb, sh, dwte, dout, C, nslices, total, stage, &next_item);
+  // every thread of this workgroup is past its last read of the counters; the
+  // last workgroup to arrive zeroes them for the next chunk
+  __syncthreads();
+  if (threadIdx.x == 0 && atomicAdd(&tb.counters[3], 1) == (int)gridDim.x - 1) {
+    tb.counters[0] = 0;
+    tb.counters[1] = 0;
+    tb.counters[2] = 0;
+    tb.counters[3] = 0;
+  }
+}
+
+__global__ void k_enc_init(EncTable t) {
   const int h = blockIdx.x * kBlock + threadIdx.x;
-  if (h < kTableMax) {
-    a.slot[h] = kFree;
-    b.slot[h] = kFree;
-  }
-  if (h < 3) {
-    a.counters[h] = 0;
-    b.counters[h] = 0;
-  }
+  if (h < kTableMax) t.slot[h] = kFree;
+  if (h < 4) t.counters[h] = 0;
 }
 
 size_t table_ints() { return (size_t)3 * kTableMax + 64; }  // slot words (2 ints each), large_j, counters
 size_t state_bytes() {
   return (size_t)kTableMax * kCap * sizeof(int) + (size_t)kChunk * sizeof(int) +
-         (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + 2 * table_ints() * sizeof(int);
+         (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + table_ints() * sizeof(int);
 }
 
-struct DevState {
-  void *mem = nullptr;
-  EncTable half[2];
-  EncShared sh;
-  int parity = 0;
-  int last_tsize[2] = {0, 0};
-};
-
-void carve(DevState &ds) {
-  char *p = static_cast<char *>(ds.mem);
-  ds.sh.rows = reinterpret_cast<int *>(p);
+// The state's arrays at their fixed places in its workspace region.
+void carve(char *p, EncTable *t, EncShared *sh) {
+  sh->rows = reinterpret_cast<int *>(p);
   p += (size_t)kTableMax * kCap * sizeof(int);
-  ds.sh.slot_of = reinterpret_cast<int *>(p);
+  sh->slot_of = reinterpret_cast<int *>(p);
   p += (size_t)kChunk * sizeof(int);
-  ds.sh.lmeta = reinterpret_cast<int4 *>(p);
+  sh->lmeta = reinterpret_cast<int4 *>(p);
   p += (size_t)kMaxLarge * sizeof(int4);
-  ds.sh.pool = reinterpret_cast<int *>(p);
+  sh->pool = reinterpret_cast<int *>(p);
   p += (size_t)kChunk * sizeof(int);
-  ds.sh.list = reinterpret_cast<int *>(p);
+  sh->list = reinterpret_cast<int *>(p);
   p += (size_t)kChunk * sizeof(int);
-  for (int k = 0; k < 2; k++) {  // each half starts 8-byte aligned (every size above is)
-    ds.half[k].slot = reinterpret_cast<u64 *>(p);
-    int *q = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
-    ds.half[k].large_j = q; q += kTableMax;
-    ds.half[k].counters = q;
-    p += table_ints() * sizeof(int);
-  }
+  t->slot = reinterpret_cast<u64 *>(p);  // 8-byte aligned: every size above is a multiple of 8
+  int *q = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
+  t->large_j = q;
+  t->counters = q + kTableMax;
 }
-
-// Per device. The state lives in the encoder's own allocation (not the shared
-// scratch, which other ops overwrite).
-DevState g_state[64];
-std::mutex g_enc_mu;
 
 }  // namespace
 
-size_t encoder_backward_scratch(int) { return state_bytes(); }
+size_t encoder_backward_scratch() { return state_bytes(); }
 
 int launch_encoder_forward(float *out, const int *inp, const float *wte, const float *wpe, int B,
                            int T, int C) {
@@ -563,11 +562,11 @@ int launch_encoder_forward(float *out, const int *inp, const float *wte, const f
   if (BT == 0 || C == 0) return 0;
   const dim3 grid(grid_for((size_t)BT, kWavesPerBlock)), block(kBlock);
   if ((C & 3) == 0 && aligned16(out) && aligned16(wte) && aligned16(wpe)) {
-    hipLaunchKernelGGL(k_enc_fwd_vec, grid, block, 0, stream(), reinterpret_cast<float4 *>(out), inp,
+    launch(k_enc_fwd_vec, grid, block, 0, reinterpret_cast<float4 *>(out), inp,
                        reinterpret_cast<const float4 *>(wte), reinterpret_cast<const float4 *>(wpe), BT,
                        T, C >> 2);
   } else {
-    hipLaunchKernelGGL(k_enc_fwd_scalar, grid, block, 0, stream(), out, inp, wte, wpe, BT, T, C);
+    launch(k_enc_fwd_scalar, grid, block, 0, out, inp, wte, wpe, BT, T, C);
   }
   return check_launch("encoder_forward");
 }
@@ -576,21 +575,15 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
                             int T, int C) {
   const int BT = B * T;
   if (BT == 0 || C == 0) return 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-    return set_error(UGK_EHIP, "encoder_backward: hipGetDevice failed");
-  std::lock_guard<std::mutex> lock(g_enc_mu);
-  DevState &ds = g_state[dev];
-  if (!ds.mem) {
-    if (hipMalloc(&ds.mem, state_bytes()) != hipSuccess) {
-      ds.mem = nullptr;
-      (void)hipGetLastError();
-      return set_error(UGK_ENOMEM, "encoder_backward: cannot allocate %zu bytes of bucket state", state_bytes());
-    }
-    carve(ds);
-    hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), ds.half[0],
-                       ds.half[1]);
-  }
+  // the bucket state lives in its own workspace region; new memory is cleared
+  // once, and every call leaves it cleared
+  bool fresh = false;
+  char *mem = static_cast<char *>(workspace(kRegEncoder, state_bytes(), &fresh));
+  if (!mem) return UGK_ENOMEM;
+  EncTable tb;
+  EncShared sh;
+  carve(mem, &tb, &sh);
+  if (fresh) hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), tb);
   const bool vec = (C & 3) == 0 && aligned16(dwte) && aligned16(dwpe) && aligned16(dout);
   const int nslices = (C + kWave - 1) / kWave;
   for (int c0 = 0; c0 < BT; c0 += kChunk) {
@@ -599,35 +592,28 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     while (tsize < kLoadInv * n && tsize < kTableMax) { tsize <<= 1; lg++; }
     const unsigned mask = (unsigned)tsize - 1u;
     const int shift = 32 - lg;
-    const int p = ds.parity;
-    const EncTable tb = ds.half[p], old = ds.half[1 - p];
     const int ins_blocks = (int)grid_for((size_t)n, kBlock);
     int pe_blocks = 0;
     if (c0 == 0) pe_blocks = (int)grid_for((size_t)T * (vec ? C / 4 : C), kBlock);
     if (vec)
       hipLaunchKernelGGL(k_enc_bwd_insert<true>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
-                         ds.sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
+                         sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     else
       hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
-                         ds.sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
+                         sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     const float *dchunk = dout + (size_t)c0 * C;
     // one wavefront per entry of K1's slot-list regions
     const dim3 g2((unsigned)ins_blocks * (kBlock / kWavesPerBlock));
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
-                         ds.last_tsize[1 - p], C, n);
+      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n);
     else
-      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, old, ds.sh, dwte, dchunk,
-                         ds.last_tsize[1 - p], C, n);
+      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n);
     // one round of workgroups (one per CU: each stages 122 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
-    // every workgroup exits at once
+    // every workgroup goes straight to the counter reset
     const int max_items = (n / (kCap + 1) + 1) * nslices;
     hipLaunchKernelGGL(k_enc_bwd_large, dim3(max_items < kLargeGrid ? max_items : kLargeGrid),
-                       dim3(kLargeThreads), 0, stream(), tb, ds.sh, dwte, dchunk, C, nslices);
-    ds.last_tsize[1 - p] = 0;
-    ds.last_tsize[p] = tsize;
-    ds.parity = 1 - p;
+                       dim3(kLargeThreads), 0, stream(), tb, sh, dwte, dchunk, C, nslices);
   }
   return check_launch("encoder_backward");
 }

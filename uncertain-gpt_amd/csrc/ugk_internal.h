@@ -1,6 +1,7 @@
 // ugk_internal.h - shared by the libugk translation units (not installed).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -16,9 +17,39 @@ constexpr int kBlock = 256;    // 4 waves per workgroup for streaming kernels
 hipStream_t stream();
 int set_error(int code, const char *fmt, ...);
 int check_launch(const char *what);
-// Scratch of at least `bytes` on the current device (nullptr on failure,
-// with the error already set).
-void *scratch(size_t bytes);
+
+// Device workspace, one region per purpose, so that a kernel's scratch is
+// never another's: the LayerNorm-backward partial rows (one slot per call, or
+// 2L+1 slots for the step driver), the encoder backward's bucket state (kept
+// between calls), the KL total's partial sums and the long-row softmax's row
+// statistics. Each region is the library's own allocation, grown when a
+// larger shape arrives (after waiting for the device), or a fixed part of a
+// workspace the caller handed over with ugk_set_workspace, which then never
+// grows. workspace() returns at least `bytes` of region r on the current
+// device, or nullptr with the error set; *fresh (if given) tells whether the
+// region's memory is new since its last use (its contents are undefined).
+enum Region { kRegLn = 0, kRegEncoder = 1, kRegKl = 2, kRegSoftmax = 3, kNumRegions = 4 };
+void *workspace(Region r, size_t bytes, bool *fresh = nullptr);
+
+// The step driver's op timer arms an event pair for the next kernel launch
+// of an op; launch() then records them with the dispatch itself
+// (hipExtLaunchKernelGGL: the kernel's own start and end, no marker packets
+// between kernels), once. Unarmed, launch() is a plain launch on stream().
+struct LaunchEvents {
+  hipEvent_t start, stop;
+};
+LaunchEvents *&armed_events();
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, unsigned shmem, Args... args) {
+  LaunchEvents *ev = armed_events();
+  if (ev) {
+    armed_events() = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream(), ev->start, ev->stop, 0u, static_cast<KArgs>(args)...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream(), static_cast<KArgs>(args)...);
+  }
+}
 
 __host__ __device__ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -73,6 +104,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // and returns the launch status through check_launch.
 int launch_residual_forward(float *out, const float *x, const float *y, size_t n);
 int launch_residual_backward(float *dx, float *dy, const float *dout, size_t n);
+// GELU form: 0 (default) the logistic form through the hardware exponential,
+// 1 the glibc-exact tanhf (bit-identical to train_bnn.c).
+void set_gelu_exact(int exact);
+int gelu_exact();
 int launch_gelu_forward(float *out, const float *inp, size_t n);
 int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n);
 int launch_bayes_materialize(float *w, const float *mu, const float *rho,
@@ -118,10 +153,22 @@ struct LnReduceJob {
   float *dweight, *dbias;
   int nblk;
 };
+// At most max_blocks partial rows (the float4 path takes up to 1024, the
+// scalar path up to 512).
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
-                                       const float *rstd, int rows, int C, int *nblk);
+                                       const float *rstd, int rows, int C, int max_blocks, int *nblk);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
+// Both passes with the partial rows in `partial` (at most max_blocks rows of
+// 2C floats), not in the workspace.
+int launch_layernorm_residual_backward_into(float *partial, int max_blocks, float *dinp, float *dweight,
+                                            float *dbias, float *dx, float *dy, const float *dout,
+                                            const float *inp, const float *weight, const float *mean,
+                                            const float *rstd, int rows, int C);
+// Partial rows one call writes with at most max_blocks of them.
+int layernorm_backward_blocks(int rows, int C, bool res, int max_blocks);
+constexpr int kMaxScalarBlocks = 512;
+constexpr int kMaxPartialRows = 1024;  // partial rows the column-sum kernel takes per call
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V);
 int launch_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int rows, int V,
@@ -131,9 +178,10 @@ int launch_encoder_forward(float *out, const int *inp, const float *wte,
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
                             const int *inp, int B, int T, int C);
 
-// Scratch sizes, for ugk_reserve.
+// Workspace sizes.
 size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
-size_t encoder_backward_scratch(int rows);
-size_t kl_forward_scratch();
+size_t encoder_backward_scratch();                   // the bucket state (fixed)
+size_t kl_forward_scratch();                         // partial sums and result (fixed)
+size_t softmax_scratch(int rows, int V);             // row statistics of rows too long for one workgroup
 
 }  // namespace ugk

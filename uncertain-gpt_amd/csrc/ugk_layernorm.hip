@@ -1,5 +1,6 @@
 // ugk_layernorm.hip - LayerNorm forward and backward (train_bnn.c:81-115,
-// :439-477).
+// :439-477), and the residual -> LayerNorm / LayerNorm -> residual pairs of
+// the reference launch sequence fused into one pass each.
 //
 // Layout: rows of C fp32 values, row-major; mean/rstd one float per row;
 // weight/bias/dweight/dbias C floats.
@@ -11,13 +12,19 @@
 // row sums added in scalar registers), rstd = 1/sqrtf(var/C + 1e-5) with IEEE
 // division and square root, exactly the CPU formula.
 //
-// Backward: one wavefront per row for dinp (two wavefront sums), and the
-// dweight/dbias column sums are accumulated per wavefront (in LDS) across the
-// rows it visits, then combined in a fixed order: the wavefronts of a
-// workgroup through an LDS tree into one partial row per workgroup (at most
-// 512 workgroups), then the partial rows in index order by a small second
-// kernel that adds the totals into dweight/dbias. No atomics, so the result
-// is identical run to run.
+// Backward: one wavefront per row for dinp (two wavefront sums). Each
+// wavefront adds the dweight/dbias terms of its rows, in row order, in
+// registers; after one barrier the workgroup's W per-wavefront sums are added
+// column by column in wavefront order into one partial row per workgroup, and
+// a second, small kernel adds the partial rows in index order into
+// dweight/dbias. No atomics, so the result is identical run to run.
+//
+// Every load of the float4 paths is unconditional: a lane's columns past the
+// row are clamped onto the row's last float4, and rows past a wavefront's
+// range repeat its last row; the values so loaded are masked out of the sums
+// (added as -0.0f, the identity of IEEE addition) and never stored. Per-lane
+// conditions around loads made the compiler wait for one row's loads before
+// it issued the next row's.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
 #include "ugk_internal.h"
 
@@ -26,83 +33,124 @@ namespace {
 
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kMaxV = 8;  // float4 per lane held in registers: C <= 2048
-constexpr int kMaxBwdBlocks = 512;
 
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// Clamped float4 column of each of a lane's V slots, and whether it is in the row.
+template <int V>
+struct Cols {
+  int col[V];
+  bool in[V];
+  __device__ __forceinline__ Cols(int lane, int C4) {
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      const int c4 = lane + v * kWave;
+      in[v] = c4 < C4;
+      col[v] = in[v] ? c4 : C4 - 1;
+    }
+  }
+};
+
+// Forward, RPW rows per wavefront (consecutive). The loads of row k+1 are
+// issued before row k is normalised and stored, so a wavefront has a row in
+// flight while it writes one.
 // kRes: the row is first formed as res = inp + inp2 (residual_forward,
 // train_bnn.c:182-186), stored to res, and normalised from the registers, the
 // pair gpt2_kernels.cuh:793-797 launches back to back.
-template <int V, bool kRes>
+template <int V, bool kRes, int RPW>
 __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, float *__restrict__ mean,
-                                                       float *__restrict__ rstd,
-                                                       const float *__restrict__ inp,
+                                                       float *__restrict__ rstd, const float *__restrict__ inp,
                                                        const float *__restrict__ weight,
                                                        const float *__restrict__ bias, int rows, int C,
                                                        float *__restrict__ res, const float *__restrict__ inp2) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int row0 = (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;
   const int C4 = C >> 2;
-  const float4 *x4 = reinterpret_cast<const float4 *>(inp + (size_t)row * C);
-  float4 xv[V];
-#pragma unroll
-  for (int v = 0; v < V; v++) {
-    const int c4 = lane + v * kWave;
-    xv[v] = (c4 < C4) ? ld_nt(x4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  if (kRes) {
-    const float4 *y4 = reinterpret_cast<const float4 *>(inp2 + (size_t)row * C);
-    float4 *r4 = reinterpret_cast<float4 *>(res + (size_t)row * C);
-    float4 yv[V];
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      const int c4 = lane + v * kWave;
-      yv[v] = (c4 < C4) ? ld_nt(y4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      xv[v] = make_float4(xv[v].x + yv[v].x, xv[v].y + yv[v].y, xv[v].z + yv[v].z, xv[v].w + yv[v].w);
-      if (lane + v * kWave < C4) st_nt(r4 + lane + v * kWave, xv[v]);
-    }
-  }
-  float s = 0.0f;
-#pragma unroll
-  for (int v = 0; v < V; v++) {
-    s += xv[v].x; s += xv[v].y; s += xv[v].z; s += xv[v].w;
-  }
-  s = wave_sum(s);
-  const float m = s / (float)C;
-  float vs = 0.0f;
-#pragma unroll
-  for (int v = 0; v < V; v++) {
-    if (lane + v * kWave < C4) {
-      float d;
-      d = xv[v].x - m; vs += d * d;
-      d = xv[v].y - m; vs += d * d;
-      d = xv[v].z - m; vs += d * d;
-      d = xv[v].w - m; vs += d * d;
-    }
-  }
-  vs = wave_sum(vs);
-  const float r = 1.0f / sqrtf(vs / (float)C + 1e-5f);
+  const Cols<V> cl(lane, C4);
+  const float4 *x4 = reinterpret_cast<const float4 *>(inp);
+  const float4 *y4 = reinterpret_cast<const float4 *>(inp2);
+  float4 *r4 = reinterpret_cast<float4 *>(res);
+  float4 *o4 = reinterpret_cast<float4 *>(out);
   const float4 *w4 = reinterpret_cast<const float4 *>(weight);
   const float4 *b4 = reinterpret_cast<const float4 *>(bias);
-  float4 *o4 = reinterpret_cast<float4 *>(out + (size_t)row * C);
+  float4 xa[V], ya[kRes ? V : 1];
+  {
+    const size_t off = (size_t)row0 * C4;
 #pragma unroll
-  for (int v = 0; v < V; v++) {
-    const int c4 = lane + v * kWave;
-    if (c4 < C4) {
-      const float4 w = w4[c4], b = b4[c4];
-      float4 o;
-      o.x = (xv[v].x - m) * r * w.x + b.x;
-      o.y = (xv[v].y - m) * r * w.y + b.y;
-      o.z = (xv[v].z - m) * r * w.z + b.z;
-      o.w = (xv[v].w - m) * r * w.w + b.w;
-      st_nt(o4 + c4, o);
+    for (int v = 0; v < V; v++) {
+      xa[v] = ld_nt(x4 + off + cl.col[v]);
+      if (kRes) ya[kRes ? v : 0] = ld_nt(y4 + off + cl.col[v]);
     }
   }
-  if (lane == 0) {
-    mean[row] = m;
-    rstd[row] = r;
+#pragma unroll
+  for (int k = 0; k < RPW; k++) {
+    const int row = row0 + k;
+    if (row >= rows) break;
+    float4 xb[V], yb[kRes ? V : 1];
+    if (k + 1 < RPW) {
+      const size_t off = (size_t)min(row + 1, rows - 1) * C4;
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        xb[v] = ld_nt(x4 + off + cl.col[v]);
+        if (kRes) yb[kRes ? v : 0] = ld_nt(y4 + off + cl.col[v]);
+      }
+    }
+    const size_t off = (size_t)row * C4;
+    float4 xv[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      xv[v] = xa[v];
+      if (kRes) {
+        xv[v] = add4(xv[v], ya[kRes ? v : 0]);
+        if (cl.in[v]) st_nt(r4 + off + cl.col[v], xv[v]);
+      }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      const bool c = cl.in[v];
+      s += c ? xv[v].x : -0.0f; s += c ? xv[v].y : -0.0f; s += c ? xv[v].z : -0.0f; s += c ? xv[v].w : -0.0f;
+    }
+    s = wave_sum(s);
+    const float m = s / (float)C;
+    float vs = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      const bool c = cl.in[v];
+      float d;
+      d = xv[v].x - m; vs += c ? d * d : -0.0f;
+      d = xv[v].y - m; vs += c ? d * d : -0.0f;
+      d = xv[v].z - m; vs += c ? d * d : -0.0f;
+      d = xv[v].w - m; vs += c ? d * d : -0.0f;
+    }
+    vs = wave_sum(vs);
+    const float r = 1.0f / sqrtf(vs / (float)C + 1e-5f);
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      if (cl.in[v]) {
+        const float4 w = w4[cl.col[v]], b = b4[cl.col[v]];
+        float4 o;
+        o.x = (xv[v].x - m) * r * w.x + b.x;
+        o.y = (xv[v].y - m) * r * w.y + b.y;
+        o.z = (xv[v].z - m) * r * w.z + b.z;
+        o.w = (xv[v].w - m) * r * w.w + b.w;
+        st_nt(o4 + off + cl.col[v], o);
+      }
+    }
+    if (lane == 0) {
+      mean[row] = m;
+      rstd[row] = r;
+    }
+    if (k + 1 < RPW) {
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        xa[v] = xb[v];
+        if (kRes) ya[kRes ? v : 0] = yb[kRes ? v : 0];
+      }
+    }
   }
 }
 
@@ -135,77 +183,86 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 
 // Backward, register-resident rows. A workgroup is W wavefronts; wavefront w
 // of workgroup g takes the rpw consecutive rows starting at (W g + w) * rpw,
-// R at a time (the loads of R rows are in flight together), writes dinp and
-// adds the dweight/dbias terms of its rows, in row order, into its own column
-// sums in LDS. The W wavefronts' sums are then folded pairwise (upper half
-// into lower half, a fixed tree) and wavefront 0 writes the workgroup's
-// partial row: partial[g] = [dweight part (C floats) | dbias part (C floats)].
+// R at a time: the loads of R rows (x and dout first, which the row sums
+// need, then dinp and the residual rows) are all issued before the first
+// arithmetic instruction. It writes dinp and adds its rows' dweight/dbias
+// terms, in row order, into its registers. After one barrier, thread t of the
+// workgroup adds float4 column t of the W wavefronts' sums in wavefront order
+// and writes the workgroup's partial row:
+// partial[g] = [dweight part (C floats) | dbias part (C floats)].
+// The weight row is read from global memory (it stays in L2), so the first
+// rows' loads go out without waiting for anything.
 //
 // kRes: the new dinp row is also added to rdx and rdy (residual_backward with
 // dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
-// gpt2_kernels.cuh:870-876 launches back to back. The rdx/rdy rows are loaded
-// with the others, before any arithmetic.
+// gpt2_kernels.cuh:870-876 launches back to back.
 template <int V, int W, int R, bool kRes>
 __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpw, float *__restrict__ rdx,
     float *__restrict__ rdy, int same) {
-  // the weight row, and each wavefront's dweight/dbias column sums, live in
-  // LDS rather than registers, which leaves the registers to the rows in
-  // flight and lets two workgroups share a CU
-  __shared__ float4 w4s[V * kWave];
-  __shared__ float4 acc[W][2][V * kWave];
+  __shared__ float4 red[W][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int C4 = C >> 2;
   const float Cf = (float)C;
+  const Cols<V> cl(lane, C4);
+  const float4 *x4 = reinterpret_cast<const float4 *>(inp);
+  const float4 *dy4 = reinterpret_cast<const float4 *>(dout);
+  float4 *dx4 = reinterpret_cast<float4 *>(dinp);
+  float4 *a4 = reinterpret_cast<float4 *>(rdx);
+  float4 *b4 = reinterpret_cast<float4 *>(rdy);
   const float4 *w4 = reinterpret_cast<const float4 *>(weight);
-  for (int e = threadIdx.x; e < V * kWave; e += W * kWave) w4s[e] = e < C4 ? w4[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 ag[V], ab[V];
 #pragma unroll
-  for (int v = 0; v < V; v++) {
-    acc[wave][0][v * kWave + lane] = make_float4(0.f, 0.f, 0.f, 0.f);
-    acc[wave][1][v * kWave + lane] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  __syncthreads();
+  for (int v = 0; v < V; v++) ag[v] = ab[v] = make_float4(0.f, 0.f, 0.f, 0.f);
   const int row0 = (blockIdx.x * W + wave) * rpw;
   const int row1 = min(row0 + rpw, rows);
   for (int row = row0; row < row1; row += R) {
     const int nr = min(R, row1 - row);
-    float4 x[R][V], dy[R][V], dx[R][V];
+    int rq[R];
+    size_t off[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      rq[q] = row + min(q, nr - 1);
+      off[q] = (size_t)rq[q] * C4;
+    }
+    float4 x[R][V], dy[R][V], dx[R][V], wv[V];
     float4 ra[kRes ? R : 1][kRes ? V : 1], rb[kRes ? R : 1][kRes ? V : 1];
     float m[R], r[R];
 #pragma unroll
-    for (int q = 0; q < R; q++) {
-      const int rq = q < nr ? row + q : row;
-      const float4 *x4 = reinterpret_cast<const float4 *>(inp + (size_t)rq * C);
-      const float4 *dy4 = reinterpret_cast<const float4 *>(dout + (size_t)rq * C);
-      const float4 *dx4 = reinterpret_cast<const float4 *>(dinp + (size_t)rq * C);
+    for (int q = 0; q < R; q++)
 #pragma unroll
-      for (int v = 0; v < V; v++) {
-        const int c4 = lane + v * kWave;
-        if (c4 < C4 && q < nr) {
-          x[q][v] = ld_nt(x4 + c4);
-          dy[q][v] = ld_nt(dy4 + c4);
-          dx[q][v] = ld_nt(dx4 + c4);
-        } else {
-          x[q][v] = dy[q][v] = dx[q][v] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-      if (kRes) {
-        const float4 *a4 = reinterpret_cast<const float4 *>(rdx + (size_t)rq * C);
-        const float4 *b4 = reinterpret_cast<const float4 *>(rdy + (size_t)rq * C);
+      for (int v = 0; v < V; v++) x[q][v] = ld_nt(x4 + off[q] + cl.col[v]);
+#pragma unroll
+    for (int q = 0; q < R; q++)
+#pragma unroll
+      for (int v = 0; v < V; v++) dy[q][v] = ld_nt(dy4 + off[q] + cl.col[v]);
+#pragma unroll
+    for (int v = 0; v < V; v++) wv[v] = w4[cl.col[v]];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      m[q] = mean[rq[q]];
+      r[q] = rstd[rq[q]];
+    }
+#pragma unroll
+    for (int q = 0; q < R; q++)
+#pragma unroll
+      for (int v = 0; v < V; v++) dx[q][v] = ld_nt(dx4 + off[q] + cl.col[v]);
+    if (kRes) {
+      // rdy is loaded even when it is rdx (same): a valid address, never used
+#pragma unroll
+      for (int q = 0; q < R; q++)
 #pragma unroll
         for (int v = 0; v < V; v++) {
-          const int c4 = lane + v * kWave;
-          const bool in = c4 < C4 && q < nr;
-          ra[q][v] = in ? ld_nt(a4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
-          rb[q][v] = (in && !same) ? ld_nt(b4 + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+          ra[kRes ? q : 0][kRes ? v : 0] = ld_nt(a4 + off[q] + cl.col[v]);
+          rb[kRes ? q : 0][kRes ? v : 0] = ld_nt(b4 + off[q] + cl.col[v]);
         }
-      }
-      m[q] = mean[rq];
-      r[q] = rstd[rq];
     }
+    // keep every load above the arithmetic (the scheduler would otherwise
+    // sink the dinp and residual loads past the row sums)
+    __builtin_amdgcn_sched_barrier(0);
     float s1[R], s2[R];
 #pragma unroll
     for (int q = 0; q < R; q++) {
@@ -213,18 +270,17 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
       s2[q] = 0.0f;
 #pragma unroll
       for (int v = 0; v < V; v++) {
-        const float4 w = w4s[v * kWave + lane];
+        const float4 w = wv[v];
         float4 xh, dn;
         xh.x = (x[q][v].x - m[q]) * r[q]; dn.x = dy[q][v].x * w.x;
         xh.y = (x[q][v].y - m[q]) * r[q]; dn.y = dy[q][v].y * w.y;
         xh.z = (x[q][v].z - m[q]) * r[q]; dn.z = dy[q][v].z * w.z;
         xh.w = (x[q][v].w - m[q]) * r[q]; dn.w = dy[q][v].w * w.w;
-        if (lane + v * kWave < C4) {
-          s1[q] += dn.x; s2[q] += dn.x * xh.x;
-          s1[q] += dn.y; s2[q] += dn.y * xh.y;
-          s1[q] += dn.z; s2[q] += dn.z * xh.z;
-          s1[q] += dn.w; s2[q] += dn.w * xh.w;
-        }
+        const bool c = cl.in[v];
+        s1[q] += c ? dn.x : -0.0f; s2[q] += c ? dn.x * xh.x : -0.0f;
+        s1[q] += c ? dn.y : -0.0f; s2[q] += c ? dn.y * xh.y : -0.0f;
+        s1[q] += c ? dn.z : -0.0f; s2[q] += c ? dn.z * xh.z : -0.0f;
+        s1[q] += c ? dn.w : -0.0f; s2[q] += c ? dn.w * xh.w : -0.0f;
       }
     }
 #pragma unroll
@@ -234,76 +290,57 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
     }
 #pragma unroll
     for (int q = 0; q < R; q++) {
-      if (q >= nr) break;
+      const bool live = q < nr;  // rows past nr repeat row nr-1: computed, neither stored nor summed
       const float dnm = s1[q] / Cf, dnxm = s2[q] / Cf;
-      float4 *dx4 = reinterpret_cast<float4 *>(dinp + (size_t)(row + q) * C);
 #pragma unroll
       for (int v = 0; v < V; v++) {
-        const int c4 = lane + v * kWave;
-        if (c4 < C4) {
-          const float4 w = w4s[c4];
-          float4 xh, dn;
-          xh.x = (x[q][v].x - m[q]) * r[q]; dn.x = dy[q][v].x * w.x;
-          xh.y = (x[q][v].y - m[q]) * r[q]; dn.y = dy[q][v].y * w.y;
-          xh.z = (x[q][v].z - m[q]) * r[q]; dn.z = dy[q][v].z * w.z;
-          xh.w = (x[q][v].w - m[q]) * r[q]; dn.w = dy[q][v].w * w.w;
-          float4 o;
-          o.x = dx[q][v].x + r[q] * (dn.x - dnm - xh.x * dnxm);
-          o.y = dx[q][v].y + r[q] * (dn.y - dnm - xh.y * dnxm);
-          o.z = dx[q][v].z + r[q] * (dn.z - dnm - xh.z * dnxm);
-          o.w = dx[q][v].w + r[q] * (dn.w - dnm - xh.w * dnxm);
-          st_nt(dx4 + c4, o);
+        const float4 w = wv[v];
+        float4 xh, dn;
+        xh.x = (x[q][v].x - m[q]) * r[q]; dn.x = dy[q][v].x * w.x;
+        xh.y = (x[q][v].y - m[q]) * r[q]; dn.y = dy[q][v].y * w.y;
+        xh.z = (x[q][v].z - m[q]) * r[q]; dn.z = dy[q][v].z * w.z;
+        xh.w = (x[q][v].w - m[q]) * r[q]; dn.w = dy[q][v].w * w.w;
+        float4 o;
+        o.x = dx[q][v].x + r[q] * (dn.x - dnm - xh.x * dnxm);
+        o.y = dx[q][v].y + r[q] * (dn.y - dnm - xh.y * dnxm);
+        o.z = dx[q][v].z + r[q] * (dn.z - dnm - xh.z * dnxm);
+        o.w = dx[q][v].w + r[q] * (dn.w - dnm - xh.w * dnxm);
+        if (cl.in[v] && live) {
+          const size_t e = off[q] + cl.col[v];
+          st_nt(dx4 + e, o);
           if (kRes) {
-            float4 *a4 = reinterpret_cast<float4 *>(rdx + (size_t)(row + q) * C);
-            float4 *b4 = reinterpret_cast<float4 *>(rdy + (size_t)(row + q) * C);
-            float4 a = ra[q][v];
-            a = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+            float4 a = add4(ra[kRes ? q : 0][kRes ? v : 0], o);
             if (same) {
-              a = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+              a = add4(a, o);
             } else {
-              const float4 b = rb[q][v];
-              st_nt(b4 + c4, make_float4(b.x + o.x, b.y + o.y, b.z + o.z, b.w + o.w));
+              st_nt(b4 + e, add4(rb[kRes ? q : 0][kRes ? v : 0], o));
             }
-            st_nt(a4 + c4, a);
+            st_nt(a4 + e, a);
           }
-          float4 g = acc[wave][0][c4], bb = acc[wave][1][c4];
-          bb.x += dy[q][v].x; g.x += dy[q][v].x * xh.x;
-          bb.y += dy[q][v].y; g.y += dy[q][v].y * xh.y;
-          bb.z += dy[q][v].z; g.z += dy[q][v].z * xh.z;
-          bb.w += dy[q][v].w; g.w += dy[q][v].w * xh.w;
-          acc[wave][0][c4] = g;
-          acc[wave][1][c4] = bb;
         }
+        const bool c = cl.in[v] && live;
+        ab[v].x += c ? dy[q][v].x : -0.0f; ag[v].x += c ? dy[q][v].x * xh.x : -0.0f;
+        ab[v].y += c ? dy[q][v].y : -0.0f; ag[v].y += c ? dy[q][v].y * xh.y : -0.0f;
+        ab[v].z += c ? dy[q][v].z : -0.0f; ag[v].z += c ? dy[q][v].z * xh.z : -0.0f;
+        ab[v].w += c ? dy[q][v].w : -0.0f; ag[v].w += c ? dy[q][v].w * xh.w : -0.0f;
       }
     }
   }
-  // fold the W wavefronts' column sums: upper half adds into lower half
 #pragma unroll
-  for (int half = W / 2; half >= 1; half >>= 1) {
-    __syncthreads();
-    if (wave < half) {
-#pragma unroll
-      for (int v = 0; v < V; v++) {
-        const int e = v * kWave + lane;
-        const float4 g = acc[wave + half][0][e], b = acc[wave + half][1][e];
-        float4 dg = acc[wave][0][e], db = acc[wave][1][e];
-        dg.x += g.x; dg.y += g.y; dg.z += g.z; dg.w += g.w;
-        db.x += b.x; db.y += b.y; db.z += b.z; db.w += b.w;
-        acc[wave][0][e] = dg;
-        acc[wave][1][e] = db;
-      }
-    }
+  for (int v = 0; v < V; v++) {
+    red[wave][0][v * kWave + lane] = ag[v];
+    red[wave][1][v * kWave + lane] = ab[v];
   }
-  if (wave == 0) {
-    float4 *pg = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C);
-    float4 *pb = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C + C);
+  __syncthreads();
+  float4 *prow = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C);
+  for (int e = threadIdx.x; e < 2 * V * kWave; e += W * kWave) {
+    const int which = e >= V * kWave ? 1 : 0;
+    const int c4 = e - which * V * kWave;
+    if (c4 < C4) {
+      float4 t = red[0][which][c4];
 #pragma unroll
-    for (int v = 0; v < V; v++) {
-      const int c4 = lane + v * kWave;
-      if (c4 < C4) {
-        pg[c4] = acc[0][0][c4];
-        pb[c4] = acc[0][1][c4];
-      }
+      for (int k = 1; k < W; k++) t = add4(t, red[k][which][c4]);
+      prow[which * C4 + c4] = t;
     }
   }
 }
@@ -354,13 +391,13 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_scalar(float *dinp, float *pa
   }
 }
 
-// Column totals of the partial rows in workgroup order, added to dweight
-// (columns [0,C)) and dbias (columns [C,2C)). Block: 64 columns x 16 groups;
-// group k sums the partial rows [k*J, (k+1)*J), J = ceil(nblk/16) <= 32, with
-// all its loads issued before the first add; the 16 group sums are then added
-// in group order.
+// Column totals of the partial rows, added to dweight (columns [0,C)) and
+// dbias (columns [C,2C)). Workgroup: 64 columns x 16 groups; group k sums the
+// partial rows [k*J, (k+1)*J), J = ceil(nblk/16) <= 64, in index order, 32
+// loads in flight per batch; the 16 group sums are then added in group order.
 constexpr int kRedGroups = 16;
-constexpr int kRedMaxPer = 32;
+constexpr int kRedBatch = 32;
+static_assert(kMaxPartialRows <= kRedGroups * 2 * kRedBatch, "two load batches per group at most");
 __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias, const float *partial, int nblk,
                                                    int C, float (*red)[kWave]) {
   const int cl = threadIdx.x & (kWave - 1);
@@ -369,13 +406,15 @@ __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias,
   const int C2 = 2 * C;
   const int J = (nblk + kRedGroups - 1) / kRedGroups;
   const int j0 = g * J, j1 = min(j0 + J, nblk);
-  float v[kRedMaxPer];
-#pragma unroll
-  for (int q = 0; q < kRedMaxPer; q++)
-    v[q] = (col < C2 && j0 + q < j1) ? partial[(size_t)(j0 + q) * C2 + col] : 0.0f;
+  const int cc = col < C2 ? col : C2 - 1;
   float acc = 0.0f;
+  for (int b = j0; b < j1; b += kRedBatch) {
+    float v[kRedBatch];
 #pragma unroll
-  for (int q = 0; q < kRedMaxPer; q++) acc += v[q];
+    for (int q = 0; q < kRedBatch; q++) v[q] = partial[(size_t)min(b + q, j1 - 1) * C2 + cc];
+#pragma unroll
+    for (int q = 0; q < kRedBatch; q++) acc += b + q < j1 ? v[q] : -0.0f;
+  }
   red[g][cl] = acc;
   __syncthreads();
   if (g == 0 && col < C2) {
@@ -389,15 +428,8 @@ __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias,
   }
 }
 
-__global__ __launch_bounds__(kWave * kRedGroups) void k_ln_bwd_reduce(float *dweight, float *dbias,
-                                                                      const float *partial, int nblk,
-                                                                      int C) {
-  __shared__ float red[kRedGroups][kWave];
-  ln_bwd_reduce_tile(dweight, dbias, partial, nblk, C, red);
-}
-
 // Several LayerNorm backwards' column totals in one launch (blockIdx.y picks
-// the job); each job is reduced exactly as k_ln_bwd_reduce would.
+// the job).
 constexpr int kMaxReduceJobs = 32;
 struct LnReduceBatch {
   LnReduceJob job[kMaxReduceJobs];
@@ -415,10 +447,10 @@ bool vec_ok(int C, std::initializer_list<const void *> ptrs) {
   return true;
 }
 
-// Scalar path: workgroups of 4 wavefronts, at most 512 of them.
-void bwd_shape(int rows, int *nblk, int *rpb) {
+// Scalar path: workgroups of 4 wavefronts, at most max_blocks of them.
+void bwd_shape(int rows, int max_blocks, int *nblk, int *rpb) {
   int nb = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (nb > kMaxBwdBlocks) nb = kMaxBwdBlocks;
+  if (nb > max_blocks) nb = max_blocks;
   if (nb < 1) nb = 1;
   int per = (rows + nb - 1) / nb;
   per = (per + kWavesPerBlock - 1) / kWavesPerBlock * kWavesPerBlock;
@@ -426,43 +458,88 @@ void bwd_shape(int rows, int *nblk, int *rpb) {
   *nblk = (rows + per - 1) / per;
 }
 
-// Rows whose loads a wavefront issues together: two while that fits the
-// registers (C <= 768; measured 43.9 -> 41.7 us for the fused pair at config
-// 5, where each wavefront then takes its two rows in one pass), else one.
-constexpr int bwd_rows(int V) { return V <= 3 ? 2 : 1; }
-// Vector path: W wavefronts per workgroup (8, or 4 when a lane holds more
-// than 4 float4 of a row, so that the registers fit without spilling), rpw
-// rows each, at most kBwdMaxBlocks workgroups, so the reduce reads at most 32
-// partial rows per group.
-constexpr int kBwdMaxBlocks = 512;
-inline int bwd_waves(int V) { return V <= 4 ? 8 : 4; }
-void bwd_shape_vec(int rows, int W, int *nblk, int *rpw) {
-  const int per_wave = (rows + kBwdMaxBlocks * W - 1) / (kBwdMaxBlocks * W);
-  *rpw = per_wave < 1 ? 1 : per_wave;
-  *nblk = (rows + W * *rpw - 1) / (W * *rpw);
+// Vector path shapes: two rows in flight per wavefront while they fit the
+// registers (C <= 768), else one; 8 wavefronts per workgroup, 4 when a lane
+// holds more than 4 float4 of a row. Each wavefront takes R rows (one pass)
+// while that leaves at most max_blocks workgroups, else more, R at a time: at
+// 16,384 x 768 one pass over 1,024 workgroups took 72 us for the fused pair
+// against 81 us with two passes over 512. The plain backward and the fused
+// pair share the shape (the rows of each wavefront and workgroup), hence the
+// order in which dweight/dbias are summed, so that the pair is bit-identical
+// to the plain backward followed by residual_backward. (A plain backward with
+// one row in flight and two workgroups per CU measured 19.5 against 20.2 us at
+// 8,192 x 768, but on 1,024 workgroups, whose sums differ.)
+struct BwdCfg {
+  int W, R;
+};
+constexpr BwdCfg bwd_cfg(int V, bool) { return BwdCfg{V <= 4 ? 8 : 4, V <= 3 ? 2 : 1}; }
+void bwd_shape_vec(int rows, BwdCfg k, int max_blocks, int *nblk, int *rpw) {
+  const int per_wave = (rows + max_blocks * k.W - 1) / (max_blocks * k.W);
+  *rpw = per_wave < k.R ? k.R : per_wave;
+  *nblk = (rows + k.W * *rpw - 1) / (k.W * *rpw);
+}
+
+int vec_blocks(int rows, int C, bool res, int max_blocks) {
+  int nblk, rpw;
+  bwd_shape_vec(rows, bwd_cfg(((C >> 2) + kWave - 1) / kWave, res), max_blocks, &nblk, &rpw);
+  return nblk;
+}
+
+// Rows per wavefront of the fused forward: two while one wavefront per row
+// would fill the GPU only once (the reads and writes of a single round of
+// wavefronts cannot overlap; measured 17.7 against 18.8 us at 8,192 x 768),
+// else one (35.0 against 37.1 us at 16,384 x 768).
+int fwd_rpw(int rows, bool res) {
+  if (!res) return 1;
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return rows <= cus[dev] * 32 ? 2 : 1;
 }
 
 }  // namespace
 
+int layernorm_backward_blocks(int rows, int C, bool res, int max_blocks) {
+  if (rows <= 0) return 0;
+  if ((C & 3) == 0 && C <= kMaxV * kWave * 4) return vec_blocks(rows, C, res, max_blocks);
+  int nblk, rpb;
+  bwd_shape(rows, max_blocks < kMaxScalarBlocks ? max_blocks : kMaxScalarBlocks, &nblk, &rpb);
+  return nblk;
+}
+
 size_t layernorm_backward_scratch(int rows, int C) {
-  int nblk, rpb, nv, rpw;
-  bwd_shape(rows, &nblk, &rpb);
-  for (int W = 4; W <= 8; W *= 2) {
-    bwd_shape_vec(rows, W, &nv, &rpw);
-    if (nv > nblk) nblk = nv;
-  }
-  return (size_t)nblk * 2 * (size_t)C * sizeof(float);
+  // the larger of the two shapes (plain or fused) and of the scalar path's
+  int nb = layernorm_backward_blocks(rows, C, false, kMaxPartialRows);
+  const int nf = layernorm_backward_blocks(rows, C, true, kMaxPartialRows);
+  if (nf > nb) nb = nf;
+  int ns, rpb;
+  bwd_shape(rows, kMaxScalarBlocks, &ns, &rpb);
+  if (ns > nb) nb = ns;
+  return (size_t)nb * 2 * (size_t)C * sizeof(float);
 }
 
 namespace {
 template <bool kRes>
 void launch_ln_fwd_vec(float *out, float *mean, float *rstd, const float *inp, const float *weight,
                        const float *bias, int rows, int C, float *res, const float *inp2) {
-  const dim3 grid(grid_for((size_t)rows, kWavesPerBlock)), block(kBlock);
   const int V = ((C >> 2) + kWave - 1) / kWave;
-  switch (V) {
-#define UGK_LN_FWD(v) \
-  case v: hipLaunchKernelGGL((k_ln_fwd_vec<v, kRes>), grid, block, 0, stream(), out, mean, rstd, inp, weight, bias, rows, C, res, inp2); break;
+  const int rpw = fwd_rpw(rows, kRes);
+  const dim3 grid(grid_for((size_t)rows, (size_t)kWavesPerBlock * rpw)), block(kBlock);
+  switch (V * 2 + (rpw - 1)) {
+#define UGK_LN_FWD(v)                                                                                           \
+  case 2 * v:                                                                                                   \
+    launch((k_ln_fwd_vec<v, kRes, 1>), grid, block, 0, out, mean, rstd, inp, weight, bias, \
+                       rows, C, res, inp2);                                                                     \
+    break;                                                                                                      \
+  case 2 * v + 1:                                                                                               \
+    launch((k_ln_fwd_vec<v, kRes, 2>), grid, block, 0, out, mean, rstd, inp, weight, bias, \
+                       rows, C, res, inp2);                                                                     \
+    break;
     UGK_LN_FWD(1) UGK_LN_FWD(2) UGK_LN_FWD(3) UGK_LN_FWD(4)
     UGK_LN_FWD(5) UGK_LN_FWD(6) UGK_LN_FWD(7) UGK_LN_FWD(8)
 #undef UGK_LN_FWD
@@ -485,11 +562,11 @@ int launch_residual_layernorm_forward(float *res, float *out, float *mean, float
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
                              const float *weight, const float *bias, int rows, int C) {
   if (rows == 0) return 0;
-  const dim3 grid(grid_for((size_t)rows, kWavesPerBlock)), block(kBlock);
   if (vec_ok(C, {out, inp, weight, bias})) {
     launch_ln_fwd_vec<false>(out, mean, rstd, inp, weight, bias, rows, C, nullptr, nullptr);
   } else {
-    hipLaunchKernelGGL(k_ln_fwd_scalar, grid, block, 0, stream(), out, mean, rstd, inp, weight, bias,
+    const dim3 grid(grid_for((size_t)rows, kWavesPerBlock)), block(kBlock);
+    launch(k_ln_fwd_scalar, grid, block, 0, out, mean, rstd, inp, weight, bias,
                        rows, C);
   }
   return check_launch("layernorm_forward");
@@ -499,16 +576,20 @@ namespace {
 template <bool kRes>
 int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const float *inp,
                       const float *weight, const float *mean, const float *rstd, int rows, int C,
-                      float *rdx, float *rdy) {
+                      float *rdx, float *rdy, int max_blocks) {
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
-  const int W = bwd_waves(V);
-  bwd_shape_vec(rows, W, &nblk, &rpw);
-  const dim3 grid(nblk), block(W * kWave);
+  const BwdCfg k = bwd_cfg(V, kRes);
+  bwd_shape_vec(rows, k, max_blocks, &nblk, &rpw);
+  const dim3 grid(nblk), block(k.W * kWave);
   const int same = rdx == rdy ? 1 : 0;
   switch (V) {
-#define UGK_LN_BWD(v) \
-  case v: hipLaunchKernelGGL((k_ln_bwd_vec<v, (v <= 4 ? 8 : 4), bwd_rows(v), kRes>), grid, block, 0, stream(), dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same); break;
+#define UGK_LN_BWD(v)                                                                                            \
+  case v:                                                                                                        \
+    launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes>), \
+                       grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx,  \
+                       rdy, same);                                                                               \
+    break;
     UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
     UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
 #undef UGK_LN_BWD
@@ -519,20 +600,21 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
 
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
-                                       const float *rstd, int rows, int C, int *nblk) {
+                                       const float *rstd, int rows, int C, int max_blocks, int *nblk) {
   *nblk = 0;
   if (rows == 0) return 0;
   const bool res = dx != nullptr;
   if (vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
     if (res)
-      *nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy);
+      *nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy, max_blocks);
     else
-      *nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr);
+      *nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr,
+                                       max_blocks);
     return check_launch("layernorm_backward");
   }
   int rpb;
-  bwd_shape(rows, nblk, &rpb);
-  hipLaunchKernelGGL(k_ln_bwd_scalar, dim3(*nblk), dim3(kBlock), 0, stream(), dinp, partial, dout, inp, weight,
+  bwd_shape(rows, max_blocks < kMaxScalarBlocks ? max_blocks : kMaxScalarBlocks, nblk, &rpb);
+  launch(k_ln_bwd_scalar, dim3(*nblk), dim3(kBlock), 0, dinp, partial, dout, inp, weight,
                      mean, rstd, rows, C, rpb);
   if (int e = check_launch("layernorm_backward")) return e;
   return res ? launch_residual_backward(dx, dy, dinp, (size_t)rows * C) : 0;
@@ -543,25 +625,32 @@ int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C) {
     LnReduceBatch b{};
     const int n = njobs - j0 < kMaxReduceJobs ? njobs - j0 : kMaxReduceJobs;
     for (int k = 0; k < n; k++) b.job[k] = jobs[j0 + k];
-    hipLaunchKernelGGL(k_ln_bwd_reduce_batch, dim3(grid_for((size_t)2 * C, kWave), n), dim3(kWave * kRedGroups), 0,
-                       stream(), b, C);
+    launch(k_ln_bwd_reduce_batch, dim3(grid_for((size_t)2 * C, kWave), n), dim3(kWave * kRedGroups), 0, b, C);
   }
   return check_launch("layernorm_backward (column sums)");
+}
+
+int launch_layernorm_residual_backward_into(float *partial, int max_blocks, float *dinp, float *dweight,
+                                            float *dbias, float *dx, float *dy, const float *dout,
+                                            const float *inp, const float *weight, const float *mean,
+                                            const float *rstd, int rows, int C) {
+  if (rows == 0) return 0;
+  int nblk;
+  if (int e = launch_layernorm_backward_partials(dinp, partial, dx, dy, dout, inp, weight, mean, rstd, rows, C,
+                                                 max_blocks, &nblk))
+    return e;
+  const LnReduceJob job{partial, dweight, dbias, nblk};
+  return launch_layernorm_reduce(&job, 1, C);
 }
 
 int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias, float *dx, float *dy,
                                        const float *dout, const float *inp, const float *weight,
                                        const float *mean, const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
-  float *partial = static_cast<float *>(scratch(layernorm_backward_scratch(rows, C)));
+  float *partial = static_cast<float *>(workspace(kRegLn, layernorm_backward_scratch(rows, C)));
   if (!partial) return UGK_ENOMEM;
-  int nblk;
-  if (int e = launch_layernorm_backward_partials(dinp, partial, dx, dy, dout, inp, weight, mean, rstd, rows, C,
-                                                 &nblk))
-    return e;
-  hipLaunchKernelGGL(k_ln_bwd_reduce, dim3(grid_for((size_t)2 * C, kWave)), dim3(kWave * kRedGroups), 0,
-                     stream(), dweight, dbias, partial, nblk, C);
-  return check_launch("layernorm_residual_backward");
+  return launch_layernorm_residual_backward_into(partial, kMaxPartialRows, dinp, dweight, dbias, dx, dy, dout, inp,
+                                                 weight, mean, rstd, rows, C);
 }
 
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const float *dout,

@@ -104,15 +104,15 @@ int run_map(const Streams<Op> &s, size_t n, const char *name) {
   size_t done = 0;
   if (vec && n >= 4) {
     const size_t n4 = n / 4;
-    hipLaunchKernelGGL(k_map_vec4<Op>, dim3(grid_for(n4, (size_t)Op::kThreads * Op::kUnroll)),
-                       dim3(Op::kThreads), 0, stream(), s, n4);
+    launch(k_map_vec4<Op>, dim3(grid_for(n4, (size_t)Op::kThreads * Op::kUnroll)),
+                       dim3(Op::kThreads), 0, s, n4);
     done = n4 * 4;
   }
   if (done < n) {
     const size_t rest = n - done;
     unsigned g = grid_for(rest, kBlock);
     if (g > 65536u) g = 65536u;
-    hipLaunchKernelGGL(k_map_scalar<Op>, dim3(g), dim3(kBlock), 0, stream(), s, done, n);
+    launch(k_map_scalar<Op>, dim3(g), dim3(kBlock), 0, s, done, n);
   }
   return check_launch(name);
 }

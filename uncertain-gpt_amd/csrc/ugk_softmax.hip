@@ -401,6 +401,13 @@ void launch_rows(float *losses, float *probs, const float *logits, const int *ta
 
 }  // namespace
 
+// Rows of more than kSplitMaxV logits take the two-pass form, whose row
+// statistics live in the workspace.
+constexpr int kSplitSlots = 768 * (42 + 25);
+constexpr int kSplitMaxV = kSplitSlots - 63;
+
+size_t softmax_scratch(int rows, int V) { return V > kSplitMaxV ? (size_t)rows * sizeof(float2) : 0; }
+
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V) {
   if (rows == 0 || V == 0) return 0;
@@ -412,14 +419,14 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
   else if (W <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
-  else if (W <= 768 * (42 + 25)) {  // 42 slots per thread in registers, 25 in LDS: two rows per CU
+  else if (W <= kSplitSlots) {  // 42 slots per thread in registers, 25 in LDS: two rows per CU
     static_assert(32768 - 63 >= 768 * 42, "the split kernel's register slots must lie inside every row it takes");
     hipLaunchKernelGGL((k_softmax_xent_split<768, 42, 25>), dim3(rows), dim3(768), 0, stream(), losses, probs,
                        logits, targets, V);
   } else {
     // Rows too long for the registers of one workgroup: a statistics pass
     // and a flat normalising pass (12 bytes per logit rather than 8).
-    float2 *stats = static_cast<float2 *>(scratch((size_t)rows * sizeof(float2)));
+    float2 *stats = static_cast<float2 *>(workspace(kRegSoftmax, softmax_scratch(rows, V)));
     if (!stats) return UGK_ENOMEM;
     hipLaunchKernelGGL(k_softmax_stats, dim3(grid_for((size_t)rows, kStatsWaves)), dim3(kStatsWaves * kWave), 0,
                        stream(), stats, logits, rows, V);

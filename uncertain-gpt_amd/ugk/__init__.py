@@ -27,7 +27,8 @@ __all__ = [
     "softmax_crossentropy", "crossentropy_softmax_backward", "bayes_sample", "bayes_backward",
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
-    "set_stream", "synchronize", "reserve", "scratch_bytes",
+    "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
+    "set_workspace", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "version",
 ]
@@ -90,9 +91,16 @@ _SIGS = {
     "ugk_set_stream": [_fp],
     "ugk_get_stream": [],
     "ugk_reserve": [_i, _i],
+    "ugk_reserve_config": [Config],
+    "ugk_workspace_bytes": [Config],
+    "ugk_set_workspace": [_fp, _sz, Config],
+    "ugk_op_timer_start": [_i],
+    "ugk_op_timer_read": [_fp, _fp, _i, ctypes.POINTER(_i)],
     "ugk_scratch_bytes": [],
     "ugk_synchronize": [],
     "ugk_version": [],
+    "ugk_set_gelu_exact": [_i],
+    "ugk_get_gelu_exact": [],
     "ugk_last_error": [],
     "ugk_param_count": [Config],
     "ugk_act_count": [Config],
@@ -114,7 +122,7 @@ _SIGS = {
     "ugk_ckpt_save": [ctypes.c_char_p, _fp, _sz, Config, _i],
     "ugk_ckpt_load": [ctypes.c_char_p, _fp, _sz, Config, ctypes.POINTER(_i)],
 }
-_RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz,
+_RET = {"ugk_last_error": ctypes.c_char_p, "ugk_get_stream": _fp, "ugk_scratch_bytes": _sz, "ugk_workspace_bytes": _sz,
         "ugk_loader_tokens": ctypes.c_long, "ugk_loader_position": ctypes.c_long,
         "ugk_param_count": _sz, "ugk_act_count": _sz}
 for _name, _args in _SIGS.items():
@@ -158,8 +166,11 @@ def _ptr(x, what: str, need: int, dtype: str):
 
 
 def _check_tokens(inp, table, C: int, what: str) -> None:
-    """Token ids must index rows of ``table`` (the reference's contract); checked when both are tensors."""
+    """Token ids must index rows of ``table`` (the reference's contract); checked when both are tensors,
+    except while the current stream is being captured into a graph (the check reads the ids back)."""
     import torch
+    if torch.cuda.is_current_stream_capturing():
+        return
     if isinstance(inp, torch.Tensor) and isinstance(table, torch.Tensor) and inp.numel() and C:
         rows = table.numel() // C
         lo, hi = int(inp.min()), int(inp.max())
@@ -347,8 +358,60 @@ def scratch_bytes() -> int:
     return int(lib.ugk_scratch_bytes())
 
 
+def reserve_config(cfg: Config) -> None:
+    """Allocate the workspace every entry point needs at shapes up to ``cfg`` now."""
+    _check(lib.ugk_reserve_config(cfg))
+
+
+def workspace_bytes(cfg: Config) -> int:
+    """Bytes of device workspace the entry points need at shapes up to ``cfg``."""
+    return int(lib.ugk_workspace_bytes(cfg))
+
+
+def set_workspace(buf, cfg: Config) -> None:
+    """Hand the library a caller-owned workspace (a uint8/float device tensor of at least
+    ``workspace_bytes(cfg)`` bytes, 256-byte aligned), or return to library-owned regions with None.
+    The tensor must stay alive until the next call of this function."""
+    if buf is None:
+        _check(lib.ugk_set_workspace(None, 0, cfg))
+        return
+    nbytes = buf.numel() * buf.element_size()
+    if not buf.is_cuda or not buf.is_contiguous():
+        raise ValueError("the workspace must be a contiguous device tensor")
+    _check(lib.ugk_set_workspace(buf.data_ptr(), nbytes, cfg))
+
+
+OP_NAMES = {1: "encoder_forward", 2: "layernorm_forward", 3: "residual_layernorm_forward", 4: "gelu_forward",
+            5: "layernorm_backward (main)", 6: "layernorm_residual_backward (main)", 7: "gelu_backward",
+            8: "layernorm column sums (batched)", 9: "encoder_backward"}
+
+
+def op_timer_start(capacity: int = 1024) -> None:
+    """Record a HIP event pair around each op the step driver issues (at most ``capacity``)."""
+    _check(lib.ugk_op_timer_start(capacity))
+
+
+def op_timer_read(capacity: int = 1024):
+    """Stop the op timer; [(op name, milliseconds)] in issue order."""
+    ms = (ctypes.c_float * capacity)()
+    ops = (ctypes.c_int * capacity)()
+    n = ctypes.c_int(0)
+    _check(lib.ugk_op_timer_read(ms, ops, capacity, ctypes.byref(n)))
+    return [(OP_NAMES.get(ops[i], str(ops[i])), float(ms[i])) for i in range(n.value)]
+
+
 def version() -> int:
     return int(lib.ugk_version())
+
+
+def set_gelu_exact(exact: bool) -> None:
+    """GELU form: False (default) the logistic form, within 1e-5 rel / 1e-6 abs of train_bnn.c on every
+    input; True the glibc-exact tanhf, bit-identical to it."""
+    _check(lib.ugk_set_gelu_exact(1 if exact else 0))
+
+
+def gelu_exact() -> bool:
+    return bool(lib.ugk_get_gelu_exact())
 
 
 def param_count(cfg: Config) -> int:
@@ -401,6 +464,8 @@ MATH_FUNCTIONS.update({f"div_shared{j}": 54 + j for j in range(8)})
 MATH_FUNCTIONS.update({"sqrtf_any": 62})
 # expf without branches for x <= 88.72 and NaN (the softmax's and softplus's)
 MATH_FUNCTIONS.update({"expf_nooverflow": 63})
+# the default (logistic-form) GELU and derivative; their "mismatches" are results outside the literal bar
+MATH_FUNCTIONS.update({"gelu_fast": 64, "gelu_grad_fast": 65})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
