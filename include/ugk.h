@@ -82,6 +82,23 @@ int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias,
                            const float *weight, const float *mean,
                            const float *rstd, int B, int T, int C);
 
+/* No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). ugk_layernorm_backward with its partial column sums in a fixed
+ * device array of 8 MiB per GPU, held until the process ends, instead of the
+ * workspace: the call allocates nothing and never waits. The array holds up to
+ * 1,024 partial rows of 2C floats, so C up to 1,048,576 (larger C is refused
+ * with UGK_EINVAL); rows are unlimited. It keeps the last call's contents and
+ * needs no clearing (every call writes the rows it reads). Calls that overlap
+ * on one GPU (other streams, other threads) race on the array. Results equal
+ * ugk_layernorm_backward's bit for bit for C <= 1,024 (the same partial rows;
+ * above that, once a call needs more partial rows than the array holds, its
+ * column sums take fewer, longer partial rows). */
+int ugk_layernorm_backward_noalloc(float *dinp, float *dweight, float *dbias,
+                                   const float *dout, const float *inp,
+                                   const float *weight, const float *mean,
+                                   const float *rstd, int B, int T, int C);
+
 /* train_bnn.c:182-186 then :81-115 on its output, in one pass: the pair
  * gpt2_kernels.cuh:793-797 (and :806 -> the next block's :784, :806 -> :813)
  * launches back to back. res = x + y (bit-identical to residual_forward);

@@ -243,6 +243,24 @@ int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias, const floa
   return ok();
 }
 
+int ugk_layernorm_backward_noalloc(float *dinp, float *dweight, float *dbias, const float *dout,
+                                   const float *inp, const float *weight, const float *mean, const float *rstd,
+                                   int B, int T, int C) {
+  const char *fn = "ugk_layernorm_backward_noalloc";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T * C == 0) return ok();
+  if (any_null({dinp, dweight, dbias, dout, inp, weight, mean, rstd})) return bad(fn, "NULL pointer");
+  if (noalloc_max_blocks(C) < 1)
+    return set_error(UGK_EINVAL, "%s: C = %d needs more than the %zu bytes of scratch (at most %zu channels)", fn, C,
+                     kNoAllocScratchBytes, kNoAllocScratchBytes / (2 * sizeof(float)));
+  float *partial = noalloc_scratch();
+  if (!partial) return UGK_EHIP;
+  if (int e = launch_layernorm_residual_backward_into(partial, noalloc_max_blocks(C), dinp, dweight, dbias, nullptr,
+                                                      nullptr, dout, inp, weight, mean, rstd, B * T, C))
+    return e;
+  return ok();
+}
+
 int ugk_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
                                    const float *y, const float *weight, const float *bias, int B, int T,
                                    int C) {

@@ -169,6 +169,13 @@ int launch_layernorm_residual_backward_into(float *partial, int max_blocks, floa
 int layernorm_backward_blocks(int rows, int C, bool res, int max_blocks);
 constexpr int kMaxScalarBlocks = 512;
 constexpr int kMaxPartialRows = 1024;  // partial rows the column-sum kernel takes per call
+// The allocation-free LayerNorm backward's partial rows live in a file-scope
+// device array of this size (one per GPU); noalloc_scratch() is its device
+// address on the current device (nullptr with the error set if the lookup
+// failed), noalloc_max_blocks(C) the partial rows of C channels it holds.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+float *noalloc_scratch();
+int noalloc_max_blocks(int C);
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V);
 int launch_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int rows, int V,

@@ -26,6 +26,8 @@
 // conditions around loads made the compiler wait for one row's loads before
 // it issued the next row's.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
+#include <mutex>
+
 #include "ugk_internal.h"
 
 namespace ugk {
@@ -651,6 +653,53 @@ int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias
   if (!partial) return UGK_ENOMEM;
   return launch_layernorm_residual_backward_into(partial, kMaxPartialRows, dinp, dweight, dbias, dx, dy, dout, inp,
                                                  weight, mean, rstd, rows, C);
+}
+
+// ---- allocation-free variant ------------------------------------------------
+// The partial rows in a file-scope device array (one copy per GPU, held until
+// the process ends) instead of the workspace. Host code never passes the
+// array's name to a kernel (on the host it stands for a host-side shadow):
+// it looks up the array's device address once per device with
+// hipGetSymbolAddress and passes that.
+}  // namespace ugk
+
+static __device__ __align__(256) float scratch[ugk::kNoAllocScratchBytes / sizeof(float)];
+
+namespace ugk {
+namespace {
+struct NoAllocAddr {
+  float *ptr = nullptr;
+  hipError_t err = hipSuccess;
+  bool looked_up = false;
+};
+NoAllocAddr g_noalloc[64];
+std::mutex g_noalloc_mu;
+}  // namespace
+
+float *noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    set_error(UGK_EHIP, "no-alloc scratch: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocAddr &a = g_noalloc[dev];
+  if (!a.looked_up) {  // once per device, with that device current
+    void *p = nullptr;
+    a.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (a.err != hipSuccess) (void)hipGetLastError();
+    a.ptr = a.err == hipSuccess ? static_cast<float *>(p) : nullptr;
+    a.looked_up = true;
+  }
+  if (!a.ptr) set_error(UGK_EHIP, "no-alloc scratch: hipGetSymbolAddress failed: %s", hipGetErrorString(a.err));
+  return a.ptr;
+}
+
+int noalloc_max_blocks(int C) {
+  const size_t per_row = 2 * (size_t)C * sizeof(float);
+  const size_t fit = kNoAllocScratchBytes / per_row;
+  return fit < (size_t)kMaxPartialRows ? (int)fit : kMaxPartialRows;
 }
 
 int launch_layernorm_backward(float *dinp, float *dweight, float *dbias, const float *dout,

@@ -72,6 +72,7 @@ _SIGS = {
     "ugk_encoder_backward": [_fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_forward": [_fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_backward": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_layernorm_backward_noalloc": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_residual_layernorm_forward": [_fp] * 8 + [_i, _i, _i],
     "ugk_layernorm_residual_backward": [_fp] * 10 + [_i, _i, _i],
     "ugk_gelu_forward": [_fp, _fp, _i],
