@@ -22,7 +22,8 @@
 // Every load of the float4 paths is unconditional: a lane's columns past the
 // row are clamped onto the row's last float4, and rows past a wavefront's
 // range repeat its last row; the values so loaded are masked out of the sums
-// (added as -0.0f, the identity of IEEE addition) and never stored. Per-lane
+// (added as -0.0f, the identity of IEEE addition) or skipped by a branch that
+// is uniform across the wavefront, and never stored. Per-lane
 // conditions around loads made the compiler wait for one row's loads before
 // it issued the next row's.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
@@ -198,8 +199,9 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // kRes: the new dinp row is also added to rdx and rdy (residual_backward with
 // dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
 // gpt2_kernels.cuh:870-876 launches back to back.
-template <int V, int W, int R, bool kRes>
-__global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
+// MINW: wavefronts per SIMD the register allocation must allow.
+template <int V, int W, int R, bool kRes, int MINW>
+__global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpw, float *__restrict__ rdx,
@@ -320,7 +322,8 @@ __global__ __launch_bounds__(W * kWave) void k_ln_bwd_vec(
             st_nt(a4 + e, a);
           }
         }
-        const bool c = cl.in[v] && live;
+        if (q > 0 && !live) continue;  // uniform across the wavefront: a branch, not a mask per lane
+        const bool c = cl.in[v];
         ab[v].x += c ? dy[q][v].x : -0.0f; ag[v].x += c ? dy[q][v].x * xh.x : -0.0f;
         ab[v].y += c ? dy[q][v].y : -0.0f; ag[v].y += c ? dy[q][v].y * xh.y : -0.0f;
         ab[v].z += c ? dy[q][v].z : -0.0f; ag[v].z += c ? dy[q][v].z * xh.z : -0.0f;
@@ -460,24 +463,28 @@ void bwd_shape(int rows, int max_blocks, int *nblk, int *rpb) {
   *nblk = (rows + per - 1) / per;
 }
 
-// Vector path shapes: two rows in flight per wavefront while they fit the
-// registers (C <= 768), else one; 8 wavefronts per workgroup, 4 when a lane
-// holds more than 4 float4 of a row. Each wavefront takes R rows (one pass)
-// while that leaves at most max_blocks workgroups, else more, R at a time: at
-// 16,384 x 768 one pass over 1,024 workgroups took 72 us for the fused pair
-// against 81 us with two passes over 512. The plain backward and the fused
-// pair share the shape (the rows of each wavefront and workgroup), hence the
-// order in which dweight/dbias are summed, so that the pair is bit-identical
-// to the plain backward followed by residual_backward. (A plain backward with
-// one row in flight and two workgroups per CU measured 19.5 against 20.2 us at
-// 8,192 x 768, but on 1,024 workgroups, whose sums differ.)
+// Vector path shapes: 8 wavefronts per workgroup, 4 when a lane holds more
+// than 4 float4 of a row. Each wavefront takes S consecutive rows (S = 2 while
+// C <= 768, else 1) while that leaves at most max_blocks workgroups, else
+// more: at 16,384 x 768 one pass over 1,024 workgroups took 72 us for the
+// fused pair against 81 us with two passes over 512. The plain backward and
+// the fused pair share this shape (the rows of each wavefront and workgroup),
+// hence the order in which dweight/dbias are summed, so that the pair is
+// bit-identical to the plain backward followed by residual_backward.
+// Rows in flight differ: the fused pair loads both of its rows at once (214
+// registers, two wavefronts per SIMD); the plain backward takes one row at a
+// time within 128 registers, four wavefronts per SIMD, which measured 18.9
+// against 20.1 us at 8,192 x 768 (35.9 against 39.5 us at 16,384) with the
+// same sums.
 struct BwdCfg {
-  int W, R;
+  int W, S, R, MINW;
 };
-constexpr BwdCfg bwd_cfg(int V, bool) { return BwdCfg{V <= 4 ? 8 : 4, V <= 3 ? 2 : 1}; }
+constexpr BwdCfg bwd_cfg(int V, bool res) {
+  return BwdCfg{V <= 4 ? 8 : 4, V <= 3 ? 2 : 1, (V <= 3 && res) ? 2 : 1, (V <= 3 && !res) ? 4 : 1};
+}
 void bwd_shape_vec(int rows, BwdCfg k, int max_blocks, int *nblk, int *rpw) {
   const int per_wave = (rows + max_blocks * k.W - 1) / (max_blocks * k.W);
-  *rpw = per_wave < k.R ? k.R : per_wave;
+  *rpw = per_wave < k.S ? k.S : per_wave;
   *nblk = (rows + k.W * *rpw - 1) / (k.W * *rpw);
 }
 
@@ -588,7 +595,7 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
   switch (V) {
 #define UGK_LN_BWD(v)                                                                                            \
   case v:                                                                                                        \
-    launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes>), \
+    launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW>), \
                        grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx,  \
                        rdy, same);                                                                               \
     break;
