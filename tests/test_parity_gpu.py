@@ -330,8 +330,12 @@ def test_encoder_repeated_token_case(gpu, oracle):
     enc_case(gpu, oracle, 2, 3, 4, 7, np.array([5, 2, 5, 0, 5, 6], np.int32), 1)
 
 
-@pytest.mark.parametrize("B,T,C,V", [(4, 64, 384, 27), (1, 1, 4, 3), (3, 5, 13, 11), (2, 33, 768, 100)])
+@pytest.mark.parametrize("B,T,C,V", [(4, 64, 384, 27), (1, 1, 4, 3), (3, 5, 13, 11), (2, 33, 768, 100),
+                                     (2, 40, 1600, 30), (1, 70, 1020, 2), (3, 50, 896, 500)])
 def test_encoder_uniform(gpu, oracle, B, T, C, V):
+    """Column groups per lane: C = 4..384 one or two float4 per lane, 768 three, 896, 1020 and 1600
+    four (two passes at 1600, ragged tails at 896, 1020, 1600); V = 2 and 30 give buckets of 2-32
+    rows (batched loads) and beyond 32 (the large-bucket kernel)."""
     enc_case(gpu, oracle, B, T, C, V, gen.tokens_uniform(gen.rng(V), B * T, V), C, reps=2)
 
 

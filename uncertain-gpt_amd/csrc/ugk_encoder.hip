@@ -216,6 +216,8 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
     return;
   }
   // dwpe[t, c] += dout[b, t, c] for b = 0..B-1, in order; 8 rows in flight.
+  // dout is read with ordinary (cached) loads: K2 reads the same rows again,
+  // and finds part of them in the cache (K2 15.8 -> 14.3 us at 8,192 x 768).
   const size_t j = (size_t)(blockIdx.x - ins_blocks) * kBlock + threadIdx.x;
   constexpr int kB = 8;
   if (kVec) {
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
       float4 d[kB];
 #pragma unroll
       for (int q = 0; q < kB; q++)
-        if (b0 + q < B) d[q] = ld_nt(g + (size_t)(b0 + q) * T * C4);
+        if (b0 + q < B) d[q] = g[(size_t)(b0 + q) * T * C4];
 #pragma unroll
       for (int q = 0; q < kB; q++)
         if (b0 + q < B) {
