@@ -110,8 +110,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 # in-step op name -> the prefix of its kernel's short name in the PMC summary
-PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main) <3, 8, 2, true, 1>",
-           "layernorm_backward (main)": "layernorm_backward (main) <3, 8, 1, false, 4>",
+PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main) <3, 8, 2, true, 1, true>",
+           "layernorm_backward (main)": "layernorm_backward (main) <3, 8, 1, false, 4, false>",
            "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
            "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 
