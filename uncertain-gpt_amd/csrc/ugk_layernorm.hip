@@ -204,8 +204,11 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // kRes, large calls write it with ordinary stores, which measured faster
 // (8,192 x 768: 17.5 against 19.0 us in the step, 22.7 against 23.9 us with
 // the column sums); below 2^21 elements, where the written rows fit the
-// caches and are flushed at the end of the launch, non-temporal stores
-// stay faster (256 x 384: 8.7 against 9.9 us).
+// caches and are written back at the end of the launch, non-temporal stores
+// are kept. The fused pair keeps non-temporal stores for all three rows:
+// an ordinary dinp store made it faster alone (35.7 against 37.2 us cold at
+// 8,192 x 768) but the step slower (3.02 against 2.93 ms), the dirty lines
+// of its 24 launches being written back during the kernels that follow.
 template <int V, int W, int R, bool kRes, int MINW, bool kNt>
 __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
