@@ -20,6 +20,11 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a GPU; calls the HIP kernels through libugk.so")
 
 
+def pytest_sessionfinish(session, exitstatus):
+    import literal_bar
+    literal_bar.write()
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from oracle import Oracle

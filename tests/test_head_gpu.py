@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import gen
+import literal_bar
 from test_oracle_head import head_inputs, special_rows
 
 pytestmark = pytest.mark.gpu
@@ -60,8 +61,8 @@ def check_forward(gpu_p, gpu_l, cpu_p, cpu_l, logits, targets):
     gl, cl = gpu_l[finite].astype(np.float64), cpu_l[finite].astype(np.float64)
     assert np.abs(gl - l64).max() <= np.abs(cl - l64).max() + 4 * EPS * np.abs(l64).max() + 1e-7
     literal = float((np.abs(gp - cp) <= 1e-6 + 1e-5 * cp).mean())
-    print(f"V={V}: probs within the literal 1e-5/1e-6 bar of the CPU: {literal:.4%}; "
-          f"max rel error vs float64: GPU {err_g:.3g}, CPU {err_c:.3g}")
+    literal_bar.record(f"softmax_crossentropy probs, V = {V}, {rows} rows", literal)
+    print(f"V={V}: max rel error vs float64: GPU {err_g:.3g}, CPU {err_c:.3g}")
 
 
 @pytest.mark.parametrize("B,T,V", [(4, 64, 27), (2, 3, 1000), (1, 5, 50257), (2, 3, 4097), (1, 3, 60000),

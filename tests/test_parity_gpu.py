@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import gen
+import literal_bar
 
 pytestmark = pytest.mark.gpu
 
@@ -261,7 +262,8 @@ def ln_case(gpu, oracle, B, T, C, seed, offset=0, reps=1):
                                    (1, 2, 3000), (3, 7, 4)])
 def test_layernorm(gpu, oracle, B, T, C):
     literal = ln_case(gpu, oracle, B, T, C, seed=B * 1000 + T * 10 + C, reps=2)
-    print(f"literal-bar pass fraction for the column sums: {literal}")
+    for name, frac in literal.items():
+        literal_bar.record(f"layernorm_backward {name}, {B * T} x {C}", frac)
 
 
 def test_layernorm_misaligned(gpu, oracle):
@@ -446,9 +448,17 @@ def test_golden_fixtures(gpu):
 
 # ---- full benchmark shapes ------------------------------------------------------------
 
+def test_full_cfg5_layernorm(gpu, oracle):
+    """The benchmark's own LayerNorm shape, 8,192 x 768."""
+    literal = ln_case(gpu, oracle, 8, 1024, 768, seed=55, reps=2)
+    for name, frac in literal.items():
+        literal_bar.record(f"layernorm_backward {name}, 8192 x 768", frac)
+
+
 def test_full_cfg2_layernorm(gpu, oracle):
     literal = ln_case(gpu, oracle, 16, 1024, 768, seed=22, reps=2)
-    print(f"16384x768 literal-bar pass fraction for the column sums: {literal}")
+    for name, frac in literal.items():
+        literal_bar.record(f"layernorm_backward {name}, 16384 x 768", frac)
 
 
 def test_full_cfg3_gelu_residual(gpu, oracle):
