@@ -78,8 +78,10 @@ def step_bytes(B, T, C, L, n_mat):
 
 
 KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
-    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwd>", "gelu_backward"),
-    ("k_map_vec4<ugk::(anonymous namespace)::GeluFwd>", "gelu_forward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwdFast>", "gelu_backward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluFwdFast>", "gelu_forward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwd>", "gelu_backward (exact form)"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluFwd>", "gelu_forward (exact form)"),
     ("k_map_vec4<ugk::(anonymous namespace)::Materialize>", "bayes_materialize"),
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualBwd>", "residual_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualFwd>", "residual_forward"),
