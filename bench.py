@@ -86,6 +86,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualBwd>", "residual_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::ResidualFwd>", "residual_forward"),
     ("k_ln_bwd_vec", "layernorm_backward (main)"),
+    ("k_ln_bwd_team", "layernorm_backward (main, row teams)"),
     ("k_ln_bwd_reduce_batch", "layernorm_backward (batched column sums)"),
     ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
     ("k_ln_fwd_vec", "layernorm_forward"),
@@ -112,8 +113,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 # in-step op name -> the prefix of its kernel's short name in the PMC summary
-PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main) <3, 8, 2, true, 1, true>",
-           "layernorm_backward (main)": "layernorm_backward (main) <3, 8, 1, false, 4, false>",
+PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true>",
+           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false>",
            "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
            "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 

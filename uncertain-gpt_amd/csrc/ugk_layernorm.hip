@@ -362,6 +362,149 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
   }
 }
 
+// Backward with each row split over a team of P wavefronts, one float4 per
+// lane (C/4 <= 64 P). T teams form a workgroup; team t of workgroup g takes the
+// rpt consecutive rows starting at (T g + t) * rpt, R at a time, all their
+// loads issued before the first arithmetic instruction. Each wavefront adds
+// its part of a row's two sums (the four components in order, then a
+// wavefront sum) and writes it to LDS; after a barrier every wavefront of the
+// team adds the P parts in part order, so all of them hold the same row sums.
+// The dweight/dbias terms of a wavefront's columns are added in registers in
+// row order; at the end the T teams' sums are added column by column in team
+// order into the workgroup's partial row, as in k_ln_bwd_vec. With four rows
+// in flight the fused pair needs 155 registers, so a 12-wavefront workgroup
+// (P = 3, T = 4) runs alone on a CU: 35.7 against 37.2 us for the
+// two-rows-per-wavefront kernel at 8,192 x 768, cold, with the same 512
+// partial rows. rpt and T fix the order of every addition; R does not, so the
+// plain backward (R = 2) and the fused pair (R = 4) give the same bits.
+template <int P, int T, int R, bool kRes, int MINW, bool kNt>
+__global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
+    float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
+    const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
+    const float *__restrict__ rstd, int rows, int C, int rpt, float *__restrict__ rdx,
+    float *__restrict__ rdy, int same) {
+  __shared__ float parts[2][T][R][P][2];  // a row's two sums by part, double-buffered by pass
+  __shared__ float4 red[T][2][P * kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int team = wave / P, part = wave - team * P;
+  const int C4 = C >> 2;
+  const float Cf = (float)C;
+  const int c4 = part * kWave + lane;
+  const bool in = c4 < C4;
+  const int col = in ? c4 : C4 - 1;  // past the row: a valid column, masked out of the sums, never stored
+  const float4 *x4 = reinterpret_cast<const float4 *>(inp);
+  const float4 *dy4 = reinterpret_cast<const float4 *>(dout);
+  float4 *dx4 = reinterpret_cast<float4 *>(dinp);
+  float4 *a4 = reinterpret_cast<float4 *>(rdx);
+  float4 *b4 = reinterpret_cast<float4 *>(rdy);
+  const float4 w = reinterpret_cast<const float4 *>(weight)[col];
+  float4 ag = make_float4(0.f, 0.f, 0.f, 0.f), ab = ag;
+  const int t0 = (blockIdx.x * T + team) * rpt;
+  const int t1 = min(t0 + rpt, rows);
+  const int last = t1 > t0 ? t1 - 1 : rows - 1;  // a team past the last row loads that row, uses nothing
+  const int passes = (rpt + R - 1) / R;  // the same for every team: all reach every barrier
+  for (int ps = 0; ps < passes; ps++) {
+    const int row = t0 + ps * R;
+    bool live[R];
+    int rq[R];
+    size_t off[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      live[q] = row + q < t1;
+      rq[q] = live[q] ? row + q : last;
+      off[q] = (size_t)rq[q] * C4 + col;
+    }
+    float4 x[R], dy[R], dx[R], ra[kRes ? R : 1], rb[kRes ? R : 1];
+    float m[R], r[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      x[q] = ld_nt(x4 + off[q]);
+      dy[q] = ld_nt(dy4 + off[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      m[q] = mean[rq[q]];
+      r[q] = rstd[rq[q]];
+    }
+#pragma unroll
+    for (int q = 0; q < R; q++) dx[q] = ld_nt(dx4 + off[q]);
+    if (kRes) {
+      // rdy is loaded even when it is rdx (same): a valid address, never used
+#pragma unroll
+      for (int q = 0; q < R; q++) {
+        ra[kRes ? q : 0] = ld_nt(a4 + off[q]);
+        rb[kRes ? q : 0] = ld_nt(b4 + off[q]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float4 xh[R], dn[R];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      xh[q].x = (x[q].x - m[q]) * r[q]; dn[q].x = dy[q].x * w.x;
+      xh[q].y = (x[q].y - m[q]) * r[q]; dn[q].y = dy[q].y * w.y;
+      xh[q].z = (x[q].z - m[q]) * r[q]; dn[q].z = dy[q].z * w.z;
+      xh[q].w = (x[q].w - m[q]) * r[q]; dn[q].w = dy[q].w * w.w;
+      float s1 = in ? ((dn[q].x + dn[q].y) + dn[q].z) + dn[q].w : -0.0f;
+      float s2 = in ? ((dn[q].x * xh[q].x + dn[q].y * xh[q].y) + dn[q].z * xh[q].z) + dn[q].w * xh[q].w : -0.0f;
+      s1 = wave_sum(s1);
+      s2 = wave_sum(s2);
+      if (lane == 0) {
+        parts[ps & 1][team][q][part][0] = s1;
+        parts[ps & 1][team][q][part][1] = s2;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      if (!live[q]) break;  // the same for the team's wavefronts; dead rows are all at the end
+      float s1 = parts[ps & 1][team][q][0][0], s2 = parts[ps & 1][team][q][0][1];
+#pragma unroll
+      for (int k = 1; k < P; k++) {
+        s1 += parts[ps & 1][team][q][k][0];
+        s2 += parts[ps & 1][team][q][k][1];
+      }
+      const float dnm = s1 / Cf, dnxm = s2 / Cf;
+      float4 o;
+      o.x = dx[q].x + r[q] * (dn[q].x - dnm - xh[q].x * dnxm);
+      o.y = dx[q].y + r[q] * (dn[q].y - dnm - xh[q].y * dnxm);
+      o.z = dx[q].z + r[q] * (dn[q].z - dnm - xh[q].z * dnxm);
+      o.w = dx[q].w + r[q] * (dn[q].w - dnm - xh[q].w * dnxm);
+      if (in) {
+        if (kNt)
+          st_nt(dx4 + off[q], o);
+        else
+          dx4[off[q]] = o;
+        if (kRes) {
+          float4 a = add4(ra[kRes ? q : 0], o);
+          if (same) {
+            a = add4(a, o);
+          } else {
+            st_nt(b4 + off[q], add4(rb[kRes ? q : 0], o));
+          }
+          st_nt(a4 + off[q], a);
+        }
+      }
+      ab.x += dy[q].x; ag.x += dy[q].x * xh[q].x;
+      ab.y += dy[q].y; ag.y += dy[q].y * xh[q].y;
+      ab.z += dy[q].z; ag.z += dy[q].z * xh[q].z;
+      ab.w += dy[q].w; ag.w += dy[q].w * xh[q].w;
+    }
+  }
+  red[team][0][c4] = ag;
+  red[team][1][c4] = ab;
+  __syncthreads();
+  float4 *prow = reinterpret_cast<float4 *>(partial + (size_t)blockIdx.x * 2 * C);
+  for (int e = threadIdx.x; e < 2 * C4; e += P * T * kWave) {
+    const int which = e >= C4 ? 1 : 0;
+    const int cc = e - which * C4;
+    float4 t = red[0][which][cc];
+#pragma unroll
+    for (int k = 1; k < T; k++) t = add4(t, red[k][which][cc]);
+    prow[which * C4 + cc] = t;
+  }
+}
+
 // Backward for any C and alignment. Phase 1: one wavefront per row writes
 // dinp. Phase 2: thread-per-channel column sums over the workgroup's rows.
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_scalar(float *dinp, float *partial, const float *dout,
@@ -500,9 +643,44 @@ void bwd_shape_vec(int rows, BwdCfg k, int max_blocks, int *nblk, int *rpw) {
   *nblk = (rows + k.W * *rpw - 1) / (k.W * *rpw);
 }
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Team path, V = 3 (C/4 in 129..192), while the rows fill the GPU at most
+// once at 32 rows per CU (8,192 on MI355X): teams of 3 wavefronts, 4 teams
+// per workgroup, at least 4 rows per team (16 per workgroup, 512 workgroups
+// at 8,192 rows), more while that would leave more than max_blocks
+// workgroups. The plain backward keeps 2 rows in flight (70 registers), the
+// fused pair 4 (156). Beyond that the two-rows-per-wavefront kernels are
+// used: at 16,384 x 768 they measured as fast for the fused pair and faster
+// for the plain backward (41.7 against 45.0 us with the column sums).
+constexpr int kTeamParts = 3, kTeams = 4, kTeamRows = 4;
+bool team_path(int rows, int C) {
+  return ((C >> 2) + kWave - 1) / kWave == kTeamParts && rows <= cu_count() * 32;
+}
+void team_shape(int rows, int max_blocks, int *nblk, int *rpt) {
+  const int per_team = (rows + max_blocks * kTeams - 1) / (max_blocks * kTeams);
+  *rpt = per_team < kTeamRows ? kTeamRows : per_team;
+  *nblk = (rows + kTeams * *rpt - 1) / (kTeams * *rpt);
+}
+
 int vec_blocks(int rows, int C, bool res, int max_blocks) {
   int nblk, rpw;
-  bwd_shape_vec(rows, bwd_cfg(((C >> 2) + kWave - 1) / kWave, res), max_blocks, &nblk, &rpw);
+  const int V = ((C >> 2) + kWave - 1) / kWave;
+  if (team_path(rows, C))
+    team_shape(rows, max_blocks, &nblk, &rpw);
+  else
+    bwd_shape_vec(rows, bwd_cfg(V, res), max_blocks, &nblk, &rpw);
   return nblk;
 }
 
@@ -512,15 +690,7 @@ int vec_blocks(int rows, int C, bool res, int max_blocks) {
 // else one (35.0 against 37.1 us at 16,384 x 768).
 int fwd_rpw(int rows, bool res) {
   if (!res) return 1;
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return rows <= cus[dev] * 32 ? 2 : 1;
+  return rows <= cu_count() * 32 ? 2 : 1;
 }
 
 }  // namespace
@@ -600,11 +770,26 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
                       float *rdx, float *rdy, int max_blocks) {
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
+  const int same = rdx == rdy ? 1 : 0;
+  const bool nt = (size_t)rows * (size_t)C < ((size_t)1 << 21);
+  if (team_path(rows, C)) {
+    int rpt;
+    team_shape(rows, max_blocks, &nblk, &rpt);
+    const dim3 grid(nblk), block(kTeamParts * kTeams * kWave);
+    if constexpr (kRes)
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true>), grid, block, 0, dinp, partial, dout, inp,
+             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+    else if (nt)
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true>), grid, block, 0, dinp, partial, dout, inp,
+             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+    else
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false>), grid, block, 0, dinp, partial, dout, inp,
+             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+    return nblk;
+  }
   const BwdCfg k = bwd_cfg(V, kRes);
   bwd_shape_vec(rows, k, max_blocks, &nblk, &rpw);
   const dim3 grid(nblk), block(k.W * kWave);
-  const int same = rdx == rdy ? 1 : 0;
-  const bool nt = (size_t)rows * (size_t)C < ((size_t)1 << 21);
   switch (V) {
 #define UGK_LN_BWD(v)                                                                                            \
   case v:                                                                                                        \
