@@ -259,7 +259,7 @@ def ln_case(gpu, oracle, B, T, C, seed, offset=0, reps=1):
 
 
 @pytest.mark.parametrize("B,T,C", [(4, 64, 384), (1, 3, 768), (2, 5, 16), (1, 2, 2048), (1, 4, 13),
-                                   (1, 2, 3000), (3, 7, 4)])
+                                   (1, 2, 3000), (3, 7, 4), (2, 50, 600), (1, 9, 516)])
 def test_layernorm(gpu, oracle, B, T, C):
     literal = ln_case(gpu, oracle, B, T, C, seed=B * 1000 + T * 10 + C, reps=2)
     for name, frac in literal.items():
