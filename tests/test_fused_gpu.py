@@ -40,12 +40,12 @@ def test_residual_layernorm_forward_fused(gpu, B, T, C, offset):
 
 @pytest.mark.parametrize("B,T,C,offset", [(8, 1024, 768, 0), (4, 64, 384, 0), (1, 5, 2048, 0), (2, 3, 13, 0),
                                           (2, 8, 384, 1), (1, 3, 3000, 0), (2, 50, 600, 0), (1, 9, 516, 0),
-                                          (16, 1024, 768, 0)])
+                                          (16, 1024, 768, 0), (1, 8192, 768, 0), (1, 8193, 768, 0)])
 @pytest.mark.parametrize("same", [False, True])
 def test_layernorm_residual_backward_fused(gpu, B, T, C, offset, same):
     """The pair equals layernorm_backward then residual_backward, bit for bit: at C = 516..768
-    (three wavefronts per row, the third partly idle at 516 and 600) up to 8,192 rows, and with
-    one wavefront per row beyond (16,384 x 768) and at other C."""
+    (three wavefronts per row, the third partly idle at 516 and 600) up to 32 rows per CU (8,192
+    on MI355X), and with one wavefront per row beyond (8,193 and 16,384 rows) and at other C."""
     g = gen.rng(B * 104729 + T * 17 + C + same)
     n, rows = B * T * C, B * T
     x, dout = gen.normal(g, (n,)), gen.normal(g, (n,))
