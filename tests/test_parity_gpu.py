@@ -473,6 +473,14 @@ def test_full_cfg3_gelu_residual(gpu, oracle):
     out = np.zeros(N, np.float32)
     oracle.residual_forward(out, x, y, N)
     assert_bits(host(t), out, "residual cfg3")
+    del t
+    # backward at the same N: both accumulators start nonzero
+    dx0, dy0 = gen.normal(g, (N,)), gen.normal(g, (N,))
+    tdx, tdy = dev(dx0), dev(dy0)
+    gpu.residual_backward(tdx, tdy, dev(x), N)
+    oracle.residual_backward(dx0, dy0, x, N)
+    assert_bits(host(tdx), dx0, "residual_backward dx cfg3")
+    assert_bits(host(tdy), dy0, "residual_backward dy cfg3")
 
 
 def test_full_cfg5_materialize(gpu, oracle):
