@@ -647,10 +647,16 @@ void bwd_shape_vec(int rows, BwdCfg k, int max_blocks, int *nblk, int *rpw) {
 int cu_count() {
   static int cus[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();  // leave no error for the next launch check to report
+    return 256;
+  }
   if (cus[dev] == 0) {
     int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
     cus[dev] = n;
   }
   return cus[dev];
@@ -674,13 +680,18 @@ void team_shape(int rows, int max_blocks, int *nblk, int *rpt) {
   *nblk = (rows + kTeams * *rpt - 1) / (kTeams * *rpt);
 }
 
+// Workgroups (partial rows) of a vector-path call, for sizing its workspace:
+// at V = 3 the larger of the two kernels' counts, so that the size does not
+// depend on the device the call later runs on.
 int vec_blocks(int rows, int C, bool res, int max_blocks) {
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
-  if (team_path(rows, C))
-    team_shape(rows, max_blocks, &nblk, &rpw);
-  else
-    bwd_shape_vec(rows, bwd_cfg(V, res), max_blocks, &nblk, &rpw);
+  bwd_shape_vec(rows, bwd_cfg(V, res), max_blocks, &nblk, &rpw);
+  if (V == kTeamParts) {
+    int nt, rpt;
+    team_shape(rows, max_blocks, &nt, &rpt);
+    if (nt > nblk) nblk = nt;
+  }
   return nblk;
 }
 
