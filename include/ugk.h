@@ -343,10 +343,11 @@ int ugk_set_workspace(void *ptr, size_t bytes, ugk_config cfg);
 /* ---- per-op timing of the step driver (no counterpart in the reference,
  * which times single launches with cudaEvents in its dev/ harnesses). While
  * started, ugk_gpt2_layers_forward/backward time each library op they issue
- * (at most `capacity`) with a pair of HIP events: an op of one kernel has
- * them recorded by its dispatch (hipExtLaunchKernelGGL), so they measure the
- * kernel itself; the encoder backward (three kernels) is bracketed by two
- * event records on the library stream. ugk_op_timer_read waits for the last
+ * (at most `capacity`) with a pair of HIP events recorded by the op's own
+ * dispatches (hipExtLaunchKernelGGL): the start with its first kernel, the
+ * stop with its last, so they measure the kernels themselves; the encoder
+ * backward (three kernels) is bracketed by two event records on the library
+ * stream instead. ugk_op_timer_read waits for the last
  * event, writes each op's duration in milliseconds and its kind (UGK_OP_*)
  * in issue order, sets *count, and stops the timer. The events are created by
  * ugk_op_timer_start. */

@@ -145,9 +145,12 @@ def test_reserve_config_then_no_growth(gpu):
     assert gpu.scratch_bytes() == held
 
 
-def test_op_timer_records_the_driver_sequence(gpu):
-    B, T, C, V, L = 2, 64, 384, 100, 2
-    cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=6, maxT=T, L=L)
+@pytest.mark.parametrize("C,NH,L", [(384, 6, 2), (384, 6, 16), (13, 1, 2)])
+def test_op_timer_records_the_driver_sequence(gpu, C, NH, L):
+    """One record per op, in issue order, also for ops of several kernels: at L = 16 the batched
+    column sums take two launches, at C = 13 (scalar path) the fused LayerNorm backward pair does."""
+    B, T, V = 2, 64, 100
+    cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=T, L=L)
     g = torch.Generator(device=DEV)
     g.manual_seed(3)
     params = torch.randn(gpu.param_count(cfg), generator=g, device=DEV) * 0.02 + 0.5
@@ -155,10 +158,10 @@ def test_op_timer_records_the_driver_sequence(gpu):
     ga = torch.randn(gpu.act_count(cfg), generator=g, device=DEV) * 0.1
     grads = torch.zeros(gpu.param_count(cfg), device=DEV)
     inp = torch.randint(0, V, (B * T,), generator=g, device=DEV, dtype=torch.int32)
-    gpu.op_timer_start(64)
+    gpu.op_timer_start(256)
     gpu.gpt2_layers_forward(acts, params, inp, cfg)
     gpu.gpt2_layers_backward(grads, ga, acts, params, inp, cfg)
-    rec = gpu.op_timer_read(64)
+    rec = gpu.op_timer_read(256)
     fwd = ["encoder_forward", "layernorm_forward"] + ["residual_layernorm_forward", "gelu_forward",
                                                       "residual_layernorm_forward"] * L
     bwd = ["layernorm_residual_backward (main)"]
@@ -170,4 +173,4 @@ def test_op_timer_records_the_driver_sequence(gpu):
     assert all(ms > 0 for _, ms in rec)
     # stopped: a further step records nothing
     gpu.gpt2_layers_forward(acts, params, inp, cfg)
-    assert gpu.op_timer_read(64) == []
+    assert gpu.op_timer_read(256) == []

@@ -633,9 +633,10 @@ int dense(int rc, const char *what) {
   return rc ? set_error(rc, "dense op callback %s returned %d", what, rc) : UGK_OK;
 }
 
-// Per-op timer of the step driver. An op of one kernel gets its event pair
-// recorded by the dispatch itself (the kernel's own duration); the encoder
-// backward, three kernels, is bracketed by two event records on the stream.
+// Per-op timer of the step driver. An op's event pair is recorded by its
+// dispatches themselves (from its first kernel's start to its last kernel's
+// end); the encoder backward, whose three kernels are launched directly, is
+// bracketed by two event records on the stream.
 struct OpTimer {
   std::vector<hipEvent_t> ev;
   std::vector<LaunchEvents> pair;
@@ -652,18 +653,23 @@ int timed(int op, F &&f) {
   const int i = t.n++;
   t.op[i] = op;
   if (op == UGK_OP_ENCODER_BACKWARD) {
-    if (hipEventRecord(t.ev[2 * i], stream()) != hipSuccess) return check_launch("op timer");
+    if (hipEventRecord(t.ev[2 * i], stream()) != hipSuccess) {
+      (void)hipGetLastError();
+      t.n--;
+      return set_error(UGK_EHIP, "op timer: hipEventRecord failed");
+    }
     const int rc = f();
-    if (hipEventRecord(t.ev[2 * i + 1], stream()) != hipSuccess) return check_launch("op timer");
+    if (hipEventRecord(t.ev[2 * i + 1], stream()) != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(UGK_EHIP, "op timer: hipEventRecord failed");
+    }
     return rc;
   }
-  t.pair[i] = {t.ev[2 * i], t.ev[2 * i + 1]};
+  t.pair[i] = {t.ev[2 * i], t.ev[2 * i + 1], false};
   armed_events() = &t.pair[i];
   const int rc = f();
-  if (armed_events()) {  // nothing was launched (an empty op): no record
-    armed_events() = nullptr;
-    t.n--;
-  }
+  armed_events() = nullptr;
+  if (!t.pair[i].started) t.n--;  // nothing was launched (an empty op): no record
   return rc;
 }
 
@@ -836,7 +842,7 @@ int ugk_op_timer_start(int capacity) {
   OpTimer &t = g_timer;
   for (hipEvent_t e : t.ev) (void)hipEventDestroy(e);
   t.ev.assign(2 * (size_t)capacity, nullptr);
-  t.pair.assign((size_t)capacity, LaunchEvents{nullptr, nullptr});
+  t.pair.assign((size_t)capacity, LaunchEvents{nullptr, nullptr, false});
   t.op.assign((size_t)capacity, 0);
   t.n = 0;
   t.on = false;

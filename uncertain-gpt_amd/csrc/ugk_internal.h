@@ -31,12 +31,15 @@ int check_launch(const char *what);
 enum Region { kRegLn = 0, kRegEncoder = 1, kRegKl = 2, kRegSoftmax = 3, kNumRegions = 4 };
 void *workspace(Region r, size_t bytes, bool *fresh = nullptr);
 
-// The step driver's op timer arms an event pair for the next kernel launch
-// of an op; launch() then records them with the dispatch itself
-// (hipExtLaunchKernelGGL: the kernel's own start and end, no marker packets
-// between kernels), once. Unarmed, launch() is a plain launch on stream().
+// The step driver's op timer arms an event pair for the kernel launches of
+// an op; launch() then records them with the dispatches themselves
+// (hipExtLaunchKernelGGL, no marker packets between kernels): the start with
+// the op's first kernel, the stop with each of its kernels, so that the pair
+// spans from the first kernel's start to the last one's end. Unarmed,
+// launch() is a plain launch on stream().
 struct LaunchEvents {
   hipEvent_t start, stop;
+  bool started;  // the start has been recorded (a kernel of the op was launched)
 };
 LaunchEvents *&armed_events();
 
@@ -44,8 +47,9 @@ template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, unsigned shmem, Args... args) {
   LaunchEvents *ev = armed_events();
   if (ev) {
-    armed_events() = nullptr;
-    hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream(), ev->start, ev->stop, 0u, static_cast<KArgs>(args)...);
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream(), ev->started ? nullptr : ev->start, ev->stop, 0u,
+                          static_cast<KArgs>(args)...);
+    ev->started = true;
   } else {
     hipLaunchKernelGGL(kernel, grid, block, shmem, stream(), static_cast<KArgs>(args)...);
   }
