@@ -91,6 +91,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
     ("k_ln_fwd_vec", "layernorm_forward"),
     ("k_enc_fwd_vec", "encoder_forward"),
+    ("k_enc_ln_fwd_vec", "encoder_layernorm_forward"),
     ("k_enc_bwd_insert", "encoder_backward (insert + dwpe)"),
     ("k_enc_bwd_add", "encoder_backward (add)"),
     ("k_enc_bwd_large", "encoder_backward (large buckets)"),
@@ -230,8 +231,9 @@ def main():
     n_mat = P - (C * V + V)  # GPT-2-124M with the head tied to wte: 124,439,808
     A = ugk.act_count(cfg)
     per, count, total_bytes = step_bytes(B, T, C, L, n_mat)
-    # the fused pairs of the driver skip 2L LayerNorm input reads and 2L residual dout reads
-    moved_bytes = total_bytes - 2 * (2 * L) * 4 * (B * T * C)
+    # the fused pairs of the driver skip 2L + 1 LayerNorm input reads (the first LayerNorm
+    # normalises the encoder's rows as it writes them) and 2L residual dout reads
+    moved_bytes = total_bytes - (2 * (2 * L) + 1) * 4 * (B * T * C)
     log(f"bench: params {P} (materialize {n_mat}), acts {A}, algorithmic bytes/step {total_bytes / 1e9:.3f} GB")
 
     g = torch.Generator(device=dev)
@@ -288,6 +290,7 @@ def main():
     N = B * T * C
     op_bytes = {  # algorithmic bytes per launch at the step shape
         "encoder_forward": per["encoder_forward"], "layernorm_forward": per["layernorm_forward"],
+        "encoder_layernorm_forward": 16 * N + 12 * B * T + 8 * C,
         "residual_layernorm_forward": 16 * N + 8 * B * T + 8 * C, "gelu_forward": per["gelu_forward"],
         "layernorm_backward (main)": 16 * N + 8 * B * T + 4 * C,
         "layernorm_residual_backward (main)": 32 * N + 8 * B * T + 4 * C,
@@ -341,6 +344,13 @@ def main():
         ugk.layernorm_forward(d["out"], d["mean"], d["rstd"], d["x"], d["w"], d["b"], B, T, C)
         return d
 
+    def mk_enc_ln():
+        d = mk_enc()
+        d.update({"ln": torch.empty(N, device=dev), "mean": torch.empty(B * T, device=dev),
+                  "rstd": torch.empty(B * T, device=dev), "w": torch.ones(C, device=dev),
+                  "b": torch.zeros(C, device=dev)})
+        return d
+
     def mk_ln_res():
         d = mk_ln()
         d["rx"], d["ry"] = rnd(N), rnd(N)
@@ -377,9 +387,13 @@ def main():
         "bayes_materialize": (mk_mat, 16 * n_mat, lambda d: chk(lib.ugk_bayes_materialize(
             P_(d["w"]), P_(d["mu"]), P_(d["rho"]), P_(d["eps"]), n_mat))),
     }
-    # the two fused pairs the step driver runs (not separate entries of `per`:
-    # their bytes are the pair's, 16 and 32 per element, see step_bytes)
+    # the fused pairs the step driver runs (not separate entries of `per`: their
+    # bytes are the pair's, 16, 16 and 32 per element, see step_bytes)
     fused_plan = {
+        "encoder_layernorm_forward (fused pair)": (mk_enc_ln, 20 * N, 16 * N + 12 * B * T + 8 * C, lambda d: chk(
+            lib.ugk_encoder_layernorm_forward(P_(d["out"]), P_(d["ln"]), P_(d["mean"]), P_(d["rstd"]),
+                                              P_(d["inp"]), P_(d["wte"]), P_(d["wpe"]), P_(d["w"]), P_(d["b"]),
+                                              B, T, C))),
         "residual_layernorm_forward (fused pair)": (mk_ln, 20 * N, 16 * N + 8 * B * T + 8 * C, lambda d: chk(
             lib.ugk_residual_layernorm_forward(P_(d["dinp"]), P_(d["out"]), P_(d["mean"]), P_(d["rstd"]),
                                                P_(d["x"]), P_(d["dout"]), P_(d["w"]), P_(d["b"]), B, T, C))),
@@ -430,7 +444,7 @@ def main():
         record(kernels, name, per[name], ms, launches, n_sets, {"per_step": count[name]})
     for name, (make, set_bytes, nbytes, fn) in fused_plan.items():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
-        record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 2 * L})
+        record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 1 if name.startswith("encoder") else 2 * L})
     # materialize over the reference's own untied layout at this shape (it stores
     # the head weight and bias, gpt2_kernels.cuh:681-683): all P parameters
     ms, launches, n_sets = time_cold(lambda: {"mu": rnd(P) * 0.02, "rho": rnd(P) * 0.1 - 5.0, "eps": rnd(P),
@@ -449,6 +463,7 @@ def main():
         "residual_forward": (2, 1, N), "residual_backward": (3, 2, N),
         "bayes_materialize": (3, 1, n_mat),
         "residual_layernorm_forward (fused pair)": (2, 2, N),
+        "encoder_layernorm_forward (fused pair)": (2, 2, N),
         "layernorm_residual_backward (fused pair)": (5, 3, N),
     }
     ceil_cache = {}

@@ -99,6 +99,18 @@ int ugk_layernorm_backward_noalloc(float *dinp, float *dweight, float *dbias,
                                    const float *weight, const float *mean,
                                    const float *rstd, int B, int T, int C);
 
+/* train_bnn.c:41-65 then :81-115 on its output, in one pass: the pair
+ * gpt2_kernels.cuh:775-776 -> :784 (block 0's first LayerNorm; -> :813 when
+ * L = 0) launches back to back. enc = the encoder output (bit-identical to
+ * encoder_forward); out, mean, rstd = layernorm_forward(enc) (identical to
+ * calling it on enc). No single counterpart in the reference;
+ * ugk_gpt2_layers_forward uses it. */
+int ugk_encoder_layernorm_forward(float *enc, float *out, float *mean,
+                                  float *rstd, const int *inp,
+                                  const float *wte, const float *wpe,
+                                  const float *weight, const float *bias,
+                                  int B, int T, int C);
+
 /* train_bnn.c:182-186 then :81-115 on its output, in one pass: the pair
  * gpt2_kernels.cuh:793-797 (and :806 -> the next block's :784, :806 -> :813)
  * launches back to back. res = x + y (bit-identical to residual_forward);
@@ -360,6 +372,7 @@ int ugk_set_workspace(void *ptr, size_t bytes, ugk_config cfg);
 #define UGK_OP_GELU_BACKWARD 7
 #define UGK_OP_LAYERNORM_COLUMN_SUMS 8            /* all LayerNorms' dweight/dbias, batched */
 #define UGK_OP_ENCODER_BACKWARD 9
+#define UGK_OP_ENCODER_LAYERNORM_FORWARD 10       /* encoder_forward + the first layernorm_forward */
 int ugk_op_timer_start(int capacity);
 int ugk_op_timer_read(float *ms, int *ops, int capacity, int *count);
 

@@ -89,6 +89,9 @@ def test_fused_pairs_reject_invalid_arguments_on_host():
     assert lib.ugk_layernorm_residual_backward(*([None] * 10), -1, 3, 4) == 1
     assert lib.ugk_residual_layernorm_forward(*([None] * 8), 0, 3, 4) == 0
     assert lib.ugk_layernorm_residual_backward(*([None] * 10), 2, 3, 0) == 0
+    assert lib.ugk_encoder_layernorm_forward(*([None] * 9), 2, 3, 4) == 1
+    assert lib.ugk_encoder_layernorm_forward(*([16] * 9), 2, 3, 0) == 1  # C = 0 with rows
+    assert lib.ugk_encoder_layernorm_forward(*([None] * 9), 0, 3, 4) == 0
 
 
 def test_param_layout_counts():

@@ -38,6 +38,29 @@ def test_residual_layernorm_forward_fused(gpu, B, T, C, offset):
         assert_bits(host(a), host(c), f"fused forward {name}")
 
 
+@pytest.mark.parametrize("B,T,C,V,offset", [(8, 1024, 768, 50257, 0), (4, 64, 384, 27, 0), (1, 5, 2048, 7, 0),
+                                            (2, 3, 13, 5, 0), (2, 8, 384, 11, 1), (64, 200, 768, 300, 0)])
+def test_encoder_layernorm_forward_fused(gpu, B, T, C, V, offset):
+    """The pass equals encoder_forward then layernorm_forward on its output, bit for bit: aligned
+    and misaligned buffers, odd C (scalar fallback: two launches), and more rows than one round of
+    wavefronts (12,800: one row per wavefront)."""
+    g = gen.rng(B * 65537 + T * 13 + C)
+    n, rows = B * T * C, B * T
+    inp = gen.tokens_uniform(g, rows, V)
+    wte, wpe = gen.normal(g, (V * C,), 0, 0.02), gen.normal(g, (T * C,), 0, 0.01)
+    w, b = gen.normal(g, (C,), 1, 0.1), gen.normal(g, (C,), 0, 0.1)
+    tinp = dev(inp)
+    twte, twpe, tw, tb = put(wte, offset), put(wpe, offset), put(w, offset), put(b, offset)
+    z = lambda k: put(np.zeros(k, np.float32), offset)
+    f_enc, f_out, f_m, f_r = z(n), z(n), z(rows), z(rows)
+    gpu.encoder_layernorm_forward(f_enc, f_out, f_m, f_r, tinp, twte, twpe, tw, tb, B, T, C)
+    u_enc, u_out, u_m, u_r = z(n), z(n), z(rows), z(rows)
+    gpu.encoder_forward(u_enc, tinp, twte, twpe, B, T, C)
+    gpu.layernorm_forward(u_out, u_m, u_r, u_enc, tw, tb, B, T, C)
+    for name, a, c in (("enc", f_enc, u_enc), ("out", f_out, u_out), ("mean", f_m, u_m), ("rstd", f_r, u_r)):
+        assert_bits(host(a), host(c), f"fused encoder forward {name}")
+
+
 @pytest.mark.parametrize("B,T,C,offset", [(8, 1024, 768, 0), (4, 64, 384, 0), (1, 5, 2048, 0), (2, 3, 13, 0),
                                           (2, 8, 384, 1), (1, 3, 3000, 0), (2, 50, 600, 0), (1, 9, 516, 0),
                                           (16, 1024, 768, 0), (1, 8192, 768, 0), (1, 8193, 768, 0)])

@@ -162,8 +162,8 @@ def test_op_timer_records_the_driver_sequence(gpu, C, NH, L):
     gpu.gpt2_layers_forward(acts, params, inp, cfg)
     gpu.gpt2_layers_backward(grads, ga, acts, params, inp, cfg)
     rec = gpu.op_timer_read(256)
-    fwd = ["encoder_forward", "layernorm_forward"] + ["residual_layernorm_forward", "gelu_forward",
-                                                      "residual_layernorm_forward"] * L
+    fwd = ["encoder_layernorm_forward"] + ["residual_layernorm_forward", "gelu_forward",
+                                           "residual_layernorm_forward"] * L
     bwd = ["layernorm_residual_backward (main)"]
     for l in range(L - 1, -1, -1):
         bwd += ["gelu_backward", "layernorm_residual_backward (main)",

@@ -261,6 +261,19 @@ int ugk_layernorm_backward_noalloc(float *dinp, float *dweight, float *dbias, co
   return ok();
 }
 
+int ugk_encoder_layernorm_forward(float *enc, float *out, float *mean, float *rstd, const int *inp,
+                                  const float *wte, const float *wpe, const float *weight, const float *bias, int B,
+                                  int T, int C) {
+  const char *fn = "ugk_encoder_layernorm_forward";
+  if (int e = check_btc(fn, B, T, C)) return e;
+  if ((long long)B * T == 0) return ok();
+  if (C == 0) return bad(fn, "C must be > 0 when B*T > 0 (mean over an empty row)");
+  if (any_null({enc, out, mean, rstd, inp, wte, wpe, weight, bias})) return bad(fn, "NULL pointer");
+  if (int e = launch_encoder_layernorm_forward(enc, out, mean, rstd, inp, wte, wpe, weight, bias, B, T, C))
+    return e;
+  return ok();
+}
+
 int ugk_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
                                    const float *y, const float *weight, const float *bias, int B, int T,
                                    int C) {
@@ -692,18 +705,20 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
   const int NBTC = M * C;
   auto A = [&](size_t l, size_t rel) { return acts + a.blk0 + l * a.bstride + rel; };
   auto P = [&](size_t l, size_t rel) { return params + p.blk0 + l * p.bstride + rel; };
-  // Every residual_forward is followed at once by a layernorm_forward of its
-  // output (the next block's LN1, or the final LN): those pairs run as one
-  // pass, ugk_residual_layernorm_forward. Buffers and values are the
-  // reference's.
-  UGK_TRY(timed(UGK_OP_ENCODER_FORWARD,
-                [&] { return ugk_encoder_forward(acts + a.enc, inputs, params + p.wte, params + p.wpe, B, T, C); }));
+  // The encoder_forward and every residual_forward are followed at once by a
+  // layernorm_forward of their output (block 0's LN1 or the final LN, the
+  // next block's LN1): those pairs run as one pass each,
+  // ugk_encoder_layernorm_forward and ugk_residual_layernorm_forward.
+  // Buffers and values are the reference's.
+  UGK_TRY(timed(UGK_OP_ENCODER_LAYERNORM_FORWARD, [&] {
+    return cfg.L > 0 ? ugk_encoder_layernorm_forward(acts + a.enc, A(0, a.lno), A(0, a.lnm), A(0, a.lnr), inputs,
+                                                     params + p.wte, params + p.wpe, P(0, p.lng), P(0, p.lnb), B,
+                                                     T, C)
+                     : ugk_encoder_layernorm_forward(acts + a.enc, acts + a.flo, acts + a.flm, acts + a.flr, inputs,
+                                                     params + p.wte, params + p.wpe, params + p.flng,
+                                                     params + p.flnb, B, T, C);
+  }));
   const float *stream_in = acts + a.enc;
-  if (cfg.L > 0)
-    UGK_TRY(timed(UGK_OP_LAYERNORM_FORWARD, [&] {
-      return ugk_layernorm_forward(A(0, a.lno), A(0, a.lnm), A(0, a.lnr), stream_in, P(0, p.lng), P(0, p.lnb), B,
-                                   T, C);
-    }));
   for (int l = 0; l < cfg.L; l++) {
     if (ops && ops->matmul_forward)
       UGK_TRY(dense(ops->matmul_forward(ops->ctx, A(l, a.qkv), A(l, a.lno), P(l, p.qw), P(l, p.qb), M, C,
@@ -739,11 +754,6 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
       }));
     stream_in = A(l, a.res1);
   }
-  if (cfg.L == 0)
-    UGK_TRY(timed(UGK_OP_LAYERNORM_FORWARD, [&] {
-      return ugk_layernorm_forward(acts + a.flo, acts + a.flm, acts + a.flr, stream_in, params + p.flng,
-                                   params + p.flnb, B, T, C);
-    }));
   return ok();
 }
 

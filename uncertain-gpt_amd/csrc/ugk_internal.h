@@ -140,6 +140,9 @@ int launch_layernorm_backward(float *dinp, float *dweight, float *dbias,
                               const float *mean, const float *rstd, int rows, int C);
 // residual_forward then layernorm_forward of its output, in one pass when the
 // float4 path applies (two launches otherwise).
+int launch_encoder_layernorm_forward(float *enc, float *out, float *mean, float *rstd, const int *inp,
+                                     const float *wte, const float *wpe, const float *weight, const float *bias,
+                                     int B, int T, int C);
 int launch_residual_layernorm_forward(float *res, float *out, float *mean, float *rstd, const float *x,
                                       const float *y, const float *weight, const float *bias, int rows,
                                       int C);

@@ -56,6 +56,53 @@ struct Cols {
   }
 };
 
+// Normalise one row held in registers (V float4 per lane) and store out, mean
+// and rstd: two-pass mean and variance with wavefront sums, IEEE 1/sqrtf.
+// Shared by every forward kernel, so that they give the same bits.
+template <int V>
+__device__ __forceinline__ void ln_row_out(const float4 (&xv)[V], const Cols<V> &cl, int C, int row, int lane,
+                                           const float4 *__restrict__ w4, const float4 *__restrict__ b4,
+                                           float4 *__restrict__ o4, float *__restrict__ mean,
+                                           float *__restrict__ rstd) {
+  const size_t off = (size_t)row * (C >> 2);
+  float s = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    const bool c = cl.in[v];
+    s += c ? xv[v].x : -0.0f; s += c ? xv[v].y : -0.0f; s += c ? xv[v].z : -0.0f; s += c ? xv[v].w : -0.0f;
+  }
+  s = wave_sum(s);
+  const float m = s / (float)C;
+  float vs = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    const bool c = cl.in[v];
+    float d;
+    d = xv[v].x - m; vs += c ? d * d : -0.0f;
+    d = xv[v].y - m; vs += c ? d * d : -0.0f;
+    d = xv[v].z - m; vs += c ? d * d : -0.0f;
+    d = xv[v].w - m; vs += c ? d * d : -0.0f;
+  }
+  vs = wave_sum(vs);
+  const float r = 1.0f / sqrtf(vs / (float)C + 1e-5f);
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    if (cl.in[v]) {
+      const float4 w = w4[cl.col[v]], b = b4[cl.col[v]];
+      float4 o;
+      o.x = (xv[v].x - m) * r * w.x + b.x;
+      o.y = (xv[v].y - m) * r * w.y + b.y;
+      o.z = (xv[v].z - m) * r * w.z + b.z;
+      o.w = (xv[v].w - m) * r * w.w + b.w;
+      st_nt(o4 + off + cl.col[v], o);
+    }
+  }
+  if (lane == 0) {
+    mean[row] = m;
+    rstd[row] = r;
+  }
+}
+
 // Forward, RPW rows per wavefront (consecutive). The loads of row k+1 are
 // issued before row k is normalised and stored, so a wavefront has a row in
 // flight while it writes one.
@@ -111,47 +158,79 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_vec(float *__restrict__ out, 
         if (cl.in[v]) st_nt(r4 + off + cl.col[v], xv[v]);
       }
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      const bool c = cl.in[v];
-      s += c ? xv[v].x : -0.0f; s += c ? xv[v].y : -0.0f; s += c ? xv[v].z : -0.0f; s += c ? xv[v].w : -0.0f;
-    }
-    s = wave_sum(s);
-    const float m = s / (float)C;
-    float vs = 0.0f;
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      const bool c = cl.in[v];
-      float d;
-      d = xv[v].x - m; vs += c ? d * d : -0.0f;
-      d = xv[v].y - m; vs += c ? d * d : -0.0f;
-      d = xv[v].z - m; vs += c ? d * d : -0.0f;
-      d = xv[v].w - m; vs += c ? d * d : -0.0f;
-    }
-    vs = wave_sum(vs);
-    const float r = 1.0f / sqrtf(vs / (float)C + 1e-5f);
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-      if (cl.in[v]) {
-        const float4 w = w4[cl.col[v]], b = b4[cl.col[v]];
-        float4 o;
-        o.x = (xv[v].x - m) * r * w.x + b.x;
-        o.y = (xv[v].y - m) * r * w.y + b.y;
-        o.z = (xv[v].z - m) * r * w.z + b.z;
-        o.w = (xv[v].w - m) * r * w.w + b.w;
-        st_nt(o4 + off + cl.col[v], o);
-      }
-    }
-    if (lane == 0) {
-      mean[row] = m;
-      rstd[row] = r;
-    }
+    ln_row_out<V>(xv, cl, C, row, lane, w4, b4, o4, mean, rstd);
     if (k + 1 < RPW) {
 #pragma unroll
       for (int v = 0; v < V; v++) {
         xa[v] = xb[v];
         if (kRes) ya[kRes ? v : 0] = yb[kRes ? v : 0];
+      }
+    }
+  }
+}
+
+// Encoder forward then LayerNorm forward of its output, RPW rows per
+// wavefront: row (b, t) is formed as wte[inp[b,t]] + wpe[t] in registers (the
+// single add of train_bnn.c:41-65, the encoder's own order), stored to enc,
+// and normalised from the registers as k_ln_fwd_vec does: the pair
+// gpt2_kernels.cuh:775 -> :784 (or :813 when L = 0) launches back to back.
+// The rows of wte and wpe are read through the cache: tokens repeat, and the
+// B rows of a position share its wpe row.
+template <int V, int RPW>
+__global__ __launch_bounds__(kBlock) void k_enc_ln_fwd_vec(float *__restrict__ enc, float *__restrict__ out,
+                                                           float *__restrict__ mean, float *__restrict__ rstd,
+                                                           const int *__restrict__ inp,
+                                                           const float *__restrict__ wte,
+                                                           const float *__restrict__ wpe,
+                                                           const float *__restrict__ weight,
+                                                           const float *__restrict__ bias, int rows, int T, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row0 = (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;
+  const int C4 = C >> 2;
+  const Cols<V> cl(lane, C4);
+  const float4 *te4 = reinterpret_cast<const float4 *>(wte);
+  const float4 *pe4 = reinterpret_cast<const float4 *>(wpe);
+  float4 *e4 = reinterpret_cast<float4 *>(enc);
+  float4 *o4 = reinterpret_cast<float4 *>(out);
+  const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+  const float4 *b4 = reinterpret_cast<const float4 *>(bias);
+  float4 xa[V], ya[V];
+  {
+    const size_t ot = (size_t)inp[row0] * C4, op = (size_t)(row0 % T) * C4;
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      xa[v] = te4[ot + cl.col[v]];
+      ya[v] = pe4[op + cl.col[v]];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < RPW; k++) {
+    const int row = row0 + k;
+    if (row >= rows) break;
+    float4 xb[V], yb[V];
+    if (k + 1 < RPW) {
+      const int nx = min(row + 1, rows - 1);
+      const size_t ot = (size_t)inp[nx] * C4, op = (size_t)(nx % T) * C4;
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        xb[v] = te4[ot + cl.col[v]];
+        yb[v] = pe4[op + cl.col[v]];
+      }
+    }
+    const size_t off = (size_t)row * C4;
+    float4 xv[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+      xv[v] = add4(xa[v], ya[v]);
+      if (cl.in[v]) st_nt(e4 + off + cl.col[v], xv[v]);
+    }
+    ln_row_out<V>(xv, cl, C, row, lane, w4, b4, o4, mean, rstd);
+    if (k + 1 < RPW) {
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        xa[v] = xb[v];
+        ya[v] = yb[v];
       }
     }
   }
@@ -759,6 +838,35 @@ int launch_residual_layernorm_forward(float *res, float *out, float *mean, float
   }
   launch_ln_fwd_vec<true>(out, mean, rstd, x, weight, bias, rows, C, res, y);
   return check_launch("residual_layernorm_forward");
+}
+
+int launch_encoder_layernorm_forward(float *enc, float *out, float *mean, float *rstd, const int *inp,
+                                     const float *wte, const float *wpe, const float *weight, const float *bias,
+                                     int B, int T, int C) {
+  const int rows = B * T;
+  if (rows == 0) return 0;
+  if (!vec_ok(C, {enc, out, wte, wpe, weight, bias})) {
+    if (int e = launch_encoder_forward(enc, inp, wte, wpe, B, T, C)) return e;
+    return launch_layernorm_forward(out, mean, rstd, enc, weight, bias, rows, C);
+  }
+  const int V = ((C >> 2) + kWave - 1) / kWave;
+  const int rpw = fwd_rpw(rows, true);
+  const dim3 grid(grid_for((size_t)rows, (size_t)kWavesPerBlock * rpw)), block(kBlock);
+  switch (V * 2 + (rpw - 1)) {
+#define UGK_ENC_LN(v)                                                                                          \
+  case 2 * v:                                                                                                  \
+    launch((k_enc_ln_fwd_vec<v, 1>), grid, block, 0, enc, out, mean, rstd, inp, wte, wpe, weight, bias, rows, \
+           T, C);                                                                                              \
+    break;                                                                                                     \
+  case 2 * v + 1:                                                                                              \
+    launch((k_enc_ln_fwd_vec<v, 2>), grid, block, 0, enc, out, mean, rstd, inp, wte, wpe, weight, bias, rows, \
+           T, C);                                                                                              \
+    break;
+    UGK_ENC_LN(1) UGK_ENC_LN(2) UGK_ENC_LN(3) UGK_ENC_LN(4)
+    UGK_ENC_LN(5) UGK_ENC_LN(6) UGK_ENC_LN(7) UGK_ENC_LN(8)
+#undef UGK_ENC_LN
+  }
+  return check_launch("encoder_layernorm_forward");
 }
 
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,

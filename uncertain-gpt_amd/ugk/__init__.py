@@ -73,6 +73,7 @@ _SIGS = {
     "ugk_layernorm_forward": [_fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_backward": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_layernorm_backward_noalloc": [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i, _i, _i],
+    "ugk_encoder_layernorm_forward": [_fp] * 9 + [_i, _i, _i],
     "ugk_residual_layernorm_forward": [_fp] * 8 + [_i, _i, _i],
     "ugk_layernorm_residual_backward": [_fp] * 10 + [_i, _i, _i],
     "ugk_gelu_forward": [_fp, _fp, _i],
@@ -220,6 +221,16 @@ def layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, B: i
                                       _ptr(dbias, "dbias", C, "f32"), _ptr(dout, "dout", n, "f32"),
                                       _ptr(inp, "inp", n, "f32"), _ptr(weight, "weight", C, "f32"),
                                       _ptr(mean, "mean", r, "f32"), _ptr(rstd, "rstd", r, "f32"), B, T, C))
+
+
+def encoder_layernorm_forward(enc, out, mean, rstd, inp, wte, wpe, weight, bias, B: int, T: int, C: int) -> None:
+    """``encoder_forward(enc, inp, wte, wpe)`` then ``layernorm_forward(out, mean, rstd, enc, ...)``, one pass."""
+    _check_tokens(inp, wte, C, "encoder_layernorm_forward")
+    n, rows = B * T * C, B * T
+    _check(lib.ugk_encoder_layernorm_forward(
+        _ptr(enc, "enc", n, "f32"), _ptr(out, "out", n, "f32"), _ptr(mean, "mean", rows, "f32"),
+        _ptr(rstd, "rstd", rows, "f32"), _ptr(inp, "inp", rows, "i32"), _ptr(wte, "wte", C, "f32"),
+        _ptr(wpe, "wpe", T * C, "f32"), _ptr(weight, "weight", C, "f32"), _ptr(bias, "bias", C, "f32"), B, T, C))
 
 
 def residual_layernorm_forward(res, out, mean, rstd, x, y, weight, bias, B: int, T: int, C: int) -> None:
@@ -384,7 +395,7 @@ def set_workspace(buf, cfg: Config) -> None:
 
 OP_NAMES = {1: "encoder_forward", 2: "layernorm_forward", 3: "residual_layernorm_forward", 4: "gelu_forward",
             5: "layernorm_backward (main)", 6: "layernorm_residual_backward (main)", 7: "gelu_backward",
-            8: "layernorm column sums (batched)", 9: "encoder_backward"}
+            8: "layernorm column sums (batched)", 9: "encoder_backward", 10: "encoder_layernorm_forward"}
 
 
 def op_timer_start(capacity: int = 1024) -> None:
