@@ -33,9 +33,11 @@
 //                  as many as table slots). A bucket of at most kCap rows is
 //                  ranked by comparison (row ids are distinct) and its rows
 //                  added in ascending order, 4 channels per lane, 8 loads in
-//                  flight. A larger bucket's wavefront scans the rows' slots
-//                  in row order (four per lane per load, 2048 per round) and
-//                  writes the matching row ids, ascending, to a list for K3.
+//                  flight. The same launch has one more workgroup per
+//                  possible large bucket (K1 lists them with their slots):
+//                  its 256 threads scan the rows' slots in row order, 6,144
+//                  per round, and write the matching row ids, ascending, to a
+//                  list for K3.
 //     K3 large   - workgroups of 16 wavefronts, one per (large bucket, 64
 //                  channels): one wavefront only adds staged rows in order,
 //                  one channel per lane, from one half of a double-buffered
@@ -46,9 +48,9 @@
 //                  waits are exact). A frequent token's serial chain of adds
 //                  thus runs without waiting for its loads.
 //   The table and its counters return to their cleared state within each
-//   chunk, on the device: K2's wavefront for a slot frees the slot once it has
-//   read it (every claimed slot has exactly one), and the last K3 workgroup to
-//   finish zeroes the counters. No state stays on the host between calls, so a
+//   chunk, on the device: K2 frees each slot once it has read it (the
+//   wavefront of its list entry, or the scan workgroup of a large bucket),
+//   and the last K3 workgroup to finish zeroes the counters. No state stays on the host between calls, so a
 //   captured HIP graph may replay any number of calls.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
@@ -113,13 +115,12 @@ __device__ __forceinline__ int slot_cnt(u64 s) { return (int)(unsigned)s; }
 struct EncTable {
   u64 *slot;       // [kTableMax] token and row count per slot, kFree when free
   int *counters;   // [0] K3 work items taken, [1] large buckets, [2] sorted-id pool use, [3] K3 workgroups done
-  int *large_j;    // [kTableMax] index of a large slot in the large-bucket list
 };
 
 struct EncShared {
   int *rows;       // [kTableMax * kCap] row ids by (slot, rank < kCap)
   int *slot_of;    // [kChunk] slot of each row of the chunk (-1: skipped)
-  int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, 0}
+  int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, slot} (K1 writes token and slot)
   int *pool;       // [kChunk] row ids of the large buckets, each bucket ascending
   int *list;       // [kChunk] slots claimed by K1 workgroup b at [256 b, 256 b + k), -1 after
 };
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_insert(EncTable tb, EncShare
       if (base < 0) {
         lslot[f] = -1;
       } else {
-        if (base <= kCap && kCap < base + c) tb.large_j[h] = atomicAdd(&tb.counters[1], 1);
+        // the workgroup whose ranks cross kCap (one per slot) lists the large bucket
+        if (base <= kCap && kCap < base + c) sh.lmeta[atomicAdd(&tb.counters[1], 1)] = make_int4(0, 0, t, (int)h);
         lslot[f] = (int)h;
         lbase[f] = base;
       }
@@ -262,20 +264,96 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// K2: one wavefront per slot-list entry (the grid covers K1's regions
-// exactly). Each frees its slot once it has read it.
+// K2, scan workgroup of large bucket j: the chunk's row ids whose slot is the
+// bucket's, in row order, to its share of the pool; 6 int4 loads of slots per
+// thread per round (6,144 slots), the round's matches placed by a workgroup
+// prefix over (load, wavefront). Frees the slot after reading its count.
+// (8 loads per round would take K2 from 48 to 58 registers, and from ten
+// wavefronts per SIMD to eight.)
+constexpr int kScanQ = 6;
+__device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int n) {
+  __shared__ int wt[kScanQ][kWavesPerBlock];
+  __shared__ int pool_base, bucket_cnt;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int4 m = sh.lmeta[j];
+  const int w = m.w;
+  if (threadIdx.x == 0) {
+    const int cnt = slot_cnt(tb.slot[w]);
+    pool_base = atomicAdd(&tb.counters[2], cnt);
+    bucket_cnt = cnt;
+    tb.slot[w] = kFree;
+  }
+  __syncthreads();
+  const int base = pool_base;
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  int run = 0;  // matches in the rounds before this one
+  for (int i0 = 0; i0 < n; i0 += kScanQ * kBlock * 4) {
+    int4 sl[kScanQ];
+#pragma unroll
+    for (int q = 0; q < kScanQ; q++) {
+      const int e = i0 + (q * kBlock + (int)threadIdx.x) * 4;
+      if (e + 3 < n) {
+        sl[q] = *reinterpret_cast<const int4 *>(sh.slot_of + e);
+      } else {
+        sl[q].x = e < n ? sh.slot_of[e] : -1;
+        sl[q].y = e + 1 < n ? sh.slot_of[e + 1] : -1;
+        sl[q].z = e + 2 < n ? sh.slot_of[e + 2] : -1;
+        sl[q].w = -1;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kScanQ; q++) {
+      const int k = __popcll(__ballot(sl[q].x == w)) + __popcll(__ballot(sl[q].y == w)) +
+                    __popcll(__ballot(sl[q].z == w)) + __popcll(__ballot(sl[q].w == w));
+      if (lane == 0) wt[q][wave] = k;
+    }
+    __syncthreads();
+    // slots are ordered by (load q, wavefront, lane, element): the matches of
+    // the (q, wavefront) pairs before this one come first
+    int off = run;
+    for (int q = 0; q < kScanQ; q++) {
+      int o = off;
+#pragma unroll
+      for (int v = 0; v < kWavesPerBlock; v++) o += v < wave ? wt[q][v] : 0;
+#pragma unroll
+      for (int v = 0; v < kWavesPerBlock; v++) off += wt[q][v];
+      const int e = i0 + (q * kBlock + (int)threadIdx.x) * 4;
+      o += __popcll(__ballot(sl[q].x == w) & below) + __popcll(__ballot(sl[q].y == w) & below) +
+           __popcll(__ballot(sl[q].z == w) & below) + __popcll(__ballot(sl[q].w == w) & below);
+      if (sl[q].x == w) sh.pool[base + o++] = e;
+      if (sl[q].y == w) sh.pool[base + o++] = e + 1;
+      if (sl[q].z == w) sh.pool[base + o++] = e + 2;
+      if (sl[q].w == w) sh.pool[base + o] = e + 3;
+    }
+    run = off;
+    __syncthreads();  // wt is rewritten by the next round
+  }
+  if (threadIdx.x == 0) sh.lmeta[j] = make_int4(base, bucket_cnt, m.z, w);
+}
+
+// K2: one scan workgroup per possible large bucket in the first nscan
+// workgroups (dispatched first, so that those with no bucket have left before
+// the adds end), then one wavefront per slot-list entry (covering K1's
+// regions exactly). A small bucket's wavefront frees its slot once it has
+// read it.
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncShared sh, float *__restrict__ dwte,
-                                                        const float *__restrict__ dout, int C, int n) {
+                                                        const float *__restrict__ dout, int C, int n, int nscan) {
   __shared__ unsigned lds[kWavesPerBlock * kCap];
+  if ((int)blockIdx.x < nscan) {
+    const int j = (int)blockIdx.x;
+    if (j < tb.counters[1]) scan_large(tb, sh, j, n);  // K1 has counted them: the same value in every thread
+    return;
+  }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   unsigned *mine = lds + (size_t)wave * kCap;
   // Wavefront g takes entry g / R of region g % R (R regions of kBlock
   // entries): the entries of one region (one K1 workgroup's tokens, where a
   // skewed batch puts its frequent tokens early) spread over all workgroups.
-  const int R = (int)(gridDim.x * kWavesPerBlock / kBlock);
-  const int gw = blockIdx.x * kWavesPerBlock + wave;
+  const int R = ((int)gridDim.x - nscan) * kWavesPerBlock / kBlock;
+  const int gw = ((int)blockIdx.x - nscan) * kWavesPerBlock + wave;
   const int w = sh.list[(gw % R) * kBlock + gw / R];  // this wavefront's slot
   if (w < 0) return;
   // the slot word and the bucket's first row ids in one round trip (ids past
@@ -285,48 +363,11 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncShared s
   asm volatile("" ::"v"(id_raw));  // keeps the compiler from sinking the ids load below the branch
   const int cnt = slot_cnt(sw);
   const int tok = slot_tok(sw);
+  // A large bucket belongs to its scan workgroup, which may already have
+  // freed the slot (the word then reads count 0).
+  if (cnt == 0 || cnt > kCap) return;
   // the slot's only reader has read it: free it for the next chunk's K1
   if (lane == 0) tb.slot[w] = kFree;
-  if (cnt > kCap) {
-    // large bucket: the rows whose slot is w, in row order, to the pool for
-    // K3; 2048 slot_of entries per round, four consecutive per lane
-    int base = 0;
-    if (lane == 0) base = atomicAdd(&tb.counters[2], cnt);
-    base = __shfl(base, 0);
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-    int off = 0;
-    constexpr int kScanQ = 8;  // int4 loads in flight per lane (more would raise the kernel's VGPR count)
-    for (int i0 = 0; i0 < n; i0 += kScanQ * kWave * 4) {
-      int4 sl[kScanQ];
-#pragma unroll
-      for (int q = 0; q < kScanQ; q++) {
-        const int e = i0 + (q * kWave + lane) * 4;
-        if (e + 3 < n) {
-          sl[q] = *reinterpret_cast<const int4 *>(sh.slot_of + e);
-        } else {
-          sl[q].x = e < n ? sh.slot_of[e] : -1;
-          sl[q].y = e + 1 < n ? sh.slot_of[e + 1] : -1;
-          sl[q].z = e + 2 < n ? sh.slot_of[e + 2] : -1;
-          sl[q].w = -1;
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < kScanQ; q++) {
-        const int e = i0 + (q * kWave + lane) * 4;
-        const bool f0 = sl[q].x == w, f1 = sl[q].y == w, f2 = sl[q].z == w, f3 = sl[q].w == w;
-        const unsigned long long m0 = __ballot(f0), m1 = __ballot(f1), m2 = __ballot(f2), m3 = __ballot(f3);
-        int o = base + off + __popcll(m0 & below) + __popcll(m1 & below) + __popcll(m2 & below) +
-                __popcll(m3 & below);
-        if (f0) sh.pool[o++] = e;
-        if (f1) sh.pool[o++] = e + 1;
-        if (f2) sh.pool[o++] = e + 2;
-        if (f3) sh.pool[o] = e + 3;
-        off += __popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3);
-      }
-    }
-    if (lane == 0) sh.lmeta[tb.large_j[w]] = make_int4(base, cnt, tok, 0);
-    return;
-  }
   // rank the bucket's row ids; ids are distinct, so ranks are a permutation
   const int id = lane < cnt ? id_raw : 0x7fffffff;
   int rank = 0;
@@ -530,7 +571,7 @@ __global__ void k_enc_init(EncTable t) {
   if (h < 4) t.counters[h] = 0;
 }
 
-size_t table_ints() { return (size_t)3 * kTableMax + 64; }  // slot words (2 ints each), large_j, counters
+size_t table_ints() { return (size_t)2 * kTableMax + 64; }  // slot words (2 ints each), counters
 size_t state_bytes() {
   return (size_t)kTableMax * kCap * sizeof(int) + (size_t)kChunk * sizeof(int) +
          (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + table_ints() * sizeof(int);
@@ -549,9 +590,7 @@ void carve(char *p, EncTable *t, EncShared *sh) {
   sh->list = reinterpret_cast<int *>(p);
   p += (size_t)kChunk * sizeof(int);
   t->slot = reinterpret_cast<u64 *>(p);  // 8-byte aligned: every size above is a multiple of 8
-  int *q = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
-  t->large_j = q;
-  t->counters = q + kTableMax;
+  t->counters = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
 }
 
 }  // namespace
@@ -604,12 +643,14 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
       hipLaunchKernelGGL(k_enc_bwd_insert<false>, dim3(ins_blocks + pe_blocks), dim3(kBlock), 0, stream(), tb,
                          sh, inp + c0, n, mask, shift, ins_blocks, dwpe, dout, B, T, C);
     const float *dchunk = dout + (size_t)c0 * C;
+    // one workgroup per possible large bucket (at most n / (kCap + 1)), then
     // one wavefront per entry of K1's slot-list regions
-    const dim3 g2((unsigned)ins_blocks * (kBlock / kWavesPerBlock));
+    const int nscan = n / (kCap + 1) + 1;
+    const dim3 g2((unsigned)(nscan + ins_blocks * (kBlock / kWavesPerBlock)));
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n);
+      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan);
     else
-      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n);
+      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan);
     // one round of workgroups (one per CU: each stages 122 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
     // every workgroup goes straight to the counter reset
