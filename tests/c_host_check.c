@@ -134,6 +134,20 @@ int main(void) {
   check("layernorm_forward mean", d_mean, mean, BT, 1e-5, 1e-6);
   check("layernorm_forward rstd", d_rstd, rstd, BT, 1e-5, 1e-6);
 
+  /* the encoder and the LayerNorm of its rows in one call: the rows bit-exact,
+     their normalisation within the LayerNorm tolerance */
+  float *enc = calloc(NB, 4), *lno = calloc(NB, 4), *lnm = calloc(BT, 4), *lnr = calloc(BT, 4);
+  float *d_enc = to_device(enc, NB * 4), *d_lno = to_device(lno, NB * 4);
+  float *d_lnm = to_device(lnm, BT * 4), *d_lnr = to_device(lnr, BT * 4);
+  call_ok(ugk_encoder_layernorm_forward(d_enc, d_lno, d_lnm, d_lnr, d_tok, d_wte, d_wpe, d_w, d_b, B, T, C),
+          "ugk_encoder_layernorm_forward");
+  oracle_encoder_forward(enc, tok, wte, wpe, B, T, C);
+  oracle_layernorm_forward(lno, lnm, lnr, enc, w, b, B, T, C);
+  check("encoder_layernorm_forward enc", d_enc, enc, NB, 0, 0);
+  check("encoder_layernorm_forward out", d_lno, lno, NB, 1e-5, 1e-6);
+  check("encoder_layernorm_forward mean", d_lnm, lnm, BT, 1e-5, 1e-6);
+  check("encoder_layernorm_forward rstd", d_lnr, lnr, BT, 1e-5, 1e-6);
+
   float *dinp = host_normal(NB, 0.0f, 1.0f), *dw = host_normal(C, 0.0f, 1.0f), *db = host_normal(C, 0.0f, 1.0f);
   float *d_dinp = to_device(dinp, NB * 4), *d_dw = to_device(dw, C * 4), *d_db = to_device(db, C * 4);
   call_ok(ugk_layernorm_backward(d_dinp, d_dw, d_db, d_dout, d_x, d_w, d_mean, d_rstd, B, T, C),

@@ -39,11 +39,12 @@ def test_residual_layernorm_forward_fused(gpu, B, T, C, offset):
 
 
 @pytest.mark.parametrize("B,T,C,V,offset", [(8, 1024, 768, 50257, 0), (4, 64, 384, 27, 0), (1, 5, 2048, 7, 0),
-                                            (2, 3, 13, 5, 0), (2, 8, 384, 11, 1), (64, 200, 768, 300, 0)])
+                                            (2, 3, 13, 5, 0), (2, 8, 384, 11, 1), (64, 200, 768, 300, 0),
+                                            (1, 3, 3000, 9, 0)])
 def test_encoder_layernorm_forward_fused(gpu, B, T, C, V, offset):
     """The pass equals encoder_forward then layernorm_forward on its output, bit for bit: aligned
-    and misaligned buffers, odd C (scalar fallback: two launches), and more rows than one round of
-    wavefronts (12,800: one row per wavefront)."""
+    and misaligned buffers, odd C and C past the vector path's 2,048 (two launches), and more rows
+    than one round of wavefronts (12,800: one row per wavefront)."""
     g = gen.rng(B * 65537 + T * 13 + C)
     n, rows = B * T * C, B * T
     inp = gen.tokens_uniform(g, rows, V)
