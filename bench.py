@@ -9,14 +9,15 @@ fp32, L=12 H=12 C=768 V=50257 B=8 T=1024, on the reference's buffer layout:
 The dense ops between them (GEMMs, attention) are not part of the path; their
 output buffers hold synthetic data. A "step" is that sequence, queued by the
 native step driver of libugk.so (ugk_gpt2_layers_forward/backward), which runs
-each residual -> LayerNorm and LayerNorm -> residual pair as one pass and adds
+the encoder -> LayerNorm pair and each residual -> LayerNorm and LayerNorm ->
+residual pair as one pass and adds
 the LayerNorm weight/bias gradients of the whole backward in one launch; its
 buffers are bit-identical to the op-by-op sequence.
 
 Printed JSON line (the last line of stdout):
     value        the reference sequence's algorithmic bytes (18.05 GB, unfused) / step
                  time: the effective rate of the reference's work; GBps_moved divides the
-                 bytes the fused sequence must move (16.84 GB) instead
+                 bytes the fused sequence must move (16.82 GB) instead
     ms_per_step  mean over --steps steps (events on the kernels' stream; median, p25, p75
                  of the per-step times beside it)
     in_step      each op of the step, timed inside the step with a HIP event pair that
