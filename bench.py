@@ -92,6 +92,7 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
     ("k_ln_fwd_vec", "layernorm_forward"),
     ("k_enc_fwd_vec", "encoder_forward"),
+    ("k_enc_fwd_row", "encoder_forward"),
     ("k_enc_ln_fwd_vec", "encoder_layernorm_forward"),
     ("k_enc_bwd_insert", "encoder_backward (insert + dwpe)"),
     ("k_enc_bwd_add", "encoder_backward (add)"),

@@ -88,6 +88,32 @@ __global__ __launch_bounds__(kBlock) void k_enc_fwd_vec(float4 *__restrict__ out
   }
 }
 
+// The same with the row held in registers: V float4 per lane (C/4 <= 64 V),
+// every load of the row issued before the first store (columns past the row
+// load the last one again and are not stored).
+template <int V>
+__global__ __launch_bounds__(kBlock) void k_enc_fwd_row(float4 *__restrict__ out, const int *__restrict__ inp,
+                                                        const float4 *__restrict__ wte,
+                                                        const float4 *__restrict__ wpe, int BT, int T, int C4) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int bt = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (bt >= BT) return;
+  const size_t ot = (size_t)inp[bt] * C4, op = (size_t)(bt % T) * C4;
+  float4 x[V], y[V];
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    const int c = min(lane + v * kWave, C4 - 1);
+    x[v] = wte[ot + c];
+    y[v] = wpe[op + c];
+  }
+  float4 *o = out + (size_t)bt * C4;
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    const int c = lane + v * kWave;
+    if (c < C4) st_nt(o + c, make_float4(x[v].x + y[v].x, x[v].y + y[v].y, x[v].z + y[v].z, x[v].w + y[v].w));
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void k_enc_fwd_scalar(float *out, const int *inp, const float *wte,
                                                            const float *wpe, int BT, int T, int C) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -603,9 +629,20 @@ int launch_encoder_forward(float *out, const int *inp, const float *wte, const f
   if (BT == 0 || C == 0) return 0;
   const dim3 grid(grid_for((size_t)BT, kWavesPerBlock)), block(kBlock);
   if ((C & 3) == 0 && aligned16(out) && aligned16(wte) && aligned16(wpe)) {
-    launch(k_enc_fwd_vec, grid, block, 0, reinterpret_cast<float4 *>(out), inp,
-                       reinterpret_cast<const float4 *>(wte), reinterpret_cast<const float4 *>(wpe), BT,
-                       T, C >> 2);
+    float4 *o4 = reinterpret_cast<float4 *>(out);
+    const float4 *te4 = reinterpret_cast<const float4 *>(wte), *pe4 = reinterpret_cast<const float4 *>(wpe);
+    const int C4 = C >> 2;
+    switch ((C4 + kWave - 1) / kWave) {
+#define UGK_ENC_ROW(v) \
+  case v:              \
+    launch(k_enc_fwd_row<v>, grid, block, 0, o4, inp, te4, pe4, BT, T, C4); \
+    break;
+      UGK_ENC_ROW(1) UGK_ENC_ROW(2) UGK_ENC_ROW(3) UGK_ENC_ROW(4)
+      UGK_ENC_ROW(5) UGK_ENC_ROW(6) UGK_ENC_ROW(7) UGK_ENC_ROW(8)
+#undef UGK_ENC_ROW
+      default:  // rows beyond 2,048 channels: the lane loop
+        launch(k_enc_fwd_vec, grid, block, 0, o4, inp, te4, pe4, BT, T, C4);
+    }
   } else {
     launch(k_enc_fwd_scalar, grid, block, 0, out, inp, wte, wpe, BT, T, C);
   }
