@@ -472,10 +472,12 @@ __device__ __forceinline__ void large_items(EncTable tb, EncShared sh, float *__
   const int group = adder ? -1 : (wave - 1) / kGroupWaves;
   const int slot = adder ? 0 : (wave - 1) % kGroupWaves;  // this loader's share of a round
   const int mine = slot * kPerWave + (lane < kPerWave ? lane : 0);  // loader: row of this lane's id
-  for (;;) {
-    // the next (bucket, slice) work item, taken from a counter so that
-    // workgroups with short buckets go on to others
-    if (threadIdx.x == 0) next_item = atomicAdd(&tb.counters[0], 1);
+  for (int first = 1;; first = 0) {
+    // the next (bucket, slice) work item: a workgroup's first is its own
+    // index (so that the grid does not start with one atomic per workgroup on
+    // one counter), later ones come from the counter, so that workgroups with
+    // short buckets go on to others
+    if (threadIdx.x == 0) next_item = first ? (int)blockIdx.x : (int)gridDim.x + atomicAdd(&tb.counters[0], 1);
     __syncthreads();
     const int wi = next_item;
     __syncthreads();
