@@ -371,6 +371,17 @@ def test_encoder_large_bucket_boundaries(gpu, oracle):
         assert_bits(host(tdwpe), dwpe, f"encoder_backward dwpe C={C}")
 
 
+def test_encoder_most_large_buckets(gpu, oracle):
+    """As many large buckets as a chunk of 8,192 rows can hold: 248 tokens of 33 rows each (one
+    row past the 32 a slot keeps) and 8 single rows, shuffled, so that every scan workgroup K2
+    launches for this chunk but one has a bucket, and K3 has 248 x 12 work items at C = 768."""
+    B, T, C = 8, 1024, 768
+    inp = np.concatenate([np.repeat(np.arange(248, dtype=np.int32), 33), np.arange(248, 256, dtype=np.int32)])
+    assert inp.size == B * T
+    inp = inp[gen.rng(31).permutation(inp.size)]
+    enc_case(gpu, oracle, B, T, C, 256, inp, 6, reps=2)
+
+
 def test_encoder_zipf_cfg4_shape(gpu, oracle):
     B, T, C, V = 16, 1024, 768, 50257
     enc_case(gpu, oracle, B, T, C, V, gen.tokens_zipf(gen.rng(11), B * T, V), 3, reps=2)
