@@ -123,6 +123,13 @@ def test_binding_rejects_cpu_tensors():
     x = torch.zeros(8)
     with pytest.raises(ValueError):
         ugk.residual_forward(x, x, x, 8)
+    tok = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError):  # the token check leaves CPU tensors to the argument checks
+        ugk.encoder_forward(x, tok, x, x, 1, 2, 4)
+    with pytest.raises(ValueError):
+        ugk.encoder_layernorm_forward(x, x, x[:2], x[:2], tok, x, x, x[:4], x[:4], 1, 2, 4)
+    with pytest.raises(ValueError):
+        ugk.softmax_crossentropy(x[:2], x, x, tok, 1, 2, 4)
 
 
 def test_product_does_not_use_the_oracle():

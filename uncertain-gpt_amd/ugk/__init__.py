@@ -171,9 +171,11 @@ def _check_tokens(inp, table, C: int, what: str) -> None:
     """Token ids must index rows of ``table`` (the reference's contract); checked when both are tensors,
     except while the current stream is being captured into a graph (the check reads the ids back)."""
     import torch
+    if not (isinstance(inp, torch.Tensor) and isinstance(table, torch.Tensor) and inp.is_cuda and table.is_cuda):
+        return  # a device address, or a tensor that the argument checks reject
     if torch.cuda.is_current_stream_capturing():
         return
-    if isinstance(inp, torch.Tensor) and isinstance(table, torch.Tensor) and inp.numel() and C:
+    if inp.numel() and C:
         rows = table.numel() // C
         lo, hi = int(inp.min()), int(inp.max())
         if lo < 0 or hi >= rows:
@@ -181,9 +183,14 @@ def _check_tokens(inp, table, C: int, what: str) -> None:
 
 
 def _check_targets(targets, V: int, rows: int, what: str) -> None:
-    """Target ids index a row of V logits (the reference's contract); checked when a tensor."""
+    """Target ids index a row of V logits (the reference's contract); checked when a GPU tensor,
+    except while the current stream is being captured into a graph (the check reads the ids back)."""
     import torch
-    if isinstance(targets, torch.Tensor) and rows:
+    if not (isinstance(targets, torch.Tensor) and targets.is_cuda):
+        return  # a device address, or a tensor that the argument checks reject
+    if torch.cuda.is_current_stream_capturing():
+        return
+    if rows:
         t = targets.reshape(-1)[:rows]
         lo, hi = int(t.min()), int(t.max())
         if lo < 0 or hi >= V:
