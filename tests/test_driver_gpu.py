@@ -178,6 +178,7 @@ def run_driver_vs_replay(gpu, B, T, C, V, NH, maxT, L, seed, dense_factory=None)
     (8, 1024, 768, 50257, 12),  # the benchmark's step: GPT-2-124M, 25 LayerNorm backwards of 512 partial rows
     (2, 64, 768, 50, 16),       # 33 LayerNorm backwards: the batched column sums take two launches
     (2, 32, 384, 27, 6),        # config 1's width and depth
+    (2, 32, 384, 27, 0),        # no block: the encoder -> LayerNorm pass writes the final LayerNorm
 ])
 def test_step_driver_equals_per_op_replay_at_shape(gpu, B, T, C, V, L):
     print(f"driver vs replay B={B} T={T} C={C} V={V} L={L}", flush=True)
