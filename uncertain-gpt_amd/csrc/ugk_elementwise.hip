@@ -54,6 +54,7 @@ struct GeluFwd : MapOp {  // train_bnn.c:163-170
 
 struct GeluFwdFast : MapOp {  // train_bnn.c:163-170, logistic form
   static constexpr int kLoads = 1, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
     st[0] = ugk_fast_gelu(ld[0]);
   }
@@ -77,6 +78,7 @@ struct GeluBwd : MapOp {  // train_bnn.c:520-533; loads inp, dout, dinp
 
 struct Materialize : MapOp {  // train_bnn.c:831-835; loads mu, rho, eps
   static constexpr int kLoads = 3, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 256;  // measured best of the map shapes
   static constexpr bool kTable = true;  // expf's 2^(i/32) table staged in LDS
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t, Params) {
     st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * ld[2];
