@@ -55,6 +55,7 @@ struct BayesSampleEps : BayesSample {
 // Loads dw, eps, rho, dmu, drho; stores dmu, drho.
 struct BayesBackward : MapOp {
   static constexpr int kLoads = 5, kStores = 2;
+  static constexpr int kUnroll = 1, kThreads = 1024;  // measured best of the map shapes
   static constexpr bool kTable = true;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t, Params) {
     st[0] = ld[3] + ld[0];
@@ -66,8 +67,8 @@ struct BayesBackward : MapOp {
 // Loads dw, rho, dmu, drho; stores dmu, drho.
 struct BayesBackwardPhilox : MapOp {
   static constexpr int kLoads = 4, kStores = 2;
+  static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
   static constexpr bool kTable = true;
-  static constexpr int kUnroll = 1;
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0];
@@ -125,6 +126,7 @@ __device__ __forceinline__ float adamw_one(float param, float g, float &m, float
 // train_bnn.c:699-717. Loads params, grads, m, v; stores params, m, v.
 struct AdamW : MapOp {
   static constexpr int kLoads = 4, kStores = 3;
+  static constexpr int kUnroll = 1, kThreads = 1024;  // measured best of the map shapes
   typedef AdamParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, const Params &p) {
     float m = ld[2], v = ld[3];
