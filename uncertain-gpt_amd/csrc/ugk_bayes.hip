@@ -93,6 +93,7 @@ __device__ __forceinline__ float div_by(float a, const SharedDivisor &d) { retur
 
 struct KlBackward : MapOp {
   static constexpr int kLoads = 4, kStores = 2;
+  static constexpr int kUnroll = 1, kThreads = 256;  // measured best of the map shapes
   static constexpr bool kTable = true;
   struct Params {
     SharedDivisor sp2;
