@@ -777,7 +777,8 @@ int vec_blocks(int rows, int C, bool res, int max_blocks) {
 // Rows per wavefront of the fused forward: two while one wavefront per row
 // would fill the GPU only once (the reads and writes of a single round of
 // wavefronts cannot overlap; measured 17.7 against 18.8 us at 8,192 x 768),
-// else one (35.0 against 37.1 us at 16,384 x 768).
+// else one (35.0 against 37.1 us at 16,384 x 768). The plain forward keeps
+// one (9.3 against 9.6 us with two at 8,192 x 768).
 int fwd_rpw(int rows, bool res) {
   if (!res) return 1;
   return rows <= cu_count() * 32 ? 2 : 1;
