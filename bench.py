@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the uncertain-gpt layer-kernel set on one MI355X.
 
-Workload: one GPT-2-124M Bayesian step's layer-kernel path,
+Workload (benchmark config 5): one GPT-2-124M Bayesian step's layer-kernel path,
 fp32, L=12 H=12 C=768 V=50257 B=8 T=1024, on the reference's buffer layout:
     bayes_materialize over n = 124,439,808 parameters (tied-head count)
     -> the layer kernels of gpt2_forward (encoder, 25 LayerNorm, 24 residual,
@@ -31,7 +31,9 @@ Printed JSON line (the last line of stdout):
                  totalling > 1.5 GiB, so neither L2 nor the 256 MB MALL holds the operands):
                  median of 5 batches of back-to-back launches (p25, p75), GB/s from
                  algorithmic bytes, fraction of 8 TB/s, and the stream ceiling of its mix
-    configs      the same kernels at BASELINE configs 2-4, cold
+    configs      the same kernels at the shapes of benchmark configs 2-4 (LayerNorm at
+                 16,384 x 768 and 256 x 384, GELU and residual at 50.3M, the encoder at
+                 B=16 T=1024 with uniform and Zipf(1.1) tokens), cold
     head         softmax + cross-entropy forward and backward over B*T rows of V = 50257
     posterior    the ops around the step over the same n parameters, cold
     cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this repo's
@@ -193,7 +195,7 @@ def main():
                     help="cold launches per timed batch of a kernel (at least one per buffer set); 5 batches")
     ap.add_argument("--op-steps", type=int, default=3, help="steps timed op by op with the library's op timer")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other BASELINE configs")
+    ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other benchmark configurations' shapes")
     ap.add_argument("--no-head", action="store_true",
                     help="skip softmax + cross-entropy forward/backward at the GPT-2 head shape")
     ap.add_argument("--no-posterior", action="store_true",
@@ -484,7 +486,7 @@ def main():
         log(f"bench: ceiling {name:34s} {nr}R{nw}W stream {ceil:8.1f} GB/s ({100 * ceil / PEAK_GBS:4.1f}% of peak);"
             f" kernel at {100 * k['GBps'] / ceil:5.1f}% of it")
 
-    # ---- the same kernels at the other BASELINE configurations' shapes (not part of the step)
+    # ---- the same kernels at the other benchmark configurations' shapes (not part of the step)
     configs = {}
     if not args.no_configs:
         import numpy as np

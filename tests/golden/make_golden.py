@@ -8,8 +8,8 @@ never runs this script; the tests read the committed files.
 
     make -C oracle ref && python tests/golden/make_golden.py
 
-Fixtures (shapes are the reference's CPU-runnable configuration, BASELINE
-config 1: C=384, V=27, B=4, T=64, and the 256x384 LayerNorm of config 2):
+Fixtures (shapes are the reference's CPU-runnable configuration, C=384, V=27,
+B=4, T=64, and the 256x384 LayerNorm of benchmark config 2):
   encoder.npz     encoder fwd + bwd, B=4 T=64 C=384 V=27, uniform tokens, plus
                   the repeated-token case of train_bnn.c:1236-1238 (tokens
                   5,2,5,0,5,6 at B=2 T=3 C=4 V=7)

@@ -97,7 +97,7 @@ def test_fused_pairs_reject_invalid_arguments_on_host():
 def test_param_layout_counts():
     """Closed-form sizes of the reference layout (gpt2_kernels.cuh:656-719)."""
     import ugk
-    # BASELINE config 1 / the paper's P: C=384 L=6 V=27 maxT=1024 -> 11,061,531
+    # the reference's CPU-runnable configuration / the paper's P: C=384 L=6 V=27 maxT=1024 -> 11,061,531
     cfg = ugk.Config(B=4, T=64, C=384, V=27, NH=6, maxT=1024, L=6)
     assert ugk.param_count(cfg) == 11_061_531
     C, V, L, maxT = 768, 50257, 12, 1024
