@@ -23,7 +23,7 @@ __all__ = [
     "UgkError", "lib", "library_path",
     "encoder_forward", "encoder_backward", "layernorm_forward", "layernorm_backward",
     "gelu_forward", "gelu_backward", "residual_forward", "residual_backward",
-    "bayes_materialize", "residual_layernorm_forward", "layernorm_residual_backward",
+    "bayes_materialize", "encoder_layernorm_forward", "residual_layernorm_forward", "layernorm_residual_backward",
     "softmax_crossentropy", "crossentropy_softmax_backward", "bayes_sample", "bayes_backward",
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
