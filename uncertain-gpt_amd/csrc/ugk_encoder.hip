@@ -63,9 +63,11 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kChunk = 65536;            // rows per bucketing pass
 constexpr int kTableMax = 2 * kChunk;    // hash slots (power of two)
 // Table slots per row of a chunk (capped at kTableMax, which keeps at least
-// 2): a quarter-full table shortens the atomicCAS probe chains of the insert,
-// measured 3.9 us faster than half-full at config 5.
-constexpr int kLoadInv = 4;
+// 2): a sparse table shortens the atomicCAS probe chains of the insert and
+// puts fewer claimed slots in one cache line. At 8,192 x 768 a quarter-full
+// table was 3.9 us faster than a half-full one, and an eighth-full one another
+// 1.2 us (no change at 16,384 rows, where the cap leaves it quarter-full).
+constexpr int kLoadInv = 8;
 constexpr int kEmpty = -1;
 
 // ---- forward ---------------------------------------------------------------
@@ -398,6 +400,41 @@ __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncShared s
   if (cnt == 0 || cnt > kCap) return;
   // the slot's only reader has read it: free it for the next chunk's K1
   if (lane == 0) tb.slot[w] = kFree;
+  // A bucket of one or two rows (nearly all of them with uniform tokens) in
+  // one pass: every load of the row issued before the first add, instead of
+  // one round trip per 64 float4 of the row. The same additions in the same
+  // order as the loop below.
+  if (kVec && cnt <= 2 && (C >> 2) <= 3 * kWave) {
+    const int C4 = C >> 2;
+    const int a = __builtin_amdgcn_readlane(id_raw, 0);
+    const int b = cnt == 2 ? __builtin_amdgcn_readlane(id_raw, 1) : a;
+    float4 *row = reinterpret_cast<float4 *>(dwte) + (size_t)tok * C4;
+    const float4 *g0 = reinterpret_cast<const float4 *>(dout) + (size_t)min(a, b) * C4;
+    const float4 *g1 = reinterpret_cast<const float4 *>(dout) + (size_t)max(a, b) * C4;
+    float4 acc[3], d0[3], d1[3];
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+      const int c4 = lane + u * kWave;
+      if (c4 < C4) {
+        acc[u] = row[c4];
+        d0[u] = ld_nt(g0 + c4);
+        if (cnt == 2) d1[u] = ld_nt(g1 + c4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 3; u++) {
+      const int c4 = lane + u * kWave;
+      if (c4 < C4) {
+        float4 v = acc[u];
+        v.x += d0[u].x; v.y += d0[u].y; v.z += d0[u].z; v.w += d0[u].w;
+        if (cnt == 2) {
+          v.x += d1[u].x; v.y += d1[u].y; v.z += d1[u].z; v.w += d1[u].w;
+        }
+        row[c4] = v;
+      }
+    }
+    return;
+  }
   // rank the bucket's row ids; ids are distinct, so ranks are a permutation
   const int id = lane < cnt ? id_raw : 0x7fffffff;
   int rank = 0;
