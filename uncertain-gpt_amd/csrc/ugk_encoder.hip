@@ -17,8 +17,8 @@
 //     K1 insert  - each workgroup of 256 rows first groups its rows by
 //                  token in an LDS hash table (local count, local rank), then
 //                  one thread per distinct token probes the global open-
-//                  addressing table (4x the chunk, power of two, linear
-//                  probing). A slot is one 64-bit word, token and row count:
+//                  addressing table (8x the chunk, at most kTableMax, power
+//                  of two, linear probing). A slot is one 64-bit word, token and row count:
 //                  a token's first workgroup claims a free slot with its
 //                  count in one atomicCAS, later ones take a block of ranks
 //                  with one atomicAdd. A frequent token thus costs one global
@@ -50,8 +50,9 @@
 //   The table and its counters return to their cleared state within each
 //   chunk, on the device: K2 frees each slot once it has read it (the
 //   wavefront of its list entry, or the scan workgroup of a large bucket),
-//   and the last K3 workgroup to finish zeroes the counters. No state stays on the host between calls, so a
-//   captured HIP graph may replay any number of calls.
+//   and the last K3 workgroup to finish zeroes the counters. No state stays
+//   on the host between calls, so a captured HIP graph may replay any number
+//   of calls.
 //   The arrival order inside a bucket depends on scheduling, but it is
 //   discarded: only the set of row ids is used, always in ascending order.
 #include "ugk_internal.h"
