@@ -11,13 +11,15 @@ output buffers hold synthetic data. A "step" is that sequence, queued by the
 native step driver of libugk.so (ugk_gpt2_layers_forward/backward), which runs
 the encoder -> LayerNorm pair and each residual -> LayerNorm and LayerNorm ->
 residual pair as one pass and adds
-the LayerNorm weight/bias gradients of the whole backward in one launch; its
-buffers are bit-identical to the op-by-op sequence.
+the LayerNorm weight/bias gradients of the whole backward in one launch; the
+buffers it writes are bit-identical to the op-by-op sequence (a LayerNorm ->
+residual pair does not write its LayerNorm's dinp back: in gpt2_backward only
+the residual_backward it fuses reads that).
 
 Printed JSON line (the last line of stdout):
     value        the reference sequence's algorithmic bytes (18.05 GB, unfused) / step
                  time: the effective rate of the reference's work; GBps_moved divides the
-                 bytes the fused sequence must move (16.82 GB) instead
+                 bytes the fused sequence must move (16.22 GB) instead
     ms_per_step  mean over --steps steps (events on the kernels' stream; median, p25, p75
                  of the per-step times beside it)
     in_step      each op of the step, timed inside the step with a HIP event pair that
@@ -118,8 +120,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 # in-step op name -> the prefix of its kernel's short name in the PMC summary
-PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true>",
-           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false>",
+PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true, false>",
+           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false, true>",
            "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
            "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 
@@ -236,8 +238,9 @@ def main():
     A = ugk.act_count(cfg)
     per, count, total_bytes = step_bytes(B, T, C, L, n_mat)
     # the fused pairs of the driver skip 2L + 1 LayerNorm input reads (the first LayerNorm
-    # normalises the encoder's rows as it writes them) and 2L residual dout reads
-    moved_bytes = total_bytes - (2 * (2 * L) + 1) * 4 * (B * T * C)
+    # normalises the encoder's rows as it writes them), 2L residual dout reads and the 2L
+    # LayerNorm dinp writes that only the fused residual_backward would read
+    moved_bytes = total_bytes - (3 * (2 * L) + 1) * 4 * (B * T * C)
     log(f"bench: params {P} (materialize {n_mat}), acts {A}, algorithmic bytes/step {total_bytes / 1e9:.3f} GB")
 
     g = torch.Generator(device=dev)
@@ -297,7 +300,7 @@ def main():
         "encoder_layernorm_forward": 16 * N + 12 * B * T + 8 * C,
         "residual_layernorm_forward": 16 * N + 8 * B * T + 8 * C, "gelu_forward": per["gelu_forward"],
         "layernorm_backward (main)": 16 * N + 8 * B * T + 4 * C,
-        "layernorm_residual_backward (main)": 32 * N + 8 * B * T + 4 * C,
+        "layernorm_residual_backward (main)": 28 * N + 8 * B * T + 4 * C,  # dinp read, not written
         "gelu_backward": per["gelu_backward"], "layernorm column sums (batched)": (2 * L + 1) * 16 * C,
         "encoder_backward": per["encoder_backward"], "bayes_materialize": per["bayes_materialize"]}
     m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -383,7 +383,12 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
 
 /* Backward from the final LayerNorm down to the encoder
  * (gpt2_kernels.cuh:846-894). On entry grads_acts holds d(final LN output)
- * at the reference's flo offset; accumulates into grads and grads_acts. The
+ * at the reference's flo offset; accumulates into grads and grads_acts,
+ * except that each LayerNorm backward fused with the residual_backward after
+ * it adds into its dinp (res1 of every block, each block's resa) without
+ * writing the sum back: the reference reads those gradients only in that
+ * residual_backward (:855,874), so their contents after the call are
+ * unspecified. Every other buffer equals the op-by-op sequence's. The
  * LayerNorm dweight/dbias column sums are completed by one launch at the end,
  * and their partial rows live in the workspace's LayerNorm region meanwhile,
  * so the dense callbacks must not call ugk_layernorm_backward or

@@ -31,6 +31,20 @@ def bits_equal_dev(a, b, what):
                              f"driver {float(a[i])!r} replay {float(b[i])!r}")
 
 
+def pair_dinp_regions(a, arel, L, NB):
+    """(offset, length) of the activation gradients the driver's fused LayerNorm -> residual
+    backward pairs read but do not write back: resa and res1 of every block. In gpt2_backward
+    (gpt2_kernels.cuh:846-894) each is read last by the residual_backward that follows its
+    LayerNorm backward, so the replay's final values there are never used."""
+    blk = lambda l, k: a["blk0"] + l * a["bstride"] + arel[k]
+    return [(blk(l, k), NB) for l in range(L) for k in ("resa", "res1")]
+
+
+def clear_regions(t, regions):
+    for off, n in regions:
+        t[off:off + n] = 0
+
+
 class Layout:
     def __init__(self, B, T, C, V, maxT, L):
         self.B, self.T, self.C, self.V, self.maxT, self.L = B, T, C, V, maxT, L
@@ -169,7 +183,10 @@ def run_driver_vs_replay(gpu, B, T, C, V, NH, maxT, L, seed, dense_factory=None)
     for d in (d_dense, r_dense):
         if d:
             d.raise_errors()
-    bits_equal_dev(d_ga, r_ga, "driver grads_acts")
+    skip = pair_dinp_regions(lay.a, lay.arel, L, lay.NB)
+    clear_regions(d_ga, skip)
+    clear_regions(r_ga, skip)
+    bits_equal_dev(d_ga, r_ga, "driver grads_acts (all but the pairs' dinp)")
     bits_equal_dev(d_g, r_g, "driver grads")
     return d_dense
 

@@ -104,7 +104,9 @@ def test_fused_backward_rejects_aliased_dinp(gpu):
 @pytest.mark.parametrize("B,T,L", [(2, 32, 3), (4, 128, 1)])
 def test_step_driver_equals_per_op_replay_on_gpu(gpu, B, T, L):
     """ugk_gpt2_layers_forward/backward (fused pairs) == the reference launch sequence issued op by
-    op through the same library, bit for bit, on every activation, gradient and parameter gradient.
+    op through the same library, bit for bit, on every activation, every parameter gradient and
+    every activation gradient but the fused backward pairs' dinp (resa and res1 of each block,
+    which the reference reads only in the residual_backward that the pair fuses).
     The driver reduces all LayerNorms' partial rows in one batched launch, the per-op path each
     in its own: the same additions in the same order (8 and 64 partial rows, 1 and 4 per group)."""
     C, V, NH = 768, 50, 12
@@ -171,5 +173,11 @@ def test_step_driver_equals_per_op_replay_on_gpu(gpu, B, T, L):
                                AC(st, NB), tpar[PO(l, "lng"):][:C], AC(AO(l, "lnm"), B * T),
                                AC(AO(l, "lnr"), B * T), B, T, C)
     gpu.encoder_backward(r_g[:V * C], r_g[V * C:V * C + maxT * C], GA(a["enc"], NB), tin, B, T, C)
-    assert_bits(host(d_ga), host(r_ga), "driver grads_acts")
+    # the pairs' dinp (resa and res1 of every block) is read but not written back by the driver
+    dga, rga = host(d_ga), host(r_ga)
+    for l in range(L):
+        for k in ("resa", "res1"):
+            dga[AO(l, k):AO(l, k) + NB] = 0
+            rga[AO(l, k):AO(l, k) + NB] = 0
+    assert_bits(dga, rga, "driver grads_acts")
     assert_bits(host(d_g), host(r_g), "driver grads")

@@ -787,9 +787,12 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                     const float *w, const float *mean, const float *rstd) -> int {
     float *part = reinterpret_cast<float *>(pbase + slot * jobs.size());
     int nblk = 0;
+    // A pair's dinp is read (the LayerNorm adds to it) but not written back:
+    // in gpt2_backward nothing reads it after the residual_backward that
+    // splits it into dx and dy (res1 of every block and each block's resa).
     if (int e = timed(dx ? UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN : UGK_OP_LAYERNORM_BACKWARD_MAIN, [&] {
           return launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C,
-                                                    kMaxPartialRows, &nblk);
+                                                    kMaxPartialRows, &nblk, /*store_dinp=*/dx == nullptr);
         }))
       return e;
     jobs.push_back({part, dw, db, nblk});

@@ -161,10 +161,13 @@ struct LnReduceJob {
   int nblk;
 };
 // At most max_blocks partial rows (the float4 path takes up to 1024, the
-// scalar path up to 512).
+// scalar path up to 512). With dx non-null and store_dinp false, the float4
+// path leaves dinp unwritten (its new rows go only into dx and dy); the
+// scalar path writes it regardless.
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
-                                       const float *rstd, int rows, int C, int max_blocks, int *nblk);
+                                       const float *rstd, int rows, int C, int max_blocks, int *nblk,
+                                       bool store_dinp = true);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
 // Both passes with the partial rows in `partial` (at most max_blocks rows of
 // 2C floats), not in the workspace.

@@ -278,6 +278,9 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // kRes: the new dinp row is also added to rdx and rdy (residual_backward with
 // dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
 // gpt2_kernels.cuh:870-876 launches back to back.
+// kStore: dinp is written. Without it (kRes only) the dinp row is read and
+// used but not written back: the step driver's pairs, whose dinp nothing
+// reads after the residual split.
 // MINW: wavefronts per SIMD the register allocation must allow.
 // kNt: dinp is written with non-temporal stores (always with kRes). Without
 // kRes, large calls write it with ordinary stores, which measured faster
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // an ordinary dinp store made it faster alone (35.7 against 37.2 us cold at
 // 8,192 x 768) but the step slower (3.02 against 2.93 ms), the dirty lines
 // of its 24 launches being written back during the kernels that follow.
-template <int V, int W, int R, bool kRes, int MINW, bool kNt>
+template <int V, int W, int R, bool kRes, int MINW, bool kNt, bool kStore>
 __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
@@ -399,10 +402,12 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
         o.w = dx[q][v].w + r[q] * (dn.w - dnm - xh.w * dnxm);
         if (cl.in[v] && live) {
           const size_t e = off[q] + cl.col[v];
-          if (kNt)
-            st_nt(dx4 + e, o);
-          else
-            dx4[e] = o;
+          if (kStore) {
+            if (kNt)
+              st_nt(dx4 + e, o);
+            else
+              dx4[e] = o;
+          }
           if (kRes) {
             float4 a = add4(ra[kRes ? q : 0][kRes ? v : 0], o);
             if (same) {
@@ -456,7 +461,7 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
 // two-rows-per-wavefront kernel at 8,192 x 768, cold, with the same 512
 // partial rows. rpt and T fix the order of every addition; R does not, so the
 // plain backward (R = 2) and the fused pair (R = 4) give the same bits.
-template <int P, int T, int R, bool kRes, int MINW, bool kNt>
+template <int P, int T, int R, bool kRes, int MINW, bool kNt, bool kStore>
 __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
@@ -550,10 +555,12 @@ __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
       o.z = dx[q].z + r[q] * (dn[q].z - dnm - xh[q].z * dnxm);
       o.w = dx[q].w + r[q] * (dn[q].w - dnm - xh[q].w * dnxm);
       if (in) {
-        if (kNt)
-          st_nt(dx4 + off[q], o);
-        else
-          dx4[off[q]] = o;
+        if (kStore) {
+          if (kNt)
+            st_nt(dx4 + off[q], o);
+          else
+            dx4[off[q]] = o;
+        }
         if (kRes) {
           float4 a = add4(ra[kRes ? q : 0], o);
           if (same) {
@@ -884,10 +891,11 @@ int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *
 }
 
 namespace {
-template <bool kRes>
+template <bool kRes, bool kStore>
 int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const float *inp,
                       const float *weight, const float *mean, const float *rstd, int rows, int C,
                       float *rdx, float *rdy, int max_blocks) {
+  static_assert(kRes || kStore, "the plain backward always writes dinp");
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
   const int same = rdx == rdy ? 1 : 0;
@@ -897,13 +905,13 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
     team_shape(rows, max_blocks, &nblk, &rpt);
     const dim3 grid(nblk), block(kTeamParts * kTeams * kWave);
     if constexpr (kRes)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kStore>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     else if (nt)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, true>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     else
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, true>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     return nblk;
   }
@@ -914,10 +922,12 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
 #define UGK_LN_BWD(v)                                                                                            \
   case v:                                                                                                        \
     if (kRes || nt)                                                                                              \
-      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, true>),     \
+      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, true,      \
+                           kStore>),                                                                           \
              grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
     else                                                                                                         \
-      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, kRes>),    \
+      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, kRes,      \
+                           kStore>),                                                                           \
              grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
     break;
     UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
@@ -930,16 +940,21 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
 
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
-                                       const float *rstd, int rows, int C, int max_blocks, int *nblk) {
+                                       const float *rstd, int rows, int C, int max_blocks, int *nblk,
+                                       bool store_dinp) {
   *nblk = 0;
   if (rows == 0) return 0;
   const bool res = dx != nullptr;
   if (vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
-    if (res)
-      *nblk = launch_ln_bwd_vec<true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy, max_blocks);
+    if (res && store_dinp)
+      *nblk = launch_ln_bwd_vec<true, true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,
+                                            max_blocks);
+    else if (res)
+      *nblk = launch_ln_bwd_vec<true, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,
+                                             max_blocks);
     else
-      *nblk = launch_ln_bwd_vec<false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr, nullptr,
-                                       max_blocks);
+      *nblk = launch_ln_bwd_vec<false, true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr,
+                                             nullptr, max_blocks);
     return check_launch("layernorm_backward");
   }
   int rpb;
