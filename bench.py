@@ -488,6 +488,18 @@ def main():
         k["frac_of_ceiling"] = round(k["GBps"] / ceil, 4)
         log(f"bench: ceiling {name:34s} {nr}R{nw}W stream {ceil:8.1f} GB/s ({100 * ceil / PEAK_GBS:4.1f}% of peak);"
             f" kernel at {100 * k['GBps'] / ceil:5.1f}% of it")
+    # the step driver's LayerNorm -> residual backward pairs read five tensors and write two
+    # (their dinp store is dead); their in-step rate against the cold stream of that mix
+    best = 0.0
+    for u, bs in ((1, 256), (2, 256), (3, 256), (1, 512), (2, 512)):
+        ms, _, _ = time_cold(lambda: torch.empty(7 * N, device=dev), 28 * N,
+                             lambda b: chk(lib.ugk_diag_stream(P_(b), N, 5, 2, u, bs)))
+        best = max(best, 28 * N / (ms * 1e-3) / 1e9)
+    pair = in_step["layernorm_residual_backward (main)"]
+    pair["stream_ceiling_GBps"] = round(best, 1)
+    pair["frac_of_ceiling"] = round(pair["GBps"] / best, 4)
+    log(f"bench: ceiling in-step layernorm_residual_backward (main)  5R2W stream {best:8.1f} GB/s "
+        f"({100 * best / PEAK_GBS:4.1f}% of peak); in-step op at {100 * pair['GBps'] / best:5.1f}% of it")
 
     # ---- the same kernels at the other benchmark configurations' shapes (not part of the step)
     configs = {}
