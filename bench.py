@@ -25,8 +25,9 @@ Printed JSON line (the last line of stdout):
     in_step      each op of the step, timed inside the step with a HIP event pair that
                  its kernel's dispatch records (the library's op timer), over --op-steps
                  further steps: launches per step, mean us, us per step, algorithmic GB/s
-    roofline     the op with the most microseconds per step (the fused LayerNorm ->
-                 residual backward), achieved = its algorithmic bytes per launch / its mean
+    roofline     the op with the most microseconds per step (GELU backward or the fused
+                 LayerNorm -> residual backward pairs, within a few percent of each other),
+                 achieved = its algorithmic bytes per launch / its mean
                  in-step duration; traffic = HBM bytes per launch from rocprofv3 --pmc
                  FETCH_SIZE and WRITE_SIZE runs (profiles/pmc_traffic_cfg5.json)
     kernels      each kernel at its step shape, cold (launches rotate over buffer sets
@@ -195,7 +196,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=40,
                     help="cold launches per timed batch of a kernel (at least one per buffer set); 5 batches")
-    ap.add_argument("--op-steps", type=int, default=3, help="steps timed op by op with the library's op timer")
+    ap.add_argument("--op-steps", type=int, default=10, help="steps timed op by op with the library's op timer")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other benchmark configurations' shapes")
     ap.add_argument("--no-head", action="store_true",
