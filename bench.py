@@ -22,6 +22,9 @@ Printed JSON line (the last line of stdout):
                  bytes the fused sequence must move (16.22 GB) instead
     ms_per_step  mean over --steps steps (events on the kernels' stream; median, p25, p75
                  of the per-step times beside it)
+    zeroed_backward  the same step with ugk_gpt2_layers_backward_zeroed (for callers that
+                 zero grads_acts before the backward, as every reference arm does; it does
+                 not read those zeros): ms per step, rates on the reference's and moved bytes
     in_step      each op of the step, timed inside the step with a HIP event pair that
                  its kernel's dispatch records (the library's op timer), over --op-steps
                  further steps: launches per step, mean us, us per step, algorithmic GB/s
@@ -290,6 +293,35 @@ def main():
     value = total_bytes / (ms_step * 1e-3) / 1e9
     log(f"bench: step {ms_step:.4f} ms (median {step_stats['median']}, host wall {wall:.4f} ms) -> {value:.1f} GB/s "
         f"on the reference's bytes, {moved_bytes / (ms_step * 1e-3) / 1e9:.1f} GB/s moved")
+
+    # ---- the same step with ugk_gpt2_layers_backward_zeroed, the backward for callers that zero
+    # grads_acts before it (every reference arm does): it does not read those zeros (GELU
+    # backward's dinp, the residual splits' dx and dy, the final LayerNorm's dinp), and on this
+    # layout it reads nothing of what those buffers hold, so the steps need no zeroing between them
+    def step_zeroed():
+        chk(lib.ugk_bayes_materialize(wp, mup, rhop, epsp, n_mat))
+        chk(lib.ugk_gpt2_layers_forward(ap_, wp, ip, cfg, None))
+        chk(lib.ugk_gpt2_layers_backward_zeroed(gp, gap, ap_, wp, ip, cfg, None))
+
+    for _ in range(args.warmup):
+        step_zeroed()
+    torch.cuda.synchronize()
+    z0, z1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    z0.record()
+    for _ in range(args.steps):
+        step_zeroed()
+    z1.record()
+    torch.cuda.synchronize()
+    ms_zeroed = z0.elapsed_time(z1) / args.steps
+    moved_zeroed = moved_bytes - (32 * L + 4) * (B * T * C)
+    zeroed = {"ms_per_step": round(ms_zeroed, 4), "value_GBps": round(total_bytes / (ms_zeroed * 1e-3) / 1e9, 1),
+              "bytes_per_step_moved": moved_zeroed,
+              "GBps_moved": round(moved_zeroed / (ms_zeroed * 1e-3) / 1e9, 1),
+              "frac_moved": round(moved_zeroed / (ms_zeroed * 1e-3) / 1e9 / PEAK_GBS, 4),
+              "note": "ugk_gpt2_layers_backward_zeroed: the precondition of every reference arm (grads_acts "
+                      "zeroed before the backward) lets it skip reading those zeros"}
+    log(f"bench: step with the zeroed-gradient backward {ms_zeroed:.4f} ms -> {zeroed['value_GBps']:.1f} GB/s on the "
+        f"reference's bytes, {zeroed['GBps_moved']:.1f} GB/s moved ({moved_zeroed / 1e9:.2f} GB)")
 
     # ---- each op inside the step: a HIP event pair recorded by the dispatch of
     # every kernel the step driver issues (ugk_op_timer; the three-kernel
@@ -659,7 +691,8 @@ def main():
         "ms_per_step_stats": step_stats, "value_basis": "reference sequence's algorithmic bytes (unfused) / step time",
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
         "bytes_per_step_moved": moved_bytes, "GBps_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9, 1),
-        "frac_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4), "in_step": in_step,
+        "frac_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4), "zeroed_backward": zeroed,
+        "in_step": in_step,
         "kernels": kernels, "configs": configs, "posterior": posterior, "head": head, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -397,6 +397,22 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                              const float *params, const int *inputs,
                              ugk_config cfg, const ugk_dense_ops *ops);
 
+/* ugk_gpt2_layers_backward for callers that zero grads_acts outside the flo
+ * region before every backward, as every reference arm does (cudaMemset of
+ * d_gacts before gpt2_backward: train_bnn_gpu.cu:475, train_bnn_vadam.cu:422,
+ * train_bnn_lowrank.cu:919, train_ensemble.cu:281, uncertain/_C.cu:482,625,777,975).
+ * No counterpart in the reference. Under that precondition every buffer
+ * equals ugk_gpt2_layers_backward's; the zeros are not read: GELU backward
+ * writes its dinp (fch), the fused residual splits write their dx and dy
+ * (resa, mlpo, apr and res1 of every block), and the final LayerNorm takes
+ * its dinp as zero. With C a multiple of 4, 16-byte aligned buffers and
+ * L >= 1 the layer kernels therefore read none of those buffers, and the
+ * result does not depend on what they hold on entry; the dense callbacks
+ * still accumulate into theirs. */
+int ugk_gpt2_layers_backward_zeroed(float *grads, float *grads_acts, const float *acts,
+                                    const float *params, const int *inputs,
+                                    ugk_config cfg, const ugk_dense_ops *ops);
+
 /* ---- file formats of an end-to-end run ----------------------------------
  * Token files (llm.c's .bin: 256 int32 header with magic 20240520 and the
  * token count in header[2], then uint16 token ids) and checkpoints (8 int32

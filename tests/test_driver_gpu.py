@@ -360,3 +360,59 @@ def test_step_driver_reports_a_failing_callback(gpu):
     ops = ugk.DenseOps(None, fail, ugk._MATMUL_BWD(), ugk._ATTN_FWD(), ugk._ATTN_BWD())
     with pytest.raises(gpu.UgkError, match="matmul_forward"):
         gpu.gpt2_layers_forward(acts, params, inputs, cfg, ops)
+
+
+def first_write_regions(lay):
+    """(offset, length) of the activation gradients that the layer kernels are the first to write in
+    gpt2_backward (gpt2_kernels.cuh:846-894) when grads_acts starts at zero outside flo: enc and
+    fch, mlpo, apr, resa and res1 of every block (GELU backward's dinp and the residual splits'
+    dx and dy; res1 of the last block is the final LayerNorm's dinp)."""
+    NB = lay.NB
+    out = [(lay.a["enc"], NB)]
+    for l in range(lay.L):
+        out += [(lay.aa(l, "fch"), 4 * NB)] + [(lay.aa(l, k), NB) for k in ("mlpo", "apr", "resa", "res1")]
+    return out
+
+
+@pytest.mark.parametrize("B,T,C,V,L,garbage", [
+    (8, 1024, 768, 50257, 12, True),  # the benchmark's step
+    (2, 64, 768, 50, 3, True),        # row teams, few rows
+    (2, 32, 384, 27, 6, True),        # the two-rows-per-wavefront kernels (C = 384)
+    (2, 32, 384, 27, 0, False),       # no block: the final LayerNorm reads enc
+    (2, 16, 30, 11, 2, False),        # C = 30: the scalar LayerNorm path reads its residual targets
+])
+def test_zeroed_driver_equals_driver(gpu, B, T, C, V, L, garbage):
+    """ugk_gpt2_layers_backward_zeroed on a grads_acts that is zero where the layer kernels write first
+    equals ugk_gpt2_layers_backward on it, bit for bit (every parameter gradient, every activation
+    gradient but the pairs' unwritten dinp). Where it reads none of those buffers (float4 path,
+    L >= 1) it is also given garbage there instead of zeros, and must not notice."""
+    print(f"zeroed driver B={B} T={T} C={C} V={V} L={L} garbage={garbage}", flush=True)
+    prev = gpu.lib.ugk_get_stream()
+    gpu.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        NH = 12 if C % 12 == 0 else (5 if C % 5 == 0 else 1)
+        cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=max(T, 64), L=L)
+        lay = Layout(B, T, C, V, max(T, 64), L)
+        params, acts, inputs, ga0 = make_inputs(gpu, lay, seed=B * 100 + L)
+        gpu.gpt2_layers_forward(acts, params, inputs, cfg)
+        first = first_write_regions(lay)
+        clear_regions(ga0, first)
+        ga_acc, ga_zero = ga0.clone(), ga0.clone()
+        if garbage:
+            g = torch.Generator(device=DEV)
+            g.manual_seed(7)
+            for off, n in first:
+                ga_zero[off:off + n] = torch.randn(n, generator=g, device=DEV) * 3.0
+        g_acc = torch.zeros(lay.p["total"], device=DEV)
+        g_zero = torch.zeros(lay.p["total"], device=DEV)
+        gpu.gpt2_layers_backward(g_acc, ga_acc, acts, params, inputs, cfg)
+        gpu.gpt2_layers_backward_zeroed(g_zero, ga_zero, acts, params, inputs, cfg)
+        torch.cuda.synchronize()
+        skip = pair_dinp_regions(lay.a, lay.arel, L, lay.NB)
+        clear_regions(ga_acc, skip)
+        clear_regions(ga_zero, skip)
+        bits_equal_dev(ga_zero, ga_acc, "zeroed driver grads_acts (all but the pairs' dinp)")
+        bits_equal_dev(g_zero, g_acc, "zeroed driver grads")
+    finally:
+        gpu.set_stream(prev)
+        torch.cuda.empty_cache()

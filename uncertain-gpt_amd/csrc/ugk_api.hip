@@ -757,10 +757,14 @@ int ugk_gpt2_layers_forward(float *acts, const float *params, const int *inputs,
   return ok();
 }
 
-// gpt2_kernels.cuh:846-894
-int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts, const float *params,
-                             const int *inputs, ugk_config cfg, const ugk_dense_ops *ops) {
-  const char *fn = "ugk_gpt2_layers_backward";
+// gpt2_kernels.cuh:846-894. zeroed: grads_acts is zero outside flo on entry
+// (the arms' memset, train_bnn_gpu.cu:475), so the buffers this pass writes
+// first are written without being read: GELU backward's dinp (fch), the
+// residual splits' dx and dy (resa, mlpo, res1, apr) and the final
+// LayerNorm's dinp (res1 of the last block).
+namespace {
+int layers_backward(const char *fn, bool zeroed, float *grads, float *grads_acts, const float *acts,
+                    const float *params, const int *inputs, ugk_config cfg, const ugk_dense_ops *ops) {
   UGK_TRY(check_cfg(fn, cfg));
   if (any_null({grads, grads_acts, acts, params, inputs})) return bad(fn, "NULL pointer");
   const POff p = poff(cfg);
@@ -784,7 +788,7 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
   std::vector<LnReduceJob> jobs;
   jobs.reserve((size_t)nln);
   auto ln_bwd = [&](float *dinp, float *dw, float *db, float *dx, float *dy, const float *dout, const float *inp,
-                    const float *w, const float *mean, const float *rstd) -> int {
+                    const float *w, const float *mean, const float *rstd, int dinp_mode = kDinpRead) -> int {
     float *part = reinterpret_cast<float *>(pbase + slot * jobs.size());
     int nblk = 0;
     // A pair's dinp is read (the LayerNorm adds to it) but not written back:
@@ -792,7 +796,8 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
     // splits it into dx and dy (res1 of every block and each block's resa).
     if (int e = timed(dx ? UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN : UGK_OP_LAYERNORM_BACKWARD_MAIN, [&] {
           return launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C,
-                                                    kMaxPartialRows, &nblk, /*store_dinp=*/dx == nullptr);
+                                                    kMaxPartialRows, &nblk, dx ? dinp_mode : kDinpRw,
+                                                    zeroed && dx != nullptr);
         }))
       return e;
     jobs.push_back({part, dw, db, nblk});
@@ -802,7 +807,7 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
   if (cfg.L > 0)
     UGK_TRY(ln_bwd(grads_acts + last, grads + p.flng, grads + p.flnb, grads_acts + A(cfg.L - 1, a.resa),
                    grads_acts + A(cfg.L - 1, a.mlpo), grads_acts + a.flo, acts + last, params + p.flng,
-                   acts + a.flm, acts + a.flr));
+                   acts + a.flm, acts + a.flr, zeroed ? kDinpNone : kDinpRead));
   else
     UGK_TRY(ln_bwd(grads_acts + last, grads + p.flng, grads + p.flnb, nullptr, nullptr, grads_acts + a.flo,
                    acts + last, params + p.flng, acts + a.flm, acts + a.flr));
@@ -813,7 +818,10 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
                                          grads + P(l, p.b2), acts + A(l, a.gelu), params + P(l, p.w2),
                                          grads_acts + A(l, a.mlpo), M, 4 * C, C), "matmul_backward(fc2)"));
     UGK_TRY(timed(UGK_OP_GELU_BACKWARD, [&] {
-      return ugk_gelu_backward(grads_acts + A(l, a.fch), acts + A(l, a.fch), grads_acts + A(l, a.gelu), NBTC * 4);
+      float *dfch = grads_acts + A(l, a.fch);
+      const float *fch = acts + A(l, a.fch), *dgelu = grads_acts + A(l, a.gelu);
+      return zeroed ? launch_gelu_backward_zero(dfch, fch, dgelu, (size_t)NBTC * 4)
+                    : launch_gelu_backward(dfch, fch, dgelu, (size_t)NBTC * 4);
     }));
     if (ops && ops->matmul_backward)
       UGK_TRY(dense(ops->matmul_backward(ops->ctx, grads_acts + A(l, a.ln2o), grads + P(l, p.w1),
@@ -847,6 +855,18 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
     return ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C);
   }));
   return ok();
+}
+}  // namespace
+
+int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts, const float *params,
+                             const int *inputs, ugk_config cfg, const ugk_dense_ops *ops) {
+  return layers_backward("ugk_gpt2_layers_backward", false, grads, grads_acts, acts, params, inputs, cfg, ops);
+}
+
+int ugk_gpt2_layers_backward_zeroed(float *grads, float *grads_acts, const float *acts, const float *params,
+                                    const int *inputs, ugk_config cfg, const ugk_dense_ops *ops) {
+  return layers_backward("ugk_gpt2_layers_backward_zeroed", true, grads, grads_acts, acts, params, inputs, cfg,
+                         ops);
 }
 
 int ugk_op_timer_start(int capacity) {

@@ -76,6 +76,25 @@ struct GeluBwd : MapOp {  // train_bnn.c:520-533; loads inp, dout, dinp
   }
 };
 
+// The same two with dinp taken as +0.0 instead of read (the zeroed-gradient
+// step driver, where GELU backward is the first writer of its dinp): +0.0 + x
+// gives the bits that the read of a zero buffer would give.
+struct GeluBwdFastZero : MapOp {  // loads inp, dout
+  static constexpr int kLoads = 2, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 1024;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
+    st[0] = 0.0f + ugk_fast_gelu_grad(ld[0]) * ld[1];
+  }
+};
+
+struct GeluBwdZero : MapOp {  // loads inp, dout
+  static constexpr int kLoads = 2, kStores = 1;
+  static constexpr int kUnroll = 1, kThreads = 512;
+  __device__ static void apply(const float *ld, float *st, const uint64_t *, size_t, Params) {
+    st[0] = 0.0f + ugk_dev_gelu_grad(ld[0]) * ld[1];
+  }
+};
+
 struct Materialize : MapOp {  // train_bnn.c:831-835; loads mu, rho, eps
   static constexpr int kLoads = 3, kStores = 1;
   static constexpr int kUnroll = 1, kThreads = 256;  // measured best of the map shapes
@@ -123,6 +142,15 @@ int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_
     return run_map(s, n, "gelu_backward");
   }
   Streams<GeluBwdFast> s{{inp, dout, dinp}, {dinp}, {}};
+  return run_map(s, n, "gelu_backward");
+}
+
+int launch_gelu_backward_zero(float *dinp, const float *inp, const float *dout, size_t n) {
+  if (gelu_exact()) {
+    Streams<GeluBwdZero> s{{inp, dout}, {dinp}, {}};
+    return run_map(s, n, "gelu_backward");
+  }
+  Streams<GeluBwdFastZero> s{{inp, dout}, {dinp}, {}};
   return run_map(s, n, "gelu_backward");
 }
 

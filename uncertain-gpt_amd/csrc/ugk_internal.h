@@ -114,6 +114,8 @@ void set_gelu_exact(int exact);
 int gelu_exact();
 int launch_gelu_forward(float *out, const float *inp, size_t n);
 int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n);
+// dinp = gelu'(inp) * dout, as launch_gelu_backward on a dinp of zeros (not read)
+int launch_gelu_backward_zero(float *dinp, const float *inp, const float *dout, size_t n);
 int launch_bayes_materialize(float *w, const float *mu, const float *rho,
                              const float *eps, size_t n);
 int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
@@ -160,14 +162,21 @@ struct LnReduceJob {
   float *dweight, *dbias;
   int nblk;
 };
+// What a fused LayerNorm -> residual backward does with its dinp (the
+// float4 path; the scalar path always reads and writes it):
+enum LnDinp {
+  kDinpRw = 0,    // read (the LayerNorm adds to it) and written
+  kDinpRead = 1,  // read, not written back (nothing reads it after the residual split)
+  kDinpNone = 2,  // neither: taken as +0.0 (the zeroed-gradient driver's first pair)
+};
 // At most max_blocks partial rows (the float4 path takes up to 1024, the
-// scalar path up to 512). With dx non-null and store_dinp false, the float4
-// path leaves dinp unwritten (its new rows go only into dx and dy); the
-// scalar path writes it regardless.
+// scalar path up to 512). With dx non-null, dinp_mode says what happens to
+// dinp, and assign_res takes dx and dy as +0.0 instead of reading them (float4
+// path; the scalar path reads and writes everything).
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
                                        const float *rstd, int rows, int C, int max_blocks, int *nblk,
-                                       bool store_dinp = true);
+                                       int dinp_mode = kDinpRw, bool assign_res = false);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
 // Both passes with the partial rows in `partial` (at most max_blocks rows of
 // 2C floats), not in the workspace.

@@ -263,6 +263,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
   }
 }
 
+__device__ __forceinline__ float4 zero4() { return make_float4(0.0f, 0.0f, 0.0f, 0.0f); }
+
 // Backward, register-resident rows. A workgroup is W wavefronts; wavefront w
 // of workgroup g takes the rpw consecutive rows starting at (W g + w) * rpw,
 // R at a time: the loads of R rows (x and dout first, which the row sums
@@ -278,9 +280,14 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // kRes: the new dinp row is also added to rdx and rdy (residual_backward with
 // dout = dinp, train_bnn.c:491-496; twice into rdx when same), the pair
 // gpt2_kernels.cuh:870-876 launches back to back.
-// kStore: dinp is written. Without it (kRes only) the dinp row is read and
-// used but not written back: the step driver's pairs, whose dinp nothing
-// reads after the residual split.
+// kDinp: kDinpRw reads and writes dinp. kDinpRead (kRes only) reads it but
+// does not write it back: the step driver's pairs, whose dinp nothing reads
+// after the residual split. kDinpNone (kRes only) neither reads nor writes
+// it, taking it as +0.0: the first pair of the zeroed-gradient driver.
+// kAssign (kRes only): rdx and rdy are not read but taken as +0.0 (the
+// zeroed-gradient driver, whose residual targets are first written there).
+// +0.0 + x is x with -0.0 turned to +0.0, so both give the bits the reads
+// would give on a zero buffer.
 // MINW: wavefronts per SIMD the register allocation must allow.
 // kNt: dinp is written with non-temporal stores (always with kRes). Without
 // kRes, large calls write it with ordinary stores, which measured faster
@@ -291,7 +298,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 // an ordinary dinp store made it faster alone (35.7 against 37.2 us cold at
 // 8,192 x 768) but the step slower (3.02 against 2.93 ms), the dirty lines
 // of its 24 launches being written back during the kernels that follow.
-template <int V, int W, int R, bool kRes, int MINW, bool kNt, bool kStore>
+template <int V, int W, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign>
 __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
@@ -344,15 +351,15 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
 #pragma unroll
     for (int q = 0; q < R; q++)
 #pragma unroll
-      for (int v = 0; v < V; v++) dx[q][v] = ld_nt(dx4 + off[q] + cl.col[v]);
+      for (int v = 0; v < V; v++) dx[q][v] = kDinp == kDinpNone ? zero4() : ld_nt(dx4 + off[q] + cl.col[v]);
     if (kRes) {
       // rdy is loaded even when it is rdx (same): a valid address, never used
 #pragma unroll
       for (int q = 0; q < R; q++)
 #pragma unroll
         for (int v = 0; v < V; v++) {
-          ra[kRes ? q : 0][kRes ? v : 0] = ld_nt(a4 + off[q] + cl.col[v]);
-          rb[kRes ? q : 0][kRes ? v : 0] = ld_nt(b4 + off[q] + cl.col[v]);
+          ra[kRes ? q : 0][kRes ? v : 0] = kAssign ? zero4() : ld_nt(a4 + off[q] + cl.col[v]);
+          rb[kRes ? q : 0][kRes ? v : 0] = kAssign ? zero4() : ld_nt(b4 + off[q] + cl.col[v]);
         }
     }
     // keep every load above the arithmetic (the scheduler would otherwise
@@ -402,7 +409,7 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
         o.w = dx[q][v].w + r[q] * (dn.w - dnm - xh.w * dnxm);
         if (cl.in[v] && live) {
           const size_t e = off[q] + cl.col[v];
-          if (kStore) {
+          if (kDinp == kDinpRw) {
             if (kNt)
               st_nt(dx4 + e, o);
             else
@@ -461,7 +468,7 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
 // two-rows-per-wavefront kernel at 8,192 x 768, cold, with the same 512
 // partial rows. rpt and T fix the order of every addition; R does not, so the
 // plain backward (R = 2) and the fused pair (R = 4) give the same bits.
-template <int P, int T, int R, bool kRes, int MINW, bool kNt, bool kStore>
+template <int P, int T, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign>
 __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
@@ -512,13 +519,13 @@ __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
       r[q] = rstd[rq[q]];
     }
 #pragma unroll
-    for (int q = 0; q < R; q++) dx[q] = ld_nt(dx4 + off[q]);
+    for (int q = 0; q < R; q++) dx[q] = kDinp == kDinpNone ? zero4() : ld_nt(dx4 + off[q]);
     if (kRes) {
       // rdy is loaded even when it is rdx (same): a valid address, never used
 #pragma unroll
       for (int q = 0; q < R; q++) {
-        ra[kRes ? q : 0] = ld_nt(a4 + off[q]);
-        rb[kRes ? q : 0] = ld_nt(b4 + off[q]);
+        ra[kRes ? q : 0] = kAssign ? zero4() : ld_nt(a4 + off[q]);
+        rb[kRes ? q : 0] = kAssign ? zero4() : ld_nt(b4 + off[q]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -555,7 +562,7 @@ __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
       o.z = dx[q].z + r[q] * (dn[q].z - dnm - xh[q].z * dnxm);
       o.w = dx[q].w + r[q] * (dn[q].w - dnm - xh[q].w * dnxm);
       if (in) {
-        if (kStore) {
+        if (kDinp == kDinpRw) {
           if (kNt)
             st_nt(dx4 + off[q], o);
           else
@@ -891,11 +898,11 @@ int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *
 }
 
 namespace {
-template <bool kRes, bool kStore>
+template <bool kRes, int kDinp, bool kAssign>
 int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const float *inp,
                       const float *weight, const float *mean, const float *rstd, int rows, int C,
                       float *rdx, float *rdy, int max_blocks) {
-  static_assert(kRes || kStore, "the plain backward always writes dinp");
+  static_assert(kRes || (kDinp == kDinpRw && !kAssign), "the plain backward reads and writes dinp");
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
   const int same = rdx == rdy ? 1 : 0;
@@ -905,13 +912,13 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
     team_shape(rows, max_blocks, &nblk, &rpt);
     const dim3 grid(nblk), block(kTeamParts * kTeams * kWave);
     if constexpr (kRes)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kStore>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kDinp, kAssign>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     else if (nt)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, true>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, kDinpRw, false>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     else
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, true>), grid, block, 0, dinp, partial, dout, inp,
+      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, kDinpRw, false>), grid, block, 0, dinp, partial, dout, inp,
              weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
     return nblk;
   }
@@ -923,11 +930,11 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
   case v:                                                                                                        \
     if (kRes || nt)                                                                                              \
       launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, true,      \
-                           kStore>),                                                                           \
+                           kDinp, kAssign>),                                                                   \
              grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
     else                                                                                                         \
       launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, kRes,      \
-                           kStore>),                                                                           \
+                           kDinp, kAssign>),                                                                   \
              grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
     break;
     UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
@@ -941,20 +948,28 @@ int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const floa
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
                                        const float *rstd, int rows, int C, int max_blocks, int *nblk,
-                                       bool store_dinp) {
+                                       int dinp_mode, bool assign_res) {
   *nblk = 0;
   if (rows == 0) return 0;
   const bool res = dx != nullptr;
   if (vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
-    if (res && store_dinp)
-      *nblk = launch_ln_bwd_vec<true, true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,
-                                            max_blocks);
-    else if (res)
-      *nblk = launch_ln_bwd_vec<true, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,
-                                             max_blocks);
+#define UGK_LN_BWD_MODE(d, a) \
+  launch_ln_bwd_vec<true, d, a>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy, max_blocks)
+    if (!res)
+      *nblk = launch_ln_bwd_vec<false, kDinpRw, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C,
+                                                       nullptr, nullptr, max_blocks);
+    else if (dinp_mode == kDinpRw && !assign_res)
+      *nblk = UGK_LN_BWD_MODE(kDinpRw, false);
+    else if (dinp_mode == kDinpRead && !assign_res)
+      *nblk = UGK_LN_BWD_MODE(kDinpRead, false);
+    else if (dinp_mode == kDinpRead)
+      *nblk = UGK_LN_BWD_MODE(kDinpRead, true);
+    else if (dinp_mode == kDinpNone && assign_res)
+      *nblk = UGK_LN_BWD_MODE(kDinpNone, true);
     else
-      *nblk = launch_ln_bwd_vec<false, true>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr,
-                                             nullptr, max_blocks);
+      return set_error(UGK_EINVAL, "layernorm_backward: unsupported dinp mode %d with assign %d", dinp_mode,
+                       (int)assign_res);
+#undef UGK_LN_BWD_MODE
     return check_launch("layernorm_backward");
   }
   int rpb;

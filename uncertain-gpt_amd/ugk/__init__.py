@@ -30,7 +30,7 @@ __all__ = [
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
     "set_workspace", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
-    "gpt2_layers_backward", "version",
+    "gpt2_layers_backward", "gpt2_layers_backward_zeroed", "version",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -108,6 +108,7 @@ _SIGS = {
     "ugk_act_count": [Config],
     "ugk_gpt2_layers_forward": [_fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
     "ugk_gpt2_layers_backward": [_fp, _fp, _fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
+    "ugk_gpt2_layers_backward_zeroed": [_fp, _fp, _fp, _fp, _fp, Config, ctypes.POINTER(DenseOps)],
     "ugk_diag_math_mismatch": [_i, ctypes.c_uint, ctypes.c_ulonglong, ctypes.POINTER(ctypes.c_ulonglong),
                                ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
@@ -455,16 +456,26 @@ def gpt2_layers_forward(acts, params, inputs, cfg: Config, ops: Optional[DenseOp
                                        ctypes.byref(ops) if ops is not None else None))
 
 
+def _layers_backward(fn, grads, grads_acts, acts, params, inputs, cfg, ops):
+    _cfg_check(cfg)
+    na, npar = act_count(cfg), param_count(cfg)
+    _check(fn(_ptr(grads, "grads", npar, "f32"), _ptr(grads_acts, "grads_acts", na, "f32"),
+              _ptr(acts, "acts", na, "f32"), _ptr(params, "params", npar, "f32"),
+              _ptr(inputs, "inputs", cfg.B * cfg.T, "i32"), cfg, ctypes.byref(ops) if ops is not None else None))
+
+
 def gpt2_layers_backward(grads, grads_acts, acts, params, inputs, cfg: Config,
                          ops: Optional[DenseOps] = None) -> None:
     """Layer-kernel half of gpt2_backward (gpt2_kernels.cuh:846-894)."""
-    _cfg_check(cfg)
-    na, npar = act_count(cfg), param_count(cfg)
-    _check(lib.ugk_gpt2_layers_backward(_ptr(grads, "grads", npar, "f32"),
-                                        _ptr(grads_acts, "grads_acts", na, "f32"),
-                                        _ptr(acts, "acts", na, "f32"), _ptr(params, "params", npar, "f32"),
-                                        _ptr(inputs, "inputs", cfg.B * cfg.T, "i32"), cfg,
-                                        ctypes.byref(ops) if ops is not None else None))
+    _layers_backward(lib.ugk_gpt2_layers_backward, grads, grads_acts, acts, params, inputs, cfg, ops)
+
+
+def gpt2_layers_backward_zeroed(grads, grads_acts, acts, params, inputs, cfg: Config,
+                                ops: Optional[DenseOps] = None) -> None:
+    """gpt2_layers_backward for a grads_acts that is zero outside the incoming gradient (flo), as
+    every reference arm leaves it before gpt2_backward (train_bnn_gpu.cu:475): the zeros are
+    not read."""
+    _layers_backward(lib.ugk_gpt2_layers_backward_zeroed, grads, grads_acts, acts, params, inputs, cfg, ops)
 
 
 MATH_FUNCTIONS = {"expf": 0, "log1pf": 1, "expm1f": 2, "tanhf": 3, "softplus": 4, "logf": 5, "cosf": 6,
