@@ -405,10 +405,10 @@ int ugk_gpt2_layers_backward(float *grads, float *grads_acts, const float *acts,
  * equals ugk_gpt2_layers_backward's; the zeros are not read: GELU backward
  * writes its dinp (fch), the fused residual splits write their dx and dy
  * (resa, mlpo, apr and res1 of every block), and the final LayerNorm takes
- * its dinp as zero. With C a multiple of 4, 16-byte aligned buffers and
- * L >= 1 the layer kernels therefore read none of those buffers, and the
- * result does not depend on what they hold on entry; the dense callbacks
- * still accumulate into theirs. */
+ * its dinp as zero. With C a multiple of 4 and at most 2,048, 16-byte
+ * aligned buffers and L >= 1 the layer kernels therefore read none of those
+ * buffers, and the result does not depend on what they hold on entry; the
+ * dense callbacks still accumulate into theirs. */
 int ugk_gpt2_layers_backward_zeroed(float *grads, float *grads_acts, const float *acts,
                                     const float *params, const int *inputs,
                                     ugk_config cfg, const ugk_dense_ops *ops);
