@@ -88,6 +88,8 @@ def step_bytes(B, T, C, L, n_mat):
 
 KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_map_vec4<ugk::(anonymous namespace)::GeluBwdFast>", "gelu_backward"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwdFastZero>", "gelu_backward (dinp not read)"),
+    ("k_map_vec4<ugk::(anonymous namespace)::GeluBwdZero>", "gelu_backward (exact form, dinp not read)"),
     ("k_map_vec4<ugk::(anonymous namespace)::GeluFwdFast>", "gelu_forward"),
     ("k_map_vec4<ugk::(anonymous namespace)::GeluBwd>", "gelu_backward (exact form)"),
     ("k_map_vec4<ugk::(anonymous namespace)::GeluFwd>", "gelu_forward (exact form)"),
@@ -124,8 +126,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 # in-step op name -> the prefix of its kernel's short name in the PMC summary
-PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true, false>",
-           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false, true>",
+PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true, 1, false>",
+           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false, 0, false>",
            "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
            "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 
