@@ -662,7 +662,8 @@ def main():
     traffic, traffic_src = None, None
     if os.path.exists(PMC_TRAFFIC):  # recorded by two rocprofv3 --pmc runs of this script
         pmc = json.load(open(PMC_TRAFFIC)).get("kernels", {})
-        key = next((k for k in pmc if k.startswith(PMC_KEY.get(dom, dom))), None)
+        want = PMC_KEY.get(dom, dom)  # an exact name, else the first one it begins
+        key = want if want in pmc else next((k for k in pmc if k.startswith(want)), None)
         if key:
             traffic, traffic_src = pmc[key]["traffic_bytes"], f"{os.path.relpath(PMC_TRAFFIC, ROOT)}: {key}"
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
