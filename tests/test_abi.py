@@ -115,6 +115,14 @@ def test_config_checks():
         ugk.gpt2_layers_forward(0, 0, 0, bad)
     lib = ugk.lib
     assert lib.ugk_gpt2_layers_forward(1, 1, 1, bad, None) == 1
+    # both backwards check the config and their pointers on the host, before any HIP call
+    for fn in (lib.ugk_gpt2_layers_backward, lib.ugk_gpt2_layers_backward_zeroed):
+        assert fn(1, 1, 1, 1, 1, bad, None) == 1
+        good = ugk.Config(B=1, T=8, C=16, V=5, NH=1, maxT=8, L=1)
+        assert fn(None, 1, 1, 1, 1, good, None) == 1
+        assert b"NULL pointer" in lib.ugk_last_error()
+    with pytest.raises(ValueError):
+        ugk.gpt2_layers_backward_zeroed(0, 0, 0, 0, 0, bad)
 
 
 def test_binding_rejects_cpu_tensors():
