@@ -416,3 +416,35 @@ def test_zeroed_driver_equals_driver(gpu, B, T, C, V, L, garbage):
     finally:
         gpu.set_stream(prev)
         torch.cuda.empty_cache()
+
+
+def test_zeroed_driver_with_dense_callbacks(gpu):
+    """With dense-op callbacks (which accumulate, as the arms' GEMMs do) and grads_acts zero outside
+    flo, the zeroed backward equals the accumulating one bit for bit."""
+    B, T, C, V, NH, L = 2, 32, 384, 27, 6, 3
+    prev = gpu.lib.ugk_get_stream()
+    gpu.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=NH, maxT=max(T, 32), L=L)
+        lay = Layout(B, T, C, V, max(T, 32), L)
+        params, acts, inputs, ga0 = make_inputs(gpu, lay, seed=91)
+        ga0[lay.a["blk0"]:lay.a["blk0"] + L * lay.a["bstride"]] = 0  # the arms' memset (flo keeps its gradient)
+        ga0[lay.a["enc"]:lay.a["enc"] + lay.NB] = 0
+        dense = TorchDense(params, acts)
+        gpu.gpt2_layers_forward(acts, params, inputs, cfg, dense.ops)
+        torch.cuda.synchronize()
+        dense.raise_errors()
+        out = []
+        for fn in (gpu.gpt2_layers_backward, gpu.gpt2_layers_backward_zeroed):
+            g, ga = torch.zeros(lay.p["total"], device=DEV), ga0.clone()
+            d = TorchDense(params, acts)
+            d.bind_backward(g, ga)
+            fn(g, ga, acts, params, inputs, cfg, d.ops)
+            torch.cuda.synchronize()
+            d.raise_errors()
+            clear_regions(ga, pair_dinp_regions(lay.a, lay.arel, L, lay.NB))
+            out.append((g, ga))
+        bits_equal_dev(out[1][1], out[0][1], "zeroed driver grads_acts with callbacks")
+        bits_equal_dev(out[1][0], out[0][0], "zeroed driver grads with callbacks")
+    finally:
+        gpu.set_stream(prev)
