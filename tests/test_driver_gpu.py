@@ -196,6 +196,8 @@ def run_driver_vs_replay(gpu, B, T, C, V, NH, maxT, L, seed, dense_factory=None)
     (2, 64, 768, 50, 16),       # 33 LayerNorm backwards: the batched column sums take two launches
     (2, 32, 384, 27, 6),        # config 1's width and depth
     (2, 32, 384, 27, 0),        # no block: the encoder -> LayerNorm pass writes the final LayerNorm
+    (2, 16, 1024, 27, 2),       # four float4 per lane (GPT-2 medium's width)
+    (1, 16, 2048, 11, 1),       # eight, the widest row held in registers
 ])
 def test_step_driver_equals_per_op_replay_at_shape(gpu, B, T, C, V, L):
     print(f"driver vs replay B={B} T={T} C={C} V={V} L={L}", flush=True)
@@ -378,6 +380,8 @@ def first_write_regions(lay):
     (8, 1024, 768, 50257, 12, True),  # the benchmark's step
     (2, 64, 768, 50, 3, True),        # row teams, few rows
     (2, 32, 384, 27, 6, True),        # the two-rows-per-wavefront kernels (C = 384)
+    (2, 16, 1024, 27, 2, True),       # four float4 per lane
+    (1, 16, 2048, 11, 1, True),       # eight float4 per lane
     (2, 32, 384, 27, 0, False),       # no block: the final LayerNorm reads enc
     (2, 16, 30, 11, 2, False),        # C = 30: the scalar LayerNorm path reads its residual targets
 ])
