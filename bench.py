@@ -118,6 +118,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_softmax_xent_split<", "softmax_crossentropy"),
     ("k_softmax_stats", "softmax_crossentropy (row statistics)"),
     ("k_softmax_norm", "softmax_crossentropy (normalise)"),
+    ("k_xent_softmax_bwd_flat4<true>", "crossentropy_softmax_backward (dlogits not read)"),
+    ("k_xent_softmax_bwd<true>", "crossentropy_softmax_backward (dlogits not read)"),
     ("k_xent_softmax_bwd", "crossentropy_softmax_backward"),
     ("k_kl_partial", "kl_forward (partial sums)"),
     ("k_kl_final", "kl_forward (final sum)"),
@@ -653,6 +655,10 @@ def main():
         ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_crossentropy_softmax_backward(
             P_(d["dlogits"]), P_(d["probs"]), P_(d["targets"]), B, T, V)))
         record(head, "crossentropy_softmax_backward", 12 * NV + 4 * rows_h, ms, l_, k_)
+        # the zeroed variant writes dlogits without reading it: 8 B per logit moved
+        ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_crossentropy_softmax_backward_zeroed(
+            P_(d["dlogits"]), P_(d["probs"]), P_(d["targets"]), B, T, V)))
+        record(head, "crossentropy_softmax_backward_zeroed", 8 * NV + 4 * rows_h, ms, l_, k_)
 
     # ---- roofline of the op with the most microseconds per step, from its in-step
     # launches (a HIP event pair around each, on the library stream)

@@ -179,6 +179,16 @@ int ugk_softmax_crossentropy(float *losses, float *probs, const float *logits,
 int ugk_crossentropy_softmax_backward(float *dlogits, const float *probs,
                                       const int *targets, int B, int T, int V);
 
+/* ugk_crossentropy_softmax_backward for callers whose dlogits is zero before
+ * the call, as in every reference arm (its memset of d_gacts, which holds the
+ * logits gradient, before the step: train_bnn_gpu.cu:475). No counterpart in
+ * the reference. dlogits = 0 + (probs - onehot(target)) * (1 / (B*T)),
+ * without reading dlogits: the same bits as ugk_crossentropy_softmax_backward
+ * on a zero buffer, whatever it holds. */
+int ugk_crossentropy_softmax_backward_zeroed(float *dlogits, const float *probs,
+                                             const int *targets, int B, int T,
+                                             int V);
+
 /* ---- the posterior update around the layer kernels ----------------------
  * Flat parameter vectors of n floats. The ops that take eps are
  * bit-identical to train_bnn.c. The *_philox ops draw

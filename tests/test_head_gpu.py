@@ -162,3 +162,19 @@ def test_full_cfg5_head(gpu, oracle):
     onehot[np.arange(pick.size), tg] = 1.0
     d = np.float32(0.0) + (p_rows - onehot) * (np.float32(1.0) / np.float32(rows))
     assert bits_equal(host(dl.view(rows, V)[ti]), d)
+
+
+@pytest.mark.parametrize("B,T,V", [(8, 1024, 50257), (2, 3, 1000), (3, 5, 27), (1, 7, 50257), (2, 2, 3)])
+def test_crossentropy_backward_zeroed(gpu, B, T, V):
+    """crossentropy_softmax_backward_zeroed over garbage == crossentropy_softmax_backward over zeros,
+    bit for bit (float4 stream and dword paths: V = 27 and 3 take the latter)."""
+    rows = B * T
+    g = torch.Generator(DEV).manual_seed(rows + V)
+    probs = torch.rand(rows * V, device=DEV, generator=g)
+    targets = torch.randint(0, V, (rows,), device=DEV, dtype=torch.int32, generator=g)
+    want = torch.zeros(rows * V, device=DEV)
+    gpu.crossentropy_softmax_backward(want, probs, targets, B, T, V)
+    got = torch.randn(rows * V, device=DEV, generator=g) * 5.0
+    gpu.crossentropy_softmax_backward_zeroed(got, probs, targets, B, T, V)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))

@@ -356,14 +356,25 @@ int ugk_softmax_crossentropy(float *losses, float *probs, const float *logits, c
   return ok();
 }
 
-int ugk_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int B, int T, int V) {
-  const char *fn = "ugk_crossentropy_softmax_backward";
+namespace {
+int xent_backward(const char *fn, bool zeroed, float *dlogits, const float *probs, const int *targets, int B, int T,
+                  int V) {
   if (int e = check_btc(fn, B, T, V)) return e;
   if ((long long)B * T * V == 0) return ok();
   if (any_null({dlogits, probs, targets})) return bad(fn, "NULL pointer");
   const float dloss = 1.0f / (B * T);  // train_bnn.c:360
-  if (int e = launch_crossentropy_softmax_backward(dlogits, probs, targets, B * T, V, dloss)) return e;
+  if (int e = launch_crossentropy_softmax_backward(dlogits, probs, targets, B * T, V, dloss, zeroed)) return e;
   return ok();
+}
+}  // namespace
+
+int ugk_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int B, int T, int V) {
+  return xent_backward("ugk_crossentropy_softmax_backward", false, dlogits, probs, targets, B, T, V);
+}
+
+int ugk_crossentropy_softmax_backward_zeroed(float *dlogits, const float *probs, const int *targets, int B, int T,
+                                             int V) {
+  return xent_backward("ugk_crossentropy_softmax_backward_zeroed", true, dlogits, probs, targets, B, T, V);
 }
 
 int ugk_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,

@@ -198,7 +198,8 @@ int noalloc_max_blocks(int C);
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V);
 int launch_crossentropy_softmax_backward(float *dlogits, const float *probs, const int *targets, int rows, int V,
-                                         float dloss);
+                                         float dloss,
+                                         bool zeroed = false);
 int launch_encoder_forward(float *out, const int *inp, const float *wte,
                            const float *wpe, int B, int T, int C);
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,

@@ -24,7 +24,8 @@ __all__ = [
     "encoder_forward", "encoder_backward", "layernorm_forward", "layernorm_backward",
     "gelu_forward", "gelu_backward", "residual_forward", "residual_backward",
     "bayes_materialize", "encoder_layernorm_forward", "residual_layernorm_forward", "layernorm_residual_backward",
-    "softmax_crossentropy", "crossentropy_softmax_backward", "bayes_sample", "bayes_backward",
+    "softmax_crossentropy", "crossentropy_softmax_backward", "crossentropy_softmax_backward_zeroed",
+    "bayes_sample", "bayes_backward",
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
@@ -83,6 +84,7 @@ _SIGS = {
     "ugk_bayes_materialize": [_fp, _fp, _fp, _fp, _sz],
     "ugk_softmax_crossentropy": [_fp, _fp, _fp, _fp, _i, _i, _i],
     "ugk_crossentropy_softmax_backward": [_fp, _fp, _fp, _i, _i, _i],
+    "ugk_crossentropy_softmax_backward_zeroed": [_fp, _fp, _fp, _i, _i, _i],
     "ugk_bayes_sample": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
     "ugk_bayes_backward": [_fp, _fp, _fp, _fp, _fp, _sz],
     "ugk_bayes_backward_philox": [_fp, _fp, _fp, _fp, _sz, _u64, _i],
@@ -305,6 +307,16 @@ def crossentropy_softmax_backward(dlogits, probs, targets, B: int, T: int, V: in
     _check_targets(targets, V, rows, "crossentropy_softmax_backward")
     _check(lib.ugk_crossentropy_softmax_backward(_ptr(dlogits, "dlogits", n, "f32"), _ptr(probs, "probs", n, "f32"),
                                                  _ptr(targets, "targets", rows, "i32"), B, T, V))
+
+
+def crossentropy_softmax_backward_zeroed(dlogits, probs, targets, B: int, T: int, V: int) -> None:
+    """crossentropy_softmax_backward for a dlogits that is zero before the call (the arms' memset of
+    the activation gradients): it is written, not read."""
+    rows, n = B * T, B * T * V
+    _check_targets(targets, V, rows, "crossentropy_softmax_backward_zeroed")
+    _check(lib.ugk_crossentropy_softmax_backward_zeroed(_ptr(dlogits, "dlogits", n, "f32"),
+                                                        _ptr(probs, "probs", n, "f32"),
+                                                        _ptr(targets, "targets", rows, "i32"), B, T, V))
 
 
 def bayes_sample(w, eps, mu, rho, n: int, seed: int, step: int) -> None:
