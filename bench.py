@@ -295,8 +295,10 @@ def main():
     step_stats = {"median": round(q(per_step, 0.5), 4), "p25": round(q(per_step, 0.25), 4),
                   "p75": round(q(per_step, 0.75), 4)}
     value = total_bytes / (ms_step * 1e-3) / 1e9
+    moved_gbs = moved_bytes / (ms_step * 1e-3) / 1e9
     log(f"bench: step {ms_step:.4f} ms (median {step_stats['median']}, host wall {wall:.4f} ms) -> {value:.1f} GB/s "
-        f"on the reference's bytes, {moved_bytes / (ms_step * 1e-3) / 1e9:.1f} GB/s moved")
+        f"({100 * value / PEAK_GBS:.1f}% of peak) on the reference's {total_bytes / 1e9:.2f} GB, {moved_gbs:.1f} GB/s "
+        f"({100 * moved_gbs / PEAK_GBS:.1f}%) on the {moved_bytes / 1e9:.2f} GB the fused sequence moves")
 
     # ---- the same step with ugk_gpt2_layers_backward_zeroed, the backward for callers that zero
     # grads_acts before it (every reference arm does): it does not read those zeros (GELU
@@ -481,14 +483,52 @@ def main():
             f"  (median of 5 batches, p25-p75 {p25 * 1e3:.2f}-{p75 * 1e3:.2f} us; {launches} launches over "
             f"{n_sets} buffer sets)")
 
+    # The encoder ops are also rated on the bytes they must move: the distinct wte rows the batch
+    # gathers or scatters into (a repeated token's row comes from cache), wpe's T rows, dout or the
+    # output once, the ids (enc_distinct_bytes). The forward lines take that as their basis (the
+    # per-element count treats every repeat of a token as a fresh row), as the config-4 lines do;
+    # the backward keeps the per-element count of the metric and gives the distinct basis beside it.
+    probe_tok = mk_enc()["inp"]
+    enc_distinct = int(torch.unique(probe_tok).numel())
+    del probe_tok
+
+    def enc_distinct_bytes(name, rows, Tn, distinct):
+        Nn = rows * C
+        if name.startswith("encoder_backward"):  # dout once, RMW of the touched wte and wpe rows, ids
+            return 4 * Nn + 8 * C * distinct + 8 * C * Tn + 4 * rows
+        extra = 4 * Nn + 8 * rows + 8 * C if name.startswith("encoder_layernorm") else 0
+        return 4 * C * (distinct + Tn) + 4 * Nn + 4 * rows + extra
+
+    def enc_record(table, name, abytes, ms, launches, n_sets, rows, Tn, distinct, extra):
+        dbytes = enc_distinct_bytes(name, rows, Tn, distinct)
+        dfrac = round(dbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)
+        afrac = round(abytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)
+        info = {"distinct_tokens": distinct, "bytes_algorithmic": abytes, "frac_algorithmic": afrac,
+                "bytes_distinct": dbytes, "frac_distinct": dfrac, **extra}
+        if name.startswith("encoder_backward"):
+            record(table, name, abytes, ms, launches, n_sets, info)
+        else:
+            record(table, name, dbytes, ms, launches, n_sets,
+                   {**info, "bytes_basis": "distinct wte rows + wpe rows + out + ids"})
+        log(f"bench: {'':34s} {100 * dfrac:5.1f}% of peak on the {dbytes / 1e6:.1f} MB it must move "
+            f"({distinct} distinct tokens), {100 * afrac:5.1f}% on the per-element count")
+
     kernels, mean_ms = {}, {}
     for name, (make, set_bytes, fn) in plan.items():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
         mean_ms[name] = ms
-        record(kernels, name, per[name], ms, launches, n_sets, {"per_step": count[name]})
+        if name.startswith("encoder"):
+            enc_record(kernels, name, per[name], ms, launches, n_sets, B * T, T, enc_distinct,
+                       {"per_step": count[name]})
+        else:
+            record(kernels, name, per[name], ms, launches, n_sets, {"per_step": count[name]})
     for name, (make, set_bytes, nbytes, fn) in fused_plan.items():
         ms, launches, n_sets = time_cold(make, set_bytes, fn)
-        record(kernels, name, nbytes, ms, launches, n_sets, {"per_step": 1 if name.startswith("encoder") else 2 * L})
+        extra = {"per_step": 1 if name.startswith("encoder") else 2 * L}
+        if name.startswith("encoder"):
+            enc_record(kernels, name, nbytes, ms, launches, n_sets, B * T, T, enc_distinct, extra)
+        else:
+            record(kernels, name, nbytes, ms, launches, n_sets, extra)
     # materialize over the reference's own untied layout at this shape (it stores
     # the head weight and bias, gpt2_kernels.cuh:681-683): all P parameters
     ms, launches, n_sets = time_cold(lambda: {"mu": rnd(P) * 0.02, "rho": rnd(P) * 0.1 - 5.0, "eps": rnd(P),
@@ -593,15 +633,10 @@ def main():
                 P_(d["out"]), P_(d["inp"]), P_(d["wte"]), P_(d["wpe"]), B2, T2, C)))
             # bytes and frac on those distinct rows (a frequent token's repeats are cache hits, so
             # the per-element count would exceed the HBM peak); the per-element count beside them
-            dbytes = 4 * C * (distinct + T2) + 4 * N4 + 4 * R2
-            abytes = 12 * N4 + 4 * R2
-            record(configs, f"cfg4 {law} encoder_forward", dbytes, ms, l_, k_,
-                   {"distinct_tokens": distinct, "bytes_basis": "distinct wte rows + wpe rows + out + ids",
-                    "bytes_algorithmic": abytes,
-                    "frac_algorithmic": round(abytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)})
+            enc_record(configs, f"cfg4 {law} encoder_forward", 12 * N4 + 4 * R2, ms, l_, k_, R2, T2, distinct, {})
             ms, l_, k_ = time_cold(mk_enc4, 16 * N4, lambda d: chk(lib.ugk_encoder_backward(
                 P_(d["wte"]), P_(d["wpe"]), P_(d["dout"]), P_(d["inp"]), B2, T2, C)))
-            record(configs, f"cfg4 {law} encoder_backward", 20 * N4 + 4 * R2, ms, l_, k_)
+            enc_record(configs, f"cfg4 {law} encoder_backward", 20 * N4 + 4 * R2, ms, l_, k_, R2, T2, distinct, {})
 
     # ---- the posterior update around the layer kernels, over the same n (not part of the step)
     posterior = {}
@@ -634,6 +669,16 @@ def main():
         for nm, nb, fn in post_plan:
             ms, l_, k_ = time_cold(mk_post, 44 * n, fn)
             record(posterior, nm, nb * n, ms, l_, k_)
+        # the Philox ops with the glibc-exact softplus/sigmoid (ugk_set_philox_exact(1)), beside the
+        # default hardware-transcendental form timed above
+        ugk.set_philox_exact(True)
+        try:
+            for nm, nb, fn in post_plan:
+                if nm in ("bayes_sample", "bayes_backward_philox", "bbb_step_fused"):
+                    ms, l_, k_ = time_cold(mk_post, 44 * n, fn)
+                    record(posterior, f"{nm} (glibc-exact softplus/sigmoid)", nb * n, ms, l_, k_)
+        finally:
+            ugk.set_philox_exact(False)
         kl_out = ctypes.c_double(0.0)
         ms, l_, k_ = time_cold(mk_post, 44 * n, lambda d: chk(lib.ugk_kl_forward(
             ctypes.byref(kl_out), P_(d["mu"]), P_(d["rho"]), n, 0.1)))

@@ -31,7 +31,9 @@
  * a region on the first call that needs it and grows it, after waiting for
  * the device, when a larger shape arrives; ugk_reserve / ugk_reserve_config
  * allocate everything up front, after which calls at those shapes neither
- * allocate nor wait. A caller that owns all device memory (as the reference's
+ * allocate nor wait. A call under HIP graph capture that would have to
+ * allocate fails with UGK_ENOMEM before launching anything (reserve first, or
+ * make one call at that shape outside the capture). A caller that owns all device memory (as the reference's
  * arms do) sizes a workspace with ugk_workspace_bytes and hands it over with
  * ugk_set_workspace; the library then never allocates. The workspace is used
  * in stream order: ugk_set_stream waits for the work already queued on the
@@ -61,13 +63,30 @@ int ugk_encoder_forward(float *out, const int *inp, const float *wte,
 
 /* train_bnn.c:647-662 / gpt2_kernels.cuh:254-263 (k_encoder_backward).
  * dwte[inp[b,t],:] += dout[b,t,:];  dwpe[t,:] += dout[b,t,:].
- * Each row's contributions are added in ascending (b,t) order, the order of
- * the CPU loop, so the result is deterministic and bit-identical to it. Rows
- * with a negative token are skipped. Its bucket table lives in the workspace
+ * dwpe, and every wte row that at most 32 rows of a 65,536-row chunk add
+ * into, take their rows in ascending (b,t) order, the order of the CPU loop,
+ * bit-identical to it. A token with more rows in a chunk is added in blocks
+ * (the default; see ugk_set_encoder_exact): its rows, ascending, in blocks of
+ * 64, each block added in row order (the first onto dwte's value, the others
+ * from zero), then the block sums in block order. That is deterministic (the
+ * same bits on every run) and, up to 64 rows, the CPU's order too. Rows with
+ * a negative token are skipped. Its bucket table lives in the workspace
  * and every call leaves it cleared, on the device, so the calls may be
- * captured in a HIP graph and replayed any number of times. */
+ * captured in a HIP graph and replayed any number of times. New workspace
+ * memory is cleared by ugk_set_workspace and ugk_reserve_config, or else by
+ * the first call; that first call, if made under graph capture, is refused
+ * (UGK_EINVAL) rather than leave the clearing inside the graph alone. */
 int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout,
                          const int *inp, int B, int T, int C);
+
+/* The order of the encoder backward's adds for a token with more than 32 rows
+ * in a chunk, for later calls from any thread: 0 (the default) in 64-row
+ * blocks as above (on the float4 path with C <= 2,048; elsewhere always 1);
+ * nonzero one add per row in ascending order, bit-identical to train_bnn.c,
+ * a serial chain as long as the token's rows. No counterpart in the
+ * reference, whose GPU kernel adds with atomicAdd in no fixed order. */
+int ugk_set_encoder_exact(int exact);
+int ugk_get_encoder_exact(void);
 
 /* train_bnn.c:81-115 / gpt2_kernels.cuh:265-288 (k_layernorm_forward).
  * eps = 1e-5; writes out (B,T,C), mean (B,T), rstd (B,T). */
@@ -189,6 +208,18 @@ int ugk_crossentropy_softmax_backward_zeroed(float *dlogits, const float *probs,
                                              const int *targets, int B, int T,
                                              int V);
 
+/* Form of the softplus and sigmoid inside the ops that draw eps on the device
+ * (ugk_bayes_sample, ugk_bayes_backward_philox, ugk_bbb_step_fused), for
+ * later calls from any thread: 0 (the default) the hardware-transcendental
+ * forms (2^x, log2 and reciprocal instructions; within a few ulp of glibc's
+ * and within 1e-6 absolute / 1e-5 relative of train_bnn.c:814-822 on every
+ * float input), nonzero the glibc-exact forms of the eps-taking ops, with which
+ * each Philox op equals its eps-taking twin fed the same eps bit for bit. The
+ * eps draw itself is the same in both. No counterpart in the reference, whose
+ * GPU arms build these ops with --use_fast_math (Makefile:13). */
+int ugk_set_philox_exact(int exact);
+int ugk_get_philox_exact(void);
+
 /* ---- the posterior update around the layer kernels ----------------------
  * Flat parameter vectors of n floats. The ops that take eps are
  * bit-identical to train_bnn.c. The *_philox ops draw
@@ -262,8 +293,24 @@ void *ugk_get_stream(void);
 int ugk_reserve(int rows, int C);
 /* Bytes of workspace held on the current device (the caller's, if set). */
 size_t ugk_scratch_bytes(void);
-/* Wait for all work queued on the library's stream. */
+/* Wait for all work queued on the library's stream. Then reports, as
+ * UGK_EINVAL naming the op, an id that ugk_ids_guard found out of range since
+ * the last report (and clears that record). */
 int ugk_synchronize(void);
+/* The device-side id check of bindings that cannot trust their callers' ids
+ * (no counterpart in the reference, where 0 <= id < V is the caller's
+ * contract and is not checked). Each of the n ids outside [0, bound) is
+ * replaced IN PLACE by fill (ids in range are not written), and `code` (> 0,
+ * one of UGK_IDS_*) is recorded in a per-device word that the next
+ * ugk_synchronize reports. Asynchronous and allocation-free (it may be
+ * captured in a graph); the op called next with the same ids can then no
+ * longer index outside its table. */
+#define UGK_IDS_ENCODER_FORWARD 1
+#define UGK_IDS_ENCODER_BACKWARD 2
+#define UGK_IDS_ENCODER_LAYERNORM_FORWARD 3
+#define UGK_IDS_SOFTMAX_CROSSENTROPY 4
+#define UGK_IDS_CROSSENTROPY_BACKWARD 5
+int ugk_ids_guard(int *ids, int n, int bound, int fill, int code);
 /* Library version, major*10000 + minor*100 + patch. */
 int ugk_version(void);
 
@@ -285,7 +332,9 @@ int ugk_version(void);
  * expf of the softmax and softplus, for x <= 88.72 (finite results) and NaN,
  * against expf; 64 and 65 the default GELU and its derivative (logistic
  * form) against fn 8 and 9's glibc-exact expressions, counting results
- * outside |a - b| <= 1e-6 + 1e-5 |b|. */
+ * outside |a - b| <= 1e-6 + 1e-5 |b|; 66 and 67 the hardware-transcendental
+ * softplus and sigmoid of the Philox ops (their default form) against the
+ * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise. */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line
@@ -299,6 +348,11 @@ int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
  * transform calls them), 7 sqrtf, 8 GELU, 9 GELU derivative; 10+s, 20+s,
  * 30+s tanhf, log1pf, expm1f with division sequence s. */
 int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n);
+/* For fn 63-67: the largest distance in ulp between the kernels' form and
+ * its reference over the same inputs (NaN against NaN 0, NaN against a
+ * number 2^32 - 1), and the input pattern where it occurs. Synchronous. */
+int ugk_diag_math_ulp(int fn, unsigned lo, unsigned long long count, unsigned *max_ulp,
+                      unsigned *at);
 /* Philox4x32-10 on the device: in holds n tuples of 6 words (counter c0..c3,
  * key k0, k1), out receives n x 4 output words. */
 int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n);
@@ -310,6 +364,22 @@ int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n);
  * kernel's size, takes the best shape, and reports how close the kernel comes
  * to what its access pattern allows. Asynchronous. */
 int ugk_diag_stream(float *buf, size_t n, int nr, int nw, int per_thread, int block);
+/* The partial rows (workgroups) a LayerNorm backward of rows x C writes
+ * (fused: the LayerNorm -> residual pair), and the bound the workspace's
+ * LayerNorm slots are sized by, which covers every call with at most `rows`
+ * rows. Host arithmetic only; no HIP call. */
+int ugk_diag_layernorm_partial_rows(int rows, int C, int fused, int *actual, int *bound);
+/* How the per-op LayerNorm backward entry points (ugk_layernorm_backward,
+ * ugk_layernorm_residual_backward, ugk_layernorm_backward_noalloc) finish
+ * their dweight/dbias column sums on the float4 path: on 0 (the default) a
+ * second launch adds the partial rows; on 1 the main launch's workgroups add
+ * them themselves, the last of each group of rows and then the last group,
+ * through device-scope stores and loads and a counter, without an L2
+ * write-back. Both add in the same order and give the same bits; the second
+ * launch is the faster on MI355X (the in-launch form's chain of dependent
+ * device-scope round trips costs more than the launch). on < 0 only
+ * queries. Returns the previous setting. */
+int ugk_diag_layernorm_tail(int on);
 
 /* ---- GPT-2 layer-kernel step driver ------------------------------------
  * gpt2_kernels.cuh:634-719 (Config, param_offsets, act_offsets) and the

@@ -157,3 +157,33 @@ def test_stream_roundtrip():
     assert ugk.lib.ugk_set_stream(None) == 0
     assert ugk.lib.ugk_get_stream() in (None, 0)
     assert ugk.version() >= 100
+
+
+def test_layernorm_workspace_bound_covers_smaller_calls():
+    """The LayerNorm slot of the workspace is sized by a bound on the partial rows that holds for
+    every call with at most the config's rows (a path's own count drops once a call would exceed its
+    cap, so sizing by the count at the config's rows alone left some smaller calls short)."""
+    import ugk
+    a, b = ctypes.c_int(0), ctypes.c_int(0)
+
+    def rows_of(rows, C, fused):
+        assert ugk.lib.ugk_diag_layernorm_partial_rows(rows, C, fused, ctypes.byref(a), ctypes.byref(b)) == 0
+        return a.value, b.value
+
+    for C in (4, 13, 384, 516, 766, 768, 772, 1024, 1030, 2048, 2052):
+        for cfg_rows in (64, 1000, 2048, 3072, 4000, 4096, 5120, 8192, 12288, 16384, 40000):
+            bound = rows_of(cfg_rows, C, 0)[1]
+            for rows in sorted({1, 2, 15, 16, 17, 255, 256, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8192, 8193,
+                                16383, 16384, 16385, cfg_rows // 3, cfg_rows // 2, cfg_rows - 1, cfg_rows}):
+                if 0 < rows <= cfg_rows:
+                    for fused in (0, 1):
+                        actual, request = rows_of(rows, C, fused)
+                        # what the call runs with, and what it asks the workspace for
+                        assert actual <= request <= bound, (C, cfg_rows, rows, fused, actual, request, bound)
+    # the case that failed: sized for B=5, T=1024 at C=768, called at B=4 (and B=3)
+    bound = rows_of(5 * 1024, 768, 0)[1]
+    assert rows_of(4 * 1024, 768, 0)[0] <= bound and rows_of(3 * 1024, 768, 1)[0] <= bound
+    # and the workspace grows with the rows it is sized for
+    sizes = [ugk.workspace_bytes(ugk.Config(B=B, T=1024, C=768, V=50257, NH=12, maxT=1024, L=12))
+             for B in range(1, 17)]
+    assert sizes == sorted(sizes)

@@ -128,9 +128,11 @@ def test_softmax_loss_at_row_edges(gpu, oracle, V):
 def test_softmax_ragged_and_empty(gpu):
     t = torch.zeros(8, device=DEV)
     gpu.softmax_crossentropy(t, t, t, torch.zeros(4, dtype=torch.int32, device=DEV), 0, 4, 2)  # B = 0
-    with pytest.raises(ValueError):
-        gpu.softmax_crossentropy(torch.empty(2, device=DEV), torch.empty(8, device=DEV), torch.zeros(8, device=DEV),
-                                 torch.tensor([0, 4], dtype=torch.int32, device=DEV), 1, 2, 4)  # target 4 >= V
+    # target 4 >= V: replaced on the device and reported by the next synchronize
+    gpu.softmax_crossentropy(torch.empty(2, device=DEV), torch.empty(8, device=DEV), torch.zeros(8, device=DEV),
+                             torch.tensor([0, 4], dtype=torch.int32, device=DEV), 1, 2, 4)
+    with pytest.raises(gpu.UgkError):
+        gpu.synchronize()
 
 
 def test_full_cfg5_head(gpu, oracle):

@@ -8,8 +8,14 @@ The Philox ops split into an exact part and a float part:
     Random123 known-answer vectors and the oracle;
   * the Box-Muller transform calls the device logf and cosf. Over every u01 value the stream can
     produce (all 79,691,777 of them) both stay within 2 ulp of the host glibc; eps is then within
-    8 ulp of the oracle's, and everything downstream of eps is bit-exact given the device's eps
-    (each Philox op equals its eps-taking twin fed with the eps the device drew).
+    8 ulp of the oracle's;
+  * with ugk_set_philox_exact(1), everything downstream of eps is bit-exact given the device's eps
+    (each Philox op equals its eps-taking twin fed with the eps the device drew);
+  * by default the Philox ops take their softplus and sigmoid in the hardware-transcendental form,
+    which is within the literal bar |a - b| <= 1e-6 + 1e-5 |b| of the glibc-exact form on every
+    float input (exhaustive, below); downstream of eps they are held to the bar that follows from
+    it (the form's bar times |eps| or |dw eps|, plus the rounding of the products and sums), and
+    the fused step equals the composition of the unfused ops in the same form bit for bit.
 """
 import ctypes
 import ctypes.util
@@ -116,6 +122,30 @@ def test_device_sqrtf_is_correctly_rounded_everywhere(gpu, oracle):
     assert_bits(host(out), oracle.sqrtf(x), "sqrtf vs host")
 
 
+@pytest.fixture
+def philox_exact(gpu):
+    """The glibc-exact softplus/sigmoid in the Philox ops for the duration of a test."""
+    gpu.set_philox_exact(True)
+    try:
+        yield
+    finally:
+        gpu.set_philox_exact(False)
+
+
+@pytest.mark.parametrize("fn", ["softplus_fast", "sigmoid_fast"])
+def test_fast_transcendentals_exhaustive(gpu, fn):
+    """The Philox ops' default softplus and sigmoid against the glibc-exact forms (train_bnn.c:814-816,
+    :820-822) on all 2^32 float inputs: none outside the literal bar, and none more than 8 ulp away
+    (the largest distance found is 5 ulp for both)."""
+    assert not gpu.philox_exact()  # the default form
+    n, first = gpu.diag_math_mismatch(fn)
+    assert n == 0, (fn, n, hex(first))
+    d, at = gpu.diag_math_ulp(fn)
+    x = np.array([at], np.uint32).view(np.float32)[0]
+    print(f"{fn}: 0 inputs outside the literal bar; at most {d} ulp from the glibc-exact form (at x = {x!r})")
+    assert d <= 8, (fn, d, hex(at))  # 5 on MI355X
+
+
 # ---- the ops ----------------------------------------------------------------------------
 
 SIZES = [1, 3, 5, 4096 + 3, (1 << 20) + 1]
@@ -207,7 +237,7 @@ def test_kl_forward_terms(gpu, oracle):
 
 @pytest.mark.parametrize("n", SIZES)
 @pytest.mark.parametrize("offset", [0, 1])
-def test_bayes_sample_and_backward_philox(gpu, oracle, n, offset):
+def test_bayes_sample_and_backward_philox(gpu, oracle, philox_exact, n, offset):
     seed, step = 0x1234_5678_9ABC, 17
     mu, rho, dw, _, _, _ = posterior_inputs(930 + n, n)
     big = lambda a: dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
@@ -233,7 +263,7 @@ def test_bayes_sample_and_backward_philox(gpu, oracle, n, offset):
 
 @pytest.mark.parametrize("klw", [0.0, 1.0 / 300000.0])
 @pytest.mark.parametrize("n,offset", [(5, 0), (4096 + 3, 1), ((1 << 20) + 1, 0)])
-def test_bbb_step_fused(gpu, oracle, klw, n, offset):
+def test_bbb_step_fused(gpu, oracle, philox_exact, klw, n, offset):
     seed, step = 77, 12
     sp, lr, b1, b2, aeps, wd = 0.1, 3e-4, 0.9, 0.999, 1e-8, 0.0
     mu, rho, dw, _, m, v = posterior_inputs(940 + n, n)
@@ -268,7 +298,7 @@ def test_bbb_step_fused(gpu, oracle, klw, n, offset):
         assert np.allclose(host(a), b, rtol=1e-5, atol=1e-7 * float(np.abs(b).max())), name
 
 
-def test_full_cfg5_bayes_sample(gpu, oracle):
+def test_full_cfg5_bayes_sample(gpu, oracle, philox_exact):
     """The sample at GPT-2-124M size: indices up to 124M map to the oracle's stream."""
     n, seed, step = CFG5_N, 0xC0FFEE, 3
     g = gen.rng(950)
@@ -288,3 +318,95 @@ def test_full_cfg5_bayes_sample(gpu, oracle):
     assert_bits(host(w[ti]), w_ref, "cfg5 w (sampled)")
     mean, var = float(eps.double().mean()), float(eps.double().var())
     assert abs(mean) < 5.0 / np.sqrt(n) and abs(var - 1.0) < 5.0 * np.sqrt(2.0 / n), (mean, var)
+
+
+# ---- the default (hardware-transcendental) form of the Philox ops ------------------------
+
+EPS32 = float(np.finfo(np.float32).eps)
+
+
+def oracle_softplus_sigmoid(oracle, rho):
+    """softplus(rho) and sigmoid(rho) as train_bnn.c computes them (materialize with mu = 0, eps = 1;
+    bayes_backward with dw = eps = 1 from zero)."""
+    n = rho.size
+    one, zero = np.ones(n, np.float32), np.zeros(n, np.float32)
+    sp = np.zeros(n, np.float32)
+    oracle.bayes_materialize(sp, zero, rho, one, n)
+    dmu, sg = zero.copy(), zero.copy()
+    oracle.bayes_backward(dmu, sg, one, one, rho, n)
+    return sp.astype(np.float64), sg.astype(np.float64)
+
+
+def assert_within(got, want, bar, what):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    bad = ~((np.abs(got - want) <= bar) | (np.isnan(got) & np.isnan(want)) | (got == want))
+    if bad.any():
+        i = int(np.argmax(bad))
+        raise AssertionError(f"{what}: {int(bad.sum())} of {got.size} outside the bar; first at {i}: "
+                             f"gpu {got[i]!r} want {want[i]!r} bar {bar.flat[i] if np.ndim(bar) else bar!r}")
+
+
+@pytest.mark.parametrize("n", [5, 4096 + 3, (1 << 20) + 1])
+def test_bayes_sample_and_backward_philox_fast(gpu, oracle, n):
+    """w = mu + softplus(rho) eps and drho += dw eps sigmoid(rho) with the fast forms, against the
+    oracle's eps-taking ops fed with the device's eps, within the bar the forms' own bar implies;
+    rho spans the special values as well as the benchmark's -5 +- 0.1."""
+    seed, step = 0x1234_5678_9ABC, 17
+    mu, rho, dw, _, _, _ = posterior_inputs(960 + n, n)
+    sp_ = gen.special_floats()
+    rho[: min(n, sp_.size)] = sp_[: min(n, sp_.size)]
+    t_mu, t_rho, t_dw = dev(mu), dev(rho), dev(dw)
+    t_w, t_eps = torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+    gpu.bayes_sample(t_w, t_eps, t_mu, t_rho, n, seed, step)
+    eps = host(t_eps)
+    assert_eps_close(eps, oracle.philox_normal_n(n, seed, step), f"eps n={n} (fast form)")
+    w_ref = np.zeros(n, np.float32)
+    oracle.bayes_materialize(w_ref, mu, rho, eps, n)
+    sp, sg = oracle_softplus_sigmoid(oracle, rho)
+    e64, m64, w64 = eps.astype(np.float64), mu.astype(np.float64), w_ref.astype(np.float64)
+    # |sp_fast - sp| <= 1e-6 + 1e-5 sp, times |eps|, plus one rounding of the product and one of the sum
+    bar = np.abs(e64) * (1e-6 + 1e-5 * sp) + EPS32 * (np.abs(sp * e64) + np.abs(w64)) + 1e-45
+    assert_within(host(t_w), w_ref, bar, "bayes_sample w (fast form)")
+    dmu0, drho0 = gen.normal(gen.rng(5), (n,), 0, 1e-3), gen.normal(gen.rng(6), (n,), 0, 1e-3)
+    t_dmu, t_drho = dev(dmu0), dev(drho0)
+    gpu.bayes_backward_philox(t_dmu, t_drho, t_dw, t_rho, n, seed, step)
+    dmu, drho = dmu0.copy(), drho0.copy()
+    oracle.bayes_backward(dmu, drho, dw, eps, rho, n)
+    assert_bits(host(t_dmu), dmu, "bayes_backward_philox dmu (no transcendental)")
+    g64 = np.abs(dw.astype(np.float64) * e64)
+    bar = g64 * (1e-6 + 1e-5 * sg) + EPS32 * (2 * g64 * sg + np.abs(drho.astype(np.float64))) + 1e-45
+    assert_within(host(t_drho), drho, bar, "bayes_backward_philox drho (fast form)")
+
+
+@pytest.mark.parametrize("klw", [0.0, 1.0 / 300000.0])
+def test_bbb_step_fused_fast(gpu, oracle, klw):
+    """The fused step in the fast form equals the device's unfused sequence in the same form bit for
+    bit when it has no KL term (bayes_backward_philox, two adamw_update, bayes_sample at step + 1);
+    with the KL term, whose standalone op keeps the glibc-exact form, it is compared with the
+    oracle's fused step as the exact form is (mu exactly; rho and the rho moments within 1e-5)."""
+    n, seed, step = 4096 + 3, 77, 12
+    sp, lr, b1, b2, aeps, wd = 0.1, 3e-4, 0.9, 0.999, 1e-8, 0.0
+    mu, rho, dw, _, m, v = posterior_inputs(970, n)
+    state = [mu, rho, m, v, (m * 0.5).astype(np.float32), (v * 0.25).astype(np.float32)]
+    bc1, bc2 = bias_corrections(b1, b2, step)
+    f = [dev(a) for a in state]
+    f_w, f_dw = torch.zeros(n, device=DEV), dev(dw)
+    gpu.bbb_step_fused(*f, f_w, f_dw, n, seed, step, sp, klw, float(bc1), float(bc2), lr, b1, b2, aeps, wd)
+    assert (host(f_dw) == 0).all()
+    if klw == 0.0:
+        c_mu, c_rho, c_m1, c_v1, c_m2, c_v2 = (dev(a) for a in state)
+        g_mu, g_rho = torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+        gpu.bayes_backward_philox(g_mu, g_rho, dev(dw), c_rho, n, seed, step)
+        gpu.adamw_update(c_mu, g_mu, c_m1, c_v1, n, step, lr, b1, b2, aeps, wd)
+        gpu.adamw_update(c_rho, g_rho, c_m2, c_v2, n, step, lr, b1, b2, aeps, wd)
+        c_w = torch.zeros(n, device=DEV)
+        gpu.bayes_sample(c_w, None, c_mu, c_rho, n, seed, step + 1)
+        names = ("mu", "rho", "m_mu", "v_mu", "m_rho", "v_rho", "w")
+        for name, a, b in zip(names, f + [f_w], [c_mu, c_rho, c_m1, c_v1, c_m2, c_v2, c_w]):
+            assert_bits(host(a), host(b), f"fused vs unfused {name} (fast form)")
+    o = [a.copy() for a in state]
+    o_w, o_dw = np.zeros(n, np.float32), dw.copy()
+    oracle.bbb_step_fused(*o, o_w, o_dw, n, seed, step, sp, klw, bc1, bc2, lr, b1, b2, aeps, wd)
+    assert_bits(host(f[0]), o[0], "fused mu vs oracle (fast form)")
+    for name, a, b in zip(("rho", "m_rho", "v_rho"), (f[1], f[4], f[5]), (o[1], o[4], o[5])):
+        assert np.allclose(host(a), b, rtol=1e-5, atol=1e-7 * float(np.abs(b).max())), name

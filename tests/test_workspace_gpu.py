@@ -2,7 +2,8 @@
 
 * The encoder backward keeps no state on the host: one call captured in a HIP graph and replayed
   three times (an odd number, with eager calls on other buffers in between) accumulates exactly
-  what three calls of train_bnn.c's encoder_backward (:647-662) accumulate.
+  what three calls of train_bnn.c's encoder_backward (:647-662) accumulate (exact mode), or three
+  of its blocked order (the default).
 * A caller-owned workspace (ugk_set_workspace, sized by ugk_workspace_bytes) gives results
   identical to the library-owned regions; a shape beyond the config it was sized for is refused
   with UGK_ENOMEM; NULL returns to library-owned regions.
@@ -14,7 +15,7 @@ import pytest
 import torch
 
 import gen
-from test_parity_gpu import assert_bits, dev, host
+from test_parity_gpu import assert_bits, blocked_encoder_backward, dev, encoder_mode, host
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -39,7 +40,16 @@ def enc_case(g, B, T, C, V, hot):
     return (inp, gen.normal(g, (B * T * C,)), gen.normal(g, (V * C,), 0, 0.02), gen.normal(g, (T * C,), 0, 0.01))
 
 
-def test_encoder_backward_graph_replays(gpu, oracle, lib_stream):
+@pytest.mark.parametrize("exact", [True, False])
+def test_encoder_backward_graph_replays(gpu, oracle, lib_stream, exact):
+    with encoder_mode(gpu, exact):
+        graph_replays(gpu, oracle, lib_stream, exact)
+
+
+def graph_replays(gpu, oracle, lib_stream, exact):
+    """Exact mode: the CPU's order (oracle); blocked mode: its numpy restatement (test_parity_gpu),
+    whose per-(bucket, slice) counters must also return to zero within each replay."""
+    backward = oracle.encoder_backward if exact else blocked_encoder_backward
     B, T, C, V = 4, 64, 384, 1000
     g = gen.rng(2718)
     inp, dout, dwte0, dwpe0 = enc_case(g, B, T, C, V, hot=100)
@@ -63,12 +73,12 @@ def test_encoder_backward_graph_replays(gpu, oracle, lib_stream):
         s.synchronize()
     want_wte, want_wpe = dwte0.copy(), dwpe0.copy()
     for _ in range(3):
-        oracle.encoder_backward(want_wte, want_wpe, dout, inp, B, T, C)
+        backward(want_wte, want_wpe, dout, inp, B, T, C)
     assert_bits(host(t_dwte), want_wte, "dwte after 3 replays")
     assert_bits(host(t_dwpe), want_wpe, "dwpe after 3 replays")
     want2_wte, want2_wpe = dwte2.copy(), dwpe2.copy()
     for _ in range(4):
-        oracle.encoder_backward(want2_wte, want2_wpe, dout2, inp2, B, T, C)
+        backward(want2_wte, want2_wpe, dout2, inp2, B, T, C)
     assert_bits(host(e_dwte), want2_wte, "dwte of the eager calls between replays")
     assert_bits(host(e_dwpe), want2_wpe, "dwpe of the eager calls between replays")
 
@@ -174,3 +184,69 @@ def test_op_timer_records_the_driver_sequence(gpu, C, NH, L):
     # stopped: a further step records nothing
     gpu.gpt2_layers_forward(acts, params, inp, cfg)
     assert gpu.op_timer_read(256) == []
+
+
+def test_workspace_sized_for_more_rows_serves_fewer(gpu):
+    """A caller-owned workspace sized for B=5, T=1024, C=768 serves every workspace user at B=4 and
+    B=3 (the LayerNorm slots are sized by a bound that holds for every smaller call), with results
+    identical to the library-owned regions."""
+    cfg = gpu.Config(B=5, T=1024, C=768, V=1000, NH=12, maxT=1024, L=2)
+    small = [gpu.Config(B=B, T=1024, C=768, V=1000, NH=12, maxT=1024, L=2) for B in (4, 3)]
+    gpu.set_workspace(None, cfg)
+    want = [run_ops(gpu, c, seed=40 + k) for k, c in enumerate(small)]
+    nbytes = gpu.workspace_bytes(cfg)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=DEV)
+    off = (-ws.data_ptr()) % 256
+    try:
+        gpu.set_workspace(ws[off:off + nbytes], cfg)
+        del ws  # the binding keeps the workspace alive while the library uses it
+        torch.cuda.empty_cache()
+        for k, c in enumerate(small):
+            got, kl = run_ops(gpu, c, seed=40 + k)
+            assert kl == want[k][1]
+            for j, (a, b) in enumerate(zip(got, want[k][0])):
+                assert torch.equal(a.view(torch.int32), b.view(torch.int32)), f"B={c.B}: output {j} differs"
+    finally:
+        gpu.set_workspace(None, cfg)
+
+
+def test_encoder_backward_capture_needs_prepared_state(gpu, oracle, lib_stream):
+    """The encoder backward's state must be allocated and cleared outside a graph capture: with the
+    library's regions just freed, a first call under capture is refused before it launches anything;
+    after ugk_set_workspace (which clears the state at once) a first call may be captured, and its
+    replays accumulate what the oracle's calls do."""
+    B, T, C, V = 4, 64, 384, 1000
+    cfg = gpu.Config(B=B, T=T, C=C, V=V, NH=6, maxT=T, L=1)
+    g = gen.rng(1618)
+    inp, dout, dwte0, dwpe0 = enc_case(g, B, T, C, V, hot=70)
+    s = lib_stream
+    t_inp, t_dout, t_dwte, t_dwpe = dev(inp), dev(dout), dev(dwte0), dev(dwpe0)
+    gpu.set_workspace(None, cfg)  # frees the library-owned regions
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        with pytest.raises(gpu.UgkError) as err:
+            gpu.encoder_backward(t_dwte, t_dwpe, t_dout, t_inp, B, T, C)
+    assert err.value.status == 3 and "capture" in str(err.value)
+    del graph
+    assert_bits(host(t_dwte), dwte0, "dwte untouched by the refused call")
+    nbytes = gpu.workspace_bytes(cfg)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=DEV)
+    off = (-ws.data_ptr()) % 256
+    try:
+        gpu.set_workspace(ws[off:off + nbytes], cfg)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):  # the first call on this workspace, captured
+            gpu.encoder_backward(t_dwte, t_dwpe, t_dout, t_inp, B, T, C)
+        for _ in range(2):
+            graph.replay()
+            torch.cuda.synchronize()
+        want_wte, want_wpe = dwte0.copy(), dwpe0.copy()
+        for _ in range(2):  # the default (blocked) order: a token of 70 rows
+            blocked_encoder_backward(want_wte, want_wpe, dout, inp, B, T, C)
+        assert_bits(host(t_dwte), want_wte, "dwte after 2 replays of a first call")
+        assert_bits(host(t_dwpe), want_wpe, "dwpe after 2 replays of a first call")
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        gpu.set_workspace(None, cfg)

@@ -58,7 +58,7 @@ void region_sizes(const ugk_config &cfg, size_t out[kNumRegions]) {
   const int rows = cfg.B * cfg.T;
   const size_t slot = align_up(layernorm_backward_scratch(rows, cfg.C));
   out[kRegLn] = slot * (size_t)(2 * (cfg.L > 0 ? cfg.L : 0) + 1);
-  out[kRegEncoder] = encoder_backward_scratch();
+  out[kRegEncoder] = encoder_backward_scratch(cfg.C);
   out[kRegKl] = kl_forward_scratch();
   out[kRegSoftmax] = softmax_scratch(rows, cfg.V);
 }
@@ -120,7 +120,16 @@ int check_launch(const char *what) {
   return UGK_OK;
 }
 
-void *workspace(Region r, size_t bytes, bool *fresh) {
+bool stream_capturing() {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream(), &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
+void *workspace(Region r, size_t bytes, bool *fresh, bool keep_fresh) {
   const int dev = current_device("workspace");
   if (dev < 0) {
     set_error(UGK_EHIP, "workspace: hipGetDevice failed");
@@ -139,12 +148,20 @@ void *workspace(Region r, size_t bytes, bool *fresh) {
     }
     p = w.user + w.off[r];
   } else {
+    if (!(w.own[r] && w.own_bytes[r] >= bytes) && stream_capturing()) {
+      // hipMalloc (and the wait before a regrowth) cannot be part of a graph
+      set_error(UGK_ENOMEM,
+                "workspace: the %s need %zu bytes, which must be allocated before graph capture "
+                "(ugk_reserve_config, ugk_set_workspace, or one call at this shape outside the capture)",
+                kRegionName[r], bytes);
+      return nullptr;
+    }
     p = own_region(w, r, bytes);
     if (!p) return nullptr;
   }
   if (fresh) {  // the fresh mark is for the region's user, not for ugk_reserve*
     *fresh = w.fresh[r];
-    w.fresh[r] = false;
+    if (!keep_fresh) w.fresh[r] = false;
   }
   return p;
 }
@@ -473,6 +490,20 @@ int ugk_set_gelu_exact(int exact) {
 
 int ugk_get_gelu_exact(void) { return gelu_exact(); }
 
+int ugk_set_philox_exact(int exact) {
+  set_philox_exact(exact);
+  return ok();
+}
+
+int ugk_get_philox_exact(void) { return philox_exact(); }
+
+int ugk_set_encoder_exact(int exact) {
+  set_encoder_exact(exact);
+  return ok();
+}
+
+int ugk_get_encoder_exact(void) { return encoder_exact(); }
+
 const char *ugk_last_error(void) { return g_err; }
 
 int ugk_set_stream(void *s) {
@@ -510,8 +541,14 @@ int ugk_reserve_config(ugk_config cfg) {
   if ((long long)cfg.B * cfg.T > INT_MAX) return bad(fn, "B*T exceeds INT_MAX");
   size_t sz[kNumRegions];
   region_sizes(cfg, sz);
-  for (int r = 0; r < kNumRegions; r++)
-    if (!workspace(static_cast<Region>(r), sz[r])) return UGK_ENOMEM;
+  for (int r = 0; r < kNumRegions; r++) {
+    bool fresh = false;
+    void *p = workspace(static_cast<Region>(r), sz[r], r == kRegEncoder ? &fresh : nullptr);
+    if (!p) return UGK_ENOMEM;
+    // the encoder backward's state is cleared now, so that its first call may be captured
+    if (fresh)
+      if (int e = launch_encoder_state_init(p)) return e;
+  }
   return ok();
 }
 
@@ -546,14 +583,61 @@ int ugk_set_workspace(void *ptr, size_t bytes, ugk_config cfg) {
     o += w.cap[r];
     w.fresh[r] = true;
   }
+  if (ptr) {  // the encoder backward's state is cleared now, so that its first call may be captured
+    if (int e = launch_encoder_state_init(w.user + w.off[kRegEncoder])) return e;
+    w.fresh[kRegEncoder] = false;
+  }
   return ok();
 }
 
 size_t ugk_scratch_bytes(void) { return workspace_bytes_current(); }
 
+namespace {
+const char *ids_op_name(int code) {
+  switch (code) {
+    case UGK_IDS_ENCODER_FORWARD: return "encoder_forward";
+    case UGK_IDS_ENCODER_BACKWARD: return "encoder_backward";
+    case UGK_IDS_ENCODER_LAYERNORM_FORWARD: return "encoder_layernorm_forward";
+    case UGK_IDS_SOFTMAX_CROSSENTROPY: return "softmax_crossentropy";
+    case UGK_IDS_CROSSENTROPY_BACKWARD: return "crossentropy_softmax_backward";
+    default: return "a guarded call";
+  }
+}
+}  // namespace
+
+int ugk_ids_guard(int *ids, int n, int bound, int fill, int code) {
+  const char *fn = "ugk_ids_guard";
+  if (n < 0 || bound < 0) return bad(fn, "n and bound must be >= 0");
+  if (code <= 0) return bad(fn, "code must be > 0");
+  if (n == 0) return ok();
+  if (!ids) return bad(fn, "NULL pointer");
+  if (int e = launch_ids_guard(ids, n, bound, fill, code)) return e;
+  return ok();
+}
+
 int ugk_synchronize(void) {
   const hipError_t e = hipStreamSynchronize(stream());
   if (e != hipSuccess) return set_error(UGK_EHIP, "ugk_synchronize: %s", hipGetErrorString(e));
+  int *word = ids_error_word();
+  if (!word) return UGK_EHIP;
+  int code = 0;
+  const int zero = 0;
+  if (hipMemcpyAsync(&code, word, sizeof code, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+      hipStreamSynchronize(stream()) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_EHIP, "ugk_synchronize: reading the id error word failed");
+  }
+  if (code != 0) {
+    if (hipMemcpyAsync(word, &zero, sizeof zero, hipMemcpyHostToDevice, stream()) != hipSuccess ||
+        hipStreamSynchronize(stream()) != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(UGK_EHIP, "ugk_synchronize: clearing the id error word failed");
+    }
+    return set_error(UGK_EINVAL,
+                     "ugk_synchronize: %s was given an id outside its table (found on the device by "
+                     "ugk_ids_guard; the out-of-range ids were replaced, so its results are not meaningful)",
+                     ids_op_name(code));
+  }
   return ok();
 }
 

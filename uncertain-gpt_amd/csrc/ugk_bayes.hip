@@ -8,6 +8,8 @@
 // square root, so every op that is given its eps is bit-identical to the CPU
 // oracle. The Philox ops draw eps on the fly (ugk_philox.h): their integer
 // stream is exact, their Box-Muller transform uses the device logf/cosf.
+#include <atomic>
+
 #include "ugk_map.h"
 #include "ugk_philox.h"
 
@@ -23,6 +25,26 @@ __device__ __forceinline__ float sigmoid_lds(float x, const uint64_t *tab) {
   return ugk_dev_recip_ge1(1.0f + expf_lds(-x, tab));
 }
 
+// The Philox ops' softplus and sigmoid: the hardware-transcendental forms by
+// default (kFast; within a few ulp of glibc's and within 1e-6 absolute / 1e-5
+// relative on every input, ugk_diag.hip fn 66 and 67), or the glibc-exact
+// forms of the eps-taking ops (bit-identical to train_bnn.c given the same
+// eps), selected by ugk_set_philox_exact.
+template <bool kFast>
+__device__ __forceinline__ float softplus_of(float x, const uint64_t *tab) {
+  if constexpr (kFast)
+    return ugk_fast_softplus(x);
+  else
+    return ugk_dev_softplusf_lds(x, tab);
+}
+template <bool kFast>
+__device__ __forceinline__ float sigmoid_of(float x, const uint64_t *tab) {
+  if constexpr (kFast)
+    return ugk_fast_sigmoid(x);
+  else
+    return sigmoid_lds(x, tab);
+}
+
 struct PhiloxParams {
   unsigned long long seed;
   int step;
@@ -30,23 +52,26 @@ struct PhiloxParams {
 
 // train_bnn_gpu.cu:93-97 (k_bayes_sample): w = mu + softplus(rho) * eps(seed,
 // step, i). Loads mu, rho.
+template <bool kFast>
 struct BayesSample : MapOp {
   static constexpr int kLoads = 2, kStores = 1;
-  static constexpr bool kTable = true;
+  static constexpr bool kTable = !kFast;
   static constexpr int kUnroll = 1;
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
-    st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * ugk_dev_philox_normal(p.seed, p.step, i);
+    st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * ugk_dev_philox_normal(p.seed, p.step, i);
   }
 };
 
 // The same draw, also storing eps (train_bnn.c:841-845's bayes_sample keeps eps
 // for the backward). Stores w, eps.
-struct BayesSampleEps : BayesSample {
+template <bool kFast>
+struct BayesSampleEps : BayesSample<kFast> {
   static constexpr int kStores = 2;
+  typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
-    st[0] = ld[0] + ugk_dev_softplusf_lds(ld[1], tab) * eps;
+    st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * eps;
     st[1] = eps;
   }
 };
@@ -65,16 +90,17 @@ struct BayesBackward : MapOp {
 
 // train_bnn_gpu.cu:99-109 (k_bayes_backward): the same with eps regenerated.
 // Loads dw, rho, dmu, drho; stores dmu, drho.
+template <bool kFast>
 struct BayesBackwardPhilox : MapOp {
   static constexpr int kLoads = 4, kStores = 2;
   static constexpr int kUnroll = 1, kThreads = 512;  // measured best of the map shapes
-  static constexpr bool kTable = true;
+  static constexpr bool kTable = !kFast;
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0];
     const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
     st[0] = ld[2] + g;
-    st[1] = ld[3] + g * eps * sigmoid_lds(ld[1], tab);
+    st[1] = ld[3] + g * eps * sigmoid_of<kFast>(ld[1], tab);
   }
 };
 
@@ -142,9 +168,10 @@ struct AdamW : MapOp {
 // and w drawn for step + 1 from the updated parameters.
 // Loads dw, rho, mu, m_mu, v_mu, m_rho, v_rho;
 // stores dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w.
+template <bool kFast>
 struct BbbStepFused : MapOp {
   static constexpr int kLoads = 7, kStores = 8;
-  static constexpr bool kTable = true;
+  static constexpr bool kTable = !kFast;
   static constexpr int kUnroll = 1;
   struct Params {
     unsigned long long seed;
@@ -155,11 +182,11 @@ struct BbbStepFused : MapOp {
   };
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0], r = ld[1], mm = ld[2];
-    const float sg = sigmoid_lds(r, tab);
+    const float sg = sigmoid_of<kFast>(r, tab);
     float gmu = g;
     float grho = g * ugk_dev_philox_normal(p.seed, p.step, i) * sg;
     if (p.klw > 0.0f) {
-      const float sigma = ugk_dev_softplusf_lds(r, tab);
+      const float sigma = softplus_of<kFast>(r, tab);
       gmu += p.klw * div_by(mm, p.sp2);
       grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
     }
@@ -173,7 +200,7 @@ struct BbbStepFused : MapOp {
     st[4] = v1;
     st[5] = m2;
     st[6] = v2;
-    st[7] = mu_new + ugk_dev_softplusf_lds(rho_new, tab) * ugk_dev_philox_normal(p.seed, p.step + 1, i);
+    st[7] = mu_new + softplus_of<kFast>(rho_new, tab) * ugk_dev_philox_normal(p.seed, p.step + 1, i);
   }
 };
 
@@ -288,14 +315,28 @@ __global__ __launch_bounds__(kBlock) void k_kl_final(double *out, const double *
 
 }  // namespace
 
-int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
-                        unsigned long long seed, int step) {
+namespace {
+std::atomic<int> g_philox_exact{0};
+}  // namespace
+
+void set_philox_exact(int exact) { g_philox_exact.store(exact ? 1 : 0); }
+int philox_exact() { return g_philox_exact.load(); }
+
+namespace {
+template <bool kFast>
+int sample(float *w, float *eps, const float *mu, const float *rho, size_t n, unsigned long long seed, int step) {
   if (eps) {
-    Streams<BayesSampleEps> s{{mu, rho}, {w, eps}, {seed, step}};
+    Streams<BayesSampleEps<kFast>> s{{mu, rho}, {w, eps}, {seed, step}};
     return run_map(s, n, "bayes_sample");
   }
-  Streams<BayesSample> s{{mu, rho}, {w}, {seed, step}};
+  Streams<BayesSample<kFast>> s{{mu, rho}, {w}, {seed, step}};
   return run_map(s, n, "bayes_sample");
+}
+}  // namespace
+
+int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
+                        unsigned long long seed, int step) {
+  return philox_exact() ? sample<false>(w, eps, mu, rho, n, seed, step) : sample<true>(w, eps, mu, rho, n, seed, step);
 }
 
 int launch_bayes_backward(float *dmu, float *drho, const float *dw, const float *eps,
@@ -306,7 +347,11 @@ int launch_bayes_backward(float *dmu, float *drho, const float *dw, const float 
 
 int launch_bayes_backward_philox(float *dmu, float *drho, const float *dw, const float *rho,
                                  size_t n, unsigned long long seed, int step) {
-  Streams<BayesBackwardPhilox> s{{dw, rho, dmu, drho}, {dmu, drho}, {seed, step}};
+  if (philox_exact()) {
+    Streams<BayesBackwardPhilox<false>> s{{dw, rho, dmu, drho}, {dmu, drho}, {seed, step}};
+    return run_map(s, n, "bayes_backward_philox");
+  }
+  Streams<BayesBackwardPhilox<true>> s{{dw, rho, dmu, drho}, {dmu, drho}, {seed, step}};
   return run_map(s, n, "bayes_backward_philox");
 }
 
@@ -328,10 +373,15 @@ int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float
                           float *w, float *dw, size_t n, unsigned long long seed, int step, float sp,
                           float klw, float bc1, float bc2, float lr, float beta1, float beta2,
                           float aeps, float wd) {
-  Streams<BbbStepFused> s{{dw, rho, mu, m_mu, v_mu, m_rho, v_rho},
-                          {dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w},
-                          {seed, step, SharedDivisor::of(sp * sp), klw,
-                           {lr, beta1, beta2, aeps, wd, SharedDivisor::of(bc1), SharedDivisor::of(bc2)}}};
+  const typename BbbStepFused<true>::Params p{
+      seed, step, SharedDivisor::of(sp * sp), klw,
+      {lr, beta1, beta2, aeps, wd, SharedDivisor::of(bc1), SharedDivisor::of(bc2)}};
+  if (philox_exact()) {
+    Streams<BbbStepFused<false>> s{{dw, rho, mu, m_mu, v_mu, m_rho, v_rho}, {dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w},
+                                   {p.seed, p.step, p.sp2, p.klw, p.adam}};
+    return run_map(s, n, "bbb_step_fused");
+  }
+  Streams<BbbStepFused<true>> s{{dw, rho, mu, m_mu, v_mu, m_rho, v_rho}, {dw, mu, rho, m_mu, v_mu, m_rho, v_rho, w}, p};
   return run_map(s, n, "bbb_step_fused");
 }
 

@@ -29,7 +29,11 @@ namespace {
 // (ugk_expf_t elsewhere; reference ugk_expf); 64 and 65: the default GELU
 // and its derivative (the logistic form, ugk_fast_gelu*) against the
 // glibc-exact expressions of fn 8 and 9, where a "mismatch" is a result
-// outside |a - b| <= 1e-6 + 1e-5 |b| (equal bits and NaN against NaN pass).
+// outside |a - b| <= 1e-6 + 1e-5 |b| (equal bits and NaN against NaN pass);
+// 66 and 67 the hardware-transcendental softplus and sigmoid of the Philox
+// ops (ugk_fast_softplus, ugk_fast_sigmoid) against the glibc-exact
+// softplus of fn 4 and train_bnn.c:820-822's 1 / (1 + expf(-x)), likewise
+// counting results outside that bar.
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -72,6 +76,8 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
                                           : ugk_expf_t<UGK_EXPF_CONTRACT>(x, UgkExp2Lds{tab});
   if (FN == 64) return ugk_fast_gelu(x);
   if (FN == 65) return ugk_fast_gelu_grad(x);
+  if (FN == 66) return ugk_fast_softplus(x);
+  if (FN == 67) return ugk_fast_sigmoid(x);
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
@@ -80,7 +86,8 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 0 || FN == 63) return ugk_expf(x);
   if (FN == 1 || (FN >= 20 && FN < 24)) return ugk_log1pf(x);
   if (FN == 3 || (FN >= 10 && FN < 14)) return ugk_tanhf(x);
-  if (FN == 4) return ugk_softplusf(x);
+  if (FN == 4 || FN == 66) return ugk_softplusf(x);
+  if (FN == 67) return 1.0f / (1.0f + ugk_expf(-x));
   if (FN == 5) return logf(x);
   if (FN == 6) return cosf(x);
   if (FN == 7) return (float)sqrt((double)x);
@@ -181,7 +188,42 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 66);
+         (fn >= 40 && fn < 68);
+}
+
+// The largest distance in ulp (as ordered integers) between the kernels' math
+// and its reference over bit patterns, packed with the input that gives it:
+// (distance << 32) | pattern, the largest pattern among ties. NaN against NaN
+// counts 0, NaN against a number 2^32 - 1.
+__device__ __forceinline__ long long ordered_bits(float v) {
+  const int i = (int)ugk_f2u(v);
+  return i < 0 ? -(long long)(i & 0x7fffffff) : (long long)i;
+}
+
+template <int FN>
+__global__ __launch_bounds__(kBlock) void k_math_ulp(unsigned long long lo, unsigned long long count,
+                                                     unsigned long long *best) {
+  __shared__ uint64_t tab[32];
+  ugk_exp2_stage(tab);
+  __syncthreads();
+  unsigned long long local = 0;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * kBlock + threadIdx.x; i < count;
+       i += (unsigned long long)gridDim.x * kBlock) {
+    const unsigned u = (unsigned)(lo + i);
+    const float x = ugk_u2f(u);
+    const float a = kernel_math<FN>(x, tab), b = reference_math<FN>(x);
+    unsigned long long d;
+    if (a != a || b != b) {
+      d = (a != a && b != b) ? 0ull : 0xffffffffull;
+    } else {
+      const long long diff = ordered_bits(a) - ordered_bits(b);
+      const unsigned long long ad = (unsigned long long)(diff < 0 ? -diff : diff);
+      d = ad > 0xffffffffull ? 0xffffffffull : ad;
+    }
+    const unsigned long long key = (d << 32) | u;
+    local = key > local ? key : local;
+  }
+  if (local) atomicMax(best, local);
 }
 int bad_fn(const char *fn) { return set_error(UGK_EINVAL, "%s: unknown fn code", fn); }
 
@@ -217,7 +259,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
       UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
       UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62) UGK_MM(63)
-      UGK_MM(64) UGK_MM(65)
+      UGK_MM(64) UGK_MM(65) UGK_MM(66) UGK_MM(67)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -246,7 +288,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
     UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
     UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62) UGK_EV(63)
-    UGK_EV(64) UGK_EV(65)
+    UGK_EV(64) UGK_EV(65) UGK_EV(66) UGK_EV(67)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");
@@ -276,4 +318,49 @@ extern "C" int ugk_diag_philox(unsigned *out, const unsigned *in, size_t n) {
   if (g > 65536u) g = 65536u;
   hipLaunchKernelGGL(k_philox, dim3(g), dim3(kBlock), 0, stream(), out, in, n);
   return check_launch("ugk_diag_philox");
+}
+
+extern "C" int ugk_diag_layernorm_partial_rows(int rows, int C, int fused, int *actual, int *bound) {
+  if (rows < 0 || C <= 0) return set_error(UGK_EINVAL, "ugk_diag_layernorm_partial_rows: need rows >= 0, C > 0");
+  if (!actual || !bound) return set_error(UGK_EINVAL, "ugk_diag_layernorm_partial_rows: NULL result pointer");
+  *actual = layernorm_backward_blocks(rows, C, fused != 0, kMaxPartialRows);
+  *bound = layernorm_backward_blocks_bound(rows, C);
+  return UGK_OK;
+}
+
+extern "C" int ugk_diag_layernorm_tail(int on) {
+  const int prev = layernorm_tail();
+  if (on >= 0) set_layernorm_tail(on);
+  return prev;
+}
+
+extern "C" int ugk_diag_math_ulp(int fn, unsigned lo, unsigned long long count, unsigned *max_ulp,
+                                 unsigned *at) {
+  if (fn < 63 || fn > 67) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: fn must be 63-67");
+  if (!max_ulp || !at) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: NULL result pointer");
+  if (count > (1ull << 32) - lo) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: range beyond 2^32");
+  unsigned long long h = 0, *d = nullptr;
+  if (hipMalloc(&d, sizeof h) != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(UGK_ENOMEM, "ugk_diag_math_ulp: hipMalloc failed");
+  }
+  int rc = UGK_OK;
+  if (hipMemcpyAsync(d, &h, sizeof h, hipMemcpyHostToDevice, stream()) != hipSuccess) rc = UGK_EHIP;
+  if (rc == UGK_OK && count) {
+    const dim3 grid(8192), block(kBlock);
+    switch (fn) {
+#define UGK_UL(f) \
+  case f: hipLaunchKernelGGL(k_math_ulp<f>, grid, block, 0, stream(), (unsigned long long)lo, count, d); break;
+      UGK_UL(63) UGK_UL(64) UGK_UL(65) UGK_UL(66) UGK_UL(67)
+#undef UGK_UL
+    }
+    rc = check_launch("ugk_diag_math_ulp");
+  }
+  if (rc == UGK_OK && hipMemcpyAsync(&h, d, sizeof h, hipMemcpyDeviceToHost, stream()) != hipSuccess) rc = UGK_EHIP;
+  if (rc == UGK_OK && hipStreamSynchronize(stream()) != hipSuccess) rc = UGK_EHIP;
+  (void)hipFree(d);
+  if (rc != UGK_OK) return rc == UGK_EHIP ? set_error(rc, "ugk_diag_math_ulp: HIP error") : rc;
+  *max_ulp = (unsigned)(h >> 32);
+  *at = (unsigned)h;
+  return UGK_OK;
 }

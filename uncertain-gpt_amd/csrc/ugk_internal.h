@@ -28,8 +28,13 @@ int check_launch(const char *what);
 // grows. workspace() returns at least `bytes` of region r on the current
 // device, or nullptr with the error set; *fresh (if given) tells whether the
 // region's memory is new since its last use (its contents are undefined).
+// With keep_fresh the fresh mark is reported but left set (for a caller that
+// cannot prepare the memory now, e.g. under graph capture).
 enum Region { kRegLn = 0, kRegEncoder = 1, kRegKl = 2, kRegSoftmax = 3, kNumRegions = 4 };
-void *workspace(Region r, size_t bytes, bool *fresh = nullptr);
+void *workspace(Region r, size_t bytes, bool *fresh = nullptr, bool keep_fresh = false);
+// Whether the library stream is being captured into a graph (false if the
+// query fails).
+bool stream_capturing();
 
 // The step driver's op timer arms an event pair for the kernel launches of
 // an op; launch() then records them with the dispatches themselves
@@ -116,6 +121,10 @@ int launch_gelu_forward(float *out, const float *inp, size_t n);
 int launch_gelu_backward(float *dinp, const float *inp, const float *dout, size_t n);
 // dinp = gelu'(inp) * dout, as launch_gelu_backward on a dinp of zeros (not read)
 int launch_gelu_backward_zero(float *dinp, const float *inp, const float *dout, size_t n);
+// Philox ops' softplus/sigmoid: 0 (default) the hardware-transcendental forms,
+// 1 the glibc-exact forms of the eps-taking ops.
+void set_philox_exact(int exact);
+int philox_exact();
 int launch_bayes_materialize(float *w, const float *mu, const float *rho,
                              const float *eps, size_t n);
 int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
@@ -178,6 +187,12 @@ int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, f
                                        const float *rstd, int rows, int C, int max_blocks, int *nblk,
                                        int dinp_mode = kDinpRw, bool assign_res = false);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
+// The per-op LayerNorm backward (launch_layernorm_residual_backward_into) on
+// the float4 path finishes its column sums in its main launch (1, default) or
+// in a second launch (0); both give the same bits. The step driver always
+// batches its column sums in one launch at the end.
+void set_layernorm_tail(int on);
+int layernorm_tail();
 // Both passes with the partial rows in `partial` (at most max_blocks rows of
 // 2C floats), not in the workspace.
 int launch_layernorm_residual_backward_into(float *partial, int max_blocks, float *dinp, float *dweight,
@@ -186,6 +201,9 @@ int launch_layernorm_residual_backward_into(float *partial, int max_blocks, floa
                                             const float *rstd, int rows, int C);
 // Partial rows one call writes with at most max_blocks of them.
 int layernorm_backward_blocks(int rows, int C, bool res, int max_blocks);
+// An upper bound on the partial rows of every call with at most `rows` rows
+// and C channels (any path, plain or fused), which sizes the workspace.
+int layernorm_backward_blocks_bound(int rows, int C);
 constexpr int kMaxScalarBlocks = 512;
 constexpr int kMaxPartialRows = 1024;  // partial rows the column-sum kernel takes per call
 // The allocation-free LayerNorm backward's partial rows live in a file-scope
@@ -204,10 +222,25 @@ int launch_encoder_forward(float *out, const int *inp, const float *wte,
                            const float *wpe, int B, int T, int C);
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
                             const int *inp, int B, int T, int C);
+// Buckets of more than 32 rows: 0 (default) blocked adds (64-row blocks, each
+// in row order, the block sums in block order; float4 path, C <= 2,048),
+// 1 one add per row in row order (bit-identical to train_bnn.c).
+void set_encoder_exact(int exact);
+int encoder_exact();
+// Clears the encoder backward's bucket state at mem (encoder_backward_scratch()
+// bytes) on the library stream: new memory must be cleared once before the
+// first call uses it.
+int launch_encoder_state_init(void *mem);
+// ids[i] outside [0, bound) are replaced by fill, and `code` is stored in the
+// per-device id error word (ids_error_word()).
+int launch_ids_guard(int *ids, int n, int bound, int fill, int code);
+// Device address of the current device's id error word (nullptr with the
+// error set if its lookup failed).
+int *ids_error_word();
 
 // Workspace sizes.
 size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
-size_t encoder_backward_scratch();                   // the bucket state (fixed)
+size_t encoder_backward_scratch(int C);              // the bucket state (and the blocked mode's sums at C)
 size_t kl_forward_scratch();                         // partial sums and result (fixed)
 size_t softmax_scratch(int rows, int V);             // row statistics of rows too long for one workgroup
 

@@ -27,6 +27,8 @@
 // conditions around loads made the compiler wait for one row's loads before
 // it issued the next row's.
 // Streamed rows (x, dout, dinp, out) use non-temporal loads and stores.
+#include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "ugk_internal.h"
@@ -265,6 +267,106 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_scalar(float *out, float *mea
 
 __device__ __forceinline__ float4 zero4() { return make_float4(0.0f, 0.0f, 0.0f, 0.0f); }
 
+// ---- column sums in the main launch (the per-op entry points) ----------------
+// Instead of a second launch over the partial rows, the workgroups finish the
+// column sums themselves, in the order the column-sum kernel uses (so with the
+// same bits): the partial rows form kTailGroups groups of J = ceil(nblk / 16)
+// consecutive rows; the last workgroup of a group to finish adds the group's
+// rows in index order, starting from +0.0f, and writes the sum over the
+// group's first row; the last group to finish adds the group sums in group
+// order (an empty group adds +0.0f) into dweight/dbias.
+//
+// Publishing without a cache write-back: the rows and group sums are written
+// with device-scope stores (sc1: written through to the point where all of the
+// device's L2 caches are coherent) and read with device-scope loads. Each
+// thread waits for its own stores to complete (s_waitcnt vmcnt(0)) before the
+// workgroup barrier after which one thread increments the group's counter (a
+// device-scope atomic), so when a counter shows a workgroup that it is the
+// last, every row it is about to read is already at the coherence point. This
+// is the release/acquire pair that an agent-scope fence would implement with
+// an L2 write-back (buffer_wbl2 sc1) and invalidation on gfx950, confined to
+// the bytes that need it; the fence itself, once per workgroup, took the call
+// from 23 to 180 us at 8,192 x 768. Without it the call still takes longer
+// than with the second launch (32.7 against 23.3 us at 8,192 x 768, 108
+// against 38 us at 4,096 x 2,048): the last workgroup's chain of dependent
+// device-scope round trips (its stores' completion, the counter, the group's
+// rows, the group sum's completion, the counter, the group sums), about
+// 0.85 us each, outlasts a launch that needs two. So it is not the default
+// (ugk_diag_layernorm_tail selects it).
+//
+// The counters are per device and zero when the code object is loaded; the
+// last arriver of each level resets its counter, so every call finds them at
+// zero. Calls that overlap on one device (other streams) would share them,
+// as they would share the workspace.
+constexpr int kTailGroups = 16;
+}  // namespace
+}  // namespace ugk
+
+static __device__ int ln_tail_count[ugk::kTailGroups + 1];
+
+namespace ugk {
+namespace {
+
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Called by every thread of a workgroup (NT threads) after it has written its
+// partial row with st_dev.
+template <int NT>
+__device__ __forceinline__ void ln_bwd_tail(float *partial, int nblk, int C, float *dweight, float *dbias) {
+  __shared__ int last;
+  constexpr int kBatch = 16;
+  const int C2 = 2 * C;
+  const int J = (nblk + kTailGroups - 1) / kTailGroups;
+  const int g = blockIdx.x / J;
+  const int j0 = g * J, j1 = min(j0 + J, nblk);
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&ln_tail_count[g], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == j1 - j0 - 1;
+    if (last) __hip_atomic_store(&ln_tail_count[g], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int c = threadIdx.x; c < C2; c += NT) {
+    float acc = 0.0f;
+    for (int b = j0; b < j1; b += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; q++) v[q] = ld_dev(partial + (size_t)min(b + q, j1 - 1) * C2 + c);
+#pragma unroll
+      for (int q = 0; q < kBatch; q++) acc += b + q < j1 ? v[q] : -0.0f;
+    }
+    st_dev(partial + (size_t)j0 * C2 + c, acc);
+  }
+  wait_stores();
+  __syncthreads();
+  const int G = (nblk + J - 1) / J;  // groups with rows
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(&ln_tail_count[kTailGroups], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == G - 1;
+    if (last) __hip_atomic_store(&ln_tail_count[kTailGroups], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int c = threadIdx.x; c < C2; c += NT) {
+    float v[kTailGroups];
+#pragma unroll
+    for (int k = 0; k < kTailGroups; k++) v[k] = ld_dev(partial + (size_t)min(k, G - 1) * J * C2 + c);
+    float t = v[0];
+#pragma unroll
+    for (int k = 1; k < kTailGroups; k++) t += k < G ? v[k] : 0.0f;
+    if (c < C)
+      dweight[c] += t;
+    else
+      dbias[c - C] += t;
+  }
+}
+
 // Backward, register-resident rows. A workgroup is W wavefronts; wavefront w
 // of workgroup g takes the rpw consecutive rows starting at (W g + w) * rpw,
 // R at a time: the loads of R rows (x and dout first, which the row sums
@@ -298,12 +400,12 @@ __device__ __forceinline__ float4 zero4() { return make_float4(0.0f, 0.0f, 0.0f,
 // an ordinary dinp store made it faster alone (35.7 against 37.2 us cold at
 // 8,192 x 768) but the step slower (3.02 against 2.93 ms), the dirty lines
 // of its 24 launches being written back during the kernels that follow.
-template <int V, int W, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign>
+template <int V, int W, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign, bool kTail>
 __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpw, float *__restrict__ rdx,
-    float *__restrict__ rdy, int same) {
+    float *__restrict__ rdy, int same, float *dweight, float *dbias) {
   __shared__ float4 red[W][2][V * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -448,9 +550,15 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
       float4 t = red[0][which][c4];
 #pragma unroll
       for (int k = 1; k < W; k++) t = add4(t, red[k][which][c4]);
-      prow[which * C4 + c4] = t;
+      if (kTail) {
+        float *q = reinterpret_cast<float *>(prow + which * C4 + c4);
+        st_dev(q, t.x); st_dev(q + 1, t.y); st_dev(q + 2, t.z); st_dev(q + 3, t.w);
+      } else {
+        prow[which * C4 + c4] = t;
+      }
     }
   }
+  if (kTail) ln_bwd_tail<W * kWave>(partial, (int)gridDim.x, C, dweight, dbias);
 }
 
 // Backward with each row split over a team of P wavefronts, one float4 per
@@ -468,12 +576,12 @@ __global__ __launch_bounds__(W * kWave, MINW) void k_ln_bwd_vec(
 // two-rows-per-wavefront kernel at 8,192 x 768, cold, with the same 512
 // partial rows. rpt and T fix the order of every addition; R does not, so the
 // plain backward (R = 2) and the fused pair (R = 4) give the same bits.
-template <int P, int T, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign>
+template <int P, int T, int R, bool kRes, int MINW, bool kNt, int kDinp, bool kAssign, bool kTail>
 __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
     float *__restrict__ dinp, float *__restrict__ partial, const float *__restrict__ dout,
     const float *__restrict__ inp, const float *__restrict__ weight, const float *__restrict__ mean,
     const float *__restrict__ rstd, int rows, int C, int rpt, float *__restrict__ rdx,
-    float *__restrict__ rdy, int same) {
+    float *__restrict__ rdy, int same, float *dweight, float *dbias) {
   __shared__ float parts[2][T][R][P][2];  // a row's two sums by part, double-buffered by pass
   __shared__ float4 red[T][2][P * kWave];
   const int lane = threadIdx.x & (kWave - 1);
@@ -594,8 +702,14 @@ __global__ __launch_bounds__(P * T * kWave, MINW) void k_ln_bwd_team(
     float4 t = red[0][which][cc];
 #pragma unroll
     for (int k = 1; k < T; k++) t = add4(t, red[k][which][cc]);
-    prow[which * C4 + cc] = t;
+    if (kTail) {
+      float *q = reinterpret_cast<float *>(prow + which * C4 + cc);
+      st_dev(q, t.x); st_dev(q + 1, t.y); st_dev(q + 2, t.z); st_dev(q + 3, t.w);
+    } else {
+      prow[which * C4 + cc] = t;
+    }
   }
+  if (kTail) ln_bwd_tail<P * T * kWave>(partial, (int)gridDim.x, C, dweight, dbias);
 }
 
 // Backward for any C and alignment. Phase 1: one wavefront per row writes
@@ -649,6 +763,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_scalar(float *dinp, float *pa
 // partial rows [k*J, (k+1)*J), J = ceil(nblk/16) <= 64, in index order, 32
 // loads in flight per batch; the 16 group sums are then added in group order.
 constexpr int kRedGroups = 16;
+static_assert(kRedGroups == kTailGroups, "the in-launch column sums follow the column-sum kernel's order");
 constexpr int kRedBatch = 32;
 static_assert(kMaxPartialRows <= kRedGroups * 2 * kRedBatch, "two load batches per group at most");
 __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias, const float *partial, int nblk,
@@ -660,6 +775,10 @@ __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias,
   const int J = (nblk + kRedGroups - 1) / kRedGroups;
   const int j0 = g * J, j1 = min(j0 + J, nblk);
   const int cc = col < C2 ? col : C2 - 1;
+  // the value the total is added to, loaded with the partial rows rather than
+  // after them (one memory round trip fewer at the end)
+  float* const dst = col < C ? dweight + col : dbias + (cc - C);
+  const float prev = g == 0 && col < C2 ? *dst : 0.0f;
   float acc = 0.0f;
   for (int b = j0; b < j1; b += kRedBatch) {
     float v[kRedBatch];
@@ -674,10 +793,7 @@ __device__ __forceinline__ void ln_bwd_reduce_tile(float *dweight, float *dbias,
     float t = red[0][cl];
 #pragma unroll
     for (int k = 1; k < kRedGroups; k++) t += red[k][cl];
-    if (col < C)
-      dweight[col] += t;
-    else
-      dbias[col - C] += t;
+    *dst = prev + t;
   }
 }
 
@@ -808,15 +924,30 @@ int layernorm_backward_blocks(int rows, int C, bool res, int max_blocks) {
   return nblk;
 }
 
+// An upper bound on the partial rows of every call with at most `rows` rows
+// and at most C channels, on any path. A path's count is not monotone in the
+// rows (once a call would exceed the cap, each workgroup takes more rows and
+// the count drops below the cap), but it never exceeds
+// min(cap, ceil(rows / floor)), where floor is the fewest rows a workgroup of
+// that path takes: 4 on the scalar path (cap 512) and on the wave-per-row path
+// above 1,024 channels (one row per wavefront, four wavefronts), 8 from 772
+// channels (eight wavefronts, one row each), 16 below (eight wavefronts of two
+// rows, or four teams of four rows; cap 1,024). Sizing a workspace by this
+// bound at a config's rows therefore covers every smaller call.
+int layernorm_backward_blocks_bound(int rows, int C) {
+  const auto cap_div = [rows](int cap, int floor) {
+    const long long q = ((long long)rows + floor - 1) / floor;
+    return (int)(q < cap ? q : cap);
+  };
+  int nb = cap_div(kMaxScalarBlocks, 4);
+  if (C > kWave * 4 * 4) nb = std::max(nb, cap_div(kMaxPartialRows, 4));
+  if (C > kWave * 4 * 3) nb = std::max(nb, cap_div(kMaxPartialRows, 8));
+  nb = std::max(nb, cap_div(kMaxPartialRows, 16));
+  return rows > 0 ? nb : 0;
+}
+
 size_t layernorm_backward_scratch(int rows, int C) {
-  // the larger of the two shapes (plain or fused) and of the scalar path's
-  int nb = layernorm_backward_blocks(rows, C, false, kMaxPartialRows);
-  const int nf = layernorm_backward_blocks(rows, C, true, kMaxPartialRows);
-  if (nf > nb) nb = nf;
-  int ns, rpb;
-  bwd_shape(rows, kMaxScalarBlocks, &ns, &rpb);
-  if (ns > nb) nb = ns;
-  return (size_t)nb * 2 * (size_t)C * sizeof(float);
+  return (size_t)layernorm_backward_blocks_bound(rows, C) * 2 * (size_t)C * sizeof(float);
 }
 
 namespace {
@@ -898,52 +1029,73 @@ int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *
 }
 
 namespace {
+// tail: the workgroups finish the column sums into dweight/dbias themselves
+// (ln_bwd_tail); only for the per-op modes (dinp read and written, residual
+// targets read).
 template <bool kRes, int kDinp, bool kAssign>
 int launch_ln_bwd_vec(float *dinp, float *partial, const float *dout, const float *inp,
                       const float *weight, const float *mean, const float *rstd, int rows, int C,
-                      float *rdx, float *rdy, int max_blocks) {
+                      float *rdx, float *rdy, int max_blocks, bool tail = false, float *dweight = nullptr,
+                      float *dbias = nullptr) {
   static_assert(kRes || (kDinp == kDinpRw && !kAssign), "the plain backward reads and writes dinp");
+  constexpr bool kTailOk = kDinp == kDinpRw && !kAssign;
   int nblk, rpw;
   const int V = ((C >> 2) + kWave - 1) / kWave;
   const int same = rdx == rdy ? 1 : 0;
   const bool nt = (size_t)rows * (size_t)C < ((size_t)1 << 21);
+  // the kernel with and without the in-launch column sums
+  const auto both = [&](auto k_plain, auto k_tail, dim3 grid, dim3 block, int rp) {
+    if (kTailOk && tail)
+      launch(k_tail, grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rp, rdx, rdy, same,
+             dweight, dbias);
+    else
+      launch(k_plain, grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rp, rdx, rdy, same,
+             nullptr, nullptr);
+  };
   if (team_path(rows, C)) {
     int rpt;
     team_shape(rows, max_blocks, &nblk, &rpt);
     const dim3 grid(nblk), block(kTeamParts * kTeams * kWave);
     if constexpr (kRes)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kDinp, kAssign>), grid, block, 0, dinp, partial, dout, inp,
-             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+      both(k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kDinp, kAssign, false>,
+           k_ln_bwd_team<kTeamParts, kTeams, 4, true, 3, true, kDinp, kAssign, kTailOk>, grid, block, rpt);
     else if (nt)
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, kDinpRw, false>), grid, block, 0, dinp, partial, dout, inp,
-             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+      both(k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, kDinpRw, false, false>,
+           k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, true, kDinpRw, false, true>, grid, block, rpt);
     else
-      launch((k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, kDinpRw, false>), grid, block, 0, dinp, partial, dout, inp,
-             weight, mean, rstd, rows, C, rpt, rdx, rdy, same);
+      both(k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, kDinpRw, false, false>,
+           k_ln_bwd_team<kTeamParts, kTeams, 2, false, 1, false, kDinpRw, false, true>, grid, block, rpt);
     return nblk;
   }
   const BwdCfg k = bwd_cfg(V, kRes);
   bwd_shape_vec(rows, k, max_blocks, &nblk, &rpw);
   const dim3 grid(nblk), block(k.W * kWave);
   switch (V) {
-#define UGK_LN_BWD(v)                                                                                            \
-  case v:                                                                                                        \
-    if (kRes || nt)                                                                                              \
-      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, true,      \
-                           kDinp, kAssign>),                                                                   \
-             grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
-    else                                                                                                         \
-      launch((k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, kRes,      \
-                           kDinp, kAssign>),                                                                   \
-             grid, block, 0, dinp, partial, dout, inp, weight, mean, rstd, rows, C, rpw, rdx, rdy, same);       \
+#define UGK_LN_BWD_K(v, ntv, tl)                                                                                    \
+  k_ln_bwd_vec<v, bwd_cfg(v, kRes).W, bwd_cfg(v, kRes).R, kRes, bwd_cfg(v, kRes).MINW, ntv, kDinp, kAssign, tl>
+#define UGK_LN_BWD(v)                                                                                               \
+  case v:                                                                                                           \
+    if (kRes || nt)                                                                                                 \
+      both(UGK_LN_BWD_K(v, true, false), UGK_LN_BWD_K(v, true, kTailOk), grid, block, rpw);                         \
+    else                                                                                                            \
+      both(UGK_LN_BWD_K(v, kRes, false), UGK_LN_BWD_K(v, kRes, kTailOk), grid, block, rpw);                         \
     break;
     UGK_LN_BWD(1) UGK_LN_BWD(2) UGK_LN_BWD(3) UGK_LN_BWD(4)
     UGK_LN_BWD(5) UGK_LN_BWD(6) UGK_LN_BWD(7) UGK_LN_BWD(8)
 #undef UGK_LN_BWD
+#undef UGK_LN_BWD_K
   }
   return nblk;
 }
+
+// Whether the per-op backward finishes its column sums in the main launch (1)
+// or in a second one (0, the default: faster, see ln_bwd_tail); both give the
+// same bits.
+std::atomic<int> g_ln_tail{0};
 }  // namespace
+
+void set_layernorm_tail(int on) { g_ln_tail.store(on ? 1 : 0); }
+int layernorm_tail() { return g_ln_tail.load(); }
 
 int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, float *dy, const float *dout,
                                        const float *inp, const float *weight, const float *mean,
@@ -995,6 +1147,16 @@ int launch_layernorm_residual_backward_into(float *partial, int max_blocks, floa
                                             const float *inp, const float *weight, const float *mean,
                                             const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
+  const bool res = dx != nullptr;
+  if (layernorm_tail() && vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
+    if (res)
+      launch_ln_bwd_vec<true, kDinpRw, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,
+                                              max_blocks, true, dweight, dbias);
+    else
+      launch_ln_bwd_vec<false, kDinpRw, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, nullptr,
+                                               nullptr, max_blocks, true, dweight, dbias);
+    return check_launch("layernorm_backward");
+  }
   int nblk;
   if (int e = launch_layernorm_backward_partials(dinp, partial, dx, dy, dout, inp, weight, mean, rstd, rows, C,
                                                  max_blocks, &nblk))

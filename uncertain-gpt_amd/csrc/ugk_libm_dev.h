@@ -401,6 +401,63 @@ __device__ __forceinline__ float ugk_fast_gelu_grad(float x) {
   return fabsf(x) <= 10.0f ? near : far;
 }
 
+// ---- hardware-transcendental softplus and sigmoid (the Philox ops' default) ----
+// e^x as 2^t with t = x log2(e) carried to about 2^-48 relative (the product's
+// rounding error and the constant's tail, by fma), then one correction
+// e (1 + dt ln 2) after the hardware 2^t (v_exp_f32). x is first clamped
+// from below to -104, where e^x is below every float (NaN passes through).
+// The hardware 2^t flushes results below 2^-126 to zero, so below t = -64
+// it takes 2^(t + 64) 2^-64, whose multiply rounds into the subnormals. Where
+// 2^t overflows, the correction (inf + inf * c) would be NaN for c < 0: the
+// overflow is kept, as is a NaN x.
+constexpr float kUgkLog2e = 1.44269502162933349609f;       // log2(e) rounded to float
+constexpr float kUgkLog2eLo = 1.92596299112661746887e-8f;  // log2(e) - kUgkLog2e
+constexpr float kUgkLn2 = 0.693147180559945309417f;
+
+__device__ __forceinline__ float ugk_fast_exp(float x) {
+  const float xc = x < -104.0f ? -104.0f : x;
+  const float t = xc * kUgkLog2e;
+  const float dt = __builtin_fmaf(xc, kUgkLog2e, -t) + xc * kUgkLog2eLo;
+  const bool tiny = t < -64.0f;
+  const float e = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t) * (tiny ? 0x1p-64f : 1.0f);
+  const float r = __builtin_fmaf(e, dt * kUgkLn2, e);
+  return r != r ? e : r;
+}
+
+// softplus(x) = log1p(e^x) (train_bnn.c:814-816's formula; x for x > 20 as
+// there). log1p(e): below e = 1/16 its series to e^6 (the remainder is below
+// e^7/7, a tenth of an ulp); above, Goldberg's form log(u) e / (u - 1)
+// with u = 1 + e rounded, whose quotient cancels the rounding of u, and the
+// hardware log2 (v_log_f32) times ln 2. Within a few ulp of glibc's
+// log1pf(expf(x)) and within 1e-6 absolute / 1e-5 relative of it on every
+// float input (ugk_diag.hip fn 66); about 20 VALU instructions, with three
+// hardware transcendentals, against some 70 for the glibc-exact form.
+__device__ __forceinline__ float ugk_fast_softplus(float x) {
+  const float e = ugk_fast_exp(x);
+  float p = __builtin_fmaf(e, -1.0f / 6.0f, 0.2f);
+  p = __builtin_fmaf(e, p, -0.25f);
+  p = __builtin_fmaf(e, p, 1.0f / 3.0f);
+  p = __builtin_fmaf(e, p, -0.5f);
+  const float series = e * __builtin_fmaf(e, p, 1.0f);
+  const float u = 1.0f + e;
+  const float goldberg = __builtin_amdgcn_logf(u) * kUgkLn2 * (e * __builtin_amdgcn_rcpf(u - 1.0f));
+  const float r = e < 0.0625f ? series : goldberg;
+  return x > 20.0f ? x : r;
+}
+
+// sigmoid(x) = 1 / (1 + e^-x) (train_bnn.c:820-822) with the hardware
+// reciprocal (v_rcp_f32); x is clamped to [-104, 104] first (NaN passes), so
+// that e^-x is 0 or inf at the ends, as there. The hardware reciprocal flushes
+// results below 2^-126 to zero, so a divisor above 2^64 is scaled by 2^-64
+// first and the quotient by 2^-64 after. Within a few ulp of the glibc-exact
+// form and within the literal bar of it everywhere (fn 67).
+__device__ __forceinline__ float ugk_fast_sigmoid(float x) {
+  const float xc = x > 104.0f ? 104.0f : (x < -104.0f ? -104.0f : x);
+  const float d = 1.0f + ugk_fast_exp(-xc);
+  const bool big = d > 0x1p64f;
+  return __builtin_amdgcn_rcpf(big ? d * 0x1p-64f : d) * (big ? 0x1p-64f : 1.0f);
+}
+
 __device__ __forceinline__ float ugk_dev_softplusf(float x) {
   return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf(x));
 }

@@ -29,7 +29,7 @@ __all__ = [
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
-    "set_workspace", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact",
+    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_encoder_exact", "encoder_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "gpt2_layers_backward_zeroed", "version",
 ]
@@ -105,6 +105,10 @@ _SIGS = {
     "ugk_version": [],
     "ugk_set_gelu_exact": [_i],
     "ugk_get_gelu_exact": [],
+    "ugk_set_philox_exact": [_i],
+    "ugk_set_encoder_exact": [_i],
+    "ugk_get_encoder_exact": [],
+    "ugk_get_philox_exact": [],
     "ugk_last_error": [],
     "ugk_param_count": [Config],
     "ugk_act_count": [Config],
@@ -115,7 +119,12 @@ _SIGS = {
                                ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_math_eval": [_i, _i, _fp, _fp, _sz],
     "ugk_diag_philox": [_fp, _fp, _sz],
+    "ugk_diag_math_ulp": [_i, ctypes.c_uint, ctypes.c_ulonglong, ctypes.POINTER(ctypes.c_uint),
+                          ctypes.POINTER(ctypes.c_uint)],
     "ugk_diag_stream": [_fp, _sz, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
+    "ugk_diag_layernorm_partial_rows": [_i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "ugk_ids_guard": [_fp, _i, _i, _i, _i],
+    "ugk_diag_layernorm_tail": [_i],
     "ugk_loader_open": [ctypes.POINTER(_fp), ctypes.c_char_p],
     "ugk_loader_count": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_long)],
     "ugk_loader_next": [_fp, _fp, _fp, _i],
@@ -170,46 +179,65 @@ def _ptr(x, what: str, need: int, dtype: str):
     return x.data_ptr()
 
 
-def _check_tokens(inp, table, C: int, what: str) -> None:
-    """Token ids must index rows of ``table`` (the reference's contract); checked when both are tensors,
-    except while the current stream is being captured into a graph (the check reads the ids back)."""
+# Token and target ids index tables (rows of wte, logits of a row): an id out of range would make a
+# kernel read or write outside them. The reference leaves 0 <= id < V to its callers unchecked.
+# Here each tensor of ids goes through ugk_ids_guard on the device first, on the library's stream:
+# ids out of range are replaced in place (so no kernel indexes outside its table; ids in range are
+# not written), and the library records the op, which the next synchronize() raises as UgkError.
+# No host round trip, so the calls stay asynchronous and may be captured in a graph.
+# set_sync_checks(True) checks on the host instead (reading the ids back, a device synchronisation
+# per call) and raises ValueError at once, leaving the ids untouched.
+_IDS_CODE = {"encoder_forward": 1, "encoder_backward": 2, "encoder_layernorm_forward": 3, "softmax_crossentropy": 4,
+             "crossentropy_softmax_backward": 5, "crossentropy_softmax_backward_zeroed": 5}
+_sync_checks = False
+
+
+def set_sync_checks(on: bool) -> None:
+    """Check token/target ids on the host before each call (a device sync per call; ValueError at
+    once) instead of the default asynchronous device-side guard (UgkError at the next synchronize)."""
+    global _sync_checks
+    _sync_checks = bool(on)
+
+
+def _guard_ids(ids, n: int, bound: int, fill: int, what: str) -> None:
+    """Guard a device tensor of ids (see above); a device address, or a tensor that the argument
+    checks reject, is left alone."""
     import torch
-    if not (isinstance(inp, torch.Tensor) and isinstance(table, torch.Tensor) and inp.is_cuda and table.is_cuda):
-        return  # a device address, or a tensor that the argument checks reject
-    if torch.cuda.is_current_stream_capturing():
+    if not (isinstance(ids, torch.Tensor) and ids.is_cuda and ids.dtype == torch.int32 and ids.is_contiguous()):
         return
-    if inp.numel() and C:
-        rows = table.numel() // C
-        lo, hi = int(inp.min()), int(inp.max())
-        if lo < 0 or hi >= rows:
-            raise ValueError(f"{what}: token ids must lie in [0, {rows}), got [{lo}, {hi}]")
+    if n <= 0 or ids.numel() < n:
+        return  # nothing to index, or the size check of the call rejects it
+    if _sync_checks and not torch.cuda.is_current_stream_capturing():
+        t = ids.reshape(-1)[:n]
+        lo, hi = int(t.min()), int(t.max())
+        if lo < 0 or hi >= bound:
+            raise ValueError(f"{what}: ids must lie in [0, {bound}), got [{lo}, {hi}]")
+        return
+    _check(lib.ugk_ids_guard(ids.data_ptr(), n, bound, fill, _IDS_CODE[what]))
+
+
+def _check_tokens(inp, table, C: int, n: int, what: str, fill: int = 0) -> None:
+    """Token ids index rows of ``table`` (``table.numel() // C`` rows)."""
+    import torch
+    if isinstance(table, torch.Tensor) and table.is_cuda and C:
+        _guard_ids(inp, n, table.numel() // C, fill, what)
 
 
 def _check_targets(targets, V: int, rows: int, what: str) -> None:
-    """Target ids index a row of V logits (the reference's contract); checked when a GPU tensor,
-    except while the current stream is being captured into a graph (the check reads the ids back)."""
-    import torch
-    if not (isinstance(targets, torch.Tensor) and targets.is_cuda):
-        return  # a device address, or a tensor that the argument checks reject
-    if torch.cuda.is_current_stream_capturing():
-        return
-    if rows:
-        t = targets.reshape(-1)[:rows]
-        lo, hi = int(t.min()), int(t.max())
-        if lo < 0 or hi >= V:
-            raise ValueError(f"{what}: target ids must lie in [0, {V}), got [{lo}, {hi}]")
+    """Target ids index a row of V logits."""
+    _guard_ids(targets, rows, V, 0, what)
 
 
 def encoder_forward(out, inp, wte, wpe, B: int, T: int, C: int) -> None:
     """train_bnn.c:41-65. ``out[b,t,:] = wte[inp[b,t],:] + wpe[t,:]``."""
-    _check_tokens(inp, wte, C, "encoder_forward")
+    _check_tokens(inp, wte, C, B * T, "encoder_forward")
     _check(lib.ugk_encoder_forward(_ptr(out, "out", B * T * C, "f32"), _ptr(inp, "inp", B * T, "i32"),
                                    _ptr(wte, "wte", C, "f32"), _ptr(wpe, "wpe", T * C, "f32"), B, T, C))
 
 
 def encoder_backward(dwte, dwpe, dout, inp, B: int, T: int, C: int) -> None:
     """train_bnn.c:647-662. ``dwte[inp[b,t],:] += dout[b,t,:]``; ``dwpe[t,:] += dout[b,t,:]``."""
-    _check_tokens(inp, dwte, C, "encoder_backward")
+    _check_tokens(inp, dwte, C, B * T, "encoder_backward", fill=-1)  # a negative id: the row is skipped
     _check(lib.ugk_encoder_backward(_ptr(dwte, "dwte", C, "f32"), _ptr(dwpe, "dwpe", T * C, "f32"),
                                     _ptr(dout, "dout", B * T * C, "f32"), _ptr(inp, "inp", B * T, "i32"),
                                     B, T, C))
@@ -235,8 +263,8 @@ def layernorm_backward(dinp, dweight, dbias, dout, inp, weight, mean, rstd, B: i
 
 def encoder_layernorm_forward(enc, out, mean, rstd, inp, wte, wpe, weight, bias, B: int, T: int, C: int) -> None:
     """``encoder_forward(enc, inp, wte, wpe)`` then ``layernorm_forward(out, mean, rstd, enc, ...)``, one pass."""
-    _check_tokens(inp, wte, C, "encoder_layernorm_forward")
     n, rows = B * T * C, B * T
+    _check_tokens(inp, wte, C, rows, "encoder_layernorm_forward")
     _check(lib.ugk_encoder_layernorm_forward(
         _ptr(enc, "enc", n, "f32"), _ptr(out, "out", n, "f32"), _ptr(mean, "mean", rows, "f32"),
         _ptr(rstd, "rstd", rows, "f32"), _ptr(inp, "inp", rows, "i32"), _ptr(wte, "wte", C, "f32"),
@@ -379,6 +407,8 @@ def set_stream(stream: Optional[int]) -> None:
 
 
 def synchronize() -> None:
+    """Wait for the library's stream; raises UgkError if the device-side id guard found an id out of
+    range in a call since the last synchronize (the op is named)."""
     _check(lib.ugk_synchronize())
 
 
@@ -400,17 +430,24 @@ def workspace_bytes(cfg: Config) -> int:
     return int(lib.ugk_workspace_bytes(cfg))
 
 
+_workspace_refs = {}  # device index -> the caller's workspace tensor, kept alive while the library uses it
+
+
 def set_workspace(buf, cfg: Config) -> None:
     """Hand the library a caller-owned workspace (a uint8/float device tensor of at least
     ``workspace_bytes(cfg)`` bytes, 256-byte aligned), or return to library-owned regions with None.
-    The tensor must stay alive until the next call of this function."""
+    The binding keeps a reference to the tensor until the next call of this function on its device,
+    so that the caching allocator cannot hand its memory to other tensors meanwhile."""
+    import torch
     if buf is None:
         _check(lib.ugk_set_workspace(None, 0, cfg))
+        _workspace_refs.pop(torch.cuda.current_device(), None)
         return
     nbytes = buf.numel() * buf.element_size()
     if not buf.is_cuda or not buf.is_contiguous():
         raise ValueError("the workspace must be a contiguous device tensor")
     _check(lib.ugk_set_workspace(buf.data_ptr(), nbytes, cfg))
+    _workspace_refs[buf.device.index] = buf
 
 
 OP_NAMES = {1: "encoder_forward", 2: "layernorm_forward", 3: "residual_layernorm_forward", 4: "gelu_forward",
@@ -444,6 +481,28 @@ def set_gelu_exact(exact: bool) -> None:
 
 def gelu_exact() -> bool:
     return bool(lib.ugk_get_gelu_exact())
+
+
+def set_philox_exact(exact: bool) -> None:
+    """Softplus/sigmoid inside the ops that draw eps on the device: False (default) the hardware-
+    transcendental forms, within 1e-5 rel / 1e-6 abs of train_bnn.c on every input; True the
+    glibc-exact forms, with which each Philox op equals its eps-taking twin bit for bit."""
+    _check(lib.ugk_set_philox_exact(1 if exact else 0))
+
+
+def philox_exact() -> bool:
+    return bool(lib.ugk_get_philox_exact())
+
+
+def set_encoder_exact(exact: bool) -> None:
+    """Encoder backward, tokens with more than 32 rows in a chunk: False (default) blocked adds (64-row
+    blocks in row order, block sums in block order; deterministic); True one add per row in row order,
+    bit-identical to train_bnn.c."""
+    _check(lib.ugk_set_encoder_exact(1 if exact else 0))
+
+
+def encoder_exact() -> bool:
+    return bool(lib.ugk_get_encoder_exact())
 
 
 def param_count(cfg: Config) -> int:
@@ -508,6 +567,8 @@ MATH_FUNCTIONS.update({"sqrtf_any": 62})
 MATH_FUNCTIONS.update({"expf_nooverflow": 63})
 # the default (logistic-form) GELU and derivative; their "mismatches" are results outside the literal bar
 MATH_FUNCTIONS.update({"gelu_fast": 64, "gelu_grad_fast": 65})
+# the hardware-transcendental softplus and sigmoid of the Philox ops (the literal bar, likewise)
+MATH_FUNCTIONS.update({"softplus_fast": 66, "sigmoid_fast": 67})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
@@ -516,6 +577,14 @@ def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
     _check(lib.ugk_diag_math_mismatch(MATH_FUNCTIONS[fn], lo, min(count, (1 << 32) - lo), ctypes.byref(n),
                                       ctypes.byref(first)))
     return int(n.value), int(first.value)
+
+
+def diag_math_ulp(fn: str, lo: int = 0, count: int = 1 << 32):
+    """(largest ulp distance, input pattern where it occurs) of a fast form against its reference."""
+    d, at = ctypes.c_uint(0), ctypes.c_uint(0)
+    _check(lib.ugk_diag_math_ulp(MATH_FUNCTIONS[fn], lo, min(count, (1 << 32) - lo), ctypes.byref(d),
+                                 ctypes.byref(at)))
+    return int(d.value), int(at.value)
 
 
 def diag_math_eval(fn: str, out, inp, variant: int = 0) -> None:
