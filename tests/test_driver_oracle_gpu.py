@@ -14,7 +14,9 @@ kernels use are filled (the logits and probabilities, 823M floats at config 5, s
 Bars: the encoder output and the residual stream are bit-exact (bit-exact ops on identical inputs);
 each LayerNorm and GELU output is within the literal bar of one op (|gpu - cpu| <= 1e-6 + 1e-5
 |cpu|); the backward's activation gradients accumulate the 2L+1 LayerNorm backwards' dinp through
-the residual splits, and are held to 1e-4 relative / 1e-5 absolute; each LayerNorm's dweight /
+the residual splits, and are held to 2e-5 of the sum of the magnitudes of what was added into
+each (the literal bar of each LayerNorm and GELU term, plus the rounding of the sums), since the
+terms (~50) can cancel to ~1e-3; each LayerNorm's dweight /
 dbias (column sums over B*T rows, whose fp32 value depends on the order) to the scale-aware bar
 1e-5 * sum of |terms| of the other LayerNorm tests; dwte / dwpe equal the oracle's encoder_backward
 of the driver's own encoder gradient bit for bit (that gradient is held to the bar above), and no
@@ -129,22 +131,40 @@ def test_step_driver_matches_oracle_replay(gpu, oracle, name):
     cg, cga, ca = np.zeros(p["total"], np.float32), ga0.copy(), gacts
     GA = lambda off, n: cga[off:][:n]
     lns = []  # (dout, x, mean, rstd, dweight offset, dbias offset) of each LayerNorm backward
+    # The scale each activation gradient is held to: the sum of the magnitudes of what was added into
+    # it. A LayerNorm or GELU backward adds a term computed afresh from given inputs (its error is
+    # relative to itself); a residual split adds its dout, carrying dout's own scale. The fp32 sums
+    # of terms of magnitude ~50 can cancel to ~1e-3, so a bar relative to the result alone is wrong.
+    scale = np.zeros(used, np.float32)
+
+    def fresh(off, n, before):
+        scale[off:off + n] += np.abs(cga[off:off + n] - before)
 
     def ln_bwd(dinp, gs, bs, dout, x, mean, rstd):
+        before = GA(dinp, NB).copy()
         oracle.layernorm_backward(GA(dinp, NB), cg[gs:][:C], cg[bs:][:C], GA(dout, NB), ca[x:][:NB],
                                   params[gs:][:C], ca[mean:][:BT], ca[rstd:][:BT], B, T, C)
+        fresh(dinp, NB, before)
         lns.append((dout, x, mean, rstd, gs, bs))
+
+    def res_bwd(dx, dy, dout):
+        oracle.residual_backward(GA(dx, NB), GA(dy, NB), GA(dout, NB), NB)
+        carried = scale[dout:dout + NB] + np.abs(GA(dout, NB))
+        scale[dx:dx + NB] += carried
+        scale[dy:dy + NB] += carried
 
     last = AO(L - 1, "res1")
     ln_bwd(last, p["flng"], p["flnb"], a["flo"], last, a["flm"], a["flr"])
     for l in range(L - 1, -1, -1):
         st = a["enc"] if l == 0 else AO(l - 1, "res1")
-        oracle.residual_backward(GA(AO(l, "resa"), NB), GA(AO(l, "mlpo"), NB), GA(AO(l, "res1"), NB), NB)
+        res_bwd(AO(l, "resa"), AO(l, "mlpo"), AO(l, "res1"))
+        before = GA(AO(l, "fch"), 4 * NB).copy()
         oracle.gelu_backward(GA(AO(l, "fch"), 4 * NB), ca[AO(l, "fch"):][:4 * NB], GA(AO(l, "gelu"), 4 * NB),
                              4 * NB)
+        fresh(AO(l, "fch"), 4 * NB, before)
         ln_bwd(AO(l, "resa"), PO(l, "ln2g"), PO(l, "ln2b"), AO(l, "ln2o"), AO(l, "resa"), AO(l, "ln2m"),
                AO(l, "ln2r"))
-        oracle.residual_backward(GA(st, NB), GA(AO(l, "apr"), NB), GA(AO(l, "resa"), NB), NB)
+        res_bwd(st, AO(l, "apr"), AO(l, "resa"))
         ln_bwd(st, PO(l, "lng"), PO(l, "lnb"), AO(l, "lno"), st, AO(l, "lnm"), AO(l, "lnr"))
     oracle.encoder_backward(cg[:V * C], cg[V * C:V * C + maxT * C], GA(a["enc"], NB), inputs, B, T, C)
     hga, hg = host(tga[:used]), host(tg)
@@ -162,9 +182,12 @@ def test_step_driver_matches_oracle_replay(gpu, oracle, name):
         for k in ("resa", "res1"):
             hga[AO(l, k):AO(l, k) + NB] = 0
             cga[AO(l, k):AO(l, k) + NB] = 0
-    assert_close(hga, cga, "activation gradients", rtol=1e-4, atol=1e-5)
-    err = np.abs(hga.astype(np.float64) - cga) / (np.abs(cga) + 1e-3)
-    print(f"{name}: activation gradients within {float(err.max()):.2e} relative (+1e-3 floor)")
+    err = np.abs(hga.astype(np.float64) - cga)
+    bar = 2e-5 * scale.astype(np.float64) + 1e-6
+    bad = err > bar
+    assert not bad.any(), (f"activation gradients: {int(bad.sum())} beyond 2e-5 of their scale; worst at "
+                           f"{int(np.argmax(err - bar))}")
+    print(f"{name}: activation gradients within {float((err / (scale + 1e-30)).max()):.2e} of their scale")
     # LayerNorm dweight / dbias: the scale-aware bar
     for dout, x, mean, rstd, gs, bs in lns:
         d64 = ga0[dout:dout + NB].astype(np.float64).reshape(BT, C)  # the dense ops' gradients, as given

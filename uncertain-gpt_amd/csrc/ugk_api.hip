@@ -58,7 +58,7 @@ void region_sizes(const ugk_config &cfg, size_t out[kNumRegions]) {
   const int rows = cfg.B * cfg.T;
   const size_t slot = align_up(layernorm_backward_scratch(rows, cfg.C));
   out[kRegLn] = slot * (size_t)(2 * (cfg.L > 0 ? cfg.L : 0) + 1);
-  out[kRegEncoder] = encoder_backward_scratch(cfg.C);
+  out[kRegEncoder] = encoder_backward_scratch();
   out[kRegKl] = kl_forward_scratch();
   out[kRegSoftmax] = softmax_scratch(rows, cfg.V);
 }

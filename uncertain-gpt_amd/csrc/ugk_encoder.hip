@@ -149,26 +149,12 @@ struct EncTable {
   int *counters;   // [0] K3 work items taken, [1] large buckets, [2] sorted-id pool use, [3] K3 workgroups done
 };
 
-// Blocked adds of the large buckets (the default; see k_enc_bwd_blocked): a
-// bucket's rows, ascending, in blocks of kBlkRows; one wavefront per (block,
-// 256-channel slice) adds its block's rows in order; the last of a (bucket,
-// slice) adds the block sums in block order onto dwte.
-constexpr int kBlkRows = 64;
-// at least the sum over buckets of ceil(count / kBlkRows); a multiple of 4
-constexpr int kMaxBlocks = (kChunk / kBlkRows + kMaxLarge + 3) / 4 * 4;
-constexpr int kMaxSlices = 8;                              // 256-channel slices: C <= 2,048
-constexpr int kBlockedMaxC = kMaxSlices * kWave * 4;
-
 struct EncShared {
   int *rows;       // [kTableMax * kCap] row ids by (slot, rank < kCap)
   int *slot_of;    // [kChunk] slot of each row of the chunk (-1: skipped)
-  int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, slot} (K1 writes token and slot);
-                   // in the blocked mode K2 puts the bucket's first block in place of the slot
+  int4 *lmeta;     // [kMaxLarge] large bucket: {pool offset, size, token, slot} (K1 writes token and slot)
   int *pool;       // [kChunk] row ids of the large buckets, each bucket ascending
   int *list;       // [kChunk] slots claimed by K1 workgroup b at [256 b, 256 b + k), -1 after
-  int *blk_owner;  // [kMaxBlocks] blocked mode: the large bucket of each block
-  int *fin;        // [kMaxLarge * kMaxSlices] blocked mode: blocks done per (bucket, slice), zero between calls
-  float *bsum;     // [kMaxBlocks * C] blocked mode: the block sums
 };
 
 __device__ __forceinline__ unsigned hash_slot(int tok, unsigned mask, int shift) {
@@ -321,9 +307,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // (8 loads per round would take K2 from 48 to 58 registers, and from ten
 // wavefronts per SIMD to eight.)
 constexpr int kScanQ = 6;
-__device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int n, bool blocked) {
+__device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int n) {
   __shared__ int wt[kScanQ][kWavesPerBlock];
-  __shared__ int pool_base, bucket_cnt, blk_base;
+  __shared__ int pool_base, bucket_cnt;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int4 m = sh.lmeta[j];
@@ -333,12 +319,8 @@ __device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int
     pool_base = atomicAdd(&tb.counters[2], cnt);
     bucket_cnt = cnt;
     tb.slot[w] = kFree;
-    // the blocked mode's blocks of this bucket: a range of the chunk's block list
-    if (blocked) blk_base = atomicAdd(&tb.counters[4], (cnt + kBlkRows - 1) / kBlkRows);
   }
   __syncthreads();
-  if (blocked)
-    for (int k = threadIdx.x; k < (bucket_cnt + kBlkRows - 1) / kBlkRows; k += kBlock) sh.blk_owner[blk_base + k] = j;
   const int base = pool_base;
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   int run = 0;  // matches in the rounds before this one
@@ -383,7 +365,7 @@ __device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int
     run = off;
     __syncthreads();  // wt is rewritten by the next round
   }
-  if (threadIdx.x == 0) sh.lmeta[j] = make_int4(base, bucket_cnt, m.z, blocked ? blk_base : w);
+  if (threadIdx.x == 0) sh.lmeta[j] = make_int4(base, bucket_cnt, m.z, w);
 }
 
 // K2: one scan workgroup per possible large bucket in the first nscan
@@ -393,12 +375,11 @@ __device__ __forceinline__ void scan_large(EncTable tb, EncShared sh, int j, int
 // read it.
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void k_enc_bwd_add(EncTable tb, EncShared sh, float *__restrict__ dwte,
-                                                        const float *__restrict__ dout, int C, int n, int nscan,
-                                                        int blocked) {
+                                                        const float *__restrict__ dout, int C, int n, int nscan) {
   __shared__ unsigned lds[kWavesPerBlock * kCap];
   if ((int)blockIdx.x < nscan) {
     const int j = (int)blockIdx.x;
-    if (j < tb.counters[1]) scan_large(tb, sh, j, n, blocked != 0);  // K1 has counted them: the same in every thread
+    if (j < tb.counters[1]) scan_large(tb, sh, j, n);  // K1 has counted them: the same value in every thread
     return;
   }
   const int lane = threadIdx.x & (kWave - 1);
@@ -657,113 +638,98 @@ __global__ __launch_bounds__(kLargeThreads) void k_enc_bwd_large(EncTable tb, En
   }
 }
 
-// K3, blocked mode (C <= 2,048, float4 path): the large buckets' rows in
-// blocks of kBlkRows, ascending; work item (block, 256-channel slice), one
-// wavefront each, taken in a grid-stride loop. The wavefront adds its block's
-// rows in row order (32 rows' loads in flight), the first block onto dwte's
-// value, the others onto -0.0f (the identity of IEEE addition), and stores the
-// block sum with device-scope stores; once they are complete it counts the
-// block for its (bucket, slice), and the last block to arrive adds the block
-// sums in block order into dwte[token]:
-//   s_0 = ((dwte + d_0) + d_1) + ... + d_63,  s_k = rows 64k .. 64k + 63 in
-//   order, dwte = ((s_0 + s_1) + s_2) + ... .
-// The same inputs give the same bits on every run, and a bucket of at most 64
-// rows (one block) gets the CPU's order. Device-scope stores, s_waitcnt vmcnt(0) and a
-// device-scope counter publish the block sums (as for the LayerNorm column
-// sums in the main launch; no L2 write-back), and the last block reads them
-// with device-scope loads. Against the chain of k_enc_bwd_large (one dependent
-// add per row), a bucket of 2,348 rows becomes 37 independent blocks.
-constexpr int kBlockedGrid = 256;
-constexpr int kBlockedWaves = kBlock / kWave;
-constexpr int kBlkBatch = 32;
+// K3, blocked mode (the default): the same (large bucket, 64-channel slice)
+// work items as k_enc_bwd_large, but the bucket's rows, ascending, are cut
+// into blocks of kBlkRows, and the workgroup's 16 wavefronts add blocks
+// w, w + 16, ... in parallel, each block's rows in row order, all its 64
+// rows' loads in flight at once (one float per lane) and the next block's
+// row ids loaded meanwhile. The first block starts from dwte's value, the
+// others from -0.0f (the identity of IEEE addition); the block sums go to
+// LDS, and wavefront 0 adds them in block order:
+//   s_0 = ((dwte + d_0) + d_1) + ... + d_63,  s_k = d_64k + ... + d_64k+63,
+//   dwte = ((s_0 + s_1) + s_2) + ...
+// in rounds of at most kLdsBlocks blocks. The same inputs give the same bits
+// on every run, and a bucket of at most 64 rows gets the CPU's order. A
+// bucket of 2,348 rows is 37 blocks, at most three per wavefront, instead of
+// a chain of 2,348 dependent adds. No state crosses workgroups: the counters
+// and their reset are k_enc_bwd_large's.
+constexpr int kBlkRows = 64;
+constexpr int kBlockedWaves = 16;
+constexpr int kLdsBlocks = 256;
 
-__device__ __forceinline__ void st_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void add4_to(float4 &a, const float4 &b) {
-  a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
-}
-
-__global__ __launch_bounds__(kBlock) void k_enc_bwd_blocked(EncTable tb, EncShared sh, float *__restrict__ dwte,
-                                                            const float *__restrict__ dout, int C) {
-  // No large bucket: every counter is still zero, nothing to reset. Otherwise
-  // every workgroup reads the same count; the counters are reset only after
-  // the last workgroup has arrived below, past all its reads.
-  const int nblocks = tb.counters[4];
-  if (nblocks == 0) return;
+__device__ __forceinline__ void blocked_items(EncTable tb, EncShared sh, float *__restrict__ dwte,
+                                              const float *__restrict__ dout, int C, int nslices, int total,
+                                              float (*bs)[kWave], int *next_item_p) {
+  int &next_item = *next_item_p;
   const int lane = threadIdx.x & (kWave - 1);
-  const int C4 = C >> 2;
-  const int nsl = (C4 + kWave - 1) / kWave;
-  const int items = nblocks * nsl;
-  const int nwaves = (int)gridDim.x * kBlockedWaves;
-  const float4 *d4 = reinterpret_cast<const float4 *>(dout);
-  float4 *w4 = reinterpret_cast<float4 *>(dwte);
-  for (int item = (int)blockIdx.x * kBlockedWaves + (int)(threadIdx.x >> 6); item < items; item += nwaves) {
-    const int b = item / nsl, sl = item - b * nsl;
-    const int j = sh.blk_owner[b];
-    const int4 m = sh.lmeta[j];  // {pool offset, rows, token, first block}
-    const int r0 = (b - m.w) * kBlkRows;
-    const int nr = min(kBlkRows, m.y - r0);
-    const int id = sh.pool[m.x + r0 + min(lane, nr - 1)];  // this block's row ids, one per lane
-    const int c4 = sl * kWave + lane;
-    const bool on = c4 < C4;
-    const int cc = on ? c4 : C4 - 1;  // a valid column for the lanes past the row, never stored
-    const size_t trow = (size_t)m.z * C4 + cc;
-    float4 acc = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
-    if (b == m.w) acc = w4[trow];  // the first block starts from dwte's value
-    for (int q0 = 0; q0 < nr; q0 += kBlkBatch) {
-      float4 v[kBlkBatch];
+  const int wave = threadIdx.x >> 6;
+  for (int first = 1;; first = 0) {
+    // a workgroup's first item is its own index, later ones come from the counter
+    if (threadIdx.x == 0) next_item = first ? (int)blockIdx.x : (int)gridDim.x + atomicAdd(&tb.counters[0], 1);
+    __syncthreads();
+    const int wi = next_item;
+    __syncthreads();
+    if (wi >= total) break;
+    const int j = wi / nslices;
+    const int c = (wi % nslices) * kWave + lane;
+    const bool on = c < C;
+    const int cc = on ? c : 0;  // a valid column for the lanes past C, never stored
+    const int4 m = sh.lmeta[j];
+    const int *ids = sh.pool + m.x;
+    const int cnt = m.y;
+    const size_t trow = (size_t)m.z * C + cc;
+    const int nb = (cnt + kBlkRows - 1) / kBlkRows;
+    float t = -0.0f;  // wavefront 0's running total of the block sums
+    for (int r0 = 0; r0 < nb; r0 += kLdsBlocks) {
+      const int r1 = min(nb, r0 + kLdsBlocks);
+      int k = r0 + wave;
+      int id = k < r1 ? ids[k * kBlkRows + min(lane, cnt - k * kBlkRows - 1)] : 0;
+      for (; k < r1; k += kBlockedWaves) {
+        const int nr = min(kBlkRows, cnt - k * kBlkRows);
+        float v[kBlkRows];
 #pragma unroll
-      for (int q = 0; q < kBlkBatch; q++)
-        v[q] = ld_nt(d4 + (size_t)__builtin_amdgcn_readlane(id, min(q0 + q, nr - 1)) * C4 + cc);
+        for (int q = 0; q < kBlkRows; q++) v[q] = dout[(size_t)__builtin_amdgcn_readlane(id, min(q, nr - 1)) * C + cc];
+        const int kn = k + kBlockedWaves;  // the next block's row ids, loaded while these rows arrive
+        if (kn < r1) id = ids[kn * kBlkRows + min(lane, cnt - kn * kBlkRows - 1)];
+        float a = k == 0 ? dwte[trow] : -0.0f;
 #pragma unroll
-      for (int q = 0; q < kBlkBatch; q++)
-        if (q0 + q < nr) add4_to(acc, v[q]);  // the same for the whole wavefront
-    }
-    float *bs = sh.bsum + (size_t)b * C + (size_t)cc * 4;
-    if (on) {
-      st_dev(bs, acc.x); st_dev(bs + 1, acc.y); st_dev(bs + 2, acc.z); st_dev(bs + 3, acc.w);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    int old = 0;
-    if (lane == 0)
-      old = __hip_atomic_fetch_add(&sh.fin[j * kMaxSlices + sl], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0);
-    const int nb = (m.y + kBlkRows - 1) / kBlkRows;
-    if (old != nb - 1) continue;
-    if (lane == 0) __hip_atomic_store(&sh.fin[j * kMaxSlices + sl], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float4 t = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
-    for (int q0 = 0; q0 < nb; q0 += kBlkBatch) {
-      float4 v[kBlkBatch];
-#pragma unroll
-      for (int q = 0; q < kBlkBatch; q++) {
-        float *p = sh.bsum + (size_t)(m.w + min(q0 + q, nb - 1)) * C + (size_t)cc * 4;
-        v[q] = make_float4(ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3));
+        for (int q = 0; q < kBlkRows; q++)
+          if (q < nr) a += v[q];  // the same for the whole wavefront
+        bs[k - r0][lane] = a;
       }
-#pragma unroll
-      for (int q = 0; q < kBlkBatch; q++)
-        if (q0 + q < nb) add4_to(t, v[q]);
+      __syncthreads();
+      if (wave == 0)
+        for (int q = 0; q < r1 - r0; q++) t += bs[q][lane];
+      __syncthreads();  // bs is rewritten by the next round
     }
-    if (on) w4[trow] = t;
+    if (wave == 0 && on) dwte[trow] = t;
   }
-  // every thread of this workgroup is past its last read of the counters; the
-  // last workgroup to arrive zeroes them for the next chunk
+}
+
+__global__ __launch_bounds__(kBlockedWaves * kWave) void k_enc_bwd_blocked(EncTable tb, EncShared sh,
+                                                                           float *__restrict__ dwte,
+                                                                           const float *__restrict__ dout, int C,
+                                                                           int nslices) {
+  __shared__ float bs[kLdsBlocks][kWave];
+  __shared__ int next_item;
+  // As k_enc_bwd_large: with no large bucket every counter is still zero;
+  // otherwise the last workgroup to arrive resets them after all their reads.
+  const int total = tb.counters[1] * nslices;
+  if (total == 0) return;
+  blocked_items(tb, sh, dwte, dout, C, nslices, total, bs, &next_item);
   __syncthreads();
   if (threadIdx.x == 0 && atomicAdd(&tb.counters[3], 1) == (int)gridDim.x - 1) {
     tb.counters[0] = 0;
     tb.counters[1] = 0;
     tb.counters[2] = 0;
     tb.counters[3] = 0;
-    tb.counters[4] = 0;
   }
 }
 
-__global__ void k_enc_init(EncTable t, EncShared sh) {
+__global__ void k_enc_init(EncTable t) {
   const int h = blockIdx.x * kBlock + threadIdx.x;
   if (h < kTableMax) t.slot[h] = kFree;
-  if (h < 8) t.counters[h] = 0;
-  if (h < kMaxLarge * kMaxSlices) sh.fin[h] = 0;
+  if (h < 4) t.counters[h] = 0;
 }
 
 // ---- id guard -----------------------------------------------------------------
@@ -789,15 +755,9 @@ __global__ __launch_bounds__(kBlock) void k_ids_guard(int *ids, int n, int bound
 }
 
 size_t table_ints() { return (size_t)2 * kTableMax + 64; }  // slot words (2 ints each), counters
-size_t fixed_bytes() {
+size_t state_bytes() {
   return (size_t)kTableMax * kCap * sizeof(int) + (size_t)kChunk * sizeof(int) +
-         (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + table_ints() * sizeof(int) +
-         (size_t)kMaxBlocks * sizeof(int) + (size_t)kMaxLarge * kMaxSlices * sizeof(int);
-}
-// The fixed part, then the blocked mode's block sums for rows of C channels
-// (none above kBlockedMaxC, where the large buckets take the exact chain).
-size_t state_bytes(int C) {
-  return fixed_bytes() + (C <= kBlockedMaxC ? (size_t)kMaxBlocks * (size_t)C * sizeof(float) : 0);
+         (size_t)kMaxLarge * sizeof(int4) + 2 * (size_t)kChunk * sizeof(int) + table_ints() * sizeof(int);
 }
 
 // The state's arrays at their fixed places in its workspace region.
@@ -814,23 +774,14 @@ void carve(char *p, EncTable *t, EncShared *sh) {
   p += (size_t)kChunk * sizeof(int);
   t->slot = reinterpret_cast<u64 *>(p);  // 8-byte aligned: every size above is a multiple of 8
   t->counters = reinterpret_cast<int *>(p + (size_t)kTableMax * sizeof(u64));
-  p += table_ints() * sizeof(int);
-  sh->blk_owner = reinterpret_cast<int *>(p);
-  p += (size_t)kMaxBlocks * sizeof(int);
-  sh->fin = reinterpret_cast<int *>(p);
-  p += (size_t)kMaxLarge * kMaxSlices * sizeof(int);
-  sh->bsum = reinterpret_cast<float *>(p);  // 16-byte aligned: fixed_bytes() is a multiple of 16
 }
-static_assert(sizeof(int4) == 16 && kMaxBlocks % 4 == 0, "the block sums start on a 16-byte boundary");
 
-// Large buckets: 0 (the default) blocked adds where they apply (float4 path,
-// C <= 2,048), 1 the exact chain in row order.
+// Large buckets: 0 (the default) blocked adds, 1 the exact chain in row order.
 std::atomic<int> g_enc_exact{0};
 
 }  // namespace
 
-static_assert(kTableMax >= kMaxLarge * kMaxSlices, "k_enc_init clears the counters with its table threads");
-size_t encoder_backward_scratch(int C) { return state_bytes(C); }
+size_t encoder_backward_scratch() { return state_bytes(); }
 
 void set_encoder_exact(int exact) { g_enc_exact.store(exact ? 1 : 0); }
 int encoder_exact() { return g_enc_exact.load(); }
@@ -839,7 +790,7 @@ int launch_encoder_state_init(void *mem) {
   EncTable tb;
   EncShared sh;
   carve(static_cast<char *>(mem), &tb, &sh);
-  hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), tb, sh);
+  hipLaunchKernelGGL(k_enc_init, dim3(grid_for(kTableMax, kBlock)), dim3(kBlock), 0, stream(), tb);
   return check_launch("encoder_backward (state init)");
 }
 
@@ -917,7 +868,7 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
   // would find the memory's raw contents: such a first call is refused.
   const bool capturing = stream_capturing();
   bool fresh = false;
-  char *mem = static_cast<char *>(workspace(kRegEncoder, state_bytes(C), &fresh, capturing));
+  char *mem = static_cast<char *>(workspace(kRegEncoder, state_bytes(), &fresh, capturing));
   if (!mem) return UGK_ENOMEM;
   if (fresh && capturing)
     return set_error(UGK_EINVAL,
@@ -930,7 +881,7 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     if (int e = launch_encoder_state_init(mem)) return e;
   const bool vec = (C & 3) == 0 && aligned16(dwte) && aligned16(dwpe) && aligned16(dout);
   const int nslices = (C + kWave - 1) / kWave;
-  const bool blocked = !encoder_exact() && vec && C <= kBlockedMaxC;
+  const bool blocked = !encoder_exact();
   for (int c0 = 0; c0 < BT; c0 += kChunk) {
     const int n = BT - c0 < kChunk ? BT - c0 : kChunk;
     int tsize = 64, lg = 6;
@@ -952,23 +903,22 @@ int launch_encoder_backward(float *dwte, float *dwpe, const float *dout, const i
     const int nscan = n / (kCap + 1) + 1;
     const dim3 g2((unsigned)(nscan + ins_blocks * (kBlock / kWavesPerBlock)));
     if (vec)
-      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan,
-                         blocked ? 1 : 0);
+      hipLaunchKernelGGL(k_enc_bwd_add<true>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan);
     else
-      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan, 0);
+      hipLaunchKernelGGL(k_enc_bwd_add<false>, g2, dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C, n, nscan);
+    const int max_items = (n / (kCap + 1) + 1) * nslices;
+    const dim3 g3(max_items < kLargeGrid ? max_items : kLargeGrid);
     if (blocked) {
-      // one wavefront per (64-row block, 256-channel slice) of the large
-      // buckets, in a grid-stride loop; with no large bucket every workgroup
-      // returns at once
-      hipLaunchKernelGGL(k_enc_bwd_blocked, dim3(kBlockedGrid), dim3(kBlock), 0, stream(), tb, sh, dwte, dchunk, C);
+      // the same work items, each bucket's blocks spread over the workgroup's
+      // wavefronts; with no large bucket every workgroup returns at once
+      hipLaunchKernelGGL(k_enc_bwd_blocked, g3, dim3(kBlockedWaves * kWave), 0, stream(), tb, sh, dwte, dchunk, C,
+                         nslices);
       continue;
     }
     // one round of workgroups (one per CU: each stages 122 KB in LDS) takes
     // the (large bucket, channel slice) work items; with no large bucket
     // every workgroup goes straight to the counter reset
-    const int max_items = (n / (kCap + 1) + 1) * nslices;
-    hipLaunchKernelGGL(k_enc_bwd_large, dim3(max_items < kLargeGrid ? max_items : kLargeGrid),
-                       dim3(kLargeThreads), 0, stream(), tb, sh, dwte, dchunk, C, nslices);
+    hipLaunchKernelGGL(k_enc_bwd_large, g3, dim3(kLargeThreads), 0, stream(), tb, sh, dwte, dchunk, C, nslices);
   }
   return check_launch("encoder_backward");
 }

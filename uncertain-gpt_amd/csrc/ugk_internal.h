@@ -223,8 +223,8 @@ int launch_encoder_forward(float *out, const int *inp, const float *wte,
 int launch_encoder_backward(float *dwte, float *dwpe, const float *dout,
                             const int *inp, int B, int T, int C);
 // Buckets of more than 32 rows: 0 (default) blocked adds (64-row blocks, each
-// in row order, the block sums in block order; float4 path, C <= 2,048),
-// 1 one add per row in row order (bit-identical to train_bnn.c).
+// in row order, the block sums in block order), 1 one add per row in row
+// order (bit-identical to train_bnn.c).
 void set_encoder_exact(int exact);
 int encoder_exact();
 // Clears the encoder backward's bucket state at mem (encoder_backward_scratch()
@@ -240,7 +240,7 @@ int *ids_error_word();
 
 // Workspace sizes.
 size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
-size_t encoder_backward_scratch(int C);              // the bucket state (and the blocked mode's sums at C)
+size_t encoder_backward_scratch();                   // the bucket state (fixed)
 size_t kl_forward_scratch();                         // partial sums and result (fixed)
 size_t softmax_scratch(int rows, int V);             // row statistics of rows too long for one workgroup
 
