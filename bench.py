@@ -106,14 +106,20 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_enc_ln_fwd_vec", "encoder_layernorm_forward"),
     ("k_enc_bwd_insert", "encoder_backward (insert + dwpe)"),
     ("k_enc_bwd_add", "encoder_backward (add)"),
-    ("k_enc_bwd_large", "encoder_backward (large buckets)"),
-    ("k_map_vec4<ugk::(anonymous namespace)::BayesSampleEps>", "bayes_sample (eps stored)"),
-    ("k_map_vec4<ugk::(anonymous namespace)::BayesSample>", "bayes_sample"),
-    ("k_map_vec4<ugk::(anonymous namespace)::BayesBackwardPhilox>", "bayes_backward_philox"),
+    ("k_enc_bwd_large", "encoder_backward (large buckets, exact order)"),
+    ("k_enc_bwd_blocked", "encoder_backward (large buckets, blocked)"),
+    ("k_ids_guard", "id guard"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesSampleEps<true>", "bayes_sample (eps stored)"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesSampleEps<false>", "bayes_sample (eps stored, glibc-exact)"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesSample<true>", "bayes_sample"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesSample<false>", "bayes_sample (glibc-exact)"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesBackwardPhilox<true>", "bayes_backward_philox"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BayesBackwardPhilox<false>", "bayes_backward_philox (glibc-exact)"),
     ("k_map_vec4<ugk::(anonymous namespace)::BayesBackward>", "bayes_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::KlBackward>", "kl_backward"),
     ("k_map_vec4<ugk::(anonymous namespace)::AdamW>", "adamw_update"),
-    ("k_map_vec4<ugk::(anonymous namespace)::BbbStepFused>", "bbb_step_fused"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BbbStepFused<true>", "bbb_step_fused"),
+    ("k_map_vec4<ugk::(anonymous namespace)::BbbStepFused<false>", "bbb_step_fused (glibc-exact)"),
     ("k_softmax_xent<", "softmax_crossentropy"),
     ("k_softmax_xent_split<", "softmax_crossentropy"),
     ("k_softmax_stats", "softmax_crossentropy (row statistics)"),
@@ -128,8 +134,9 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
 ]
 PMC_TRAFFIC = os.path.join(ROOT, "profiles", "pmc_traffic_cfg5.json")
 # in-step op name -> the prefix of its kernel's short name in the PMC summary
-PMC_KEY = {"layernorm_residual_backward (main)": "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true, 1, false>",
-           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false, 0, false>",
+PMC_KEY = {"layernorm_residual_backward (main)":
+           "layernorm_backward (main, row teams) <3, 4, 4, true, 3, true, 1, false, false>",
+           "layernorm_backward (main)": "layernorm_backward (main, row teams) <3, 4, 2, false, 1, false, 0, false, false>",
            "residual_layernorm_forward": "layernorm_forward <3, true", "layernorm_forward": "layernorm_forward <3, false",
            "layernorm column sums (batched)": "layernorm_backward (batched column sums)"}
 
@@ -494,9 +501,9 @@ def main():
 
     def enc_distinct_bytes(name, rows, Tn, distinct):
         Nn = rows * C
-        if name.startswith("encoder_backward"):  # dout once, RMW of the touched wte and wpe rows, ids
+        if "encoder_backward" in name:  # dout once, RMW of the touched wte and wpe rows, ids
             return 4 * Nn + 8 * C * distinct + 8 * C * Tn + 4 * rows
-        extra = 4 * Nn + 8 * rows + 8 * C if name.startswith("encoder_layernorm") else 0
+        extra = 4 * Nn + 8 * rows + 8 * C if "encoder_layernorm" in name else 0
         return 4 * C * (distinct + Tn) + 4 * Nn + 4 * rows + extra
 
     def enc_record(table, name, abytes, ms, launches, n_sets, rows, Tn, distinct, extra):
@@ -505,7 +512,7 @@ def main():
         afrac = round(abytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)
         info = {"distinct_tokens": distinct, "bytes_algorithmic": abytes, "frac_algorithmic": afrac,
                 "bytes_distinct": dbytes, "frac_distinct": dfrac, **extra}
-        if name.startswith("encoder_backward"):
+        if "encoder_backward" in name:
             record(table, name, abytes, ms, launches, n_sets, info)
         else:
             record(table, name, dbytes, ms, launches, n_sets,

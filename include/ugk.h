@@ -81,10 +81,10 @@ int ugk_encoder_backward(float *dwte, float *dwpe, const float *dout,
 
 /* The order of the encoder backward's adds for a token with more than 32 rows
  * in a chunk, for later calls from any thread: 0 (the default) in 64-row
- * blocks as above (on the float4 path with C <= 2,048; elsewhere always 1);
- * nonzero one add per row in ascending order, bit-identical to train_bnn.c,
- * a serial chain as long as the token's rows. No counterpart in the
- * reference, whose GPU kernel adds with atomicAdd in no fixed order. */
+ * blocks as above, the blocks of a token spread over a workgroup's 16
+ * wavefronts; nonzero one add per row in ascending order, bit-identical to
+ * train_bnn.c, a serial chain as long as the token's rows. No counterpart in
+ * the reference, whose GPU kernel adds with atomicAdd in no fixed order. */
 int ugk_set_encoder_exact(int exact);
 int ugk_get_encoder_exact(void);
 
