@@ -334,7 +334,10 @@ int ugk_version(void);
  * form) against fn 8 and 9's glibc-exact expressions, counting results
  * outside |a - b| <= 1e-6 + 1e-5 |b|; 66 and 67 the hardware-transcendental
  * softplus and sigmoid of the Philox ops (their default form) against the
- * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise. */
+ * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise; 68 and 69
+ * the Box-Muller transform's logf (normal x > 0) and cosf (0 <= x < 2^17)
+ * against the device library's logf and cosf (the library's own functions
+ * outside those domains). */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

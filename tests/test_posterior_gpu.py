@@ -146,6 +146,16 @@ def test_fast_transcendentals_exhaustive(gpu, fn):
     assert d <= 8, (fn, d, hex(at))  # 5 on MI355X
 
 
+@pytest.mark.parametrize("fn", ["logf_normal", "cosf_small"])
+def test_box_muller_math_is_the_device_library(gpu, fn):
+    """The Box-Muller transform's logf (for normal x > 0) and cosf (for 0 <= x < 2^17) are the device
+    library's sequences without its cases for other arguments: the same bits as the library's logf and
+    cosf on every one of the 2^32 float inputs (the library's functions outside those domains), so eps
+    is unchanged by them. u1 = u01(w) lies in [2^-33, 1] and the angle fl(2 pi u2) in (0, 2 pi]."""
+    n, first = gpu.diag_math_mismatch(fn)
+    assert n == 0, (fn, n, hex(first))
+
+
 # ---- the ops ----------------------------------------------------------------------------
 
 SIZES = [1, 3, 5, 4096 + 3, (1 << 20) + 1]

@@ -57,9 +57,16 @@ struct BayesSample : MapOp {
   static constexpr int kLoads = 2, kStores = 1;
   static constexpr bool kTable = !kFast;
   static constexpr int kUnroll = 1;
+  // eps for all four of a thread's elements while mu and rho load: with the
+  // branches of the fast softplus, 296-299 against 349 us (select form, eps in
+  // place) over 124.4M; the glibc-exact form 402 against 427 us
+  static constexpr bool kPre = true;
+  typedef float Pre;
   typedef PhiloxParams Params;
-  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
-    st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * ugk_dev_philox_normal(p.seed, p.step, i);
+  __device__ static float pre(size_t i, const Params &p) { return ugk_dev_philox_normal(p.seed, p.step, i); }
+  __device__ static void apply_pre(const float *ld, float *st, const uint64_t *tab, size_t, const Params &,
+                                   float eps) {
+    st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * eps;
   }
 };
 
@@ -69,8 +76,8 @@ template <bool kFast>
 struct BayesSampleEps : BayesSample<kFast> {
   static constexpr int kStores = 2;
   typedef PhiloxParams Params;
-  __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
-    const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
+  __device__ static void apply_pre(const float *ld, float *st, const uint64_t *tab, size_t, const Params &,
+                                   float eps) {
     st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * eps;
     st[1] = eps;
   }
@@ -97,10 +104,13 @@ struct BayesBackwardPhilox : MapOp {
   // for the fast one (506 us at 512, 515 at 256, 484 at 1024 over 124.4M)
   static constexpr int kUnroll = 1, kThreads = kFast ? 1024 : 512;
   static constexpr bool kTable = !kFast;
+  // eps drawn in place: drawing all four of a thread's eps while the streams
+  // load (kPre) measured 488-510 against 483-496 us. The glibc-exact form
+  // takes the library's logf and cosf (the same bits): 485-487 against 496 us.
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0];
-    const float eps = ugk_dev_philox_normal(p.seed, p.step, i);
+    const float eps = ugk_dev_philox_normal<!kFast>(p.seed, p.step, i);
     st[0] = ld[2] + g;
     st[1] = ld[3] + g * eps * sigmoid_of<kFast>(ld[1], tab);
   }
@@ -175,6 +185,12 @@ struct BbbStepFused : MapOp {
   static constexpr int kLoads = 7, kStores = 8;
   static constexpr bool kTable = !kFast;
   static constexpr int kUnroll = 1;
+  // The fast form fits 8 wavefronts per SIMD in its registers but runs best at
+  // 6 (24 KiB of LDS per 256-thread workgroup leaves room for 6 per CU):
+  // 1338-1419 us at 8, 1327-1407 at 7, 1325-1345 at 6, 1337-1345 at 5 and
+  // 1355 at 4 over 124.4M (cold, two boxes). The glibc-exact form is best
+  // at 8 (1422 us; 1444 at 6).
+  static constexpr unsigned kLdsReserve = kFast ? 24576u : 0u;
   struct Params {
     unsigned long long seed;
     int step;
@@ -182,6 +198,39 @@ struct BbbStepFused : MapOp {
     float klw;
     AdamParams adam;
   };
+  // Both draws while the streams load (kPre) in the glibc-exact form: 1407
+  // against 1436 us in place; the fast form draws in place (1324-1378 against
+  // 1339-1391 us with kPre).
+  static constexpr bool kPre = !kFast;
+  struct Pre {
+    float eps, eps_next;
+  };
+  __device__ static Pre pre(size_t i, const Params &p) {
+    return Pre{ugk_dev_philox_normal(p.seed, p.step, i), ugk_dev_philox_normal(p.seed, p.step + 1, i)};
+  }
+  __device__ static void apply_pre(const float *ld, float *st, const uint64_t *tab, size_t, const Params &p,
+                                   const Pre &e) {
+    const float g = ld[0], r = ld[1], mm = ld[2];
+    const float sg = sigmoid_of<kFast>(r, tab);
+    float gmu = g;
+    float grho = g * e.eps * sg;
+    if (p.klw > 0.0f) {
+      const float sigma = softplus_of<kFast>(r, tab);
+      gmu += p.klw * div_by(mm, p.sp2);
+      grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
+    }
+    float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
+    const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
+    const float rho_new = adamw_one(r, grho, m2, v2, p.adam);
+    st[0] = 0.0f;
+    st[1] = mu_new;
+    st[2] = rho_new;
+    st[3] = m1;
+    st[4] = v1;
+    st[5] = m2;
+    st[6] = v2;
+    st[7] = mu_new + softplus_of<kFast>(rho_new, tab) * e.eps_next;
+  }
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0], r = ld[1], mm = ld[2];
     const float sg = sigmoid_of<kFast>(r, tab);

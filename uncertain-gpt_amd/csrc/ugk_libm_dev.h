@@ -128,6 +128,47 @@ __device__ __forceinline__ float ugk_dev_sqrtf_large(float x) {
   return t;
 }
 
+// The device library's logf (ROCm-Device-Libs ocml, as hipcc builds it for
+// gfx950) for a normal finite x > 0: the hardware log2 (v_log_f32) times ln 2
+// held as a float pair (0x1.62e42ep-1 + 0x1.efa39ep-25), the product's low
+// part recovered with a fused multiply-add. The library also scales inputs
+// below 2^-126 by 2^32 first (subtracting 32 ln 2 after) and passes an
+// infinite log2 through; neither applies on this domain, the Box-Muller
+// transform's u1 in [2^-33, 1]. Bit-identical to logf on every normal finite
+// x > 0 (ugk_diag.hip fn 68).
+__device__ __forceinline__ float ugk_dev_logf_normal(float x) {
+  const float l = __builtin_amdgcn_logf(x);
+  const float hi = l * 0x1.62e42ep-1f;
+  const float lo = __builtin_fmaf(l, 0x1.efa39ep-25f, __builtin_fmaf(l, 0x1.62e42ep-1f, -hi));
+  return hi + lo;
+}
+
+// The device library's cosf (ocml, as hipcc builds it for gfx950) on its
+// small-argument path, 0 <= x < 2^17: k = rint(x 2/pi), the remainder
+// x - k pi/2 by three fused multiply-adds (Cody-Waite, pi/2 in three
+// parts), the sine and cosine polynomials of the remainder, and the quadrant
+// k mod 4 choosing cos, -sin, -cos or sin. Larger x take the library's
+// Payne-Hanek reduction and infinities its NaN case, neither of which the
+// Box-Muller angle 2 pi u2 in (0, 2 pi] reaches. Bit-identical to cosf on
+// 0 <= x < 2^17 (ugk_diag.hip fn 69).
+__device__ __forceinline__ float ugk_dev_cosf_small(float x) {
+  const float kf = __builtin_rintf(x * 0x1.45f306p-1f);
+  const int q = (int)kf;
+  float r = __builtin_fmaf(kf, -0x1.921fb4p0f, x);
+  r = __builtin_fmaf(kf, -0x1.4442d0p-24f, r);
+  r = __builtin_fmaf(kf, -0x1.846988p-48f, r);
+  const float s = r * r;
+  float p = __builtin_fmaf(s, -0x1.983304p-13f, 0x1.110388p-7f);
+  p = __builtin_fmaf(s, p, -0x1.55553ap-3f);
+  const float sn = __builtin_fmaf(r, s * p, r);
+  float c = __builtin_fmaf(s, 0x1.aea668p-16f, -0x1.6c9e76p-10f);
+  c = __builtin_fmaf(s, c, 0x1.5557eep-5f);
+  c = __builtin_fmaf(s, c, -0x1.000008p-1f);
+  const float cs = __builtin_fmaf(s, c, 1.0f);
+  const float v = (q & 1) ? -sn : cs;
+  return __uint_as_float(__float_as_uint(v) ^ (((uint32_t)q << 30) & 0x80000000u));
+}
+
 // sqrtf for any input: ugk_dev_sqrtf_large on its domain, the library's
 // sqrtf (which rescales) for the rare tiny or negative inputs (fn 62).
 __device__ __forceinline__ float ugk_dev_sqrtf(float x) {
@@ -406,56 +447,75 @@ __device__ __forceinline__ float ugk_fast_gelu_grad(float x) {
 // rounding error and the constant's tail, by fma), then one correction
 // e (1 + dt ln 2) after the hardware 2^t (v_exp_f32). x is first clamped
 // from below to -104, where e^x is below every float (NaN passes through).
-// The hardware 2^t flushes results below 2^-126 to zero, so below t = -64
-// it takes 2^(t + 64) 2^-64, whose multiply rounds into the subnormals. Where
-// 2^t overflows, the correction (inf + inf * c) would be NaN for c < 0: the
-// overflow is kept, as is a NaN x.
+// The hardware 2^t flushes results below 2^-126 to zero; with kSubnormal,
+// below t = -64 it takes 2^(t + 64) 2^-64 instead, whose multiply rounds into
+// the subnormals (a branch, which wavefronts of ordinary arguments skip).
+// Where 2^t overflows, the correction (inf + inf * c) would be NaN for c < 0:
+// with kKeepOverflow the overflow is kept, as is a NaN x.
 constexpr float kUgkLog2e = 1.44269502162933349609f;       // log2(e) rounded to float
 constexpr float kUgkLog2eLo = 1.92596299112661746887e-8f;  // log2(e) - kUgkLog2e
 constexpr float kUgkLn2 = 0.693147180559945309417f;
 
-__device__ __forceinline__ float ugk_fast_exp(float x) {
+template <bool kSubnormal, bool kKeepOverflow>
+__device__ __forceinline__ float ugk_fast_exp_t(float x) {
   const float xc = x < -104.0f ? -104.0f : x;
   const float t = xc * kUgkLog2e;
   const float dt = __builtin_fmaf(xc, kUgkLog2e, -t) + xc * kUgkLog2eLo;
-  const bool tiny = t < -64.0f;
-  const float e = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t) * (tiny ? 0x1p-64f : 1.0f);
+  float e = __builtin_amdgcn_exp2f(t);
+  if (kSubnormal && t < -64.0f) {
+    asm volatile("");  // keeps the rare case a branch rather than a second 2^t and a select
+    e = __builtin_amdgcn_exp2f(t + 64.0f) * 0x1p-64f;
+  }
   const float r = __builtin_fmaf(e, dt * kUgkLn2, e);
-  return r != r ? e : r;
+  return (kKeepOverflow && r != r) ? e : r;
 }
+
+__device__ __forceinline__ float ugk_fast_exp(float x) { return ugk_fast_exp_t<true, true>(x); }
 
 // softplus(x) = log1p(e^x) (train_bnn.c:814-816's formula; x for x > 20 as
 // there). log1p(e): below e = 1/16 its series to e^6 (the remainder is below
 // e^7/7, a tenth of an ulp); above, Goldberg's form log(u) e / (u - 1)
 // with u = 1 + e rounded, whose quotient cancels the rounding of u, and the
-// hardware log2 (v_log_f32) times ln 2. Within a few ulp of glibc's
-// log1pf(expf(x)) and within 1e-6 absolute / 1e-5 relative of it on every
-// float input (ugk_diag.hip fn 66); about 20 VALU instructions, with three
-// hardware transcendentals, against some 70 for the glibc-exact form.
+// hardware log2 (v_log_f32) times ln 2. The two forms are branches: the
+// arguments of a wavefront (a run of rho) mostly lie on one side of
+// x = ln(1/16). e^x's overflow need not be kept: above x = 20 the result is x.
+// Within a few ulp of glibc's log1pf(expf(x)) and within 1e-6 absolute /
+// 1e-5 relative of it on every float input (ugk_diag.hip fn 66); about 20
+// VALU instructions on one branch, with two hardware transcendentals, against
+// some 70 for the glibc-exact form.
 __device__ __forceinline__ float ugk_fast_softplus(float x) {
-  const float e = ugk_fast_exp(x);
-  float p = __builtin_fmaf(e, -1.0f / 6.0f, 0.2f);
-  p = __builtin_fmaf(e, p, -0.25f);
-  p = __builtin_fmaf(e, p, 1.0f / 3.0f);
-  p = __builtin_fmaf(e, p, -0.5f);
-  const float series = e * __builtin_fmaf(e, p, 1.0f);
-  const float u = 1.0f + e;
-  const float goldberg = __builtin_amdgcn_logf(u) * kUgkLn2 * (e * __builtin_amdgcn_rcpf(u - 1.0f));
-  const float r = e < 0.0625f ? series : goldberg;
+  const float e = ugk_fast_exp_t<true, false>(x);
+  float r;
+  if (e < 0.0625f) {
+    float p = __builtin_fmaf(e, -1.0f / 6.0f, 0.2f);
+    p = __builtin_fmaf(e, p, -0.25f);
+    p = __builtin_fmaf(e, p, 1.0f / 3.0f);
+    p = __builtin_fmaf(e, p, -0.5f);
+    r = e * __builtin_fmaf(e, p, 1.0f);
+  } else {
+    const float u = 1.0f + e;
+    r = __builtin_amdgcn_logf(u) * kUgkLn2 * (e * __builtin_amdgcn_rcpf(u - 1.0f));
+  }
   return x > 20.0f ? x : r;
 }
 
 // sigmoid(x) = 1 / (1 + e^-x) (train_bnn.c:820-822) with the hardware
 // reciprocal (v_rcp_f32); x is clamped to [-104, 104] first (NaN passes), so
-// that e^-x is 0 or inf at the ends, as there. The hardware reciprocal flushes
-// results below 2^-126 to zero, so a divisor above 2^64 is scaled by 2^-64
-// first and the quotient by 2^-64 after. Within a few ulp of the glibc-exact
-// form and within the literal bar of it everywhere (fn 67).
+// that e^-x is 0 or inf at the ends, as there. Below 2^-64, e^-x leaves
+// 1 + e^-x at 1 whether or not it is flushed, so the exponential skips the
+// subnormal case. The hardware reciprocal flushes results below 2^-126 to
+// zero, so a divisor above 2^64 (x below -44) is scaled by 2^-64 first and
+// the quotient by 2^-64 after (a branch, rarely taken). Within a few ulp of
+// the glibc-exact form and within the literal bar of it everywhere (fn 67).
 __device__ __forceinline__ float ugk_fast_sigmoid(float x) {
   const float xc = x > 104.0f ? 104.0f : (x < -104.0f ? -104.0f : x);
-  const float d = 1.0f + ugk_fast_exp(-xc);
-  const bool big = d > 0x1p64f;
-  return __builtin_amdgcn_rcpf(big ? d * 0x1p-64f : d) * (big ? 0x1p-64f : 1.0f);
+  const float d = 1.0f + ugk_fast_exp_t<false, true>(-xc);
+  float q = __builtin_amdgcn_rcpf(d);
+  if (d > 0x1p64f) {
+    asm volatile("");  // a branch, not a second reciprocal and a select
+    q = __builtin_amdgcn_rcpf(d * 0x1p-64f) * 0x1p-64f;
+  }
+  return q;
 }
 
 __device__ __forceinline__ float ugk_dev_softplusf(float x) {

@@ -16,8 +16,16 @@
 //   kLoads, kStores          stream counts;
 //   kTable                   stage expf's 2^(i/32) table in LDS (tab != null);
 //   kUnroll, kThreads        float4 slots per thread, threads per workgroup;
+//   kLdsReserve              bytes of LDS each workgroup reserves without
+//                            using them (0: none), which caps the workgroups
+//                            resident on a CU (160 KiB of LDS each);
 //   Params                   per-launch scalars passed by value;
-//   apply(ld, st, tab, i, p) the per-element body; i is the element index.
+//   apply(ld, st, tab, i, p) the per-element body; i is the element index;
+//   kPre, Pre, pre(i, p)     optionally (kPre true), the part of the body that
+//                            reads no stream (a Philox draw): the kernel
+//                            computes it for all of a thread's elements while
+//                            their loads are in flight and hands it to
+//                            apply_pre(ld, st, tab, i, p, pre) instead.
 #pragma once
 
 #include "ugk_internal.h"
@@ -31,6 +39,9 @@ struct MapOp {
   static constexpr bool kTable = false;
   static constexpr int kUnroll = 2;
   static constexpr int kThreads = kBlock;
+  static constexpr unsigned kLdsReserve = 0;
+  static constexpr bool kPre = false;
+  struct Pre {};
 };
 
 template <class Op>
@@ -58,6 +69,17 @@ __global__ __launch_bounds__(Op::kThreads) void k_map_vec4(Streams<Op> s, size_t
       for (int l = 0; l < Op::kLoads; l++) v[u][l] = ld_nt(reinterpret_cast<const float4 *>(s.ld[l]) + i);
     }
   }
+  typename Op::Pre pre[kU][4];
+  if constexpr (Op::kPre) {
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const size_t i = base + (size_t)u * kT;
+      if (i < n4) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) pre[u][e] = Op::pre(4 * i + e, s.p);
+      }
+    }
+  }
 #pragma unroll
   for (int u = 0; u < kU; u++) {
     const size_t i = base + (size_t)u * kT;
@@ -69,7 +91,12 @@ __global__ __launch_bounds__(Op::kThreads) void k_map_vec4(Streams<Op> s, size_t
         in[2][l] = v[u][l].z; in[3][l] = v[u][l].w;
       }
 #pragma unroll
-      for (int e = 0; e < 4; e++) Op::apply(in[e], out[e], tab, 4 * i + e, s.p);
+      for (int e = 0; e < 4; e++) {
+        if constexpr (Op::kPre)
+          Op::apply_pre(in[e], out[e], tab, 4 * i + e, s.p, pre[u][e]);
+        else
+          Op::apply(in[e], out[e], tab, 4 * i + e, s.p);
+      }
 #pragma unroll
       for (int o = 0; o < Op::kStores; o++)
         st_nt(reinterpret_cast<float4 *>(s.st[o]) + i, make_float4(out[0][o], out[1][o], out[2][o], out[3][o]));
@@ -89,7 +116,10 @@ __global__ __launch_bounds__(kBlock) void k_map_scalar(Streams<Op> s, size_t beg
     float in[Op::kLoads], out[Op::kStores];
 #pragma unroll
     for (int l = 0; l < Op::kLoads; l++) in[l] = s.ld[l][i];
-    Op::apply(in, out, tab, i, s.p);
+    if constexpr (Op::kPre)
+      Op::apply_pre(in, out, tab, i, s.p, Op::pre(i, s.p));
+    else
+      Op::apply(in, out, tab, i, s.p);
 #pragma unroll
     for (int o = 0; o < Op::kStores; o++) s.st[o][i] = out[o];
   }
@@ -105,7 +135,7 @@ int run_map(const Streams<Op> &s, size_t n, const char *name) {
   if (vec && n >= 4) {
     const size_t n4 = n / 4;
     launch(k_map_vec4<Op>, dim3(grid_for(n4, (size_t)Op::kThreads * Op::kUnroll)),
-                       dim3(Op::kThreads), 0, s, n4);
+                       dim3(Op::kThreads), Op::kLdsReserve, s, n4);
     done = n4 * 4;
   }
   if (done < n) {

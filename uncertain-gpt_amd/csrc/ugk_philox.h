@@ -93,15 +93,24 @@ __device__ __forceinline__ UgkPhilox4 ugk_dev_philox_words_uniform(unsigned long
 // Box-Muller, cosine branch: sqrt(-2 ln u1) * cos(2 pi u2), with 2 pi rounded
 // to float and the product rounded before the cosine. u1 in [2^-33, 1] puts
 // -2 ln u1 at -0 or in [1.1e-7, 46]: inside the domain of the correctly
-// rounded square root without rescaling.
+// rounded square root without rescaling. u1 is a normal float and 2 pi u2 lies
+// in (0, 2 pi], so logf and cosf are the device library's own sequences for
+// those domains, without its cases for subnormal, infinite and large
+// arguments (the same bits). kLibrary calls the library's logf and cosf
+// themselves, which one kernel runs faster with (the glibc-exact form of
+// bayes_backward_philox).
+template <bool kLibrary = false>
 __device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
   const float u1 = ugk_u01(a), u2 = ugk_u01(b);
-  return ugk_dev_sqrtf_large(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+  const float l = kLibrary ? logf(u1) : ugk_dev_logf_normal(u1);
+  const float x = 6.28318530717958647692f * u2;
+  return ugk_dev_sqrtf_large(-2.0f * l) * (kLibrary ? cosf(x) : ugk_dev_cosf_small(x));
 }
 
 // eps(seed, step, index); seed and step must be the same across the wavefront.
+template <bool kLibrary = false>
 __device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {
   const UgkPhilox4 o = ugk_dev_philox_words_uniform(seed, step, index);
-  return ugk_dev_box_muller(o.w[0], o.w[1]);
+  return ugk_dev_box_muller<kLibrary>(o.w[0], o.w[1]);
 }
 #endif

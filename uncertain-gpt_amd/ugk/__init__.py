@@ -569,6 +569,8 @@ MATH_FUNCTIONS.update({"expf_nooverflow": 63})
 MATH_FUNCTIONS.update({"gelu_fast": 64, "gelu_grad_fast": 65})
 # the hardware-transcendental softplus and sigmoid of the Philox ops (the literal bar, likewise)
 MATH_FUNCTIONS.update({"softplus_fast": 66, "sigmoid_fast": 67})
+# the Box-Muller transform's logf and cosf on their domains, against the device library's
+MATH_FUNCTIONS.update({"logf_normal": 68, "cosf_small": 69})
 
 
 def diag_math_mismatch(fn: str, lo: int = 0, count: int = 1 << 32):
