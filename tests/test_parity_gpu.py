@@ -403,6 +403,13 @@ def enc_case(gpu, oracle, B, T, C, V, inp, seed, reps=1, modes=("exact", "blocke
             assert (np.abs(got_w - dwte) <= 1e-5 * scale).all(), "blocked dwte beyond the scale-aware bar"
             e_gpu, e_cpu = np.abs(got_w - f64), np.abs(dwte - f64)
             assert e_gpu.max() <= e_cpu.max() + 1e-6 * scale.max(), "blocked dwte less accurate than the CPU's"
+            counts = np.bincount(inp[valid], minlength=V)
+            big = np.nonzero(counts > ENC_BLK)[0]  # rows whose order differs from the CPU's
+            if r == 0 and big.size:
+                g_t, c_t = got_w.reshape(-1, C)[big], dwte.reshape(-1, C)[big]
+                frac = (np.abs(g_t - c_t) <= 1e-6 + 1e-5 * np.abs(c_t)).mean()
+                literal_bar.record(f"encoder_backward dwte (blocked order), the {big.size} rows of tokens with more "
+                                   f"than {ENC_BLK} rows, B={B} T={T} C={C}", frac)
 
 
 def test_encoder_repeated_token_case(gpu, oracle):
