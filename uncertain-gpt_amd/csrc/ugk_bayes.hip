@@ -208,50 +208,37 @@ struct BbbStepFused : MapOp {
   __device__ static Pre pre(size_t i, const Params &p) {
     return Pre{ugk_dev_philox_normal(p.seed, p.step, i), ugk_dev_philox_normal(p.seed, p.step + 1, i)};
   }
+  // The step, with eps(k) the draw for step + k (k = 0 the gradient's, 1 the
+  // next sample's), evaluated where the step uses it.
+  template <class Eps>
+  __device__ static void body(const float *ld, float *st, const uint64_t *tab, const Params &p, Eps eps) {
+    const float g = ld[0], r = ld[1], mm = ld[2];
+    const float sg = sigmoid_of<kFast>(r, tab);
+    float gmu = g;
+    float grho = g * eps(0) * sg;
+    if (p.klw > 0.0f) {
+      const float sigma = softplus_of<kFast>(r, tab);
+      gmu += p.klw * div_by(mm, p.sp2);
+      grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
+    }
+    float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
+    const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
+    const float rho_new = adamw_one(r, grho, m2, v2, p.adam);
+    st[0] = 0.0f;
+    st[1] = mu_new;
+    st[2] = rho_new;
+    st[3] = m1;
+    st[4] = v1;
+    st[5] = m2;
+    st[6] = v2;
+    st[7] = mu_new + softplus_of<kFast>(rho_new, tab) * eps(1);
+  }
   __device__ static void apply_pre(const float *ld, float *st, const uint64_t *tab, size_t, const Params &p,
                                    const Pre &e) {
-    const float g = ld[0], r = ld[1], mm = ld[2];
-    const float sg = sigmoid_of<kFast>(r, tab);
-    float gmu = g;
-    float grho = g * e.eps * sg;
-    if (p.klw > 0.0f) {
-      const float sigma = softplus_of<kFast>(r, tab);
-      gmu += p.klw * div_by(mm, p.sp2);
-      grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
-    }
-    float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
-    const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
-    const float rho_new = adamw_one(r, grho, m2, v2, p.adam);
-    st[0] = 0.0f;
-    st[1] = mu_new;
-    st[2] = rho_new;
-    st[3] = m1;
-    st[4] = v1;
-    st[5] = m2;
-    st[6] = v2;
-    st[7] = mu_new + softplus_of<kFast>(rho_new, tab) * e.eps_next;
+    body(ld, st, tab, p, [&](int k) { return k ? e.eps_next : e.eps; });
   }
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
-    const float g = ld[0], r = ld[1], mm = ld[2];
-    const float sg = sigmoid_of<kFast>(r, tab);
-    float gmu = g;
-    float grho = g * ugk_dev_philox_normal(p.seed, p.step, i) * sg;
-    if (p.klw > 0.0f) {
-      const float sigma = softplus_of<kFast>(r, tab);
-      gmu += p.klw * div_by(mm, p.sp2);
-      grho += p.klw * (div_by(sigma, p.sp2) - 1.0f / sigma) * sg;
-    }
-    float m1 = ld[3], v1 = ld[4], m2 = ld[5], v2 = ld[6];
-    const float mu_new = adamw_one(mm, gmu, m1, v1, p.adam);
-    const float rho_new = adamw_one(r, grho, m2, v2, p.adam);
-    st[0] = 0.0f;
-    st[1] = mu_new;
-    st[2] = rho_new;
-    st[3] = m1;
-    st[4] = v1;
-    st[5] = m2;
-    st[6] = v2;
-    st[7] = mu_new + softplus_of<kFast>(rho_new, tab) * ugk_dev_philox_normal(p.seed, p.step + 1, i);
+    body(ld, st, tab, p, [&](int k) { return ugk_dev_philox_normal(p.seed, p.step + k, i); });
   }
 };
 
