@@ -215,8 +215,12 @@ int ugk_crossentropy_softmax_backward_zeroed(float *dlogits, const float *probs,
  * and within 1e-6 absolute / 1e-5 relative of train_bnn.c:814-822 on every
  * float input), nonzero the glibc-exact forms of the eps-taking ops, with which
  * each Philox op equals its eps-taking twin fed the same eps bit for bit. The
- * eps draw itself is the same in both. No counterpart in the reference, whose
- * GPU arms build these ops with --use_fast_math (Makefile:13). */
+ * eps draw's radius sqrt(-2 ln u1) follows the same setting: the hardware log2
+ * and square root by default, the device library's logf and a correctly
+ * rounded square root otherwise (both within a few ulp of train_bnn.c's eps;
+ * they differ from each other in the last place on some draws). No
+ * counterpart in the reference, whose GPU arms build these ops with
+ * --use_fast_math (Makefile:13). */
 int ugk_set_philox_exact(int exact);
 int ugk_get_philox_exact(void);
 
@@ -337,7 +341,10 @@ int ugk_version(void);
  * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise; 68 and 69
  * the Box-Muller transform's logf (normal x > 0) and cosf (0 <= x < 2^17)
  * against the device library's logf and cosf (the library's own functions
- * outside those domains). */
+ * outside those domains); 70 and 71 the Box-Muller radius sqrt(-2 ln u1) for
+ * u1 in [2^-33, 1] as the Philox ops' default form (hardware log2 and square
+ * root) and their glibc-exact form compute it, against the double radius
+ * rounded to float (ugk_diag_math_ulp only). */
 
 /* Over the inputs whose bit patterns are lo, lo+1, ..., lo+count-1, count
  * those where the kernels' SIMD-shaped math differs from its line-by-line

@@ -6,9 +6,11 @@ bbb_step_fused).
 The Philox ops split into an exact part and a float part:
   * the integer stream (Philox4x32-10 and u01) is bit-exact, checked on the device against the
     Random123 known-answer vectors and the oracle;
-  * the Box-Muller transform calls the device logf and cosf. Over every u01 value the stream can
-    produce (all 79,691,777 of them) both stay within 2 ulp of the host glibc; eps is then within
-    8 ulp of the oracle's;
+  * the Box-Muller transform calls the device logf and cosf (the glibc-exact form) or takes its
+    radius from the hardware log2 and square root (the default form). Over every u01 value the
+    stream can produce (all 79,691,777 of them) logf and cosf stay within 2 ulp of the host glibc,
+    and over every float in u01's range both radii stay within 2 ulp of the correctly rounded one;
+    eps is then within 8 ulp of the oracle's in both forms;
   * with ugk_set_philox_exact(1), everything downstream of eps is bit-exact given the device's eps
     (each Philox op equals its eps-taking twin fed with the eps the device drew);
   * by default the Philox ops take their softplus and sigmoid in the hardware-transcendental form,
@@ -150,10 +152,25 @@ def test_fast_transcendentals_exhaustive(gpu, fn):
 def test_box_muller_math_is_the_device_library(gpu, fn):
     """The Box-Muller transform's logf (for normal x > 0) and cosf (for 0 <= x < 2^17) are the device
     library's sequences without its cases for other arguments: the same bits as the library's logf and
-    cosf on every one of the 2^32 float inputs (the library's functions outside those domains), so eps
-    is unchanged by them. u1 = u01(w) lies in [2^-33, 1] and the angle fl(2 pi u2) in (0, 2 pi]."""
+    cosf on every one of the 2^32 float inputs (the library's functions outside those domains), so the
+    glibc-exact form's eps is the library's. u1 = u01(w) lies in [2^-33, 1] and the angle fl(2 pi u2) in
+    (0, 2 pi]."""
     n, first = gpu.diag_math_mismatch(fn)
     assert n == 0, (fn, n, hex(first))
+
+
+@pytest.mark.parametrize("fn", ["bm_radius_fast", "bm_radius"])
+def test_box_muller_radius_ulp(gpu, fn):
+    """The radius sqrt(-2 ln u1) of the Box-Muller transform on every float u1 in [2^-33, 1] (a superset
+    of u01's image) against the double radius rounded to float: the default form (hardware log2 and
+    square root) and the glibc-exact form (the library's logf, the correctly rounded root). Both are
+    within 2 ulp on MI355X (the rounding of -2 ln u1 carries through the root)."""
+    lo = int(np.array([2.0 ** -33], np.float32).view(np.uint32)[0])
+    hi = int(np.array([1.0], np.float32).view(np.uint32)[0])
+    d, at = gpu.diag_math_ulp(fn, lo, hi - lo + 1)
+    x = np.array([at], np.uint32).view(np.float32)[0]
+    print(f"{fn}: at most {d} ulp from the correctly rounded radius (at u1 = {x!r})")
+    assert d <= 2, (fn, d, x)
 
 
 # ---- the ops ----------------------------------------------------------------------------

@@ -50,6 +50,13 @@ struct PhiloxParams {
   int step;
 };
 
+// eps(seed, step, i) in the op's form: the hardware radius in the default form,
+// the library's logf and square root in the glibc-exact one.
+template <bool kFast>
+__device__ __forceinline__ float draw(unsigned long long seed, int step, size_t i) {
+  return kFast ? ugk_dev_philox_normal_fast(seed, step, i) : ugk_dev_philox_normal(seed, step, i);
+}
+
 // train_bnn_gpu.cu:93-97 (k_bayes_sample): w = mu + softplus(rho) * eps(seed,
 // step, i). Loads mu, rho.
 template <bool kFast>
@@ -63,7 +70,7 @@ struct BayesSample : MapOp {
   static constexpr bool kPre = true;
   typedef float Pre;
   typedef PhiloxParams Params;
-  __device__ static float pre(size_t i, const Params &p) { return ugk_dev_philox_normal(p.seed, p.step, i); }
+  __device__ static float pre(size_t i, const Params &p) { return draw<kFast>(p.seed, p.step, i); }
   __device__ static void apply_pre(const float *ld, float *st, const uint64_t *tab, size_t, const Params &,
                                    float eps) {
     st[0] = ld[0] + softplus_of<kFast>(ld[1], tab) * eps;
@@ -110,7 +117,7 @@ struct BayesBackwardPhilox : MapOp {
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0];
-    const float eps = ugk_dev_philox_normal<!kFast>(p.seed, p.step, i);
+    const float eps = kFast ? draw<true>(p.seed, p.step, i) : ugk_dev_philox_normal<true>(p.seed, p.step, i);
     st[0] = ld[2] + g;
     st[1] = ld[3] + g * eps * sigmoid_of<kFast>(ld[1], tab);
   }
@@ -206,7 +213,7 @@ struct BbbStepFused : MapOp {
     float eps, eps_next;
   };
   __device__ static Pre pre(size_t i, const Params &p) {
-    return Pre{ugk_dev_philox_normal(p.seed, p.step, i), ugk_dev_philox_normal(p.seed, p.step + 1, i)};
+    return Pre{draw<kFast>(p.seed, p.step, i), draw<kFast>(p.seed, p.step + 1, i)};
   }
   // The step, with eps(k) the draw for step + k (k = 0 the gradient's, 1 the
   // next sample's), evaluated where the step uses it.
@@ -238,7 +245,7 @@ struct BbbStepFused : MapOp {
     body(ld, st, tab, p, [&](int k) { return k ? e.eps_next : e.eps; });
   }
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
-    body(ld, st, tab, p, [&](int k) { return ugk_dev_philox_normal(p.seed, p.step + k, i); });
+    body(ld, st, tab, p, [&](int k) { return draw<kFast>(p.seed, p.step + k, i); });
   }
 };
 

@@ -36,7 +36,10 @@ namespace {
 // counting results outside that bar; 68: ugk_dev_logf_normal on normal
 // finite x > 0 and 69: ugk_dev_cosf_small on 0 <= x < 2^17, the Box-Muller
 // transform's logf and cosf (the library's logf and cosf elsewhere; reference:
-// the library's logf and cosf).
+// the library's logf and cosf); 70 and 71 the Box-Muller radius
+// sqrt(-2 ln u1) on u1 in [2^-33, 1] (the reference elsewhere), 70 as the
+// Philox ops' default form computes it (hardware log2 and square root), 71 as
+// the glibc-exact form does, against the double radius rounded to float.
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -83,6 +86,10 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 67) return ugk_fast_sigmoid(x);
   if (FN == 68) return (x >= 0x1p-126f && x < __builtin_inff()) ? ugk_dev_logf_normal(x) : logf(x);
   if (FN == 69) return (x >= 0.0f && x < 0x1p17f) ? ugk_dev_cosf_small(x) : cosf(x);
+  if (FN == 70 || FN == 71) {
+    if (!(x >= 0x1p-33f && x <= 1.0f)) return (float)sqrt(-2.0 * log((double)x));
+    return FN == 70 ? ugk_dev_bm_radius_fast(x) : ugk_dev_sqrtf_large(-2.0f * ugk_dev_logf_normal(x));
+  }
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
 
@@ -93,6 +100,7 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 3 || (FN >= 10 && FN < 14)) return ugk_tanhf(x);
   if (FN == 4 || FN == 66) return ugk_softplusf(x);
   if (FN == 67) return 1.0f / (1.0f + ugk_expf(-x));
+  if (FN == 70 || FN == 71) return (float)sqrt(-2.0 * log((double)x));
   if (FN == 5 || FN == 68) return logf(x);
   if (FN == 6 || FN == 69) return cosf(x);
   if (FN == 7) return (float)sqrt((double)x);
@@ -193,7 +201,7 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 70);
+         (fn >= 40 && fn < 72);
 }
 
 // The largest distance in ulp (as ordered integers) between the kernels' math
@@ -264,7 +272,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
       UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
       UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62) UGK_MM(63)
-      UGK_MM(64) UGK_MM(65) UGK_MM(66) UGK_MM(67) UGK_MM(68) UGK_MM(69)
+      UGK_MM(64) UGK_MM(65) UGK_MM(66) UGK_MM(67) UGK_MM(68) UGK_MM(69) UGK_MM(70) UGK_MM(71)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -293,7 +301,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
     UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
     UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62) UGK_EV(63)
-    UGK_EV(64) UGK_EV(65) UGK_EV(66) UGK_EV(67) UGK_EV(68) UGK_EV(69)
+    UGK_EV(64) UGK_EV(65) UGK_EV(66) UGK_EV(67) UGK_EV(68) UGK_EV(69) UGK_EV(70) UGK_EV(71)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");
@@ -341,7 +349,8 @@ extern "C" int ugk_diag_layernorm_tail(int on) {
 
 extern "C" int ugk_diag_math_ulp(int fn, unsigned lo, unsigned long long count, unsigned *max_ulp,
                                  unsigned *at) {
-  if (fn < 63 || fn > 67) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: fn must be 63-67");
+  if (fn < 63 || fn > 71 || fn == 68 || fn == 69)
+    return set_error(UGK_EINVAL, "ugk_diag_math_ulp: fn must be 63-67, 70 or 71");
   if (!max_ulp || !at) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: NULL result pointer");
   if (count > (1ull << 32) - lo) return set_error(UGK_EINVAL, "ugk_diag_math_ulp: range beyond 2^32");
   unsigned long long h = 0, *d = nullptr;
@@ -356,7 +365,7 @@ extern "C" int ugk_diag_math_ulp(int fn, unsigned lo, unsigned long long count, 
     switch (fn) {
 #define UGK_UL(f) \
   case f: hipLaunchKernelGGL(k_math_ulp<f>, grid, block, 0, stream(), (unsigned long long)lo, count, d); break;
-      UGK_UL(63) UGK_UL(64) UGK_UL(65) UGK_UL(66) UGK_UL(67)
+      UGK_UL(63) UGK_UL(64) UGK_UL(65) UGK_UL(66) UGK_UL(67) UGK_UL(70) UGK_UL(71)
 #undef UGK_UL
     }
     rc = check_launch("ugk_diag_math_ulp");

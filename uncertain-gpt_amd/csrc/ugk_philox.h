@@ -107,10 +107,28 @@ __device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
   return ugk_dev_sqrtf_large(-2.0f * l) * (kLibrary ? cosf(x) : ugk_dev_cosf_small(x));
 }
 
+// The same transform with the radius from the hardware log2 and square root
+// (v_log_f32, v_sqrt_f32), as a fast-math build computes it: -2 ln u1 as
+// log2(u1) times -2 ln 2, rounded once, and a square root within 1 ulp; the
+// cosine as above. The Philox ops' default form.
+__device__ __forceinline__ float ugk_dev_bm_radius_fast(float u1) {
+  return __builtin_amdgcn_sqrtf((-2.0f * __builtin_amdgcn_logf(u1)) * 0x1.62e43p-1f);
+}
+
+__device__ __forceinline__ float ugk_dev_box_muller_fast(uint32_t a, uint32_t b) {
+  const float u1 = ugk_u01(a), u2 = ugk_u01(b);
+  return ugk_dev_bm_radius_fast(u1) * ugk_dev_cosf_small(6.28318530717958647692f * u2);
+}
+
 // eps(seed, step, index); seed and step must be the same across the wavefront.
 template <bool kLibrary = false>
 __device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {
   const UgkPhilox4 o = ugk_dev_philox_words_uniform(seed, step, index);
   return ugk_dev_box_muller<kLibrary>(o.w[0], o.w[1]);
+}
+
+__device__ __forceinline__ float ugk_dev_philox_normal_fast(unsigned long long seed, int step, uint64_t index) {
+  const UgkPhilox4 o = ugk_dev_philox_words_uniform(seed, step, index);
+  return ugk_dev_box_muller_fast(o.w[0], o.w[1]);
 }
 #endif
