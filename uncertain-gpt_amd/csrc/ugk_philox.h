@@ -12,7 +12,8 @@
 // The integer part is exact on host and device. The float part uses the
 // device logf and cosf (AMD's device library), which round differently from
 // the host glibc in the last place on a small share of inputs, and a
-// correctly rounded square root.
+// correctly rounded square root; or, in the ops' default (fast-math) form, the
+// radius from the hardware log2 and square root (ugk_dev_box_muller_fast).
 #pragma once
 
 #include <stdint.h>
