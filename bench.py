@@ -676,14 +676,15 @@ def main():
         for nm, nb, fn in post_plan:
             ms, l_, k_ = time_cold(mk_post, 44 * n, fn)
             record(posterior, nm, nb * n, ms, l_, k_)
-        # the Philox ops with the glibc-exact softplus/sigmoid (ugk_set_philox_exact(1)), beside the
-        # default hardware-transcendental form timed above
+        # the Philox ops in their glibc-exact form (ugk_set_philox_exact(1): glibc-exact softplus and
+        # sigmoid, the device library's logf and a correctly rounded root in the Box-Muller radius),
+        # beside the default hardware-transcendental form timed above
         ugk.set_philox_exact(True)
         try:
             for nm, nb, fn in post_plan:
                 if nm in ("bayes_sample", "bayes_backward_philox", "bbb_step_fused"):
                     ms, l_, k_ = time_cold(mk_post, 44 * n, fn)
-                    record(posterior, f"{nm} (glibc-exact softplus/sigmoid)", nb * n, ms, l_, k_)
+                    record(posterior, f"{nm} (glibc-exact form)", nb * n, ms, l_, k_)
         finally:
             ugk.set_philox_exact(False)
         kl_out = ctypes.c_double(0.0)
