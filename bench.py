@@ -43,7 +43,7 @@ Printed JSON line (the last line of stdout):
     head         softmax + cross-entropy forward and backward over B*T rows of V = 50257
     posterior    the ops around the step over the same n parameters, cold
     cpu_baseline the reference's own train_bnn.c ops (oracle/_ref, else this repo's
-                 bit-identical restatement) on one pinned host core: median of 5 runs per
+                 bit-identical restatement) on one pinned host core: median of 9 runs per
                  op at the config-5 step shapes (composed by launch count) and at configs
                  2-4, with nproc, the CPU model and the glibc version
 """
@@ -781,9 +781,9 @@ def host_facts():
 
 def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes):
     """The reference's CPU ops (train_bnn.c, single-threaded) on one pinned core: the median of
-    5 runs of each op at the config-5 step shapes, composed by launch count into a step, and at
+    9 runs of each op at the config-5 step shapes, composed by launch count into a step, and at
     the shapes of configs 2-4 (GELU/residual over 50.3M values on a 1/8 slice, scaled;
-    materialize on a 1/8 slice, scaled). About 10-20 s of CPU work in all."""
+    materialize on a 1/8 slice, scaled). About 10 s of CPU work in all."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, REF_SO
@@ -796,7 +796,7 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes):
     try:
         rng = np.random.Generator(np.random.Philox(key=7))
         f = lambda n: rng.standard_normal(n, dtype=np.float32)
-        reps = 5
+        reps = 9
         t_sample = 0.0
 
         def med(fn, scale=1.0):
@@ -808,7 +808,7 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes):
                 ts.append(time.perf_counter() - t0)
             t_sample += sum(ts)
             ts.sort()
-            return ts[reps // 2] * scale, ts[1] * scale, ts[3] * scale
+            return ts[reps // 2] * scale, ts[reps // 4] * scale, ts[3 * reps // 4] * scale
 
         # config 5, the step's shapes
         N = B * T * C
@@ -883,7 +883,7 @@ def cpu_baseline(B, T, C, V, L, n_mat, per, count, total_bytes, moved_bytes):
             "per_op_ms": {k: round(v * 1e3, 2) for k, v in t_op.items()},
             "per_op_ms_p25_p75": {k: [round(a * 1e3, 2), round(b * 1e3, 2)] for k, (a, b) in spread.items()},
             "configs_ms": {k: round(v * 1e3, 3) for k, v in cfgs.items()},
-            "sample": "train_bnn.c's ops on one pinned core, median of 5 runs each: at the config-5 step "
+            "sample": "train_bnn.c's ops on one pinned core, median of 9 runs each: at the config-5 step "
                       "shapes (materialize on a 1/8 slice, scaled) composed by launch count per step, and at the "
                       "config 2-4 shapes (config-3 ops on a 1/8 slice, scaled); "
                       f"{t_sample:.1f} s of CPU work"}
