@@ -127,7 +127,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_xent_softmax_bwd_flat4<true>", "crossentropy_softmax_backward (dlogits not read)"),
     ("k_xent_softmax_bwd<true>", "crossentropy_softmax_backward (dlogits not read)"),
     ("k_xent_softmax_bwd", "crossentropy_softmax_backward"),
-    ("k_kl_partial", "kl_forward (partial sums)"),
+    ("k_kl_partial<true>", "kl_forward (partial sums)"),
+    ("k_kl_partial<false>", "kl_forward (partial sums, glibc-exact)"),
     ("k_kl_final", "kl_forward (final sum)"),
     ("__amd_rocclr_copyBuffer", "calibration copy 1 GiB"),
     ("k_stream<", "stream ceiling probe"),
@@ -688,9 +689,16 @@ def main():
         finally:
             ugk.set_philox_exact(False)
         kl_out = ctypes.c_double(0.0)
-        ms, l_, k_ = time_cold(mk_post, 44 * n, lambda d: chk(lib.ugk_kl_forward(
-            ctypes.byref(kl_out), P_(d["mu"]), P_(d["rho"]), n, 0.1)))
-        record(posterior, "kl_forward (incl. result copy + sync)", 8 * n, ms, l_, k_)
+        kl_fn = lambda d: chk(lib.ugk_kl_forward(ctypes.byref(kl_out), P_(d["mu"]), P_(d["rho"]), n, 0.1))
+        ms, l_, k_ = time_cold(mk_post, 44 * n, kl_fn)
+        record(posterior, "kl_forward (incl. the result's wait)", 8 * n, ms, l_, k_)
+        # its glibc-exact form (ugk_set_kl_exact(1)), beside the default one
+        ugk.set_kl_exact(True)
+        try:
+            ms, l_, k_ = time_cold(mk_post, 44 * n, kl_fn)
+            record(posterior, "kl_forward (incl. the result's wait, glibc-exact form)", 8 * n, ms, l_, k_)
+        finally:
+            ugk.set_kl_exact(False)
 
     # ---- softmax + cross-entropy at the head shape, B*T rows of V logits (not part of the step)
     head = {}

@@ -253,10 +253,22 @@ int ugk_bayes_backward_philox(float *dmu, float *drho, const float *dw,
 /* train_bnn.c:941-957. *kl (a HOST pointer) = sum over i of
  * log(sp/sigma_i) + (sigma_i^2 + mu_i^2)/(2 sp^2) - 1/2 in double, with
  * sigma_i = softplus(rho_i) and sp = sigma_prior. Summed in a fixed tree
- * order (deterministic; within double rounding of the CPU's sequential sum).
- * Waits for the library stream. */
+ * order (deterministic). The float sigma_i follows ugk_set_kl_exact: by
+ * default the hardware-transcendental softplus while rho_i >= -80 (within
+ * 8 ulp of train_bnn.c's sigma_i, so each term within
+ * 8 * 2^-23 * (1 + sigma_i^2/sp^2) of the CPU's), otherwise train_bnn.c's
+ * own sigma_i (the total then within double rounding of the CPU's sequential
+ * sum). Waits for the library stream. */
 int ugk_kl_forward(double *kl, const float *mu, const float *rho, size_t n,
                    float sigma_prior);
+
+/* Form of ugk_kl_forward's softplus for later calls from any thread: 0 (the
+ * default) the hardware-transcendental form where sigma is a normal float,
+ * nonzero the glibc-exact form throughout. No counterpart in the reference,
+ * whose GPU KL (k_kl_stats, train_bnn_gpu.cu:225-250) is built with
+ * --use_fast_math (Makefile:13) and takes each term in float. */
+int ugk_set_kl_exact(int exact);
+int ugk_get_kl_exact(void);
 
 /* train_bnn.c:966-979 / train_bnn_gpu.cu:111-119 (k_kl_backward).
  * dmu += weight * mu / sp^2; drho += weight * (sigma/sp^2 - 1/sigma) *

@@ -1,6 +1,7 @@
 """GPU parity of the posterior-update ops of libugk.so (called through the C-ABI) against the
-CPU oracle: bayes_backward, kl_backward, adamw_update (bit-exact), kl_forward (double, within
-summation-order rounding), and the Philox ops (bayes_sample, bayes_backward_philox,
+CPU oracle: bayes_backward, kl_backward, adamw_update (bit-exact), kl_forward (double; within
+summation-order rounding with ugk_set_kl_exact(1), within the bar its softplus implies by
+default), and the Philox ops (bayes_sample, bayes_backward_philox,
 bbb_step_fused).
 
 The Philox ops split into an exact part and a float part:
@@ -208,7 +209,7 @@ def test_bayes_backward_kl_backward_adamw(gpu, oracle, n, offset):
         assert_bits(host(tv), v_, f"adamw t={t} v")
 
 
-def test_golden_posterior_on_gpu(gpu):
+def test_golden_posterior_on_gpu(gpu, oracle):
     import os
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "posterior.npz")
     with np.load(path, allow_pickle=False) as z:
@@ -222,8 +223,14 @@ def test_golden_posterior_on_gpu(gpu):
     gpu.kl_backward(k_dmu, k_drho, dev(d["mu"]), dev(d["rho"]), n, 0.1, 1.0 / 300000.0)
     assert_bits(host(k_dmu), d["kmu"], "golden kl_backward dmu")
     assert_bits(host(k_drho), d["krho"], "golden kl_backward drho")
-    kl = gpu.kl_forward(dev(d["mu"]), dev(d["rho"]), n, 0.1)
+    gpu.set_kl_exact(True)
+    try:
+        kl = gpu.kl_forward(dev(d["mu"]), dev(d["rho"]), n, 0.1)
+    finally:
+        gpu.set_kl_exact(False)
     assert abs(kl - float(d["kl"])) <= 1e-12 * abs(float(d["kl"]))
+    kl = gpu.kl_forward(dev(d["mu"]), dev(d["rho"]), n, 0.1)
+    assert abs(kl - float(d["kl"])) <= kl_fast_bar(oracle, d["rho"], 0.1) + 1e-12 * abs(float(d["kl"]))
     for t in (1, 7):
         tp, tm, tv = dev(d["mu"]), dev(d["m0"]), dev(d["v0"])
         gpu.adamw_update(tp, dev(d["dw"]), tm, tv, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01)
@@ -232,8 +239,36 @@ def test_golden_posterior_on_gpu(gpu):
         assert_bits(host(tv), d[f"v{t}"], f"golden adamw v t={t}")
 
 
+@pytest.fixture
+def kl_exact(gpu):
+    """The glibc-exact softplus in kl_forward for the duration of a test."""
+    gpu.set_kl_exact(True)
+    try:
+        yield
+    finally:
+        gpu.set_kl_exact(False)
+
+
+KL_FAST_ULP = 8  # the fast softplus against the glibc-exact one, over every float input (fn 66)
+
+
+def kl_fast_terms_bar(oracle, rho, sp):
+    """Per term, how far the default form's KL term may lie from train_bnn.c's. The default form's
+    sigma' = sigma (1 + d) with |d| <= 8 ulp / sigma <= 8 * 2^-23 while rho >= -80 (sigma a normal
+    float); the term log(sp/sigma) + (sigma^2 + mu^2)/(2 sp^2) - 1/2 then moves by
+    -log(1 + d) + sigma^2 (2 d + d^2)/(2 sp^2), at most |d| (1 + sigma^2/sp^2) to first order (the
+    factor 1.001 covers the second). Below -80 the exact form is taken: no difference."""
+    sigma, _ = oracle_softplus_sigmoid(oracle, np.ascontiguousarray(rho, np.float32))
+    d = KL_FAST_ULP * 2.0 ** -23
+    return np.where(np.asarray(rho) >= -80.0, 1.001 * d * (1.0 + sigma ** 2 / np.float64(sp) ** 2), 0.0)
+
+
+def kl_fast_bar(oracle, rho, sp):
+    return float(kl_fast_terms_bar(oracle, rho, sp).sum())
+
+
 @pytest.mark.parametrize("n", [1, 1000, 5_000_003])
-def test_kl_forward(gpu, oracle, n):
+def test_kl_forward(gpu, oracle, kl_exact, n):
     mu, rho, _, _, _, _ = posterior_inputs(920 + n, n)
     want = oracle.kl_forward(mu, rho, n, 0.1)
     tm, tr = dev(mu), dev(rho)
@@ -243,16 +278,40 @@ def test_kl_forward(gpu, oracle, n):
     assert gpu.kl_forward(tm, tr, 0, 0.1) == 0.0
 
 
-def test_kl_forward_terms(gpu, oracle):
-    """Single KL terms across the range of sigma = softplus(rho): subnormal and zero sigma
-    (rho below -87 and -103), the x > 20 shortcut, every cell of the logarithm's table
-    (sigma with all 128 leading fraction patterns), against the oracle's double terms."""
-    rho = [-200.0, -104.0, -100.0, -90.0, -88.0, -50.0, -5.0, -1.0, 0.0, 0.5, 5.0, 20.0, 20.5, 100.0, 1e30]
+@pytest.mark.parametrize("n", [1, 1000, 5_000_003])
+def test_kl_forward_fast(gpu, oracle, n):
+    """The default form (hardware-transcendental softplus) against train_bnn.c's KL: within the sum
+    of the per-term bars above plus the exact form's summation-order bar, deterministic, and within
+    the literal bar |a - b| <= 1e-6 + 1e-5 |b|."""
+    assert not gpu.kl_exact()
+    mu, rho, _, _, _, _ = posterior_inputs(920 + n, n)
+    want = oracle.kl_forward(mu, rho, n, 0.1)
+    tm, tr = dev(mu), dev(rho)
+    got = gpu.kl_forward(tm, tr, n, 0.1)
+    bar = kl_fast_bar(oracle, rho, 0.1)
+    print(f"kl_forward n={n}: default form {abs(got - want):.3g} from train_bnn.c (bar {bar:.3g}, "
+          f"{abs(got - want) / abs(want):.3g} relative)")
+    assert abs(got - want) <= bar + 1e-10 * abs(want), (got, want, bar)
+    assert abs(got - want) <= 1e-6 + 1e-5 * abs(want), (got, want)
+    assert gpu.kl_forward(tm, tr, n, 0.1) == got  # fixed summation order
+    assert gpu.kl_forward(tm, tr, 0, 0.1) == 0.0
+
+
+def kl_term_inputs():
+    rho = [-200.0, -104.0, -100.0, -90.0, -88.0, -80.5, -79.5, -50.0, -5.0, -1.0, 0.0, 0.5, 5.0, 20.0,
+           20.5, 100.0, 1e30]
     g = gen.rng(77)
     rho += list(np.log(np.expm1(np.float64(1.0) + (np.arange(128) + g.random(128)) / 128.0)).astype(np.float32))
     rho += list(gen.normal(g, (64,), -5.0, 3.0))
     mu = gen.normal(g, (len(rho),), 0, 0.05)
-    rho = np.array(rho, np.float32)
+    return mu, np.array(rho, np.float32)
+
+
+def test_kl_forward_terms(gpu, oracle, kl_exact):
+    """Single KL terms across the range of sigma = softplus(rho): subnormal and zero sigma
+    (rho below -87 and -103), the x > 20 shortcut, every cell of the logarithm's table
+    (sigma with all 128 leading fraction patterns), against the oracle's double terms."""
+    mu, rho = kl_term_inputs()
     for k in range(len(rho)):
         want = oracle.kl_forward(mu[k:k + 1], rho[k:k + 1], 1, 0.1)
         got = gpu.kl_forward(dev(mu[k:k + 1]), dev(rho[k:k + 1]), 1, 0.1)
@@ -260,6 +319,26 @@ def test_kl_forward_terms(gpu, oracle):
             assert got == want, (k, rho[k], got, want)
         else:
             assert abs(got - want) <= 1e-14 * max(1.0, abs(want)), (k, rho[k], got, want)
+
+
+def test_kl_forward_terms_fast(gpu, oracle):
+    """The same single terms in the default form: within the per-term bar where rho >= -80, and the
+    exact form's term below (subnormal and zero sigma, where a few ulp would be a large share of
+    sigma, take the glibc-exact softplus)."""
+    mu, rho = kl_term_inputs()
+    bars = kl_fast_terms_bar(oracle, rho, 0.1)
+    worst = 0.0
+    for k in range(len(rho)):
+        want = oracle.kl_forward(mu[k:k + 1], rho[k:k + 1], 1, 0.1)
+        got = gpu.kl_forward(dev(mu[k:k + 1]), dev(rho[k:k + 1]), 1, 0.1)
+        if np.isinf(want):
+            assert got == want, (k, rho[k], got, want)
+            continue
+        err = abs(got - want)
+        if rho[k] >= -80.0:
+            worst = max(worst, err / bars[k])
+        assert err <= bars[k] + 1e-14 * max(1.0, abs(want)), (k, rho[k], got, want, bars[k])
+    print(f"kl_forward single terms, default form: at most {worst:.3f} of the per-term bar")
 
 
 @pytest.mark.parametrize("n", SIZES)

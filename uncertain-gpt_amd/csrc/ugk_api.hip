@@ -85,6 +85,29 @@ void *own_region(DevWorkspace &w, Region r, size_t bytes) {
   return w.own[r];
 }
 
+// Per device, one double of pinned host memory that ugk_kl_forward's last
+// kernel writes its total into (held until the process ends).
+volatile double *g_kl_slot[kMaxDevices] = {};
+
+volatile double *kl_result_slot() {
+  const int dev = current_device("ugk_kl_forward");
+  if (dev < 0) {
+    set_error(UGK_EHIP, "ugk_kl_forward: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (!g_kl_slot[dev]) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, kAlign, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      set_error(UGK_ENOMEM, "ugk_kl_forward: cannot allocate the pinned result slot");
+      return nullptr;
+    }
+    g_kl_slot[dev] = static_cast<volatile double *>(p);
+  }
+  return g_kl_slot[dev];
+}
+
 void free_own(DevWorkspace &w) {
   bool any = false;
   for (int r = 0; r < kNumRegions; r++) any = any || w.own[r];
@@ -434,14 +457,15 @@ int ugk_kl_forward(double *kl, const float *mu, const float *rho, size_t n, floa
   if (any_null({mu, rho})) return bad(fn, "NULL pointer");
   double *buf = static_cast<double *>(workspace(kRegKl, kl_forward_scratch()));
   if (!buf) return UGK_ENOMEM;
-  if (int e = launch_kl_forward(buf, buf + 1, mu, rho, n, sigma_prior)) return e;
-  double h = 0.0;
-  if (hipMemcpyAsync(&h, buf, sizeof h, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
-      hipStreamSynchronize(stream()) != hipSuccess) {
+  volatile double *slot = kl_result_slot();
+  if (!slot) return UGK_ENOMEM;
+  // the final-sum kernel stores the total straight into the pinned slot: no copy to wait for
+  if (int e = launch_kl_forward(const_cast<double *>(slot), buf, mu, rho, n, sigma_prior)) return e;
+  if (hipStreamSynchronize(stream()) != hipSuccess) {
     const hipError_t err = hipGetLastError();
     return set_error(UGK_EHIP, "%s: %s", fn, hipGetErrorString(err));
   }
-  *kl = h;
+  *kl = *slot;
   return ok();
 }
 
@@ -496,6 +520,13 @@ int ugk_set_philox_exact(int exact) {
 }
 
 int ugk_get_philox_exact(void) { return philox_exact(); }
+
+int ugk_set_kl_exact(int exact) {
+  set_kl_exact(exact);
+  return ok();
+}
+
+int ugk_get_kl_exact(void) { return kl_exact(); }
 
 int ugk_set_encoder_exact(int exact) {
   set_encoder_exact(exact);

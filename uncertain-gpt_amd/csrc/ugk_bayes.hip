@@ -250,61 +250,77 @@ struct BbbStepFused : MapOp {
 };
 
 // ---- KL total (train_bnn.c:941-957) -----------------------------------------
-// Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2,
-// evaluated as (log sp - log sigma) + (sigma^2 + mu^2) * (1 / (2 sp^2)) - 1/2
-// with the logarithm below: the same value to within a few units of 2^-53
-// relative per term. Summed in a fixed order: every thread over a fixed
+// Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2.
+// Summed without a logarithm per term: for a sigma that is a normal float,
+// sum_i log sigma_i = log prod_i sigma_i, the product kept as a double
+// mantissa M and a binary exponent E (an integer sum): M takes each sigma (a
+// double product, rounded once: the logarithm moves by at most 2^-53 per
+// factor, as a per-term logarithm's own rounding would) and gives its exponent
+// to E after every float4 of sigma (four factors keep M inside the double
+// range). sigma^2 + mu^2 is summed as it comes and scaled by 1/(2 sp^2) at the
+// end, and the constant log sp - 1/2 is counted: a thread's share is
+// k (log sp - 1/2) - (E ln 2 + log M) + Q / (2 sp^2), one double logarithm per
+// thread. Subnormal sigma are normal doubles and join the product (four
+// factors of at least 2^-149 keep M above 2^-600). The terms of the other
+// sigma are not finite and do not need evaluating: +inf for sigma = 0 (log of
+// sp/0), NaN for sigma = +inf (-inf + inf) and NaN, as train_bnn.c's
+// evaluation gives; they go to a separate sum (a branch, rarely taken), which
+// the total then takes whatever the finite terms are. Summed in a fixed order: every thread over a fixed
 // stride of float4 slots, then a wavefront butterfly, then the block's waves
 // in order, then one block over the per-block partials. Deterministic for a
-// given n.
+// given n; within double rounding of the CPU's sequential sum of terms.
 constexpr int kKlBlocks = 2048;
-constexpr int kKlLogCells = 128;
 
-// log of a float argument, in double. x = 2^e m with m in [1, 2); c is the
-// centre of m's cell (the top seven fraction bits i: c = 1 + (i + 1/2)/128),
-// and log x = e ln2 + log c + log1p(r), r = (m - c)/c in [-2^-8, 2^-8], with
-// log1p by its series to r^6 (the remainder is below 2^-56 |r|). m - c is
-// formed exactly from the bits below the cell's; r carries the rounding of
-// 1/c. Per-cell log c and 1/c come from the device library, once per
-// workgroup. 0 gives -inf, +inf and NaN themselves.
-struct KlLogTable {
-  double logc[kKlLogCells];
-  double invc[kKlLogCells];
-};
-
-__device__ __forceinline__ void kl_log_stage(KlLogTable *t) {
-  for (int i = threadIdx.x; i < kKlLogCells; i += blockDim.x) {
-    const double c = 1.0 + (i + 0.5) / kKlLogCells;
-    t->logc[i] = log(c);
-    t->invc[i] = 1.0 / c;
+// The KL's sigma = softplus(rho): the glibc-exact form, or (kFast) the
+// hardware-transcendental form while rho >= -80, where sigma is a normal float
+// and that form is within 8 ulp of the exact one (ugk_diag.hip fn 66 over every
+// float input), so each term moves by at most 8 * 2^-23 * (1 + sigma^2/sp^2).
+// Below -80 sigma nears the subnormal range, where a few ulp are a large share
+// of sigma and of its logarithm, so the exact form is taken there (a branch,
+// rarely taken).
+template <bool kFast>
+__device__ __forceinline__ float kl_softplus(float rho, const uint64_t *tab) {
+  if (!kFast) return ugk_dev_softplusf_lds(rho, tab);
+  float s = ugk_fast_softplus(rho);
+  if (rho < -80.0f) {
+    asm volatile("");  // a branch, not both forms and a select
+    s = ugk_dev_softplusf_lds(rho, tab);
   }
+  return s;
 }
 
-__device__ __forceinline__ double kl_log(float x, const KlLogTable *t) {
-  const uint64_t u = ugk_d2u((double)x);
-  const uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
-  const int e = (int)(hi >> 20) - 1023;
-  const uint32_t i = (hi >> 13) & (kKlLogCells - 1);
-  // 1 + (the fraction bits below the cell's), minus the cell's half-width
-  const double d = ugk_hilo2d((hi & 0x1fffu) | 0x3ff00000u, lo) - (1.0 + 0.5 / kKlLogCells);
-  const double r = d * t->invc[i];
-  double p = -1.0 / 6;
-  p = __builtin_fma(p, r, 1.0 / 5);
-  p = __builtin_fma(p, r, -1.0 / 4);
-  p = __builtin_fma(p, r, 1.0 / 3);
-  p = __builtin_fma(p, r, -1.0 / 2);
-  p = p * r;
-  const double res = __builtin_fma((double)e, 0.69314718055994530942, t->logc[i] + __builtin_fma(p, r, r));
-  const bool finite_pos = x > 0.0f && x < __builtin_huge_valf();
-  return finite_pos ? res : (x == 0.0f ? -__builtin_huge_val() : (double)x);
-}
+// One thread's share of the KL total. The exponent sum stays within 150 per
+// element, far inside an int for any n that fits in memory.
+struct KlAcc {
+  double q = 0.0;     // sum of sigma^2 + mu^2 over the product's elements
+  double m = 1.0;     // mantissa product
+  double cnt = 0.0;   // elements in the product
+  double rare = 0.0;  // the terms of sigma = 0, +inf, NaN (+inf or NaN)
+  int e = 0;          // exponent sum
 
-__device__ __forceinline__ double kl_term(float mu, float rho, double log_sp, double inv_two_sp2,
-                                          const uint64_t *tab, const KlLogTable *lt) {
-  const float sigma_f = ugk_dev_softplusf_lds(rho, tab);
-  const double sigma = (double)sigma_f, m = (double)mu;
-  return (log_sp - kl_log(sigma_f, lt)) + (sigma * sigma + m * m) * inv_two_sp2 - 0.5;
-}
+  __device__ __forceinline__ void add(float mu, float sigma_f) {
+    if (sigma_f > 0.0f && sigma_f < __builtin_huge_valf()) {
+      const double s = (double)sigma_f, u = (double)mu;
+      q += s * s + u * u;
+      m *= s;
+      cnt += 1.0;
+    } else {
+      asm volatile("");  // a branch, rarely taken
+      rare += sigma_f == 0.0f ? __builtin_huge_val() : __builtin_nan("");
+    }
+  }
+  // M's exponent into E; M to [1, 2)
+  __device__ __forceinline__ void renorm() {
+    const uint64_t b = ugk_d2u(m);
+    e += (int)((b >> 52) & 0x7ff) - 1023;
+    m = ugk_u2d((b & 0x800fffffffffffffull) | 0x3ff0000000000000ull);
+  }
+  __device__ __forceinline__ double total(double log_sp, double inv_two_sp2) {
+    renorm();
+    return cnt * (log_sp - 0.5) - __builtin_fma((double)e, 0.69314718055994530942, log(m)) +
+           q * inv_two_sp2 + rare;
+  }
+};
 
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -323,37 +339,51 @@ __device__ __forceinline__ double block_sum_d(double v, double *lds) {
   return t;
 }
 
+template <bool kFast>
 __global__ __launch_bounds__(kBlock) void k_kl_partial(double *part, const float *mu, const float *rho,
                                                        size_t n, float sigma_prior, float sp2) {
   __shared__ uint64_t tab[32];
   __shared__ double lds[kBlock / kWave];
-  __shared__ KlLogTable lt;
   ugk_exp2_stage(tab);
-  kl_log_stage(&lt);
   __syncthreads();
   const double log_sp = log((double)sigma_prior), inv_two_sp2 = 1.0 / (2.0 * (double)sp2);
-  double acc = 0.0;
+  KlAcc acc;
   const size_t stride = (size_t)gridDim.x * kBlock;
   const bool vec = aligned16(mu) && aligned16(rho);
   const size_t n4 = vec ? n / 4 : 0;
+  // (issuing the next slot's loads before the current slot's terms was slower: 192 against 176 us
+  // per call at n = 124,439,808, the result's wait included)
   for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
     const float4 m = ld_nt(reinterpret_cast<const float4 *>(mu) + i);
     const float4 r = ld_nt(reinterpret_cast<const float4 *>(rho) + i);
-    acc += kl_term(m.x, r.x, log_sp, inv_two_sp2, tab, &lt);
-    acc += kl_term(m.y, r.y, log_sp, inv_two_sp2, tab, &lt);
-    acc += kl_term(m.z, r.z, log_sp, inv_two_sp2, tab, &lt);
-    acc += kl_term(m.w, r.w, log_sp, inv_two_sp2, tab, &lt);
+    acc.add(m.x, kl_softplus<kFast>(r.x, tab));
+    acc.add(m.y, kl_softplus<kFast>(r.y, tab));
+    acc.add(m.z, kl_softplus<kFast>(r.z, tab));
+    acc.add(m.w, kl_softplus<kFast>(r.w, tab));
+    acc.renorm();
   }
-  for (size_t i = 4 * n4 + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-    acc += kl_term(mu[i], rho[i], log_sp, inv_two_sp2, tab, &lt);
-  const double t = block_sum_d(acc, lds);
+  for (size_t i = 4 * n4 + (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    acc.add(mu[i], kl_softplus<kFast>(rho[i], tab));
+    acc.renorm();
+  }
+  const double t = block_sum_d(acc.total(log_sp, inv_two_sp2), lds);
   if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
+// The per-block partials, summed by one block: thread k adds partials k,
+// k + 256, ... in that order (all its loads in flight at once), then the
+// block's sum as above. out may be host memory mapped for the device.
+static_assert(kKlBlocks % kBlock == 0, "whole rounds of partials per thread");
 __global__ __launch_bounds__(kBlock) void k_kl_final(double *out, const double *part, int nparts) {
   __shared__ double lds[kBlock / kWave];
+  constexpr int kPer = kKlBlocks / kBlock;
+  double v[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; k++) v[k] = part[min((int)threadIdx.x + k * kBlock, nparts - 1)];
   double acc = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += kBlock) acc += part[i];
+#pragma unroll
+  for (int k = 0; k < kPer; k++)
+    if ((int)threadIdx.x + k * kBlock < nparts) acc += v[k];
   const double t = block_sum_d(acc, lds);
   if (threadIdx.x == 0) out[0] = t;
 }
@@ -362,10 +392,13 @@ __global__ __launch_bounds__(kBlock) void k_kl_final(double *out, const double *
 
 namespace {
 std::atomic<int> g_philox_exact{0};
+std::atomic<int> g_kl_exact{0};
 }  // namespace
 
 void set_philox_exact(int exact) { g_philox_exact.store(exact ? 1 : 0); }
 int philox_exact() { return g_philox_exact.load(); }
+void set_kl_exact(int exact) { g_kl_exact.store(exact ? 1 : 0); }
+int kl_exact() { return g_kl_exact.load(); }
 
 namespace {
 template <bool kFast>
@@ -430,16 +463,20 @@ int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float
   return run_map(s, n, "bbb_step_fused");
 }
 
-size_t kl_forward_scratch() { return (kKlBlocks + 1) * sizeof(double); }
+size_t kl_forward_scratch() { return kKlBlocks * sizeof(double); }
 
-int launch_kl_forward(double *out_dev, double *part, const float *mu, const float *rho, size_t n,
+int launch_kl_forward(double *out, double *part, const float *mu, const float *rho, size_t n,
                       float sigma_prior) {
   const float sp2 = sigma_prior * sigma_prior;
   size_t want = (n + 4ull * kBlock - 1) / (4ull * kBlock);
   const int blocks = (int)(want < 1 ? 1 : (want > (size_t)kKlBlocks ? (size_t)kKlBlocks : want));
-  hipLaunchKernelGGL(k_kl_partial, dim3(blocks), dim3(kBlock), 0, stream(), part, mu, rho, n,
-                     sigma_prior, sp2);
-  hipLaunchKernelGGL(k_kl_final, dim3(1), dim3(kBlock), 0, stream(), out_dev, part, blocks);
+  if (kl_exact())
+    hipLaunchKernelGGL(k_kl_partial<false>, dim3(blocks), dim3(kBlock), 0, stream(), part, mu, rho, n,
+                       sigma_prior, sp2);
+  else
+    hipLaunchKernelGGL(k_kl_partial<true>, dim3(blocks), dim3(kBlock), 0, stream(), part, mu, rho, n,
+                       sigma_prior, sp2);
+  hipLaunchKernelGGL(k_kl_final, dim3(1), dim3(kBlock), 0, stream(), out, part, blocks);
   return check_launch("kl_forward");
 }
 

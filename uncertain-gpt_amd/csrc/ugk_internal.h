@@ -125,6 +125,10 @@ int launch_gelu_backward_zero(float *dinp, const float *inp, const float *dout, 
 // 1 the glibc-exact forms of the eps-taking ops.
 void set_philox_exact(int exact);
 int philox_exact();
+// kl_forward's softplus: 0 (default) the hardware-transcendental form where
+// sigma is a normal float, 1 the glibc-exact form throughout.
+void set_kl_exact(int exact);
+int kl_exact();
 int launch_bayes_materialize(float *w, const float *mu, const float *rho,
                              const float *eps, size_t n);
 int launch_bayes_sample(float *w, float *eps, const float *mu, const float *rho, size_t n,
@@ -141,8 +145,9 @@ int launch_bbb_step_fused(float *mu, float *rho, float *m_mu, float *v_mu, float
                           float *w, float *dw, size_t n, unsigned long long seed, int step, float sp,
                           float klw, float bc1, float bc2, float lr, float beta1, float beta2,
                           float aeps, float wd);
-// KL total into out_dev[0]; part holds kl_forward_scratch() bytes.
-int launch_kl_forward(double *out_dev, double *part, const float *mu, const float *rho, size_t n,
+// KL total into out[0] (device memory, or host memory mapped for the device);
+// part holds kl_forward_scratch() bytes.
+int launch_kl_forward(double *out, double *part, const float *mu, const float *rho, size_t n,
                       float sigma_prior);
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
                              const float *weight, const float *bias, int rows, int C);
@@ -241,7 +246,7 @@ int *ids_error_word();
 // Workspace sizes.
 size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
 size_t encoder_backward_scratch();                   // the bucket state (fixed)
-size_t kl_forward_scratch();                         // partial sums and result (fixed)
+size_t kl_forward_scratch();                         // partial sums (fixed)
 size_t softmax_scratch(int rows, int V);             // row statistics of rows too long for one workgroup
 
 }  // namespace ugk

@@ -29,7 +29,7 @@ __all__ = [
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
-    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_encoder_exact", "encoder_exact",
+    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_kl_exact", "kl_exact", "set_encoder_exact", "encoder_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "gpt2_layers_backward_zeroed", "version",
 ]
@@ -109,6 +109,8 @@ _SIGS = {
     "ugk_set_encoder_exact": [_i],
     "ugk_get_encoder_exact": [],
     "ugk_get_philox_exact": [],
+    "ugk_set_kl_exact": [_i],
+    "ugk_get_kl_exact": [],
     "ugk_last_error": [],
     "ugk_param_count": [Config],
     "ugk_act_count": [Config],
@@ -492,6 +494,17 @@ def set_philox_exact(exact: bool) -> None:
 
 def philox_exact() -> bool:
     return bool(lib.ugk_get_philox_exact())
+
+
+def set_kl_exact(exact: bool) -> None:
+    """Softplus inside kl_forward: False (default) the hardware-transcendental form where sigma is a
+    normal float (each term within 8 * 2^-23 * (1 + sigma^2/sp^2) of train_bnn.c's); True the
+    glibc-exact form throughout (the total within double rounding of train_bnn.c's)."""
+    _check(lib.ugk_set_kl_exact(1 if exact else 0))
+
+
+def kl_exact() -> bool:
+    return bool(lib.ugk_get_kl_exact())
 
 
 def set_encoder_exact(exact: bool) -> None:
