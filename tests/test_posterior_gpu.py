@@ -267,11 +267,17 @@ def kl_fast_bar(oracle, rho, sp):
     return float(kl_fast_terms_bar(oracle, rho, sp).sum())
 
 
+def shifted(a, offset):
+    """a on the device, starting `offset` floats past a 16-byte boundary (offset 1: the scalar path)."""
+    return dev(np.concatenate([np.zeros(offset, np.float32), a]))[offset:]
+
+
 @pytest.mark.parametrize("n", [1, 1000, 5_000_003])
-def test_kl_forward(gpu, oracle, kl_exact, n):
+@pytest.mark.parametrize("offset", [0, 1])
+def test_kl_forward(gpu, oracle, kl_exact, n, offset):
     mu, rho, _, _, _, _ = posterior_inputs(920 + n, n)
     want = oracle.kl_forward(mu, rho, n, 0.1)
-    tm, tr = dev(mu), dev(rho)
+    tm, tr = shifted(mu, offset), shifted(rho, offset)
     got = gpu.kl_forward(tm, tr, n, 0.1)
     assert abs(got - want) <= 1e-10 * abs(want), (got, want)
     assert gpu.kl_forward(tm, tr, n, 0.1) == got  # fixed summation order
@@ -279,22 +285,49 @@ def test_kl_forward(gpu, oracle, kl_exact, n):
 
 
 @pytest.mark.parametrize("n", [1, 1000, 5_000_003])
-def test_kl_forward_fast(gpu, oracle, n):
+@pytest.mark.parametrize("offset", [0, 1])
+def test_kl_forward_fast(gpu, oracle, n, offset):
     """The default form (hardware-transcendental softplus) against train_bnn.c's KL: within the sum
     of the per-term bars above plus the exact form's summation-order bar, deterministic, and within
     the literal bar |a - b| <= 1e-6 + 1e-5 |b|."""
     assert not gpu.kl_exact()
     mu, rho, _, _, _, _ = posterior_inputs(920 + n, n)
     want = oracle.kl_forward(mu, rho, n, 0.1)
-    tm, tr = dev(mu), dev(rho)
+    tm, tr = shifted(mu, offset), shifted(rho, offset)
     got = gpu.kl_forward(tm, tr, n, 0.1)
     bar = kl_fast_bar(oracle, rho, 0.1)
-    print(f"kl_forward n={n}: default form {abs(got - want):.3g} from train_bnn.c (bar {bar:.3g}, "
-          f"{abs(got - want) / abs(want):.3g} relative)")
+    print(f"kl_forward n={n} offset={offset}: default form {abs(got - want):.3g} from train_bnn.c "
+          f"(bar {bar:.3g}, {abs(got - want) / abs(want):.3g} relative)")
     assert abs(got - want) <= bar + 1e-10 * abs(want), (got, want, bar)
     assert abs(got - want) <= 1e-6 + 1e-5 * abs(want), (got, want)
     assert gpu.kl_forward(tm, tr, n, 0.1) == got  # fixed summation order
     assert gpu.kl_forward(tm, tr, 0, 0.1) == 0.0
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_kl_forward_nonfinite_terms(gpu, oracle, exact):
+    """A term that is not finite decides the total in both forms, as in train_bnn.c's sum: sigma = 0
+    (rho = -inf, or below about -104) gives +inf, sigma = +inf (rho = +inf) and NaN give NaN; a NaN
+    term wins over an infinite one. Everything else in the vector is ordinary."""
+    n = 4099
+    mu, rho, _, _, _, _ = posterior_inputs(977, n)
+    cases = {"rho=-inf": {17: -np.inf}, "rho=-200": {4000: -200.0}, "rho=+inf": {5: np.inf},
+             "rho=nan": {2048: np.nan}, "mu=inf": {-1: None}, "-inf and nan": {3: -np.inf, 4097: np.nan}}
+    gpu.set_kl_exact(exact)
+    try:
+        for name, edits in cases.items():
+            m, r = mu.copy(), rho.copy()
+            for k, v in edits.items():
+                if v is None:
+                    m[k] = np.inf
+                else:
+                    r[k] = v
+            want = oracle.kl_forward(m, r, n, 0.1)
+            got = gpu.kl_forward(dev(m), dev(r), n, 0.1)
+            assert (np.isnan(got) and np.isnan(want)) or got == want, (name, got, want)
+            assert not np.isfinite(want), (name, want)
+    finally:
+        gpu.set_kl_exact(False)
 
 
 def kl_term_inputs():
