@@ -251,24 +251,24 @@ struct BbbStepFused : MapOp {
 
 // ---- KL total (train_bnn.c:941-957) -----------------------------------------
 // Each term in double: log(sp / sigma) + (sigma^2 + mu^2) / (2 sp^2) - 1/2.
-// Summed without a logarithm per term: for a sigma that is a normal float,
-// sum_i log sigma_i = log prod_i sigma_i, the product kept as a double
-// mantissa M and a binary exponent E (an integer sum): M takes each sigma (a
-// double product, rounded once: the logarithm moves by at most 2^-53 per
-// factor, as a per-term logarithm's own rounding would) and gives its exponent
-// to E after every float4 of sigma (four factors keep M inside the double
-// range). sigma^2 + mu^2 is summed as it comes and scaled by 1/(2 sp^2) at the
-// end, and the constant log sp - 1/2 is counted: a thread's share is
-// k (log sp - 1/2) - (E ln 2 + log M) + Q / (2 sp^2), one double logarithm per
-// thread. Subnormal sigma are normal doubles and join the product (four
-// factors of at least 2^-149 keep M above 2^-600). The terms of the other
-// sigma are not finite and do not need evaluating: +inf for sigma = 0 (log of
-// sp/0), NaN for sigma = +inf (-inf + inf) and NaN, as train_bnn.c's
-// evaluation gives; they go to a separate sum (a branch, rarely taken), which
-// the total then takes whatever the finite terms are. Summed in a fixed order: every thread over a fixed
-// stride of float4 slots, then a wavefront butterfly, then the block's waves
-// in order, then one block over the per-block partials. Deterministic for a
-// given n; within double rounding of the CPU's sequential sum of terms.
+// Summed without a logarithm per term: sum_i log sigma_i = log prod_i sigma_i,
+// the product kept as a double mantissa M and a binary exponent E (an integer
+// sum). M takes each sigma (exact as a double; the product rounds once, which
+// moves the logarithm by at most 2^-53, as a per-term logarithm's own rounding
+// would) and gives its exponent to E after every float4 of sigma: four factors
+// in [2^-149, 2^128] keep M inside the double range, subnormal sigma included.
+// sigma^2 + mu^2 is summed as it comes and scaled by 1/(2 sp^2) at the end, and
+// the constant log sp - 1/2 is counted, so a thread's share is
+//   k (log sp - 1/2) - (E ln 2 + log M) + Q / (2 sp^2),
+// one double logarithm per thread. The terms of sigma = 0, +inf or NaN are not
+// finite and are not evaluated: +inf for sigma = 0 (the log of sp/0), NaN for
+// +inf (-inf + inf) and for NaN, as train_bnn.c's evaluation gives. They go to
+// a separate sum (a branch, rarely taken), which then decides the total.
+// Summed in a fixed order: every thread over a fixed stride of float4 slots,
+// then a wavefront butterfly, then the block's waves in order, then one block
+// over the per-block partials. Deterministic for a given n; it differs from the
+// CPU's sequential sum of terms by the rounding of a double sum in another
+// order.
 constexpr int kKlBlocks = 2048;
 
 // The KL's sigma = softplus(rho): the glibc-exact form, or (kFast) the
