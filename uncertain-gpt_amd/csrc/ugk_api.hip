@@ -908,6 +908,7 @@ int layers_backward(const char *fn, bool zeroed, float *grads, float *grads_acts
   // (nothing in between reads those gradients), instead of a reduce launch
   // after each.
   const size_t slot = align_up(layernorm_backward_scratch(M, C));
+  const int slot_rows = layernorm_backward_blocks_bound(M, C);  // partial rows a slot holds
   const int nln = 2 * cfg.L + 1;
   char *pbase = static_cast<char *>(workspace(kRegLn, slot * (size_t)nln));
   if (!pbase) return UGK_ENOMEM;
@@ -921,9 +922,8 @@ int layers_backward(const char *fn, bool zeroed, float *grads, float *grads_acts
     // in gpt2_backward nothing reads it after the residual_backward that
     // splits it into dx and dy (res1 of every block and each block's resa).
     if (int e = timed(dx ? UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN : UGK_OP_LAYERNORM_BACKWARD_MAIN, [&] {
-          return launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C,
-                                                    kMaxPartialRows, &nblk, dx ? dinp_mode : kDinpRw,
-                                                    zeroed && dx != nullptr);
+          return launch_layernorm_backward_partials(dinp, part, dx, dy, dout, inp, w, mean, rstd, M, C, slot_rows,
+                                                    &nblk, dx ? dinp_mode : kDinpRw, zeroed && dx != nullptr);
         }))
       return e;
     jobs.push_back({part, dw, db, nblk});

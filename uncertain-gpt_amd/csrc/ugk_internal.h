@@ -193,13 +193,13 @@ int launch_layernorm_backward_partials(float *dinp, float *partial, float *dx, f
                                        int dinp_mode = kDinpRw, bool assign_res = false);
 int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
 // The per-op LayerNorm backward (launch_layernorm_residual_backward_into) on
-// the float4 path finishes its column sums in its main launch (1, default) or
-// in a second launch (0); both give the same bits. The step driver always
+// the float4 path finishes its column sums in its main launch (1) or in a
+// second launch (0, the default); both give the same bits. The step driver always
 // batches its column sums in one launch at the end.
 void set_layernorm_tail(int on);
 int layernorm_tail();
-// Both passes with the partial rows in `partial` (at most max_blocks rows of
-// 2C floats), not in the workspace.
+// Both passes with the partial rows in `partial` (room for max_blocks rows of
+// 2C floats; every shape takes at most max_blocks), not in the workspace.
 int launch_layernorm_residual_backward_into(float *partial, int max_blocks, float *dinp, float *dweight,
                                             float *dbias, float *dx, float *dy, const float *dout,
                                             const float *inp, const float *weight, const float *mean,

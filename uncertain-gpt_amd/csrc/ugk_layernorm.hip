@@ -1177,8 +1177,10 @@ int launch_layernorm_residual_backward(float *dinp, float *dweight, float *dbias
   if (rows == 0) return 0;
   float *partial = static_cast<float *>(workspace(kRegLn, layernorm_backward_scratch(rows, C)));
   if (!partial) return UGK_ENOMEM;
-  return launch_layernorm_residual_backward_into(partial, kMaxPartialRows, dinp, dweight, dbias, dx, dy, dout, inp,
-                                                 weight, mean, rstd, rows, C);
+  // the workspace holds the bound's number of partial rows, and no shape takes
+  // more workgroups than the cap it is given
+  return launch_layernorm_residual_backward_into(partial, layernorm_backward_blocks_bound(rows, C), dinp, dweight,
+                                                 dbias, dx, dy, dout, inp, weight, mean, rstd, rows, C);
 }
 
 // ---- allocation-free variant ------------------------------------------------
