@@ -187,3 +187,20 @@ def test_layernorm_workspace_bound_covers_smaller_calls():
     sizes = [ugk.workspace_bytes(ugk.Config(B=B, T=1024, C=768, V=50257, NH=12, maxT=1024, L=12))
              for B in range(1, 17)]
     assert sizes == sorted(sizes)
+
+
+def test_layernorm_partial_rows_within_bound_dense():
+    """Every LayerNorm backward shape makes at most as many partial rows as the workspace bound at its
+    own rows, for every row count up to 4,100, every 37th up to 70,000 and a few powers of two, at 14
+    widths, plain and fused: the bound sizes the slot, and the launchers cap the workgroups at it."""
+    import ugk
+    a, b = ctypes.c_int(0), ctypes.c_int(0)
+    rows_list = sorted(set(range(1, 4101)) | set(range(4100, 70000, 37)) | {8192, 16384, 32768, 65536, 131072})
+    bad = []
+    for C in (4, 64, 384, 512, 768, 772, 1024, 1028, 1030, 1600, 2048, 3072, 4096, 8192):
+        for rows in rows_list:
+            for fused in (0, 1):
+                assert ugk.lib.ugk_diag_layernorm_partial_rows(rows, C, fused, ctypes.byref(a), ctypes.byref(b)) == 0
+                if a.value > b.value:
+                    bad.append((rows, C, fused, a.value, b.value))
+    assert not bad, bad[:5]
