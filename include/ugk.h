@@ -21,7 +21,8 @@
  * are within 1e-5 relative / 1e-6 absolute of it on every input, and
  * bit-identical after ugk_set_gelu_exact(1); LayerNorm row statistics and dinp
  * are within fp32 rounding of it, and LayerNorm dweight/dbias are reduced in a
- * fixed, run-to-run deterministic order.
+ * fixed, run-to-run deterministic order (bit-identical to it after
+ * ugk_set_layernorm_exact(1)).
  *
  * The library never allocates inside a kernel. A few entry points need device
  * workspace beyond their arguments: the LayerNorm backward's partial column
@@ -100,6 +101,21 @@ int ugk_layernorm_backward(float *dinp, float *dweight, float *dbias,
                            const float *dout, const float *inp,
                            const float *weight, const float *mean,
                            const float *rstd, int B, int T, int C);
+
+/* LayerNorm order of additions for later calls from any thread: 0 (the
+ * default) the kernels above, whose row sums are trees (within fp32 rounding
+ * of train_bnn.c) and whose dweight/dbias are summed over per-workgroup
+ * partial rows (deterministic, within the scale-aware bar of the CPU's serial
+ * sums); nonzero train_bnn.c's own order, each row's sums one column at a
+ * time and dweight/dbias one row at a time, so that every LayerNorm output
+ * (out, mean, rstd, dinp, dweight, dbias) is bit-identical to it. Every
+ * LayerNorm entry point follows it, the fused pairs (as the two ops in
+ * sequence), the allocation-free backward and the step driver included. The
+ * exact form takes about twice the time of the default or more. No
+ * counterpart in the reference, whose CPU and GPU builds each sum in their
+ * own order. */
+int ugk_set_layernorm_exact(int exact);
+int ugk_get_layernorm_exact(void);
 
 /* No counterpart in the reference: for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

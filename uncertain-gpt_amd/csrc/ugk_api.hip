@@ -528,6 +528,13 @@ int ugk_set_kl_exact(int exact) {
 
 int ugk_get_kl_exact(void) { return kl_exact(); }
 
+int ugk_set_layernorm_exact(int exact) {
+  set_layernorm_exact(exact);
+  return ok();
+}
+
+int ugk_get_layernorm_exact(void) { return layernorm_exact(); }
+
 int ugk_set_encoder_exact(int exact) {
   set_encoder_exact(exact);
   return ok();
@@ -914,8 +921,13 @@ int layers_backward(const char *fn, bool zeroed, float *grads, float *grads_acts
   if (!pbase) return UGK_ENOMEM;
   std::vector<LnReduceJob> jobs;
   jobs.reserve((size_t)nln);
+  const bool exact = layernorm_exact() != 0;
   auto ln_bwd = [&](float *dinp, float *dw, float *db, float *dx, float *dy, const float *dout, const float *inp,
                     const float *w, const float *mean, const float *rstd, int dinp_mode = kDinpRead) -> int {
+    if (exact)  // the reference's LayerNorm backward then residual_backward, each in its own order
+      return timed(dx ? UGK_OP_LAYERNORM_RESIDUAL_BACKWARD_MAIN : UGK_OP_LAYERNORM_BACKWARD_MAIN, [&] {
+        return launch_layernorm_residual_backward(dinp, dw, db, dx, dy, dout, inp, w, mean, rstd, M, C);
+      });
     float *part = reinterpret_cast<float *>(pbase + slot * jobs.size());
     int nblk = 0;
     // A pair's dinp is read (the LayerNorm adds to it) but not written back:
@@ -976,7 +988,9 @@ int layers_backward(const char *fn, bool zeroed, float *grads, float *grads_acts
                      grads_acts + A(l, a.lno), acts + st, params + P(l, p.lng), acts + A(l, a.lnm),
                      acts + A(l, a.lnr)));
   }
-  UGK_TRY(timed(UGK_OP_LAYERNORM_COLUMN_SUMS, [&] { return launch_layernorm_reduce(jobs.data(), (int)jobs.size(), C); }));
+  if (!jobs.empty())
+    UGK_TRY(timed(UGK_OP_LAYERNORM_COLUMN_SUMS,
+                  [&] { return launch_layernorm_reduce(jobs.data(), (int)jobs.size(), C); }));
   UGK_TRY(timed(UGK_OP_ENCODER_BACKWARD, [&] {
     return ugk_encoder_backward(grads + p.wte, grads + p.wpe, grads_acts + a.enc, inputs, B, T, C);
   }));

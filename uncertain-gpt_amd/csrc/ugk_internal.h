@@ -198,6 +198,15 @@ int launch_layernorm_reduce(const LnReduceJob *jobs, int njobs, int C);
 // batches its column sums in one launch at the end.
 void set_layernorm_tail(int on);
 int layernorm_tail();
+// LayerNorm forward and backward in train_bnn.c's order of every addition (1)
+// or the default kernels (0); every LayerNorm entry point and the step driver
+// follow it.
+void set_layernorm_exact(int on);
+int layernorm_exact();
+int launch_layernorm_forward_exact(float *out, float *mean, float *rstd, const float *inp, const float *weight,
+                                   const float *bias, int rows, int C);
+int launch_layernorm_backward_exact(float *dinp, float *dweight, float *dbias, const float *dout, const float *inp,
+                                    const float *weight, const float *mean, const float *rstd, int rows, int C);
 // Both passes with the partial rows in `partial` (room for max_blocks rows of
 // 2C floats; every shape takes at most max_blocks), not in the workspace.
 int launch_layernorm_residual_backward_into(float *partial, int max_blocks, float *dinp, float *dweight,

@@ -983,7 +983,7 @@ int launch_residual_layernorm_forward(float *res, float *out, float *mean, float
                                       const float *y, const float *weight, const float *bias, int rows,
                                       int C) {
   if (rows == 0) return 0;
-  if (!vec_ok(C, {res, out, x, y, weight, bias})) {
+  if (layernorm_exact() || !vec_ok(C, {res, out, x, y, weight, bias})) {
     if (int e = launch_residual_forward(res, x, y, (size_t)rows * C)) return e;
     return launch_layernorm_forward(out, mean, rstd, res, weight, bias, rows, C);
   }
@@ -996,7 +996,7 @@ int launch_encoder_layernorm_forward(float *enc, float *out, float *mean, float 
                                      int B, int T, int C) {
   const int rows = B * T;
   if (rows == 0) return 0;
-  if (!vec_ok(C, {enc, out, wte, wpe, weight, bias})) {
+  if (layernorm_exact() || !vec_ok(C, {enc, out, wte, wpe, weight, bias})) {
     if (int e = launch_encoder_forward(enc, inp, wte, wpe, B, T, C)) return e;
     return launch_layernorm_forward(out, mean, rstd, enc, weight, bias, rows, C);
   }
@@ -1020,9 +1020,264 @@ int launch_encoder_layernorm_forward(float *enc, float *out, float *mean, float 
   return check_launch("encoder_layernorm_forward");
 }
 
+namespace {
+// ---- exact mode: train_bnn.c's order of every addition ------------------------
+// train_bnn.c:81-115 and :439-477 add each row's terms one column at a time
+// (c = 0, 1, ..., C-1), and dweight/dbias one row at a time. The exact kernels
+// keep those orders, each sum a serial chain in one lane:
+//   k_ln_rows_exact: a workgroup per 64 rows. Fifteen loader wavefronts stage
+//     64-column tiles of the rows in LDS (row pitch 65 floats, so that the
+//     chains' column reads do not conflict), three tiles ahead in registers;
+//     wavefront 0 runs one chain per row (lane = row) over each tile as it
+//     arrives. The forward streams the tiles twice (the sum, then the squared
+//     deviations from the mean, as the CPU loop does), the backward once (both
+//     of its row sums). Then every wavefront writes out (or adds to dinp)
+//     whole rows with the row statistics.
+//   k_ln_cols_exact: a workgroup per 32 columns. The loaders stage 128-row
+//     tiles of the dweight terms dout * xhat (rounded as the CPU rounds them)
+//     and the dbias terms dout; lanes 0-31 of wavefront 0 chain dweight, lanes
+//     32-63 dbias, one row after another, from the values the arrays hold.
+// No product is contracted into an fma, and the square root and quotients are
+// IEEE's, so every result is train_bnn.c's bit for bit. Scalar loads and
+// stores: any C, any alignment.
+constexpr int kExLoaders = 15;
+constexpr int kExThreads = (kExLoaders + 1) * kWave;
+constexpr int kExLoadLanes = kExLoaders * kWave;
+constexpr int kExDepth = 3;  // tiles in registers ahead of the chains
+constexpr int kExRows = 64;  // rows per workgroup of the row kernel (one chain per lane)
+constexpr int kExTile = 64;  // columns per tile of the row kernel
+constexpr int kExPitch = kExTile + 1;
+constexpr int kExSlots = (kExRows * kExTile + kExLoadLanes - 1) / kExLoadLanes;
+constexpr int kExCols = 32;      // columns per workgroup of the column kernel
+constexpr int kExColRows = 128;  // rows per tile of the column kernel
+constexpr int kExColSlots = (kExColRows * kExCols + kExLoadLanes - 1) / kExLoadLanes;
+static_assert(kExRows == kWave && 2 * kExCols == kWave, "one chain per lane of wavefront 0");
+
+template <bool kBwd>
+__global__ __launch_bounds__(kExThreads) void k_ln_rows_exact(float *__restrict__ outp, float *__restrict__ mean,
+                                                              float *__restrict__ rstd, const float *__restrict__ inp,
+                                                              const float *__restrict__ dout,
+                                                              const float *__restrict__ weight,
+                                                              const float *__restrict__ bias, int rows, int C) {
+  constexpr int kArr = kBwd ? 2 : 1;  // staged arrays: inp (and dout)
+  __shared__ float tile[2][kArr][kExRows * kExPitch];
+  __shared__ float wtile[2][kExTile];
+  __shared__ float2 stat[kExRows];  // per row: mean, rstd
+  __shared__ float2 rsum[kExRows];  // backward: the two row sums over C
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int r0 = blockIdx.x * kExRows;
+  const int nt = (C + kExTile - 1) / kExTile;
+  const int nu = (kBwd ? 1 : 2) * nt;  // tiles streamed: the forward reads every tile twice
+  const float Cf = (float)C;
+  // the chain of wavefront 0's lane: row r0 + lane
+  float cm = 0.0f, cr = 0.0f, s1 = 0.0f, s2 = 0.0f;
+  if (kBwd) {
+    const int crow = min(r0 + lane, rows - 1);
+    cm = mean[crow];
+    cr = rstd[crow];
+  }
+  // loader wavefront lw takes tile rows lw + 15 s, column lane
+  const int lw = wave - 1;
+  float reg[kExDepth][kArr][kExSlots];
+  float wreg[kExDepth];
+  auto load_tile = [&](int u, int k) {
+    const int col = min((u % nt) * kExTile + lane, C - 1);
+#pragma unroll
+    for (int s = 0; s < kExSlots; s++) {
+      const int ri = min(lw + kExLoaders * s, kExRows - 1);
+      const size_t off = (size_t)min(r0 + ri, rows - 1) * C + col;
+      reg[k][0][s] = inp[off];
+      if (kBwd) reg[k][kArr - 1][s] = dout[off];
+    }
+    wreg[k] = kBwd ? weight[col] : 0.0f;
+  };
+  auto store_tile = [&](int u, int k) {
+    const int b = u & 1;
+#pragma unroll
+    for (int s = 0; s < kExSlots; s++) {
+      const int ri = lw + kExLoaders * s;
+      if (ri < kExRows) {
+#pragma unroll
+        for (int a = 0; a < kArr; a++) tile[b][a][ri * kExPitch + lane] = reg[k][a][s];
+      }
+    }
+    if (kBwd && lw == 0) wtile[b][lane] = wreg[k];
+  };
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < kExDepth; k++)
+      if (k < nu) load_tile(k, k);
+  }
+  for (int u0 = 0; u0 < nu; u0 += kExDepth) {
+#pragma unroll
+    for (int k = 0; k < kExDepth; k++) {
+      const int u = u0 + k;
+      if (u >= nu) break;  // the same in every thread
+      if (wave > 0) {
+        store_tile(u, k);
+        if (u + kExDepth < nu) load_tile(u + kExDepth, k);
+      }
+      // tile u is staged in buffer u & 1; the buffer written next round was
+      // last read before this barrier
+      __syncthreads();
+      if (wave == 0) {
+        const int b = u & 1, t = u % nt;
+        const int cmax = min(kExTile, C - t * kExTile);
+        const float *X = &tile[b][0][lane * kExPitch];
+        if (kBwd) {
+          const float *Y = &tile[b][kArr - 1][lane * kExPitch];
+          const float *W = wtile[b];
+          for (int c = 0; c < cmax; c++) {
+            const float xh = (X[c] - cm) * cr;
+            const float dn = Y[c] * W[c];
+            s1 = s1 + dn;
+            s2 = s2 + dn * xh;
+          }
+        } else if (u < nt) {
+          for (int c = 0; c < cmax; c++) s1 = s1 + X[c];
+        } else {
+          if (u == nt) cm = s1 / Cf;
+          for (int c = 0; c < cmax; c++) {
+            const float d = X[c] - cm;
+            s2 = s2 + d * d;
+          }
+        }
+      }
+    }
+  }
+  if (wave == 0) {
+    if (kBwd) {
+      stat[lane] = make_float2(cm, cr);
+      rsum[lane] = make_float2(s1 / Cf, s2 / Cf);
+    } else {
+      const float r = 1.0f / sqrtf(s2 / Cf + 1e-5f);
+      if (r0 + lane < rows) {
+        mean[r0 + lane] = cm;
+        rstd[r0 + lane] = r;
+      }
+      stat[lane] = make_float2(cm, r);
+    }
+  }
+  __syncthreads();
+  // the rows' elements, every wavefront on whole rows (inp and dout again,
+  // from the cache)
+  for (int ri = wave; ri < kExRows; ri += kExLoaders + 1) {
+    const int row = r0 + ri;
+    if (row >= rows) break;
+    const float m = stat[ri].x, r = stat[ri].y;
+    const size_t base = (size_t)row * C;
+    if (kBwd) {
+      const float dnm = rsum[ri].x, dnxm = rsum[ri].y;
+      for (int c = lane; c < C; c += kWave) {
+        const float xh = (inp[base + c] - m) * r;
+        const float dn = dout[base + c] * weight[c];
+        outp[base + c] += r * (dn - dnm - xh * dnxm);
+      }
+    } else {
+      for (int c = lane; c < C; c += kWave) outp[base + c] = (inp[base + c] - m) * r * weight[c] + bias[c];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kExThreads) void k_ln_cols_exact(float *__restrict__ dweight, float *__restrict__ dbias,
+                                                              const float *__restrict__ dout,
+                                                              const float *__restrict__ inp,
+                                                              const float *__restrict__ mean,
+                                                              const float *__restrict__ rstd, int rows, int C) {
+  constexpr int kPitch = 2 * kExCols;  // per row: the 32 dweight terms, then the 32 dbias terms
+  __shared__ float tile[2][kExColRows * kPitch];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int c0 = blockIdx.x * kExCols;
+  const int nt = (rows + kExColRows - 1) / kExColRows;
+  // loader wavefront lw takes tile rows 2 lw + 30 s + lane / 32, column lane % 32
+  const int lw = wave - 1;
+  const int lcol = min(c0 + (lane & (kExCols - 1)), C - 1);
+  float rx[kExDepth][kExColSlots], ry[kExDepth][kExColSlots], rm[kExDepth][kExColSlots], rr[kExDepth][kExColSlots];
+  auto tile_row = [&](int s) { return 2 * lw + 2 * kExLoaders * s + (lane >> 5); };
+  auto load_tile = [&](int t, int k) {
+#pragma unroll
+    for (int s = 0; s < kExColSlots; s++) {
+      const int row = min(t * kExColRows + min(tile_row(s), kExColRows - 1), rows - 1);
+      const size_t off = (size_t)row * C + lcol;
+      rx[k][s] = inp[off];
+      ry[k][s] = dout[off];
+      rm[k][s] = mean[row];
+      rr[k][s] = rstd[row];
+    }
+  };
+  auto store_tile = [&](int t, int k) {
+    float *T = tile[t & 1];
+#pragma unroll
+    for (int s = 0; s < kExColSlots; s++) {
+      const int ri = tile_row(s);
+      if (ri < kExColRows) {
+        const float xh = (rx[k][s] - rm[k][s]) * rr[k][s];
+        T[ri * kPitch + (lane & (kExCols - 1))] = ry[k][s] * xh;
+        T[ri * kPitch + kExCols + (lane & (kExCols - 1))] = ry[k][s];
+      }
+    }
+  };
+  // the chain of wavefront 0's lane: dweight (lanes 0-31) or dbias (32-63) of column c0 + lane % 32
+  const int cc = c0 + (lane & (kExCols - 1));
+  float *const dst = (lane < kExCols ? dweight : dbias) + min(cc, C - 1);
+  float acc = wave == 0 ? *dst : 0.0f;
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < kExDepth; k++)
+      if (k < nt) load_tile(k, k);
+  }
+  for (int t0 = 0; t0 < nt; t0 += kExDepth) {
+#pragma unroll
+    for (int k = 0; k < kExDepth; k++) {
+      const int t = t0 + k;
+      if (t >= nt) break;  // the same in every thread
+      if (wave > 0) {
+        store_tile(t, k);
+        if (t + kExDepth < nt) load_tile(t + kExDepth, k);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const float *T = tile[t & 1] + lane;
+        const int rmax = min(kExColRows, rows - t * kExColRows);
+        for (int i = 0; i < rmax; i++) acc = acc + T[i * kPitch];
+      }
+    }
+  }
+  if (wave == 0 && cc < C) *dst = acc;
+}
+
+}  // namespace
+
+namespace {
+std::atomic<int> g_ln_exact{0};
+}  // namespace
+
+void set_layernorm_exact(int on) { g_ln_exact.store(on ? 1 : 0); }
+int layernorm_exact() { return g_ln_exact.load(); }
+
+int launch_layernorm_forward_exact(float *out, float *mean, float *rstd, const float *inp, const float *weight,
+                                   const float *bias, int rows, int C) {
+  if (rows == 0 || C == 0) return 0;
+  launch(k_ln_rows_exact<false>, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, out, mean, rstd, inp,
+         static_cast<const float *>(nullptr), weight, bias, rows, C);
+  return check_launch("layernorm_forward (exact)");
+}
+
+int launch_layernorm_backward_exact(float *dinp, float *dweight, float *dbias, const float *dout, const float *inp,
+                                    const float *weight, const float *mean, const float *rstd, int rows, int C) {
+  if (rows == 0 || C == 0) return 0;
+  launch(k_ln_rows_exact<true>, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, dinp,
+         const_cast<float *>(mean), const_cast<float *>(rstd), inp, dout, weight, static_cast<const float *>(nullptr),
+         rows, C);
+  launch(k_ln_cols_exact, dim3(grid_for((size_t)C, kExCols)), dim3(kExThreads), 0, dweight, dbias, dout, inp, mean,
+         rstd, rows, C);
+  return check_launch("layernorm_backward (exact)");
+}
+
 int launch_layernorm_forward(float *out, float *mean, float *rstd, const float *inp,
                              const float *weight, const float *bias, int rows, int C) {
   if (rows == 0) return 0;
+  if (layernorm_exact()) return launch_layernorm_forward_exact(out, mean, rstd, inp, weight, bias, rows, C);
   if (vec_ok(C, {out, inp, weight, bias})) {
     launch_ln_fwd_vec<false>(out, mean, rstd, inp, weight, bias, rows, C, nullptr, nullptr);
   } else {
@@ -1154,6 +1409,11 @@ int launch_layernorm_residual_backward_into(float *partial, int max_blocks, floa
                                             const float *rstd, int rows, int C) {
   if (rows == 0) return 0;
   const bool res = dx != nullptr;
+  if (layernorm_exact()) {  // no partial rows: the exact kernels keep their chains in LDS and registers
+    if (int e = launch_layernorm_backward_exact(dinp, dweight, dbias, dout, inp, weight, mean, rstd, rows, C))
+      return e;
+    return res ? launch_residual_backward(dx, dy, dinp, (size_t)rows * C) : 0;
+  }
   if (layernorm_tail() && vec_ok(C, {dinp, dout, inp, weight}) && (!res || vec_ok(C, {dx, dy}))) {
     if (res)
       launch_ln_bwd_vec<true, kDinpRw, false>(dinp, partial, dout, inp, weight, mean, rstd, rows, C, dx, dy,

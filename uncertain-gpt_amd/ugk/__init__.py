@@ -29,7 +29,7 @@ __all__ = [
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
-    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_kl_exact", "kl_exact", "set_encoder_exact", "encoder_exact",
+    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_kl_exact", "kl_exact", "set_layernorm_exact", "layernorm_exact", "set_encoder_exact", "encoder_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "gpt2_layers_backward_zeroed", "version",
 ]
@@ -111,6 +111,8 @@ _SIGS = {
     "ugk_get_philox_exact": [],
     "ugk_set_kl_exact": [_i],
     "ugk_get_kl_exact": [],
+    "ugk_set_layernorm_exact": [_i],
+    "ugk_get_layernorm_exact": [],
     "ugk_last_error": [],
     "ugk_param_count": [Config],
     "ugk_act_count": [Config],
@@ -505,6 +507,18 @@ def set_kl_exact(exact: bool) -> None:
 
 def kl_exact() -> bool:
     return bool(lib.ugk_get_kl_exact())
+
+
+def set_layernorm_exact(exact: bool) -> None:
+    """LayerNorm order of additions: False (default) tree row sums and per-workgroup partial column
+    sums (within fp32 rounding and the scale-aware bar of train_bnn.c); True train_bnn.c's own serial
+    order, every LayerNorm output bit-identical to it (fused pairs, the allocation-free backward and
+    the step driver included)."""
+    _check(lib.ugk_set_layernorm_exact(1 if exact else 0))
+
+
+def layernorm_exact() -> bool:
+    return bool(lib.ugk_get_layernorm_exact())
 
 
 def set_encoder_exact(exact: bool) -> None:
