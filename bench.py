@@ -25,6 +25,9 @@ Printed JSON line (the last line of stdout):
     zeroed_backward  the same step with ugk_gpt2_layers_backward_zeroed (for callers that
                  zero grads_acts before the backward, as every reference arm does; it does
                  not read those zeros): ms per step, rates on the reference's and moved bytes
+    exact_forms  the same step with every exact mode on (GELU, encoder backward, LayerNorm: the
+                 layer kernels' outputs bit-identical to train_bnn.c's), and the LayerNorm and
+                 GELU kernels alone in their exact forms, cold, at the step's shapes
     in_step      each op of the step, timed inside the step with a HIP event pair that
                  its kernel's dispatch records (the library's op timer), over --op-steps
                  further steps: launches per step, mean us, us per step, algorithmic GB/s
@@ -100,6 +103,8 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_ln_bwd_team", "layernorm_backward (main, row teams)"),
     ("k_ln_bwd_reduce_batch", "layernorm_backward (batched column sums)"),
     ("k_ln_bwd_reduce", "layernorm_backward (reduce)"),
+    ("k_ln_fwd_exact", "layernorm_forward (exact form)"),
+    ("k_ln_bwd_exact", "layernorm_backward (exact form: rows and columns in one launch)"),
     ("k_ln_fwd_vec", "layernorm_forward"),
     ("k_enc_fwd_vec", "encoder_forward"),
     ("k_enc_fwd_row", "encoder_forward"),
@@ -216,6 +221,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the kernels at the other benchmark configurations' shapes")
     ap.add_argument("--no-head", action="store_true",
                     help="skip softmax + cross-entropy forward/backward at the GPT-2 head shape")
+    ap.add_argument("--no-exact", action="store_true",
+                    help="skip the exact forms (train_bnn.c's order of every addition, or its libm)")
     ap.add_argument("--no-posterior", action="store_true",
                     help="skip the posterior-update ops (Philox sample, bayes/KL backward, AdamW, fused step)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -336,6 +343,34 @@ def main():
                       "zeroed before the backward) lets it skip reading those zeros"}
     log(f"bench: step with the zeroed-gradient backward {ms_zeroed:.4f} ms -> {zeroed['value_GBps']:.1f} GB/s on the "
         f"reference's bytes, {zeroed['GBps_moved']:.1f} GB/s moved ({moved_zeroed / 1e9:.2f} GB)")
+
+    # ---- the same step with every exact mode on (GELU's glibc tanhf, the encoder backward's and
+    # LayerNorm's train_bnn.c orders): every buffer the layer kernels write is train_bnn.c's, bit for bit
+    exact_forms = {}
+    exact_setters = (ugk.set_gelu_exact, ugk.set_encoder_exact, ugk.set_layernorm_exact)
+    if not args.no_exact:
+        for f in exact_setters:
+            f(True)
+        try:
+            for _ in range(args.warmup):
+                step()
+            torch.cuda.synchronize()
+            x0, x1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            x0.record()
+            for _ in range(args.steps):
+                step()
+            x1.record()
+            torch.cuda.synchronize()
+        finally:
+            for f in exact_setters:
+                f(False)
+        ms_exact = x0.elapsed_time(x1) / args.steps
+        exact_forms["step (every exact mode)"] = {
+            "ms_per_step": round(ms_exact, 4), "GBps": round(total_bytes / (ms_exact * 1e-3) / 1e9, 1),
+            "note": "ugk_set_gelu_exact, ugk_set_encoder_exact, ugk_set_layernorm_exact: the layer kernels' "
+                    "outputs bit-identical to train_bnn.c's"}
+        log(f"bench: step with every exact mode {ms_exact:.4f} ms -> "
+            f"{exact_forms['step (every exact mode)']['GBps']:.1f} GB/s on the reference's bytes")
 
     # ---- each op inside the step: a HIP event pair recorded by the dispatch of
     # every kernel the step driver issues (ugk_op_timer; the three-kernel
@@ -544,6 +579,18 @@ def main():
                                      lambda d: chk(lib.ugk_bayes_materialize(P_(d["w"]), P_(d["mu"]), P_(d["rho"]),
                                                                              P_(d["eps"]), P)))
     record(kernels, f"bayes_materialize (untied layout, n={P})", 16 * P, ms, launches, n_sets, {"per_step": 0})
+    # the exact forms of the kernels that have one, cold at the same shapes (into exact_forms)
+    if not args.no_exact:
+        for names, setter in ((("layernorm_forward", "layernorm_backward"), ugk.set_layernorm_exact),
+                              (("gelu_forward", "gelu_backward"), ugk.set_gelu_exact)):
+            setter(True)
+            try:
+                for name in names:
+                    make, set_bytes, fn = plan[name]
+                    ms, launches, n_sets = time_cold(make, set_bytes, fn)
+                    record(exact_forms, f"{name} (exact form)", per[name], ms, launches, n_sets)
+            finally:
+                setter(False)
 
     # ---- the practical HBM ceiling of each kernel's load/store mix: a pure
     # stream (ugk_diag_stream) with the same number of input and output
@@ -761,7 +808,7 @@ def main():
         "ms_per_step_stats": step_stats, "value_basis": "reference sequence's algorithmic bytes (unfused) / step time",
         "frac_of_peak": round(value / PEAK_GBS, 4), "bytes_per_step": total_bytes,
         "bytes_per_step_moved": moved_bytes, "GBps_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9, 1),
-        "frac_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4), "zeroed_backward": zeroed,
+        "frac_moved": round(moved_bytes / (ms_step * 1e-3) / 1e9 / PEAK_GBS, 4), "zeroed_backward": zeroed, "exact_forms": exact_forms,
         "in_step": in_step,
         "kernels": kernels, "configs": configs, "posterior": posterior, "head": head, "roofline": roofline, "cpu_baseline": cpu,
     }

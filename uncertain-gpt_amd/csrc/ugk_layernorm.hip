@@ -1025,47 +1025,53 @@ namespace {
 // train_bnn.c:81-115 and :439-477 add each row's terms one column at a time
 // (c = 0, 1, ..., C-1), and dweight/dbias one row at a time. The exact kernels
 // keep those orders, each sum a serial chain in one lane:
-//   k_ln_rows_exact: a workgroup per 64 rows. Fifteen loader wavefronts stage
-//     64-column tiles of the rows in LDS (row pitch 65 floats, so that the
-//     chains' column reads do not conflict), three tiles ahead in registers;
+//   rows: a workgroup per 64 rows. Fifteen loader wavefronts stage 64-column
+//     tiles of the rows in LDS (row pitch 65 floats, so that the chains'
+//     column reads do not conflict), three tiles ahead in registers;
 //     wavefront 0 runs one chain per row (lane = row) over each tile as it
 //     arrives. The forward streams the tiles twice (the sum, then the squared
 //     deviations from the mean, as the CPU loop does), the backward once (both
 //     of its row sums). Then every wavefront writes out (or adds to dinp)
-//     whole rows with the row statistics.
-//   k_ln_cols_exact: a workgroup per 32 columns. The loaders stage 128-row
-//     tiles of the dweight terms dout * xhat (rounded as the CPU rounds them)
-//     and the dbias terms dout; lanes 0-31 of wavefront 0 chain dweight, lanes
-//     32-63 dbias, one row after another, from the values the arrays hold.
-// No product is contracted into an fma, and the square root and quotients are
-// IEEE's, so every result is train_bnn.c's bit for bit. Scalar loads and
-// stores: any C, any alignment.
+//     whole rows with the row statistics, eight loads per lane in flight.
+//   columns: a workgroup per 16 columns. The loaders stage 256-row tiles of
+//     the dweight terms dout * xhat (rounded as the CPU rounds them) and the
+//     dbias terms dout; lanes 0-15 of wavefront 0 chain dweight, lanes 16-31
+//     dbias, one row after another, from the values the arrays hold.
+// The backward's row and column workgroups are independent and share one
+// launch. No product is contracted into an fma, and the square root and
+// quotients are IEEE's, so every result is train_bnn.c's bit for bit. Scalar
+// loads and stores: any C, any alignment.
 constexpr int kExLoaders = 15;
 constexpr int kExThreads = (kExLoaders + 1) * kWave;
 constexpr int kExLoadLanes = kExLoaders * kWave;
 constexpr int kExDepth = 3;  // tiles in registers ahead of the chains
-constexpr int kExRows = 64;  // rows per workgroup of the row kernel (one chain per lane)
-constexpr int kExTile = 64;  // columns per tile of the row kernel
+constexpr int kExRows = 64;  // rows per row workgroup (one chain per lane)
+constexpr int kExTile = 64;  // columns per tile of a row workgroup
 constexpr int kExPitch = kExTile + 1;
 constexpr int kExSlots = (kExRows * kExTile + kExLoadLanes - 1) / kExLoadLanes;
-constexpr int kExCols = 32;      // columns per workgroup of the column kernel
-constexpr int kExColRows = 128;  // rows per tile of the column kernel
+constexpr int kExApply = 8;       // elements per lane in flight when the rows are written
+constexpr int kExCols = 16;       // columns per column workgroup (two chains each)
+constexpr int kExColRows = 256;   // rows per tile of a column workgroup
+constexpr int kExColPitch = 2 * kExCols;  // a tile row: the dweight terms, then the dbias terms
 constexpr int kExColSlots = (kExColRows * kExCols + kExLoadLanes - 1) / kExLoadLanes;
-static_assert(kExRows == kWave && 2 * kExCols == kWave, "one chain per lane of wavefront 0");
+static_assert(kExRows == kWave && kWave % kExCols == 0 && kExColPitch <= kWave, "chains in wavefront 0");
+// LDS of a row workgroup (floats): tiles, weight tiles, per-row statistics and sums
+constexpr int ex_row_lds(int arrays) { return 2 * arrays * kExRows * kExPitch + 2 * kExTile + 4 * kExRows; }
+constexpr int kExColLds = 2 * kExColRows * kExColPitch;
+constexpr int kExBwdLds = ex_row_lds(2) > kExColLds ? ex_row_lds(2) : kExColLds;
 
 template <bool kBwd>
-__global__ __launch_bounds__(kExThreads) void k_ln_rows_exact(float *__restrict__ outp, float *__restrict__ mean,
-                                                              float *__restrict__ rstd, const float *__restrict__ inp,
-                                                              const float *__restrict__ dout,
-                                                              const float *__restrict__ weight,
-                                                              const float *__restrict__ bias, int rows, int C) {
+__device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__restrict__ outp, float *__restrict__ mean,
+                                              float *__restrict__ rstd, const float *__restrict__ inp,
+                                              const float *__restrict__ dout, const float *__restrict__ weight,
+                                              const float *__restrict__ bias, int rows, int C) {
   constexpr int kArr = kBwd ? 2 : 1;  // staged arrays: inp (and dout)
-  __shared__ float tile[2][kArr][kExRows * kExPitch];
-  __shared__ float wtile[2][kExTile];
-  __shared__ float2 stat[kExRows];  // per row: mean, rstd
-  __shared__ float2 rsum[kExRows];  // backward: the two row sums over C
+  float *const tile = lds;                                      // [2][kArr][kExRows * kExPitch]
+  float *const wtile = lds + 2 * kArr * kExRows * kExPitch;     // [2][kExTile]
+  float2 *const stat = reinterpret_cast<float2 *>(wtile + 2 * kExTile);  // [kExRows]: mean, rstd
+  float2 *const rsum = stat + kExRows;                                   // [kExRows]: the backward's row sums / C
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
-  const int r0 = blockIdx.x * kExRows;
+  const int r0 = blk * kExRows;
   const int nt = (C + kExTile - 1) / kExTile;
   const int nu = (kBwd ? 1 : 2) * nt;  // tiles streamed: the forward reads every tile twice
   const float Cf = (float)C;
@@ -1092,16 +1098,16 @@ __global__ __launch_bounds__(kExThreads) void k_ln_rows_exact(float *__restrict_
     wreg[k] = kBwd ? weight[col] : 0.0f;
   };
   auto store_tile = [&](int u, int k) {
-    const int b = u & 1;
+    float *const T = tile + (u & 1) * kArr * kExRows * kExPitch;
 #pragma unroll
     for (int s = 0; s < kExSlots; s++) {
       const int ri = lw + kExLoaders * s;
       if (ri < kExRows) {
 #pragma unroll
-        for (int a = 0; a < kArr; a++) tile[b][a][ri * kExPitch + lane] = reg[k][a][s];
+        for (int a = 0; a < kArr; a++) T[a * kExRows * kExPitch + ri * kExPitch + lane] = reg[k][a][s];
       }
     }
-    if (kBwd && lw == 0) wtile[b][lane] = wreg[k];
+    if (kBwd && lw == 0) wtile[(u & 1) * kExTile + lane] = wreg[k];
   };
   if (wave > 0) {
 #pragma unroll
@@ -1121,12 +1127,12 @@ __global__ __launch_bounds__(kExThreads) void k_ln_rows_exact(float *__restrict_
       // last read before this barrier
       __syncthreads();
       if (wave == 0) {
-        const int b = u & 1, t = u % nt;
+        const int t = u % nt;
         const int cmax = min(kExTile, C - t * kExTile);
-        const float *X = &tile[b][0][lane * kExPitch];
+        const float *X = tile + (u & 1) * kArr * kExRows * kExPitch + lane * kExPitch;
         if (kBwd) {
-          const float *Y = &tile[b][kArr - 1][lane * kExPitch];
-          const float *W = wtile[b];
+          const float *Y = X + kExRows * kExPitch;
+          const float *W = wtile + (u & 1) * kExTile;
           for (int c = 0; c < cmax; c++) {
             const float xh = (X[c] - cm) * cr;
             const float dn = Y[c] * W[c];
@@ -1160,40 +1166,57 @@ __global__ __launch_bounds__(kExThreads) void k_ln_rows_exact(float *__restrict_
   }
   __syncthreads();
   // the rows' elements, every wavefront on whole rows (inp and dout again,
-  // from the cache)
+  // from the cache), kExApply loads per lane and array issued together
   for (int ri = wave; ri < kExRows; ri += kExLoaders + 1) {
     const int row = r0 + ri;
     if (row >= rows) break;
     const float m = stat[ri].x, r = stat[ri].y;
+    const float2 rs = kBwd ? rsum[ri] : make_float2(0.0f, 0.0f);
     const size_t base = (size_t)row * C;
-    if (kBwd) {
-      const float dnm = rsum[ri].x, dnxm = rsum[ri].y;
-      for (int c = lane; c < C; c += kWave) {
-        const float xh = (inp[base + c] - m) * r;
-        const float dn = dout[base + c] * weight[c];
-        outp[base + c] += r * (dn - dnm - xh * dnxm);
+    for (int c0 = 0; c0 < C; c0 += kExApply * kWave) {
+      float xv[kExApply], wv[kExApply], yv[kExApply], dv[kExApply];
+#pragma unroll
+      for (int k = 0; k < kExApply; k++) {
+        const int c = min(c0 + k * kWave + lane, C - 1);
+        xv[k] = inp[base + c];
+        wv[k] = weight[c];
+        yv[k] = kBwd ? dout[base + c] : bias[c];
+        dv[k] = kBwd ? outp[base + c] : 0.0f;
       }
-    } else {
-      for (int c = lane; c < C; c += kWave) outp[base + c] = (inp[base + c] - m) * r * weight[c] + bias[c];
+#pragma unroll
+      for (int k = 0; k < kExApply; k++) {
+        const int c = c0 + k * kWave + lane;
+        if (c < C) {
+          if (kBwd) {
+            const float xh = (xv[k] - m) * r;
+            const float dn = yv[k] * wv[k];
+            outp[base + c] = dv[k] + r * (dn - rs.x - xh * rs.y);
+          } else {
+            outp[base + c] = (xv[k] - m) * r * wv[k] + yv[k];
+          }
+        }
+      }
     }
   }
 }
 
-__global__ __launch_bounds__(kExThreads) void k_ln_cols_exact(float *__restrict__ dweight, float *__restrict__ dbias,
-                                                              const float *__restrict__ dout,
-                                                              const float *__restrict__ inp,
-                                                              const float *__restrict__ mean,
-                                                              const float *__restrict__ rstd, int rows, int C) {
-  constexpr int kPitch = 2 * kExCols;  // per row: the 32 dweight terms, then the 32 dbias terms
-  __shared__ float tile[2][kExColRows * kPitch];
+__device__ __forceinline__ void ln_cols_exact(float *lds, int blk, float *__restrict__ dweight,
+                                              float *__restrict__ dbias, const float *__restrict__ dout,
+                                              const float *__restrict__ inp, const float *__restrict__ mean,
+                                              const float *__restrict__ rstd, int rows, int C) {
+  float *const tile = lds;  // [2][kExColRows * kExColPitch]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
-  const int c0 = blockIdx.x * kExCols;
+  const int c0 = blk * kExCols;
   const int nt = (rows + kExColRows - 1) / kExColRows;
-  // loader wavefront lw takes tile rows 2 lw + 30 s + lane / 32, column lane % 32
+  // loader wavefront lw takes tile rows 4 lw + 60 s + lane / 16, column lane % 16
+  constexpr int kRowsPerLoad = kWave / kExCols;
   const int lw = wave - 1;
-  const int lcol = min(c0 + (lane & (kExCols - 1)), C - 1);
+  const int lc = lane & (kExCols - 1);
+  const int lcol = min(c0 + lc, C - 1);
   float rx[kExDepth][kExColSlots], ry[kExDepth][kExColSlots], rm[kExDepth][kExColSlots], rr[kExDepth][kExColSlots];
-  auto tile_row = [&](int s) { return 2 * lw + 2 * kExLoaders * s + (lane >> 5); };
+  auto tile_row = [&](int s) {
+    return kRowsPerLoad * lw + kRowsPerLoad * kExLoaders * s + lane / kExCols;
+  };
   auto load_tile = [&](int t, int k) {
 #pragma unroll
     for (int s = 0; s < kExColSlots; s++) {
@@ -1206,21 +1229,23 @@ __global__ __launch_bounds__(kExThreads) void k_ln_cols_exact(float *__restrict_
     }
   };
   auto store_tile = [&](int t, int k) {
-    float *T = tile[t & 1];
+    float *const T = tile + (t & 1) * kExColRows * kExColPitch;
 #pragma unroll
     for (int s = 0; s < kExColSlots; s++) {
       const int ri = tile_row(s);
       if (ri < kExColRows) {
         const float xh = (rx[k][s] - rm[k][s]) * rr[k][s];
-        T[ri * kPitch + (lane & (kExCols - 1))] = ry[k][s] * xh;
-        T[ri * kPitch + kExCols + (lane & (kExCols - 1))] = ry[k][s];
+        T[ri * kExColPitch + lc] = ry[k][s] * xh;
+        T[ri * kExColPitch + kExCols + lc] = ry[k][s];
       }
     }
   };
-  // the chain of wavefront 0's lane: dweight (lanes 0-31) or dbias (32-63) of column c0 + lane % 32
-  const int cc = c0 + (lane & (kExCols - 1));
+  // the chain of wavefront 0's lane: dweight (lanes 0-15) or dbias (16-31) of
+  // column c0 + lane % 16; lanes 32-63 follow a copy and store nothing
+  const bool chain = wave == 0 && lane < kExColPitch;
+  const int cc = c0 + lc;
   float *const dst = (lane < kExCols ? dweight : dbias) + min(cc, C - 1);
-  float acc = wave == 0 ? *dst : 0.0f;
+  float acc = chain ? *dst : 0.0f;
   if (wave > 0) {
 #pragma unroll
     for (int k = 0; k < kExDepth; k++)
@@ -1237,13 +1262,37 @@ __global__ __launch_bounds__(kExThreads) void k_ln_cols_exact(float *__restrict_
       }
       __syncthreads();
       if (wave == 0) {
-        const float *T = tile[t & 1] + lane;
+        const float *T = tile + (t & 1) * kExColRows * kExColPitch + (lane & (kExColPitch - 1));
         const int rmax = min(kExColRows, rows - t * kExColRows);
-        for (int i = 0; i < rmax; i++) acc = acc + T[i * kPitch];
+        for (int i = 0; i < rmax; i++) acc = acc + T[i * kExColPitch];
       }
     }
   }
-  if (wave == 0 && cc < C) *dst = acc;
+  if (chain && cc < C) *dst = acc;
+}
+
+__global__ __launch_bounds__(kExThreads) void k_ln_fwd_exact(float *__restrict__ out, float *__restrict__ mean,
+                                                             float *__restrict__ rstd, const float *__restrict__ inp,
+                                                             const float *__restrict__ weight,
+                                                             const float *__restrict__ bias, int rows, int C) {
+  __shared__ float lds[ex_row_lds(1)];
+  ln_rows_exact<false>(lds, blockIdx.x, out, mean, rstd, inp, nullptr, weight, bias, rows, C);
+}
+
+// workgroups [0, nrow) the rows (dinp), the others the columns (dweight, dbias)
+__global__ __launch_bounds__(kExThreads) void k_ln_bwd_exact(float *__restrict__ dinp, float *__restrict__ dweight,
+                                                             float *__restrict__ dbias, const float *__restrict__ dout,
+                                                             const float *__restrict__ inp,
+                                                             const float *__restrict__ weight,
+                                                             const float *__restrict__ mean,
+                                                             const float *__restrict__ rstd, int rows, int C,
+                                                             int nrow) {
+  __shared__ float lds[kExBwdLds];
+  if ((int)blockIdx.x < nrow)
+    ln_rows_exact<true>(lds, blockIdx.x, dinp, const_cast<float *>(mean), const_cast<float *>(rstd), inp, dout,
+                        weight, nullptr, rows, C);
+  else
+    ln_cols_exact(lds, (int)blockIdx.x - nrow, dweight, dbias, dout, inp, mean, rstd, rows, C);
 }
 
 }  // namespace
@@ -1258,19 +1307,17 @@ int layernorm_exact() { return g_ln_exact.load(); }
 int launch_layernorm_forward_exact(float *out, float *mean, float *rstd, const float *inp, const float *weight,
                                    const float *bias, int rows, int C) {
   if (rows == 0 || C == 0) return 0;
-  launch(k_ln_rows_exact<false>, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, out, mean, rstd, inp,
-         static_cast<const float *>(nullptr), weight, bias, rows, C);
+  launch(k_ln_fwd_exact, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, out, mean, rstd, inp, weight,
+         bias, rows, C);
   return check_launch("layernorm_forward (exact)");
 }
 
 int launch_layernorm_backward_exact(float *dinp, float *dweight, float *dbias, const float *dout, const float *inp,
                                     const float *weight, const float *mean, const float *rstd, int rows, int C) {
   if (rows == 0 || C == 0) return 0;
-  launch(k_ln_rows_exact<true>, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, dinp,
-         const_cast<float *>(mean), const_cast<float *>(rstd), inp, dout, weight, static_cast<const float *>(nullptr),
-         rows, C);
-  launch(k_ln_cols_exact, dim3(grid_for((size_t)C, kExCols)), dim3(kExThreads), 0, dweight, dbias, dout, inp, mean,
-         rstd, rows, C);
+  const int nrow = (int)grid_for((size_t)rows, kExRows), ncol = (int)grid_for((size_t)C, kExCols);
+  launch(k_ln_bwd_exact, dim3(nrow + ncol), dim3(kExThreads), 0, dinp, dweight, dbias, dout, inp, weight, mean, rstd,
+         rows, C, nrow);
   return check_launch("layernorm_backward (exact)");
 }
 
