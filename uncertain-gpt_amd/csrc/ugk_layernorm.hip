@@ -1024,90 +1024,204 @@ namespace {
 // ---- exact mode: train_bnn.c's order of every addition ------------------------
 // train_bnn.c:81-115 and :439-477 add each row's terms one column at a time
 // (c = 0, 1, ..., C-1), and dweight/dbias one row at a time. The exact kernels
-// keep those orders, each sum a serial chain in one lane:
-//   rows: a workgroup per 64 rows. Fifteen loader wavefronts stage 64-column
-//     tiles of the rows in LDS (row pitch 65 floats, so that the chains'
-//     column reads do not conflict), three tiles ahead in registers;
-//     wavefront 0 runs one chain per row (lane = row) over each tile as it
-//     arrives. The forward streams the tiles twice (the sum, then the squared
-//     deviations from the mean, as the CPU loop does), the backward once (both
-//     of its row sums). Then every wavefront writes out (or adds to dinp)
-//     whole rows with the row statistics, eight loads per lane in flight.
-//   columns: a workgroup per 16 columns. The loaders stage 256-row tiles of
-//     the dweight terms dout * xhat (rounded as the CPU rounds them) and the
-//     dbias terms dout; lanes 0-15 of wavefront 0 chain dweight, lanes 16-31
-//     dbias, one row after another, from the values the arrays hold.
-// The backward's row and column workgroups are independent and share one
-// launch. No product is contracted into an fma, and the square root and
-// quotients are IEEE's, so every result is train_bnn.c's bit for bit. Scalar
-// loads and stores: any C, any alignment.
+// keep those orders, each sum a serial chain in one lane of wavefront 0, which
+// does nothing but the chains' additions; fifteen loader wavefronts keep it fed:
+//   rows: a workgroup per 60 rows. The loaders stream 64-column tiles of the
+//     rows, three tiles ahead in registers, and stage each row's terms in LDS
+//     (the forward: x, then (x - mean)^2; the backward: dout * w and
+//     dout * w * xhat), row-major at a pitch of 68 floats, so that the chains
+//     read four terms at a time without bank conflicts. One chain per row
+//     (lane = row; lanes 60-63 follow copies and store nothing; 60 rows make a
+//     tile whole loader slots, scalar and float4). Then every wavefront writes out (or adds to dinp) whole
+//     rows with the row statistics.
+//   columns: a workgroup per 16 columns. The loaders stage 240-row tiles of
+//     the dweight terms dout * xhat and the dbias terms dout, transposed (a
+//     column's terms contiguous, pitch 244 floats); lanes 0-15 chain dweight,
+//     lanes 16-31 dbias, one row after another, from the values the arrays hold.
+// Every term is rounded as the CPU rounds it (no product is contracted into an
+// fma; the square root and quotients are IEEE's), so every result is
+// train_bnn.c's bit for bit. The backward's row and column workgroups are
+// independent and share one launch. kVec: C a multiple of 4 and the row
+// arrays 16-byte aligned, every global access of the rows a float4 (a quarter
+// of the memory instructions, which bound these kernels); otherwise scalar
+// accesses, any C, any alignment.
 constexpr int kExLoaders = 15;
 constexpr int kExThreads = (kExLoaders + 1) * kWave;
 constexpr int kExLoadLanes = kExLoaders * kWave;
 constexpr int kExDepth = 3;  // tiles in registers ahead of the chains
-constexpr int kExRows = 64;  // rows per row workgroup (one chain per lane)
+constexpr int kExRows = 60;  // rows per row workgroup (one chain per lane of wavefront 0)
 constexpr int kExTile = 64;  // columns per tile of a row workgroup
-constexpr int kExPitch = kExTile + 1;
+constexpr int kExPitch = kExTile + 4;
 constexpr int kExSlots = (kExRows * kExTile + kExLoadLanes - 1) / kExLoadLanes;
-constexpr int kExApply = 8;       // elements per lane in flight when the rows are written
+constexpr int kExVecSlots = (kExRows * kExTile / 4 + kExLoadLanes - 1) / kExLoadLanes;
+constexpr int kExApply = 8;       // scalar elements per lane in flight when the rows are written
+constexpr int kExApplyVec = 4;    // float4 per lane in flight when the rows are written
 constexpr int kExCols = 16;       // columns per column workgroup (two chains each)
-constexpr int kExColRows = 256;   // rows per tile of a column workgroup
-constexpr int kExColPitch = 2 * kExCols;  // a tile row: the dweight terms, then the dbias terms
-constexpr int kExColSlots = (kExColRows * kExCols + kExLoadLanes - 1) / kExLoadLanes;
-static_assert(kExRows == kWave && kWave % kExCols == 0 && kExColPitch <= kWave, "chains in wavefront 0");
-// LDS of a row workgroup (floats): tiles, weight tiles, per-row statistics and sums
-constexpr int ex_row_lds(int arrays) { return 2 * arrays * kExRows * kExPitch + 2 * kExTile + 4 * kExRows; }
-constexpr int kExColLds = 2 * kExColRows * kExColPitch;
+constexpr int kExChains = 2 * kExCols;
+constexpr int kExColRows = 240;   // rows per tile of a column workgroup
+constexpr int kExColPitch = kExColRows + 4;
+constexpr int kExColSlots = kExColRows * kExCols / kExLoadLanes;
+// float4 reads per chain and batch (two batches in flight): 32 additions a
+// batch in the row chains; 24 in the column chains, whose loaders hold more
+// registers
+constexpr int kExBatch = 8;
+constexpr int kExColBatch = 6;
+static_assert(kExRows <= kWave && kWave % kExCols == 0 && kExChains <= kWave, "chains in wavefront 0");
+static_assert(kExRows * kExTile == kExSlots * kExLoadLanes && kExRows * kExTile / 4 == kExVecSlots * kExLoadLanes,
+              "a row tile is whole loader slots, scalar and float4");
+static_assert(kExColRows * kExCols == kExColSlots * kExLoadLanes && kExColRows * kExCols / 4 == kExLoadLanes,
+              "a column tile is whole loader slots, scalar and float4");
+static_assert(kExTile % (8 * kExBatch) == 0 && kExColRows % (8 * kExColBatch) == 0, "whole batch pairs per tile");
+static_assert(kExLoadLanes % (kExTile / 4) == 0, "a loader lane keeps its float4 column in every slot");
+// LDS of a row workgroup (floats): term tiles (a row per lane of wavefront 0),
+// per-row statistics and sums
+constexpr int ex_row_lds(int arrays) { return 2 * arrays * kWave * kExPitch + 4 * kWave; }
+constexpr int kExColLds = 2 * kExChains * kExColPitch;
 constexpr int kExBwdLds = ex_row_lds(2) > kExColLds ? ex_row_lds(2) : kExColLds;
 
-template <bool kBwd>
+// s = (((s + t[0]) + t[1]) + ...) + t[4 n4 - 1] for each of kArr chains, the
+// terms of chain a at t[a]; n4 float4 reads per chain, a multiple of 2 kB.
+// The reads of a batch (kB float4 per chain) are issued before the additions
+// of the batch before, which cover the LDS latency; the scheduling barriers
+// keep the compiler from sinking the reads down to their use.
+template <int kArr, int kB>
+__device__ __forceinline__ void ex_chain4(float (&s)[kArr], const float4 *const (&t)[kArr], int n4) {
+  float4 a[kArr][kB], b[kArr][kB];
+#pragma unroll
+  for (int r = 0; r < kArr; r++)
+#pragma unroll
+    for (int k = 0; k < kB; k++) a[r][k] = t[r][k];
+  for (int q = 0; q < n4; q += 2 * kB) {
+#pragma unroll
+    for (int r = 0; r < kArr; r++)
+#pragma unroll
+      for (int k = 0; k < kB; k++) b[r][k] = t[r][q + kB + k];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kB; k++)
+#pragma unroll
+      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + a[r][k].x) + a[r][k].y) + a[r][k].z) + a[r][k].w;
+    __builtin_amdgcn_sched_barrier(0);
+    if (q + 2 * kB < n4) {
+#pragma unroll
+      for (int r = 0; r < kArr; r++)
+#pragma unroll
+        for (int k = 0; k < kB; k++) a[r][k] = t[r][q + 2 * kB + k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kB; k++)
+#pragma unroll
+      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + b[r][k].x) + b[r][k].y) + b[r][k].z) + b[r][k].w;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ float f4_get(const float4 &v, int j) {
+  return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
+template <bool kBwd, bool kVec>
 __device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__restrict__ outp, float *__restrict__ mean,
                                               float *__restrict__ rstd, const float *__restrict__ inp,
                                               const float *__restrict__ dout, const float *__restrict__ weight,
                                               const float *__restrict__ bias, int rows, int C) {
-  constexpr int kArr = kBwd ? 2 : 1;  // staged arrays: inp (and dout)
-  float *const tile = lds;                                      // [2][kArr][kExRows * kExPitch]
-  float *const wtile = lds + 2 * kArr * kExRows * kExPitch;     // [2][kExTile]
-  float2 *const stat = reinterpret_cast<float2 *>(wtile + 2 * kExTile);  // [kExRows]: mean, rstd
-  float2 *const rsum = stat + kExRows;                                   // [kExRows]: the backward's row sums / C
+  constexpr int kArr = kBwd ? 2 : 1;  // staged term arrays
+  constexpr int kTileF = kWave * kExPitch;
+  constexpr int kSlots = kVec ? kExVecSlots : kExSlots;
+  constexpr int kW = kVec ? 4 : 1;  // floats per lane and slot
+  float *const tile = lds;  // [2][kArr][kTileF]
+  float2 *const stat = reinterpret_cast<float2 *>(lds + 2 * kArr * kTileF);  // [kWave]: mean, rstd
+  float2 *const rsum = stat + kWave;  // [kWave]: the backward's row sums / C
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
   const int r0 = blk * kExRows;
   const int nt = (C + kExTile - 1) / kExTile;
   const int nu = (kBwd ? 1 : 2) * nt;  // tiles streamed: the forward reads every tile twice
   const float Cf = (float)C;
-  // the chain of wavefront 0's lane: row r0 + lane
-  float cm = 0.0f, cr = 0.0f, s1 = 0.0f, s2 = 0.0f;
+  float s[kArr];  // the chains of wavefront 0's lane: row r0 + lane
+#pragma unroll
+  for (int a = 0; a < kArr; a++) s[a] = 0.0f;
   if (kBwd) {
-    const int crow = min(r0 + lane, rows - 1);
-    cm = mean[crow];
-    cr = rstd[crow];
-  }
-  // loader wavefront lw takes tile rows lw + 15 s, column lane
-  const int lw = wave - 1;
-  float reg[kExDepth][kArr][kExSlots];
-  float wreg[kExDepth];
-  auto load_tile = [&](int u, int k) {
-    const int col = min((u % nt) * kExTile + lane, C - 1);
-#pragma unroll
-    for (int s = 0; s < kExSlots; s++) {
-      const int ri = min(lw + kExLoaders * s, kExRows - 1);
-      const size_t off = (size_t)min(r0 + ri, rows - 1) * C + col;
-      reg[k][0][s] = inp[off];
-      if (kBwd) reg[k][kArr - 1][s] = dout[off];
+    // the rows' statistics, for the loaders' terms and the writes
+    if (wave == 0) {
+      const int crow = min(r0 + lane, rows - 1);
+      stat[lane] = make_float2(mean[crow], rstd[crow]);
     }
-    wreg[k] = kBwd ? weight[col] : 0.0f;
-  };
-  auto store_tile = [&](int u, int k) {
-    float *const T = tile + (u & 1) * kArr * kExRows * kExPitch;
+    __syncthreads();
+  }
+  // Loader lane L = 64 lw + lane. Scalar: slot sl holds tile row lw + 15 sl,
+  // column lane. float4: slot sl holds float4 f = L + 960 sl of the tile (row
+  // f / 16, columns 4 (f % 16) + 0..3), the column the same in every slot.
+  const int lw = wave - 1;
+  const int L = lw * kWave + lane;
+  float reg[kExDepth][kArr][kSlots][kW];
+  float wreg[kExDepth][kW];
+  auto slot_row = [&](int sl) { return kVec ? (L + kExLoadLanes * sl) / (kExTile / 4) : lw + kExLoaders * sl; };
+  const int lcol = kVec ? 4 * (L % (kExTile / 4)) : lane;
+  auto load_tile = [&](int u, int k) {
+    const int col = min((u % nt) * kExTile + lcol, C - kW);
 #pragma unroll
-    for (int s = 0; s < kExSlots; s++) {
-      const int ri = lw + kExLoaders * s;
-      if (ri < kExRows) {
-#pragma unroll
-        for (int a = 0; a < kArr; a++) T[a * kExRows * kExPitch + ri * kExPitch + lane] = reg[k][a][s];
+    for (int sl = 0; sl < kSlots; sl++) {
+      const int ri = min(slot_row(sl), kExRows - 1);
+      const size_t off = (size_t)min(r0 + ri, rows - 1) * C + col;
+      if constexpr (kVec) {
+        const float4 x = *reinterpret_cast<const float4 *>(inp + off);
+        reg[k][0][sl][0] = x.x, reg[k][0][sl][1] = x.y, reg[k][0][sl][2] = x.z, reg[k][0][sl][3] = x.w;
+        if (kBwd) {
+          const float4 y = *reinterpret_cast<const float4 *>(dout + off);
+          reg[k][kArr - 1][sl][0] = y.x, reg[k][kArr - 1][sl][1] = y.y;
+          reg[k][kArr - 1][sl][2] = y.z, reg[k][kArr - 1][sl][3] = y.w;
+        }
+      } else {
+        reg[k][0][sl][0] = inp[off];
+        if (kBwd) reg[k][kArr - 1][sl][0] = dout[off];
       }
     }
-    if (kBwd && lw == 0) wtile[(u & 1) * kExTile + lane] = wreg[k];
+    if constexpr (kBwd) {
+      if constexpr (kVec) {
+        const float4 w = *reinterpret_cast<const float4 *>(weight + col);
+        wreg[k][0] = w.x, wreg[k][1] = w.y, wreg[k][2] = w.z, wreg[k][3] = w.w;
+      } else {
+        wreg[k][0] = weight[col];
+      }
+    }
+  };
+  auto store_tile = [&](int u, int k) {
+    float *const T = tile + (u & 1) * kArr * kTileF;
+#pragma unroll
+    for (int sl = 0; sl < kSlots; sl++) {
+      const int ri = slot_row(sl);
+      if (ri < kExRows) {
+        float t0[kW], t1[kW];
+        if (kBwd) {
+          const float2 st = stat[ri];
+#pragma unroll
+          for (int j = 0; j < kW; j++) {
+            const float xh = (reg[k][0][sl][j] - st.x) * st.y;
+            t0[j] = reg[k][kArr - 1][sl][j] * wreg[k][j];
+            t1[j] = t0[j] * xh;
+          }
+        } else if (u < nt) {
+#pragma unroll
+          for (int j = 0; j < kW; j++) t0[j] = reg[k][0][sl][j];
+        } else {
+          const float m = stat[ri].x;
+#pragma unroll
+          for (int j = 0; j < kW; j++) {
+            const float d = reg[k][0][sl][j] - m;
+            t0[j] = d * d;
+          }
+        }
+        float *const p = T + ri * kExPitch + lcol;
+        if constexpr (kVec) {
+          *reinterpret_cast<float4 *>(p) = make_float4(t0[0], t0[1], t0[2], t0[3]);
+          if (kBwd) *reinterpret_cast<float4 *>(p + kTileF) = make_float4(t1[0], t1[1], t1[2], t1[3]);
+        } else {
+          p[0] = t0[0];
+          if (kBwd) p[kTileF] = t1[0];
+        }
+      }
+    }
   };
   if (wave > 0) {
 #pragma unroll
@@ -1119,6 +1233,11 @@ __device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__rest
     for (int k = 0; k < kExDepth; k++) {
       const int u = u0 + k;
       if (u >= nu) break;  // the same in every thread
+      if (!kBwd && u == nt) {
+        // the second pass's terms need the means: wavefront 0 has written them
+        // after its last first-pass tile
+        __syncthreads();
+      }
       if (wave > 0) {
         store_tile(u, k);
         if (u + kExDepth < nu) load_tile(u + kExDepth, k);
@@ -1127,72 +1246,106 @@ __device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__rest
       // last read before this barrier
       __syncthreads();
       if (wave == 0) {
-        const int t = u % nt;
-        const int cmax = min(kExTile, C - t * kExTile);
-        const float *X = tile + (u & 1) * kArr * kExRows * kExPitch + lane * kExPitch;
-        if (kBwd) {
-          const float *Y = X + kExRows * kExPitch;
-          const float *W = wtile + (u & 1) * kExTile;
-          for (int c = 0; c < cmax; c++) {
-            const float xh = (X[c] - cm) * cr;
-            const float dn = Y[c] * W[c];
-            s1 = s1 + dn;
-            s2 = s2 + dn * xh;
-          }
-        } else if (u < nt) {
-          for (int c = 0; c < cmax; c++) s1 = s1 + X[c];
+        const int cmax = min(kExTile, C - (u % nt) * kExTile);
+        const float *X = tile + (u & 1) * kArr * kTileF + lane * kExPitch;
+        if (cmax == kExTile) {
+          const float4 *t[kArr];
+#pragma unroll
+          for (int a = 0; a < kArr; a++) t[a] = reinterpret_cast<const float4 *>(X + a * kTileF);
+          ex_chain4<kArr, kExBatch / kArr>(s, t, kExTile / 4);
         } else {
-          if (u == nt) cm = s1 / Cf;
           for (int c = 0; c < cmax; c++) {
-            const float d = X[c] - cm;
-            s2 = s2 + d * d;
+#pragma unroll
+            for (int a = 0; a < kArr; a++) s[a] = s[a] + X[a * kTileF + c];
           }
+        }
+        if (!kBwd && u == nt - 1) {
+          stat[lane].x = s[0] / Cf;
+          s[0] = 0.0f;
         }
       }
     }
   }
   if (wave == 0) {
     if (kBwd) {
-      stat[lane] = make_float2(cm, cr);
-      rsum[lane] = make_float2(s1 / Cf, s2 / Cf);
+      rsum[lane] = make_float2(s[0] / Cf, s[kArr - 1] / Cf);
     } else {
-      const float r = 1.0f / sqrtf(s2 / Cf + 1e-5f);
-      if (r0 + lane < rows) {
-        mean[r0 + lane] = cm;
+      const float m = stat[lane].x;
+      const float r = 1.0f / sqrtf(s[0] / Cf + 1e-5f);
+      if (lane < kExRows && r0 + lane < rows) {
+        mean[r0 + lane] = m;
         rstd[r0 + lane] = r;
       }
-      stat[lane] = make_float2(cm, r);
+      stat[lane].y = r;
     }
   }
   __syncthreads();
   // the rows' elements, every wavefront on whole rows (inp and dout again,
-  // from the cache), kExApply loads per lane and array issued together
+  // from the cache), all the loads of a batch issued together
   for (int ri = wave; ri < kExRows; ri += kExLoaders + 1) {
     const int row = r0 + ri;
     if (row >= rows) break;
     const float m = stat[ri].x, r = stat[ri].y;
     const float2 rs = kBwd ? rsum[ri] : make_float2(0.0f, 0.0f);
     const size_t base = (size_t)row * C;
-    for (int c0 = 0; c0 < C; c0 += kExApply * kWave) {
-      float xv[kExApply], wv[kExApply], yv[kExApply], dv[kExApply];
+    if constexpr (kVec) {
+      const int C4 = C >> 2;
+      const float4 *x4 = reinterpret_cast<const float4 *>(inp + base);
+      const float4 *y4 = reinterpret_cast<const float4 *>(kBwd ? dout + base : bias);
+      const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+      float4 *o4 = reinterpret_cast<float4 *>(outp + base);
+      for (int q0 = 0; q0 < C4; q0 += kExApplyVec * kWave) {
+        float4 xv[kExApplyVec], wv[kExApplyVec], yv[kExApplyVec], dv[kExApplyVec];
 #pragma unroll
-      for (int k = 0; k < kExApply; k++) {
-        const int c = min(c0 + k * kWave + lane, C - 1);
-        xv[k] = inp[base + c];
-        wv[k] = weight[c];
-        yv[k] = kBwd ? dout[base + c] : bias[c];
-        dv[k] = kBwd ? outp[base + c] : 0.0f;
+        for (int k = 0; k < kExApplyVec; k++) {
+          const int q = min(q0 + k * kWave + lane, C4 - 1);
+          xv[k] = x4[q];
+          wv[k] = w4[q];
+          yv[k] = y4[q];
+          if (kBwd) dv[k] = o4[q];
+        }
+#pragma unroll
+        for (int k = 0; k < kExApplyVec; k++) {
+          const int q = q0 + k * kWave + lane;
+          if (q < C4) {
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const float xj = f4_get(xv[k], j), wj = f4_get(wv[k], j), yj = f4_get(yv[k], j);
+              if (kBwd) {
+                const float xh = (xj - m) * r;
+                const float dn = yj * wj;
+                o[j] = f4_get(dv[k], j) + r * (dn - rs.x - xh * rs.y);
+              } else {
+                o[j] = (xj - m) * r * wj + yj;
+              }
+            }
+            o4[q] = make_float4(o[0], o[1], o[2], o[3]);
+          }
+        }
       }
+    } else {
+      for (int c0 = 0; c0 < C; c0 += kExApply * kWave) {
+        float xv[kExApply], wv[kExApply], yv[kExApply], dv[kExApply];
 #pragma unroll
-      for (int k = 0; k < kExApply; k++) {
-        const int c = c0 + k * kWave + lane;
-        if (c < C) {
-          if (kBwd) {
-            const float xh = (xv[k] - m) * r;
-            const float dn = yv[k] * wv[k];
-            outp[base + c] = dv[k] + r * (dn - rs.x - xh * rs.y);
-          } else {
-            outp[base + c] = (xv[k] - m) * r * wv[k] + yv[k];
+        for (int k = 0; k < kExApply; k++) {
+          const int c = min(c0 + k * kWave + lane, C - 1);
+          xv[k] = inp[base + c];
+          wv[k] = weight[c];
+          yv[k] = kBwd ? dout[base + c] : bias[c];
+          dv[k] = kBwd ? outp[base + c] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kExApply; k++) {
+          const int c = c0 + k * kWave + lane;
+          if (c < C) {
+            if (kBwd) {
+              const float xh = (xv[k] - m) * r;
+              const float dn = yv[k] * wv[k];
+              outp[base + c] = dv[k] + r * (dn - rs.x - xh * rs.y);
+            } else {
+              outp[base + c] = (xv[k] - m) * r * wv[k] + yv[k];
+            }
           }
         }
       }
@@ -1200,52 +1353,66 @@ __device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__rest
   }
 }
 
+template <bool kVec>
 __device__ __forceinline__ void ln_cols_exact(float *lds, int blk, float *__restrict__ dweight,
                                               float *__restrict__ dbias, const float *__restrict__ dout,
                                               const float *__restrict__ inp, const float *__restrict__ mean,
                                               const float *__restrict__ rstd, int rows, int C) {
-  float *const tile = lds;  // [2][kExColRows * kExColPitch]
+  constexpr int kTileF = kExChains * kExColPitch;
+  constexpr int kSlots = kVec ? 1 : kExColSlots;
+  constexpr int kW = kVec ? 4 : 1;  // floats per lane and slot
+  float *const tile = lds;  // [2][kExChains][kExColPitch]: chain j's terms of the tile's rows
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
   const int c0 = blk * kExCols;
   const int nt = (rows + kExColRows - 1) / kExColRows;
-  // loader wavefront lw takes tile rows 4 lw + 60 s + lane / 16, column lane % 16
-  constexpr int kRowsPerLoad = kWave / kExCols;
+  // Loader lane L = 64 lw + lane. Scalar: slot sl holds tile row
+  // 4 lw + 60 sl + lane / 16, column lane % 16. float4: tile row L / 4,
+  // columns 4 (L % 4) + 0..3.
   const int lw = wave - 1;
-  const int lc = lane & (kExCols - 1);
-  const int lcol = min(c0 + lc, C - 1);
-  float rx[kExDepth][kExColSlots], ry[kExDepth][kExColSlots], rm[kExDepth][kExColSlots], rr[kExDepth][kExColSlots];
-  auto tile_row = [&](int s) {
-    return kRowsPerLoad * lw + kRowsPerLoad * kExLoaders * s + lane / kExCols;
+  const int L = lw * kWave + lane;
+  const int lc = kVec ? 4 * (L & 3) : (lane & (kExCols - 1));
+  const int lcol = min(c0 + lc, C - kW);
+  float rx[kExDepth][kSlots][kW], ry[kExDepth][kSlots][kW], rm[kExDepth][kSlots], rr[kExDepth][kSlots];
+  auto tile_row = [&](int sl) {
+    return kVec ? L >> 2 : (kWave / kExCols) * (lw + kExLoaders * sl) + lane / kExCols;
   };
   auto load_tile = [&](int t, int k) {
 #pragma unroll
-    for (int s = 0; s < kExColSlots; s++) {
-      const int row = min(t * kExColRows + min(tile_row(s), kExColRows - 1), rows - 1);
+    for (int sl = 0; sl < kSlots; sl++) {
+      const int row = min(t * kExColRows + tile_row(sl), rows - 1);
       const size_t off = (size_t)row * C + lcol;
-      rx[k][s] = inp[off];
-      ry[k][s] = dout[off];
-      rm[k][s] = mean[row];
-      rr[k][s] = rstd[row];
+      if constexpr (kVec) {
+        const float4 x = *reinterpret_cast<const float4 *>(inp + off);
+        const float4 y = *reinterpret_cast<const float4 *>(dout + off);
+        rx[k][sl][0] = x.x, rx[k][sl][1] = x.y, rx[k][sl][2] = x.z, rx[k][sl][3] = x.w;
+        ry[k][sl][0] = y.x, ry[k][sl][1] = y.y, ry[k][sl][2] = y.z, ry[k][sl][3] = y.w;
+      } else {
+        rx[k][sl][0] = inp[off];
+        ry[k][sl][0] = dout[off];
+      }
+      rm[k][sl] = mean[row];
+      rr[k][sl] = rstd[row];
     }
   };
   auto store_tile = [&](int t, int k) {
-    float *const T = tile + (t & 1) * kExColRows * kExColPitch;
+    float *const T = tile + (t & 1) * kTileF;
 #pragma unroll
-    for (int s = 0; s < kExColSlots; s++) {
-      const int ri = tile_row(s);
-      if (ri < kExColRows) {
-        const float xh = (rx[k][s] - rm[k][s]) * rr[k][s];
-        T[ri * kExColPitch + lc] = ry[k][s] * xh;
-        T[ri * kExColPitch + kExCols + lc] = ry[k][s];
+    for (int sl = 0; sl < kSlots; sl++) {
+      const int ri = tile_row(sl);
+#pragma unroll
+      for (int j = 0; j < kW; j++) {
+        const float xh = (rx[k][sl][j] - rm[k][sl]) * rr[k][sl];
+        T[(lc + j) * kExColPitch + ri] = ry[k][sl][j] * xh;
+        T[(kExCols + lc + j) * kExColPitch + ri] = ry[k][sl][j];
       }
     }
   };
   // the chain of wavefront 0's lane: dweight (lanes 0-15) or dbias (16-31) of
   // column c0 + lane % 16; lanes 32-63 follow a copy and store nothing
-  const bool chain = wave == 0 && lane < kExColPitch;
-  const int cc = c0 + lc;
+  const bool chain = wave == 0 && lane < kExChains;
+  const int cc = c0 + (lane & (kExCols - 1));
   float *const dst = (lane < kExCols ? dweight : dbias) + min(cc, C - 1);
-  float acc = chain ? *dst : 0.0f;
+  float acc[1] = {chain ? *dst : 0.0f};
   if (wave > 0) {
 #pragma unroll
     for (int k = 0; k < kExDepth; k++)
@@ -1262,24 +1429,31 @@ __device__ __forceinline__ void ln_cols_exact(float *lds, int blk, float *__rest
       }
       __syncthreads();
       if (wave == 0) {
-        const float *T = tile + (t & 1) * kExColRows * kExColPitch + (lane & (kExColPitch - 1));
+        const float *T = tile + (t & 1) * kTileF + (lane & (kExChains - 1)) * kExColPitch;
         const int rmax = min(kExColRows, rows - t * kExColRows);
-        for (int i = 0; i < rmax; i++) acc = acc + T[i * kExColPitch];
+        if (rmax == kExColRows) {
+          const float4 *t4[1] = {reinterpret_cast<const float4 *>(T)};
+          ex_chain4<1, kExColBatch>(acc, t4, kExColRows / 4);
+        } else {
+          for (int i = 0; i < rmax; i++) acc[0] = acc[0] + T[i];
+        }
       }
     }
   }
-  if (chain && cc < C) *dst = acc;
+  if (chain && cc < C) *dst = acc[0];
 }
 
+template <bool kVec>
 __global__ __launch_bounds__(kExThreads) void k_ln_fwd_exact(float *__restrict__ out, float *__restrict__ mean,
                                                              float *__restrict__ rstd, const float *__restrict__ inp,
                                                              const float *__restrict__ weight,
                                                              const float *__restrict__ bias, int rows, int C) {
-  __shared__ float lds[ex_row_lds(1)];
-  ln_rows_exact<false>(lds, blockIdx.x, out, mean, rstd, inp, nullptr, weight, bias, rows, C);
+  __shared__ __align__(16) float lds[ex_row_lds(1)];
+  ln_rows_exact<false, kVec>(lds, blockIdx.x, out, mean, rstd, inp, nullptr, weight, bias, rows, C);
 }
 
 // workgroups [0, nrow) the rows (dinp), the others the columns (dweight, dbias)
+template <bool kVec>
 __global__ __launch_bounds__(kExThreads) void k_ln_bwd_exact(float *__restrict__ dinp, float *__restrict__ dweight,
                                                              float *__restrict__ dbias, const float *__restrict__ dout,
                                                              const float *__restrict__ inp,
@@ -1287,12 +1461,12 @@ __global__ __launch_bounds__(kExThreads) void k_ln_bwd_exact(float *__restrict__
                                                              const float *__restrict__ mean,
                                                              const float *__restrict__ rstd, int rows, int C,
                                                              int nrow) {
-  __shared__ float lds[kExBwdLds];
+  __shared__ __align__(16) float lds[kExBwdLds];
   if ((int)blockIdx.x < nrow)
-    ln_rows_exact<true>(lds, blockIdx.x, dinp, const_cast<float *>(mean), const_cast<float *>(rstd), inp, dout,
-                        weight, nullptr, rows, C);
+    ln_rows_exact<true, kVec>(lds, blockIdx.x, dinp, const_cast<float *>(mean), const_cast<float *>(rstd), inp, dout,
+                              weight, nullptr, rows, C);
   else
-    ln_cols_exact(lds, (int)blockIdx.x - nrow, dweight, dbias, dout, inp, mean, rstd, rows, C);
+    ln_cols_exact<kVec>(lds, (int)blockIdx.x - nrow, dweight, dbias, dout, inp, mean, rstd, rows, C);
 }
 
 }  // namespace
@@ -1307,17 +1481,25 @@ int layernorm_exact() { return g_ln_exact.load(); }
 int launch_layernorm_forward_exact(float *out, float *mean, float *rstd, const float *inp, const float *weight,
                                    const float *bias, int rows, int C) {
   if (rows == 0 || C == 0) return 0;
-  launch(k_ln_fwd_exact, dim3(grid_for((size_t)rows, kExRows)), dim3(kExThreads), 0, out, mean, rstd, inp, weight,
-         bias, rows, C);
+  const bool vec = C % 4 == 0 && aligned16(out) && aligned16(inp) && aligned16(weight) && aligned16(bias);
+  const dim3 grid(grid_for((size_t)rows, kExRows)), block(kExThreads);
+  if (vec)
+    launch(k_ln_fwd_exact<true>, grid, block, 0, out, mean, rstd, inp, weight, bias, rows, C);
+  else
+    launch(k_ln_fwd_exact<false>, grid, block, 0, out, mean, rstd, inp, weight, bias, rows, C);
   return check_launch("layernorm_forward (exact)");
 }
 
 int launch_layernorm_backward_exact(float *dinp, float *dweight, float *dbias, const float *dout, const float *inp,
                                     const float *weight, const float *mean, const float *rstd, int rows, int C) {
   if (rows == 0 || C == 0) return 0;
+  const bool vec = C % 4 == 0 && aligned16(dinp) && aligned16(dout) && aligned16(inp) && aligned16(weight);
   const int nrow = (int)grid_for((size_t)rows, kExRows), ncol = (int)grid_for((size_t)C, kExCols);
-  launch(k_ln_bwd_exact, dim3(nrow + ncol), dim3(kExThreads), 0, dinp, dweight, dbias, dout, inp, weight, mean, rstd,
-         rows, C, nrow);
+  const dim3 grid(nrow + ncol), block(kExThreads);
+  if (vec)
+    launch(k_ln_bwd_exact<true>, grid, block, 0, dinp, dweight, dbias, dout, inp, weight, mean, rstd, rows, C, nrow);
+  else
+    launch(k_ln_bwd_exact<false>, grid, block, 0, dinp, dweight, dbias, dout, inp, weight, mean, rstd, rows, C, nrow);
   return check_launch("layernorm_backward (exact)");
 }
 
