@@ -3,8 +3,9 @@
 train_bnn.c:81-115 and :439-477 sum each row one column at a time and dweight/dbias one row at a
 time; in exact mode the library keeps those orders (serial chains, one per lane), so every output
 (out, mean, rstd, dinp, dweight, dbias) equals the oracle's, which is itself bit-identical to
-train_bnn.c compiled here. Covered: ragged shapes (rows not a multiple of the 64-row workgroups,
-C not a multiple of the 64-column tiles or of 4, a single element), misaligned buffers, the
+train_bnn.c compiled here. Covered: ragged shapes (rows a multiple of the 60-row workgroups and the
+240-row column tiles or not, C a multiple of the 64-column tiles or not, C a multiple of 4, which
+takes the float4 kernels, or not, a single element), misaligned buffers (the scalar kernels), the
 benchmark shapes (8,192 and 16,384 rows of 768), backward accumulation into nonzero gradients,
 the fused entry points (as the two reference ops in sequence), the allocation-free backward, the
 golden fixture written by the reference build, and the mode switch restoring the default kernels.
@@ -77,7 +78,7 @@ def exact_case(gpu, oracle, B, T, C, seed, offset=0):
 
 @pytest.mark.parametrize("B,T,C", [(4, 64, 384), (1, 3, 768), (2, 5, 16), (1, 2, 2048), (1, 4, 13), (1, 2, 3000),
                                    (3, 7, 4), (2, 50, 600), (1, 9, 516), (1, 1, 1), (1, 65, 64), (1, 129, 130),
-                                   (2, 300, 65)])
+                                   (2, 300, 65), (1, 240, 64), (4, 120, 32)])
 def test_layernorm_exact(gpu, oracle, B, T, C):
     exact_case(gpu, oracle, B, T, C, seed=B * 1000 + T * 10 + C)
 
