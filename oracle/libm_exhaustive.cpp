@@ -6,7 +6,10 @@
 // compares ugk_<fn>(x) against glibc <fn>(x); two NaNs count as equal.
 //
 // usage: libm_exhaustive <fn> [stride] [threads]
-//   fn in expf0 expf1 expf2 expf log1pf expm1f tanhf softplus
+//   fn in expf0 expf1 expf2 expf log1pf expm1f tanhf softplus, and
+//   logf_normal[0] (ugk_logf_normal_t on normal finite x > 0, glibc's logf
+//   elsewhere) and cosf_small[0] (ugk_cosf_small_t on |x| < 120, glibc's cosf
+//   elsewhere), with fused (default) or unfused (0) multiply-adds
 // Prints "<fn> checked=<n> mismatches=<m>" and up to 8 mismatching inputs;
 // exits 1 if any mismatch.
 #include <math.h>
@@ -35,6 +38,14 @@ static float g_expf(float x) { return expf(x); }
 static float g_log1pf(float x) { return log1pf(x); }
 static float g_expm1f(float x) { return expm1f(x); }
 static float g_tanhf(float x) { return tanhf(x); }
+static bool logf_dom(float x) { return x >= 0x1p-126f && x <= 0x1.fffffep127f; }
+static bool cosf_dom(float x) { return fabsf(x) < 120.0f; }
+static float mine_logf1(float x) { return logf_dom(x) ? ugk_logf_normal_t<1>(x, UgkLogfTable{}) : logf(x); }
+static float mine_logf0(float x) { return logf_dom(x) ? ugk_logf_normal_t<0>(x, UgkLogfTable{}) : logf(x); }
+static float mine_cosf1(float x) { return cosf_dom(x) ? ugk_cosf_small_t<1>(x) : cosf(x); }
+static float mine_cosf0(float x) { return cosf_dom(x) ? ugk_cosf_small_t<0>(x) : cosf(x); }
+static float g_logf(float x) { return logf(x); }
+static float g_cosf(float x) { return cosf(x); }
 
 int main(int argc, char **argv) {
   if (argc < 2) {
@@ -53,6 +64,10 @@ int main(int argc, char **argv) {
   else if (!strcmp(name, "expm1f")) { mine = mine_expm1f; ref = g_expm1f; }
   else if (!strcmp(name, "tanhf")) { mine = mine_tanhf; ref = g_tanhf; }
   else if (!strcmp(name, "softplus")) { mine = mine_softplus; ref = glibc_softplus; }
+  else if (!strcmp(name, "logf_normal")) { mine = mine_logf1; ref = g_logf; }
+  else if (!strcmp(name, "logf_normal0")) { mine = mine_logf0; ref = g_logf; }
+  else if (!strcmp(name, "cosf_small")) { mine = mine_cosf1; ref = g_cosf; }
+  else if (!strcmp(name, "cosf_small0")) { mine = mine_cosf0; ref = g_cosf; }
   else { fprintf(stderr, "unknown fn %s\n", name); return 2; }
 
   std::atomic<uint64_t> bad{0}, checked{0};

@@ -7,13 +7,13 @@ bbb_step_fused).
 The Philox ops split into an exact part and a float part:
   * the integer stream (Philox4x32-10 and u01) is bit-exact, checked on the device against the
     Random123 known-answer vectors and the oracle;
-  * the Box-Muller transform calls the device logf and cosf (the glibc-exact form) or takes its
-    radius from the hardware log2 and square root (the default form). Over every u01 value the
-    stream can produce (all 79,691,777 of them) logf and cosf stay within 2 ulp of the host glibc,
-    and over every float in u01's range both radii stay within 2 ulp of the correctly rounded one;
-    eps is then within 8 ulp of the oracle's in both forms;
-  * with ugk_set_philox_exact(1), everything downstream of eps is bit-exact given the device's eps
-    (each Philox op equals its eps-taking twin fed with the eps the device drew);
+  * the Box-Muller transform takes glibc's logf and cosf (restated in ugk_libm.h; the glibc-exact
+    form) or its radius from the hardware log2 and square root and the device library's cosf (the
+    default form). Over every u01 value the stream can produce (all 79,691,777 of them) and every
+    angle 2 pi u01 the restated logf and cosf equal the host glibc bit for bit, so in the
+    glibc-exact form eps is the oracle's bit for bit; by default it is within 8 ulp of it;
+  * with ugk_set_philox_exact(1), every output of every Philox op equals the oracle's bit for bit
+    (the fused step included), and each Philox op equals its eps-taking twin fed the same eps;
   * by default the Philox ops take their softplus and sigmoid in the hardware-transcendental form,
     which is within the literal bar |a - b| <= 1e-6 + 1e-5 |b| of the glibc-exact form on every
     float input (exhaustive, below); downstream of eps they are held to the bar that follows from
@@ -100,18 +100,43 @@ def test_philox_device_known_answers_and_oracle(gpu, oracle):
 # ---- the float transform over its whole input domain ------------------------------------
 
 def test_device_logf_cosf_over_the_u01_domain(gpu, oracle):
+    """The glibc-exact form's logf and cosf on the device (ugk_libm.h's restatements of glibc's) equal
+    the host glibc on every u01 value the stream can produce and on every angle fl(2 pi u) of them:
+    the Box-Muller transform's whole domain. The device library's own logf and cosf (variant 1) are
+    printed for comparison (within 2 ulp)."""
     u = u01_domain()
     theta = np.float32(6.28318530717958647692) * u
     for fn, x, want in (("logf", u, oracle.logf(u)), ("cosf", theta, oracle.cosf(theta))):
         tx = dev(x)
         out = torch.empty_like(tx)
-        gpu.diag_math_eval(fn, out, tx)
-        got = host(out)
-        d = ulp_dist(got, want)
-        print(f"device {fn} vs glibc over {x.size} inputs: {(d == 0).mean():.4%} identical, "
+        gpu.diag_math_eval(fn, out, tx, 0)
+        assert_bits(host(out), want, f"device {fn} (glibc restatement) vs host glibc over {x.size} inputs")
+        gpu.diag_math_eval(fn, out, tx, 1)
+        d = ulp_dist(host(out), want)
+        print(f"device library {fn} vs glibc over {x.size} inputs: {(d == 0).mean():.4%} identical, "
               f"{int((d == 1).sum())} at 1 ulp, max {int(d.max())} ulp")
         assert d.max() <= 2, (fn, int(d.max()), float(x[np.argmax(d)]))
         del tx, out
+
+
+@pytest.mark.parametrize("fn", ["logf", "cosf"])
+def test_device_logf_cosf_strided_over_their_domains(gpu, oracle, fn):
+    """The restated logf on every 61st normal float x > 0 and cosf on every 61st float of |x| < 120
+    (the domains of the restatements, which the CPU checks against glibc on every input) equal the
+    host glibc on the device too."""
+    if fn == "logf":
+        lo, hi = 0x00800000, 0x7F800000
+        x = np.arange(lo, hi, 61, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        want = oracle.logf(x)
+    else:
+        top = int(np.array([120.0], np.float32).view(np.uint32)[0])
+        pos = np.arange(0, top, 61, dtype=np.uint64).astype(np.uint32)
+        x = np.concatenate([pos, pos | np.uint32(0x80000000)]).view(np.float32)
+        want = oracle.cosf(x)
+    tx = dev(x)
+    out = torch.empty_like(tx)
+    gpu.diag_math_eval(fn, out, tx, 0)
+    assert_bits(host(out), want, f"device {fn} (glibc restatement) vs host glibc, {x.size} inputs")
 
 
 def test_device_sqrtf_is_correctly_rounded_everywhere(gpu, oracle):
@@ -149,13 +174,11 @@ def test_fast_transcendentals_exhaustive(gpu, fn):
     assert d <= 8, (fn, d, hex(at))  # 5 on MI355X
 
 
-@pytest.mark.parametrize("fn", ["logf_normal", "cosf_small"])
+@pytest.mark.parametrize("fn", ["cosf_small"])
 def test_box_muller_math_is_the_device_library(gpu, fn):
-    """The Box-Muller transform's logf (for normal x > 0) and cosf (for 0 <= x < 2^17) are the device
-    library's sequences without its cases for other arguments: the same bits as the library's logf and
-    cosf on every one of the 2^32 float inputs (the library's functions outside those domains), so the
-    glibc-exact form's eps is the library's. u1 = u01(w) lies in [2^-33, 1] and the angle fl(2 pi u2) in
-    (0, 2 pi]."""
+    """The default form's Box-Muller cosf (for 0 <= x < 2^17) is the device library's sequence without
+    its cases for other arguments: the same bits as the library's cosf on every one of the 2^32 float
+    inputs (the library's function outside that domain). The angle fl(2 pi u2) lies in (0, 2 pi]."""
     n, first = gpu.diag_math_mismatch(fn)
     assert n == 0, (fn, n, hex(first))
 
@@ -164,8 +187,8 @@ def test_box_muller_math_is_the_device_library(gpu, fn):
 def test_box_muller_radius_ulp(gpu, fn):
     """The radius sqrt(-2 ln u1) of the Box-Muller transform on every float u1 in [2^-33, 1] (a superset
     of u01's image) against the double radius rounded to float: the default form (hardware log2 and
-    square root) and the glibc-exact form (the library's logf, the correctly rounded root). Both are
-    within 2 ulp on MI355X (the rounding of -2 ln u1 carries through the root)."""
+    square root) and the glibc-exact form (glibc's logf, the correctly rounded root). Both are within
+    2 ulp on MI355X (the rounding of -2 ln u1 carries through the root)."""
     lo = int(np.array([2.0 ** -33], np.float32).view(np.uint32)[0])
     hi = int(np.array([1.0], np.float32).view(np.uint32)[0])
     d, at = gpu.diag_math_ulp(fn, lo, hi - lo + 1)
@@ -385,7 +408,7 @@ def test_bayes_sample_and_backward_philox(gpu, oracle, philox_exact, n, offset):
     gpu.bayes_sample(t_w, t_eps, t_mu, t_rho, n, seed, step)
     gpu.bayes_sample(t_w2, None, t_mu, t_rho, n, seed, step)
     eps_dev = host(t_eps)
-    assert_eps_close(eps_dev, oracle.philox_normal_n(n, seed, step), f"eps n={n}")
+    assert_bits(eps_dev, oracle.philox_normal_n(n, seed, step), f"eps n={n}")
     # downstream of eps: bit-exact
     w = np.zeros(n, np.float32)
     oracle.bayes_materialize(w, mu, rho, eps_dev, n)
@@ -427,14 +450,13 @@ def test_bbb_step_fused(gpu, oracle, philox_exact, klw, n, offset):
     for name, a, b in zip(names, f + [f_w], [c_mu, c_rho, c_m1, c_v1, c_m2, c_v2, c_w]):
         assert_bits(host(a), host(b), f"fused vs unfused {name}")
     assert (host(f_dw) == 0).all()
-    # and against the oracle's fused step: equal up to the eps of the two draws
+    # and against the oracle's fused step (the same eps): bit-exact
     o = [a.copy() for a in state]
     o_w, o_dw = np.zeros(n, np.float32), dw.copy()
     oracle.bbb_step_fused(*o, o_w, o_dw, n, seed, step, sp, klw, bc1, bc2, lr, b1, b2, aeps, wd)
-    got_mu = host(f[0])
-    assert_bits(got_mu, o[0], "fused mu vs oracle")  # the data gradient onto mu carries no eps
-    for name, a, b in zip(("rho", "m_rho", "v_rho"), (f[1], f[4], f[5]), (o[1], o[4], o[5])):
-        assert np.allclose(host(a), b, rtol=1e-5, atol=1e-7 * float(np.abs(b).max())), name
+    for name, a, b in zip(names, f + [f_w], o + [o_w]):
+        assert_bits(host(a), b, f"fused {name} vs oracle")
+    assert (o_dw == 0).all()
 
 
 def test_full_cfg5_bayes_sample(gpu, oracle, philox_exact):
@@ -451,7 +473,7 @@ def test_full_cfg5_bayes_sample(gpu, oracle, philox_exact):
     ti = torch.from_numpy(idx).to(DEV)
     e_dev = host(eps[ti])
     e_ref = np.array([oracle.philox_normal(seed, step, int(i)) for i in idx[:20000]], np.float32)
-    assert_eps_close(e_dev[:20000], e_ref, "cfg5 eps (sampled)")
+    assert_bits(e_dev[:20000], e_ref, "cfg5 eps (sampled)")
     w_ref = np.zeros(idx.size, np.float32)
     oracle.bayes_materialize(w_ref, host(mu[ti]), host(rho[ti]), e_dev, idx.size)
     assert_bits(host(w[ti]), w_ref, "cfg5 w (sampled)")

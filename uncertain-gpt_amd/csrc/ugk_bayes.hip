@@ -51,7 +51,8 @@ struct PhiloxParams {
 };
 
 // eps(seed, step, i) in the op's form: the hardware radius in the default form,
-// the library's logf and square root in the glibc-exact one.
+// glibc's logf and cosf and the correctly rounded square root in the
+// glibc-exact one.
 template <bool kFast>
 __device__ __forceinline__ float draw(unsigned long long seed, int step, size_t i) {
   return kFast ? ugk_dev_philox_normal_fast(seed, step, i) : ugk_dev_philox_normal(seed, step, i);
@@ -112,12 +113,11 @@ struct BayesBackwardPhilox : MapOp {
   static constexpr int kUnroll = 1, kThreads = kFast ? 1024 : 512;
   static constexpr bool kTable = !kFast;
   // eps drawn in place: drawing all four of a thread's eps while the streams
-  // load (kPre) measured 488-510 against 483-496 us. The glibc-exact form
-  // takes the library's logf and cosf (the same bits): 485-487 against 496 us.
+  // load (kPre) measured 488-510 against 483-496 us.
   typedef PhiloxParams Params;
   __device__ static void apply(const float *ld, float *st, const uint64_t *tab, size_t i, const Params &p) {
     const float g = ld[0];
-    const float eps = kFast ? draw<true>(p.seed, p.step, i) : ugk_dev_philox_normal<true>(p.seed, p.step, i);
+    const float eps = draw<kFast>(p.seed, p.step, i);
     st[0] = ld[2] + g;
     st[1] = ld[3] + g * eps * sigmoid_of<kFast>(ld[1], tab);
   }

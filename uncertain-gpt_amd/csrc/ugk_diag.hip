@@ -11,8 +11,10 @@ namespace ugk {
 namespace {
 
 // fn codes: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf, 4 softplus (the kernels'
-// math); 5 logf, 6 cosf (the device library's, as the Box-Muller transform
-// calls them; evaluation only), 7 sqrtf (its reference: the double square
+// math); 5 logf, 6 cosf (evaluation only: the Box-Muller transform's glibc
+// restatements, ugk_logf_normal on normal finite x > 0 and ugk_cosf_small on
+// |x| < 120, the device library's elsewhere; variant 1 the device library's
+// everywhere), 7 sqrtf (its reference: the double square
 // root rounded to float, which is the correctly rounded result); 8 GELU and
 // 9 its derivative as the GELU kernels evaluate them (reference: the same
 // expressions over ugk_tanhf);
@@ -33,13 +35,13 @@ namespace {
 // 66 and 67 the hardware-transcendental softplus and sigmoid of the Philox
 // ops (ugk_fast_softplus, ugk_fast_sigmoid) against the glibc-exact
 // softplus of fn 4 and train_bnn.c:820-822's 1 / (1 + expf(-x)), likewise
-// counting results outside that bar; 68: ugk_dev_logf_normal on normal
-// finite x > 0 and 69: ugk_dev_cosf_small on 0 <= x < 2^17, the Box-Muller
-// transform's logf and cosf (the library's logf and cosf elsewhere; reference:
-// the library's logf and cosf); 70 and 71 the Box-Muller radius
+// counting results outside that bar; 69: ugk_dev_cosf_small on
+// 0 <= x < 2^17, the default form's Box-Muller cosf (the library's cosf
+// elsewhere; reference: the library's cosf); 70 and 71 the Box-Muller radius
 // sqrt(-2 ln u1) on u1 in [2^-33, 1] (the reference elsewhere), 70 as the
 // Philox ops' default form computes it (hardware log2 and square root), 71 as
-// the glibc-exact form does, against the double radius rounded to float.
+// the glibc-exact form does (glibc's logf, the correctly rounded root),
+// against the double radius rounded to float.
 __constant__ float kDivisors[8] = {1.0f, 3.0f, 50257.0f, 0x1.fffffep0f, 0x1.fffffep15f, 0x1.000002p0f, 12345.678f,
                                    0x1.5p14f};
 
@@ -64,8 +66,8 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 2) return ugk_dev_expm1f(x);
   if (FN == 3) return ugk_dev_tanhf(x);
   if (FN == 4) return ugk_dev_softplusf_lds(x, tab);
-  if (FN == 5) return logf(x);
-  if (FN == 6) return cosf(x);
+  if (FN == 5) return (x >= 0x1p-126f && x <= 0x1.fffffep127f) ? ugk_logf_normal(x) : logf(x);
+  if (FN == 6) return fabsf(x) < 120.0f ? ugk_cosf_small(x) : cosf(x);
   if (FN == 7) return sqrtf(x);
   if (FN == 8) return ugk_dev_gelu(x);
   if (FN == 9) return ugk_dev_gelu_grad(x);
@@ -84,11 +86,10 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 65) return ugk_fast_gelu_grad(x);
   if (FN == 66) return ugk_fast_softplus(x);
   if (FN == 67) return ugk_fast_sigmoid(x);
-  if (FN == 68) return (x >= 0x1p-126f && x < __builtin_inff()) ? ugk_dev_logf_normal(x) : logf(x);
   if (FN == 69) return (x >= 0.0f && x < 0x1p17f) ? ugk_dev_cosf_small(x) : cosf(x);
   if (FN == 70 || FN == 71) {
     if (!(x >= 0x1p-33f && x <= 1.0f)) return (float)sqrt(-2.0 * log((double)x));
-    return FN == 70 ? ugk_dev_bm_radius_fast(x) : ugk_dev_sqrtf_large(-2.0f * ugk_dev_logf_normal(x));
+    return FN == 70 ? ugk_dev_bm_radius_fast(x) : ugk_dev_sqrtf_large(-2.0f * ugk_logf_normal(x));
   }
   return ugk_dev_expm1f_t<(FN >= 30 ? FN - 30 : 0)>(x);
 }
@@ -101,7 +102,7 @@ __device__ __forceinline__ float reference_math(float x) {
   if (FN == 4 || FN == 66) return ugk_softplusf(x);
   if (FN == 67) return 1.0f / (1.0f + ugk_expf(-x));
   if (FN == 70 || FN == 71) return (float)sqrt(-2.0 * log((double)x));
-  if (FN == 5 || FN == 68) return logf(x);
+  if (FN == 5) return logf(x);
   if (FN == 6 || FN == 69) return cosf(x);
   if (FN == 7) return (float)sqrt((double)x);
   if (FN == 8 || FN == 64) return ugk_gelu_with(x, [](float u) { return ugk_tanhf(u); });
@@ -201,7 +202,7 @@ int launch_stream(float4 *b, size_t n4, int per_thread, int block) {
 
 bool fn_ok(int fn) {
   return (fn >= 0 && fn <= 9) || (fn >= 10 && fn < 14) || (fn >= 20 && fn < 24) || (fn >= 30 && fn < 34) ||
-         (fn >= 40 && fn < 72);
+         (fn >= 40 && fn < 72 && fn != 68);
 }
 
 // The largest distance in ulp (as ordered integers) between the kernels' math
@@ -272,7 +273,7 @@ extern "C" int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long co
       UGK_MM(40) UGK_MM(41) UGK_MM(42) UGK_MM(43) UGK_MM(44) UGK_MM(45) UGK_MM(46) UGK_MM(47)
       UGK_MM(48) UGK_MM(49) UGK_MM(50) UGK_MM(51) UGK_MM(52) UGK_MM(53)
       UGK_MM(54) UGK_MM(55) UGK_MM(56) UGK_MM(57) UGK_MM(58) UGK_MM(59) UGK_MM(60) UGK_MM(61) UGK_MM(62) UGK_MM(63)
-      UGK_MM(64) UGK_MM(65) UGK_MM(66) UGK_MM(67) UGK_MM(68) UGK_MM(69) UGK_MM(70) UGK_MM(71)
+      UGK_MM(64) UGK_MM(65) UGK_MM(66) UGK_MM(67) UGK_MM(69) UGK_MM(70) UGK_MM(71)
 #undef UGK_MM
     }
     rc = check_launch("ugk_diag_math_mismatch");
@@ -301,7 +302,7 @@ extern "C" int ugk_diag_math_eval(int fn, int variant, float *out, const float *
     UGK_EV(40) UGK_EV(41) UGK_EV(42) UGK_EV(43) UGK_EV(44) UGK_EV(45) UGK_EV(46) UGK_EV(47)
     UGK_EV(48) UGK_EV(49) UGK_EV(50) UGK_EV(51) UGK_EV(52) UGK_EV(53)
     UGK_EV(54) UGK_EV(55) UGK_EV(56) UGK_EV(57) UGK_EV(58) UGK_EV(59) UGK_EV(60) UGK_EV(61) UGK_EV(62) UGK_EV(63)
-    UGK_EV(64) UGK_EV(65) UGK_EV(66) UGK_EV(67) UGK_EV(68) UGK_EV(69) UGK_EV(70) UGK_EV(71)
+    UGK_EV(64) UGK_EV(65) UGK_EV(66) UGK_EV(67) UGK_EV(69) UGK_EV(70) UGK_EV(71)
 #undef UGK_EV
   }
   return check_launch("ugk_diag_math_eval");

@@ -18,6 +18,15 @@
 //             rational approximation of expm1 on the reduced argument.
 //   tanhf   - glibc sysdeps/ieee754/flt-32/s_tanhf.c (fdlibm) on top of
 //             expm1f.
+//   logf    - glibc sysdeps/ieee754/flt-32/e_logf.c (ARM optimized-routines),
+//             for normal finite x > 0: a 16-entry table of 1/c and log(c),
+//             a polynomial in z/c - 1, all in double.
+//   cosf    - glibc sysdeps/ieee754/flt-32/s_cosf.c (ARM optimized-routines),
+//             for |x| < 120: the reduction by pi/2 in double and the sine and
+//             cosine polynomials of sincosf.
+// logf and cosf serve the Box-Muller transform (train_bnn.c's
+// sqrtf(-2 logf(u1)) cosf(2 pi u2)); the other arguments of those functions
+// (zero, subnormal, negative, large, infinite and NaN) are not restated.
 //
 // Every operation here is a single IEEE-754 binary32/binary64 operation with
 // round-to-nearest-even, an explicit fma(), an integer operation on the bit
@@ -35,9 +44,10 @@
 //   Permission to use, copy, modify, and distribute this
 //   software is freely granted, provided that this notice
 //   is preserved.
-// expf restates ARM optimized-routines' expf (Copyright (c) 2017-2018 Arm
-// Limited; MIT OR Apache-2.0 WITH LLVM-exception). The LICENSE file at the
-// repository root repeats both notices.
+// expf, logf and cosf restate ARM optimized-routines' expf, logf and
+// sincosf (Copyright (c) 2017-2018 Arm Limited; MIT OR Apache-2.0 WITH
+// LLVM-exception). The LICENSE file at the repository root repeats both
+// notices.
 #pragma once
 
 #include <stdint.h>
@@ -344,3 +354,116 @@ UGK_HD float ugk_expf(float x) { return ugk_expf_v<UGK_EXPF_CONTRACT>(x); }
 UGK_HD float ugk_softplusf(float x) {
   return x > 20.0f ? x : ugk_log1pf(ugk_expf(x));
 }
+
+// logf's table: for each of 16 subintervals of [0x1.6666p-1, 0x1.6666p0)
+// (the top 4 fraction bits of x - 0x3f330000) the double 1/c for a c near
+// its centre, and log(c). GPU code reads it from constant memory, one load
+// per lane (a table in the function's body becomes a branch tree there).
+#define UGK_LOGF_TABLE                                                                                      \
+  {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2, 0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2,               \
+   0x1.49539f0f010bp+0,  -0x1.01eae7f513a67p-2, 0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3,               \
+   0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3, 0x1.25e227b0b8eap+0,  -0x1.1aa2bc79c81p-3,                 \
+   0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4, 0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4,               \
+   0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5, 0x1p+0,               0x0p+0,                              \
+   0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5,  0x1.ca4b31f026aap-1,  0x1.c5e53aa362eb4p-4,                \
+   0x1.b2036576afce6p-1, 0x1.526e57720db08p-3,  0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3,                 \
+   0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2,  0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}
+
+struct UgkLogfEntry {
+  double invc, logc;
+};
+
+#if defined(__HIPCC__)
+static __constant__ double ugk_logf_tab_dev[32] = UGK_LOGF_TABLE;
+#endif
+static const double ugk_logf_tab_host[32] = UGK_LOGF_TABLE;
+
+UGK_HD UgkLogfEntry ugk_logf_entry(uint32_t i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const double2 e = reinterpret_cast<const double2 *>(ugk_logf_tab_dev)[i];
+  return UgkLogfEntry{e.x, e.y};
+#else
+  return UgkLogfEntry{ugk_logf_tab_host[2 * i], ugk_logf_tab_host[2 * i + 1]};
+#endif
+}
+
+struct UgkLogfTable {
+  UGK_HD_MEMBER UgkLogfEntry operator()(uint32_t i) const { return ugk_logf_entry(i); }
+};
+
+template <int kContract, class Tab>
+UGK_HD float ugk_logf_normal_t(float x, Tab tab) {
+  const double kLn2 = 0x1.62e42fefa39efp-1;
+  const double kA0 = -0x1.00ea348b88334p-2, kA1 = 0x1.5575b0be00b6ap-2, kA2 = -0x1.ffffef20a4123p-2;
+  const uint32_t ix = ugk_f2u(x);
+  const uint32_t tmp = ix - 0x3f330000u;
+  const uint32_t i = (tmp >> 19) & 15u;
+  const int k = (int32_t)tmp >> 23;
+  const uint32_t iz = ix - (tmp & 0xff800000u);
+  const UgkLogfEntry e = tab(i);
+  const double z = (double)ugk_u2f(iz);
+  double r, y0, y;
+  if (kContract) {
+    r = __builtin_fma(z, e.invc, -1.0);
+    y0 = __builtin_fma((double)k, kLn2, e.logc);
+  } else {
+    r = z * e.invc - 1.0;
+    y0 = e.logc + (double)k * kLn2;
+  }
+  const double r2 = r * r;
+  if (kContract) {
+    y = __builtin_fma(kA1, r, kA2);
+    y = __builtin_fma(kA0, r2, y);
+    y = __builtin_fma(y, r2, y0 + r);
+  } else {
+    y = kA1 * r + kA2;
+    y = kA0 * r2 + y;
+    y = y * r2 + (y0 + r);
+  }
+  return (float)y;
+}
+
+UGK_HD float ugk_logf_normal(float x) { return ugk_logf_normal_t<1>(x, UgkLogfTable{}); }
+
+// cosf for |x| < 120 (sincosf's fast path): x - n pi/2 with n = round(x 2/pi)
+// (from the product with 2^24 2/pi and an integer shift), then the sine or
+// cosine polynomial of the remainder by n's parity, negated for n mod 4 = 1
+// or 2; all in double, rounded to float once. glibc also branches for
+// |x| < 0x1p-12 (the result 1) and below about pi/4 (the cosine polynomial of
+// x unreduced); the general path gives the same bits there (n = 0, an exact
+// remainder, the polynomial rounding to 1 below 0x1p-12), and the sign flips
+// glibc takes from its two coefficient tables are exact negations of the
+// result, so this form evaluates both polynomials and selects, without
+// branches. The multiply-adds are fused as in the x86_64 glibc's FMA build
+// (the unfused form differs from it on 22 inputs near |x| = 64;
+// oracle/libm_exhaustive.cpp checks both).
+template <int kContract>
+UGK_HD float ugk_cosf_small_t(float y) {
+  const double kC0 = 0x1p0, kC1 = -0x1.ffffffd0c621cp-2, kC2 = 0x1.55553e1068f19p-5;
+  const double kC3 = -0x1.6c087e89a359dp-10, kC4 = 0x1.99343027bf8c3p-16;
+  const double kS1 = -0x1.555545995a603p-3, kS2 = 0x1.1107605230bc4p-7, kS3 = -0x1.994eb3774cf24p-13;
+  const double kHpi = 0x1.921fb54442d18p0;
+  const double x0 = (double)y;
+  const double r = x0 * 0x1.45f306dc9c883p+23;  // x 2/pi 2^24
+  const int n = ((int32_t)r + 0x800000) >> 24;
+  const double x = kContract ? __builtin_fma(-(double)n, kHpi, x0) : x0 - n * kHpi;
+  const double x2 = x * x;
+  const double x3 = x * x2, x4 = x2 * x2;
+  const double x6 = x4 * x2, x7 = x3 * x2;
+  double sv, cv;
+  if (kContract) {
+    sv = __builtin_fma(x7, __builtin_fma(x2, kS3, kS2), __builtin_fma(x3, kS1, x));
+    const double c2 = __builtin_fma(x2, kC4, kC3);
+    const double c = __builtin_fma(x4, kC2, __builtin_fma(x2, kC1, kC0));
+    cv = __builtin_fma(x6, c2, c);
+  } else {
+    sv = (x + x3 * kS1) + x7 * (kS2 + x2 * kS3);
+    const double c2 = kC3 + x2 * kC4;
+    const double c = (kC0 + x2 * kC1) + x4 * kC2;
+    cv = c + x6 * c2;
+  }
+  const float v = (float)((n & 1) ? sv : cv);
+  return ((n + 1) & 2) ? -v : v;
+}
+
+UGK_HD float ugk_cosf_small(float x) { return ugk_cosf_small_t<1>(x); }

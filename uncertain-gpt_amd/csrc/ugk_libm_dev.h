@@ -128,21 +128,6 @@ __device__ __forceinline__ float ugk_dev_sqrtf_large(float x) {
   return t;
 }
 
-// The device library's logf (ROCm-Device-Libs ocml, as hipcc builds it for
-// gfx950) for a normal finite x > 0: the hardware log2 (v_log_f32) times ln 2
-// held as a float pair (0x1.62e42ep-1 + 0x1.efa39ep-25), the product's low
-// part recovered with a fused multiply-add. The library also scales inputs
-// below 2^-126 by 2^32 first (subtracting 32 ln 2 after) and passes an
-// infinite log2 through; neither applies on this domain, the Box-Muller
-// transform's u1 in [2^-33, 1]. Bit-identical to logf on every normal finite
-// x > 0 (ugk_diag.hip fn 68).
-__device__ __forceinline__ float ugk_dev_logf_normal(float x) {
-  const float l = __builtin_amdgcn_logf(x);
-  const float hi = l * 0x1.62e42ep-1f;
-  const float lo = __builtin_fmaf(l, 0x1.efa39ep-25f, __builtin_fmaf(l, 0x1.62e42ep-1f, -hi));
-  return hi + lo;
-}
-
 // The device library's cosf (ocml, as hipcc builds it for gfx950) on its
 // small-argument path, 0 <= x < 2^17: k = rint(x 2/pi), the remainder
 // x - k pi/2 by three fused multiply-adds (Cody-Waite, pi/2 in three
@@ -150,7 +135,9 @@ __device__ __forceinline__ float ugk_dev_logf_normal(float x) {
 // k mod 4 choosing cos, -sin, -cos or sin. Larger x take the library's
 // Payne-Hanek reduction and infinities its NaN case, neither of which the
 // Box-Muller angle 2 pi u2 in (0, 2 pi] reaches. Bit-identical to cosf on
-// 0 <= x < 2^17 (ugk_diag.hip fn 69).
+// 0 <= x < 2^17 (ugk_diag.hip fn 69). The default (fast-math) form of the
+// Philox ops' Box-Muller transform; the glibc-exact form takes glibc's cosf
+// (ugk_cosf_small in ugk_libm.h).
 __device__ __forceinline__ float ugk_dev_cosf_small(float x) {
   const float kf = __builtin_rintf(x * 0x1.45f306p-1f);
   const int q = (int)kf;

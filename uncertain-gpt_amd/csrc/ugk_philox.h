@@ -9,11 +9,12 @@
 // output words mapped to (0,1) as ((float)x + 0.5f) * 2^-32, and one
 // Box-Muller cosine branch per index.
 //
-// The integer part is exact on host and device. The float part uses the
-// device logf and cosf (AMD's device library), which round differently from
-// the host glibc in the last place on a small share of inputs, and a
-// correctly rounded square root; or, in the ops' default (fast-math) form, the
-// radius from the hardware log2 and square root (ugk_dev_box_muller_fast).
+// The integer part is exact on host and device. The float part, in the
+// glibc-exact form, takes glibc's logf and cosf as ugk_libm.h restates them
+// (equal to the host glibc on every input of their domains) and the correctly
+// rounded square root, so that eps equals the host's bit for bit; in the ops'
+// default (fast-math) form, the radius from the hardware log2 and square root
+// and the device library's cosf sequence (ugk_dev_box_muller_fast).
 #pragma once
 
 #include <stdint.h>
@@ -91,27 +92,25 @@ __device__ __forceinline__ UgkPhilox4 ugk_dev_philox_words_uniform(unsigned long
   return UgkPhilox4{{c0, c1, c2, c3}};
 }
 
-// Box-Muller, cosine branch: sqrt(-2 ln u1) * cos(2 pi u2), with 2 pi rounded
-// to float and the product rounded before the cosine. u1 in [2^-33, 1] puts
-// -2 ln u1 at -0 or in [1.1e-7, 46]: inside the domain of the correctly
-// rounded square root without rescaling. u1 is a normal float and 2 pi u2 lies
-// in (0, 2 pi], so logf and cosf are the device library's own sequences for
-// those domains, without its cases for subnormal, infinite and large
-// arguments (the same bits). kLibrary calls the library's logf and cosf
-// themselves, which one kernel runs faster with (the glibc-exact form of
-// bayes_backward_philox).
-template <bool kLibrary = false>
+// Box-Muller, cosine branch, as gpt2_kernels.cuh:181-192 writes it and the
+// host builds it: sqrtf(-2 logf(u1)) * cosf(2 pi u2), with 2 pi rounded to
+// float and the product rounded before the cosine. u1 in [2^-33, 1] is a
+// normal float and 2 pi u2 lies in (0, 2 pi], inside the domains of the
+// restated logf and cosf (ugk_logf_normal, ugk_cosf_small); -2 ln u1 is -0 or
+// in [1.1e-7, 46], inside the domain of the correctly rounded square root
+// without rescaling. The same bits as the host's for every u1, u2.
 __device__ __forceinline__ float ugk_dev_box_muller(uint32_t a, uint32_t b) {
   const float u1 = ugk_u01(a), u2 = ugk_u01(b);
-  const float l = kLibrary ? logf(u1) : ugk_dev_logf_normal(u1);
+  const float l = ugk_logf_normal(u1);
   const float x = 6.28318530717958647692f * u2;
-  return ugk_dev_sqrtf_large(-2.0f * l) * (kLibrary ? cosf(x) : ugk_dev_cosf_small(x));
+  return ugk_dev_sqrtf_large(-2.0f * l) * ugk_cosf_small(x);
 }
 
 // The same transform with the radius from the hardware log2 and square root
 // (v_log_f32, v_sqrt_f32), as a fast-math build computes it: -2 ln u1 as
 // log2(u1) times -2 ln 2, rounded once, and a square root within 1 ulp; the
-// cosine as above. The Philox ops' default form.
+// cosine the device library's (ugk_dev_cosf_small, float arithmetic). The
+// Philox ops' default form.
 __device__ __forceinline__ float ugk_dev_bm_radius_fast(float u1) {
   return __builtin_amdgcn_sqrtf((-2.0f * __builtin_amdgcn_logf(u1)) * 0x1.62e43p-1f);
 }
@@ -122,10 +121,9 @@ __device__ __forceinline__ float ugk_dev_box_muller_fast(uint32_t a, uint32_t b)
 }
 
 // eps(seed, step, index); seed and step must be the same across the wavefront.
-template <bool kLibrary = false>
 __device__ __forceinline__ float ugk_dev_philox_normal(unsigned long long seed, int step, uint64_t index) {
   const UgkPhilox4 o = ugk_dev_philox_words_uniform(seed, step, index);
-  return ugk_dev_box_muller<kLibrary>(o.w[0], o.w[1]);
+  return ugk_dev_box_muller(o.w[0], o.w[1]);
 }
 
 __device__ __forceinline__ float ugk_dev_philox_normal_fast(unsigned long long seed, int step, uint64_t index) {

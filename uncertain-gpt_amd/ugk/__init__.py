@@ -596,8 +596,8 @@ MATH_FUNCTIONS.update({"expf_nooverflow": 63})
 MATH_FUNCTIONS.update({"gelu_fast": 64, "gelu_grad_fast": 65})
 # the hardware-transcendental softplus and sigmoid of the Philox ops (the literal bar, likewise)
 MATH_FUNCTIONS.update({"softplus_fast": 66, "sigmoid_fast": 67})
-# the Box-Muller transform's logf and cosf on their domains, against the device library's
-MATH_FUNCTIONS.update({"logf_normal": 68, "cosf_small": 69})
+# the default form's Box-Muller cosf on its domain, against the device library's
+MATH_FUNCTIONS.update({"cosf_small": 69})
 # the Box-Muller radius sqrt(-2 ln u1) on [2^-33, 1]: the default form's and the glibc-exact form's
 MATH_FUNCTIONS.update({"bm_radius_fast": 70, "bm_radius": 71})
 
