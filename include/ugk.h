@@ -231,12 +231,13 @@ int ugk_crossentropy_softmax_backward_zeroed(float *dlogits, const float *probs,
  * and within 1e-6 absolute / 1e-5 relative of train_bnn.c:814-822 on every
  * float input), nonzero the glibc-exact forms of the eps-taking ops, with which
  * each Philox op equals its eps-taking twin fed the same eps bit for bit. The
- * eps draw's radius sqrt(-2 ln u1) follows the same setting: the hardware log2
- * and square root by default, the device library's logf and a correctly
- * rounded square root otherwise (both within a few ulp of train_bnn.c's eps;
- * they differ from each other in the last place on some draws). No
- * counterpart in the reference, whose GPU arms build these ops with
- * --use_fast_math (Makefile:13). */
+ * eps draw follows the same setting: by default its radius from the hardware
+ * log2 and square root and its cosine from the device library's sequence
+ * (within a few ulp of the host's eps); otherwise glibc's logf and cosf
+ * (restated) and the correctly rounded square root, so that eps, and every
+ * output of every Philox op, equals the host's bit for bit. No counterpart in
+ * the reference, whose GPU arms build these ops with --use_fast_math
+ * (Makefile:13). */
 int ugk_set_philox_exact(int exact);
 int ugk_get_philox_exact(void);
 
@@ -246,9 +247,9 @@ int ugk_get_philox_exact(void);
  *     eps_i = philox_normal(seed, step, i)
  * on the fly (gpt2_kernels.cuh:148-192: Philox4x32-10 with counter
  * {i low, i high, step, 0} and key {seed low, seed high}, Box-Muller cosine
- * branch); the integer stream is exact, the transform uses the device
- * logf/cosf, which differ from glibc's by at most an ulp on a small share of
- * inputs. Buffers written by one call must not overlap each other. */
+ * branch); the integer stream is exact, and the transform is the host's bit
+ * for bit in the glibc-exact form (ugk_set_philox_exact), within a few ulp of
+ * it by default. Buffers written by one call must not overlap each other. */
 
 /* train_bnn.c:841-845 with the draw of train_bnn_gpu.cu:93-97 (k_bayes_sample):
  * w = mu + softplus(rho) * eps_i. eps may be NULL (the GPU arms regenerate
@@ -366,10 +367,9 @@ int ugk_version(void);
  * form) against fn 8 and 9's glibc-exact expressions, counting results
  * outside |a - b| <= 1e-6 + 1e-5 |b|; 66 and 67 the hardware-transcendental
  * softplus and sigmoid of the Philox ops (their default form) against the
- * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise; 68 and 69
- * the Box-Muller transform's logf (normal x > 0) and cosf (0 <= x < 2^17)
- * against the device library's logf and cosf (the library's own functions
- * outside those domains); 70 and 71 the Box-Muller radius sqrt(-2 ln u1) for
+ * glibc-exact softplus and train_bnn.c:820-822's sigmoid, likewise; 69 the
+ * default form's Box-Muller cosf (0 <= x < 2^17) against the device library's
+ * cosf (the library's own function outside that domain); 70 and 71 the Box-Muller radius sqrt(-2 ln u1) for
  * u1 in [2^-33, 1] as the Philox ops' default form (hardware log2 and square
  * root) and their glibc-exact form compute it, against the double radius
  * rounded to float (ugk_diag_math_ulp only). */

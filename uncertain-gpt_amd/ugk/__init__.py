@@ -488,9 +488,10 @@ def gelu_exact() -> bool:
 
 
 def set_philox_exact(exact: bool) -> None:
-    """Softplus/sigmoid inside the ops that draw eps on the device: False (default) the hardware-
-    transcendental forms, within 1e-5 rel / 1e-6 abs of train_bnn.c on every input; True the
-    glibc-exact forms, with which each Philox op equals its eps-taking twin bit for bit."""
+    """Softplus/sigmoid and the eps draw's logf/cosf inside the ops that draw eps on the device:
+    False (default) the hardware-transcendental forms, within 1e-5 rel / 1e-6 abs of train_bnn.c on
+    every input (eps within a few ulp); True the glibc-exact forms, with which eps and every output
+    of each Philox op equal the host's bit for bit."""
     _check(lib.ugk_set_philox_exact(1 if exact else 0))
 
 
