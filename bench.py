@@ -128,7 +128,10 @@ KERNEL_KEYS = [  # (substring of the rocprof kernel name, short name)
     ("k_softmax_xent<", "softmax_crossentropy"),
     ("k_softmax_xent_split<", "softmax_crossentropy"),
     ("k_softmax_stats", "softmax_crossentropy (row statistics)"),
+    ("k_softmax_norm_rows", "softmax_crossentropy (exact form, normalise)"),
     ("k_softmax_norm", "softmax_crossentropy (normalise)"),
+    ("k_softmax_rowmax", "softmax_crossentropy (exact form, row max)"),
+    ("k_softmax_sum_exact", "softmax_crossentropy (exact form, serial row sums)"),
     ("k_xent_softmax_bwd_flat4<true>", "crossentropy_softmax_backward (dlogits not read)"),
     ("k_xent_softmax_bwd<true>", "crossentropy_softmax_backward (dlogits not read)"),
     ("k_xent_softmax_bwd", "crossentropy_softmax_backward"),
@@ -767,6 +770,15 @@ def main():
         ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_crossentropy_softmax_backward_zeroed(
             P_(d["dlogits"]), P_(d["probs"]), P_(d["targets"]), B, T, V)))
         record(head, "crossentropy_softmax_backward_zeroed", 8 * NV + 4 * rows_h, ms, l_, k_)
+        # the forward in its exact form (ugk_set_softmax_exact(1): train_bnn.c's serial row sums)
+        if not args.no_exact:
+            ugk.set_softmax_exact(True)
+            try:
+                ms, l_, k_ = time_cold(mk_head, 12 * NV, lambda d: chk(lib.ugk_softmax_crossentropy(
+                    P_(d["losses"]), P_(d["probs"]), P_(d["logits"]), P_(d["targets"]), B, T, V)))
+                record(head, "softmax_crossentropy (exact form)", 8 * NV + 8 * rows_h, ms, l_, k_)
+            finally:
+                ugk.set_softmax_exact(False)
 
     # ---- roofline of the op with the most microseconds per step, from its in-step
     # launches (a HIP event pair around each, on the library stream)

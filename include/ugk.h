@@ -200,13 +200,21 @@ int ugk_bayes_materialize(float *w, const float *mu, const float *rho,
 
 /* train_bnn.c:279-304 / gpt2_kernels.cuh:352-374 (k_softmax_crossentropy).
  * Per (b,t) row of V logits: probs = softmax (max-shifted, glibc-exact expf,
- * each e divided by the row sum), losses[b,t] = -log(probs[target]). The
- * exps are the CPU's bit for bit; the row sum is added in a fixed tree order
- * (deterministic, within float rounding of the CPU's sequential sum), so
- * probs and losses agree to a few ulp. 0 <= targets[i] < V is the caller's
- * contract, as in the reference. */
+ * each e divided by the row sum), losses[b,t] = -logf(probs[target]) with
+ * glibc's logf. The exps are the CPU's bit for bit; by default the row sum is
+ * added in a fixed tree order (deterministic, within float rounding of the
+ * CPU's sequential sum), so probs and losses agree to a few ulp; with
+ * ugk_set_softmax_exact(1) in the CPU's order, and both are the CPU's bit for
+ * bit. 0 <= targets[i] < V is the caller's contract, as in the reference. */
 int ugk_softmax_crossentropy(float *losses, float *probs, const float *logits,
                              const int *targets, int B, int T, int V);
+
+/* Order of ugk_softmax_crossentropy's row sums for later calls from any
+ * thread: 0 (the default) a fixed tree, nonzero train_bnn.c's serial order
+ * (v = 0, 1, ..., V-1; one chain per row, about twice the default's time).
+ * No counterpart in the reference, whose GPU kernel sums in its own tree. */
+int ugk_set_softmax_exact(int exact);
+int ugk_get_softmax_exact(void);
 
 /* train_bnn.c:358-378 / gpt2_kernels.cuh:376-384
  * (k_crossentropy_softmax_backward). dlogits += (probs - onehot(target)) *

@@ -9,7 +9,8 @@
 //   fn in expf0 expf1 expf2 expf log1pf expm1f tanhf softplus, and
 //   logf_normal[0] (ugk_logf_normal_t on normal finite x > 0, glibc's logf
 //   elsewhere) and cosf_small[0] (ugk_cosf_small_t on |x| < 120, glibc's cosf
-//   elsewhere), with fused (default) or unfused (0) multiply-adds
+//   elsewhere), with fused (default) or unfused (0) multiply-adds; logf
+//   (ugk_logf, every input)
 // Prints "<fn> checked=<n> mismatches=<m>" and up to 8 mismatching inputs;
 // exits 1 if any mismatch.
 #include <math.h>
@@ -45,6 +46,7 @@ static float mine_logf0(float x) { return logf_dom(x) ? ugk_logf_normal_t<0>(x, 
 static float mine_cosf1(float x) { return cosf_dom(x) ? ugk_cosf_small_t<1>(x) : cosf(x); }
 static float mine_cosf0(float x) { return cosf_dom(x) ? ugk_cosf_small_t<0>(x) : cosf(x); }
 static float g_logf(float x) { return logf(x); }
+static float mine_logf_all(float x) { return ugk_logf(x); }
 static float g_cosf(float x) { return cosf(x); }
 
 int main(int argc, char **argv) {
@@ -65,6 +67,7 @@ int main(int argc, char **argv) {
   else if (!strcmp(name, "tanhf")) { mine = mine_tanhf; ref = g_tanhf; }
   else if (!strcmp(name, "softplus")) { mine = mine_softplus; ref = glibc_softplus; }
   else if (!strcmp(name, "logf_normal")) { mine = mine_logf1; ref = g_logf; }
+  else if (!strcmp(name, "logf")) { mine = mine_logf_all; ref = g_logf; }
   else if (!strcmp(name, "logf_normal0")) { mine = mine_logf0; ref = g_logf; }
   else if (!strcmp(name, "cosf_small")) { mine = mine_cosf1; ref = g_cosf; }
   else if (!strcmp(name, "cosf_small0")) { mine = mine_cosf0; ref = g_cosf; }

@@ -280,12 +280,13 @@ LIBM_BIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__
 
 
 @pytest.mark.parametrize("fn", ["expf", "log1pf", "expm1f", "tanhf", "softplus", "logf_normal", "logf_normal0",
-                                "cosf_small"])
+                                "cosf_small", "logf"])
 def test_libm_replica_strided(fn):
     """ugk_libm.h equals glibc on every 1021st bit pattern (the full 2^32 sweep is
     `oracle/libm_exhaustive <fn> 1`; see oracle/Makefile). logf_normal and cosf_small are the
     Box-Muller transform's logf and cosf on their domains (normal x > 0, |x| < 120), with fused
-    multiply-adds; logf_normal0 the unfused logf, which gives the same floats."""
+    multiply-adds; logf_normal0 the unfused logf, which gives the same floats; logf the loss's logf
+    on every input (zero, subnormal, negative, infinite and NaN included)."""
     if not os.path.exists(LIBM_BIN):
         subprocess.run(["make", "-C", os.path.dirname(LIBM_BIN), "libm_exhaustive"], check=True,
                        capture_output=True)

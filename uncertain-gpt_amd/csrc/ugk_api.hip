@@ -528,6 +528,13 @@ int ugk_set_kl_exact(int exact) {
 
 int ugk_get_kl_exact(void) { return kl_exact(); }
 
+int ugk_set_softmax_exact(int exact) {
+  set_softmax_exact(exact);
+  return ok();
+}
+
+int ugk_get_softmax_exact(void) { return softmax_exact(); }
+
 int ugk_set_layernorm_exact(int exact) {
   set_layernorm_exact(exact);
   return ok();

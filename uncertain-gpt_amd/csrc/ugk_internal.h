@@ -109,6 +109,46 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Serial float sums in a fixed order (the CPU loops' order), one chain per
+// lane, fed from LDS four terms at a time:
+// s = (((s + t[0]) + t[1]) + ...) + t[4 n4 - 1] for each of kArr chains, the
+// terms of chain a at t[a]; n4 float4 reads per chain, a multiple of 2 kB.
+// The reads of a batch (kB float4 per chain) are issued before the additions
+// of the batch before, which cover the LDS latency; the scheduling barriers
+// keep the compiler from sinking the reads down to their use.
+template <int kArr, int kB>
+__device__ __forceinline__ void chain_add4(float (&s)[kArr], const float4 *const (&t)[kArr], int n4) {
+  float4 a[kArr][kB], b[kArr][kB];
+#pragma unroll
+  for (int r = 0; r < kArr; r++)
+#pragma unroll
+    for (int k = 0; k < kB; k++) a[r][k] = t[r][k];
+  for (int q = 0; q < n4; q += 2 * kB) {
+#pragma unroll
+    for (int r = 0; r < kArr; r++)
+#pragma unroll
+      for (int k = 0; k < kB; k++) b[r][k] = t[r][q + kB + k];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kB; k++)
+#pragma unroll
+      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + a[r][k].x) + a[r][k].y) + a[r][k].z) + a[r][k].w;
+    __builtin_amdgcn_sched_barrier(0);
+    if (q + 2 * kB < n4) {
+#pragma unroll
+      for (int r = 0; r < kArr; r++)
+#pragma unroll
+        for (int k = 0; k < kB; k++) a[r][k] = t[r][q + 2 * kB + k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kB; k++)
+#pragma unroll
+      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + b[r][k].x) + b[r][k].y) + b[r][k].z) + b[r][k].w;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Launchers, one per kernel family. Each validates nothing (ugk_api.hip does)
 // and returns the launch status through check_launch.
 int launch_residual_forward(float *out, const float *x, const float *y, size_t n);
@@ -256,6 +296,9 @@ int *ids_error_word();
 size_t layernorm_backward_scratch(int rows, int C);  // bytes of one call's partial rows
 size_t encoder_backward_scratch();                   // the bucket state (fixed)
 size_t kl_forward_scratch();                         // partial sums (fixed)
-size_t softmax_scratch(int rows, int V);             // row statistics of rows too long for one workgroup
+size_t softmax_scratch(int rows, int V);             // row statistics: long rows, and the exact mode
+// softmax's row sum: 0 (default) a fixed tree, 1 train_bnn.c's serial order
+void set_softmax_exact(int exact);
+int softmax_exact();
 
 }  // namespace ugk

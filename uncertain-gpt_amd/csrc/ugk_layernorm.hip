@@ -1079,44 +1079,6 @@ constexpr int ex_row_lds(int arrays) { return 2 * arrays * kWave * kExPitch + 4 
 constexpr int kExColLds = 2 * kExChains * kExColPitch;
 constexpr int kExBwdLds = ex_row_lds(2) > kExColLds ? ex_row_lds(2) : kExColLds;
 
-// s = (((s + t[0]) + t[1]) + ...) + t[4 n4 - 1] for each of kArr chains, the
-// terms of chain a at t[a]; n4 float4 reads per chain, a multiple of 2 kB.
-// The reads of a batch (kB float4 per chain) are issued before the additions
-// of the batch before, which cover the LDS latency; the scheduling barriers
-// keep the compiler from sinking the reads down to their use.
-template <int kArr, int kB>
-__device__ __forceinline__ void ex_chain4(float (&s)[kArr], const float4 *const (&t)[kArr], int n4) {
-  float4 a[kArr][kB], b[kArr][kB];
-#pragma unroll
-  for (int r = 0; r < kArr; r++)
-#pragma unroll
-    for (int k = 0; k < kB; k++) a[r][k] = t[r][k];
-  for (int q = 0; q < n4; q += 2 * kB) {
-#pragma unroll
-    for (int r = 0; r < kArr; r++)
-#pragma unroll
-      for (int k = 0; k < kB; k++) b[r][k] = t[r][q + kB + k];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < kB; k++)
-#pragma unroll
-      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + a[r][k].x) + a[r][k].y) + a[r][k].z) + a[r][k].w;
-    __builtin_amdgcn_sched_barrier(0);
-    if (q + 2 * kB < n4) {
-#pragma unroll
-      for (int r = 0; r < kArr; r++)
-#pragma unroll
-        for (int k = 0; k < kB; k++) a[r][k] = t[r][q + 2 * kB + k];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < kB; k++)
-#pragma unroll
-      for (int r = 0; r < kArr; r++) s[r] = (((s[r] + b[r][k].x) + b[r][k].y) + b[r][k].z) + b[r][k].w;
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
 __device__ __forceinline__ float f4_get(const float4 &v, int j) {
   return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
 }
@@ -1252,7 +1214,7 @@ __device__ __forceinline__ void ln_rows_exact(float *lds, int blk, float *__rest
           const float4 *t[kArr];
 #pragma unroll
           for (int a = 0; a < kArr; a++) t[a] = reinterpret_cast<const float4 *>(X + a * kTileF);
-          ex_chain4<kArr, kExBatch / kArr>(s, t, kExTile / 4);
+          chain_add4<kArr, kExBatch / kArr>(s, t, kExTile / 4);
         } else {
           for (int c = 0; c < cmax; c++) {
 #pragma unroll
@@ -1433,7 +1395,7 @@ __device__ __forceinline__ void ln_cols_exact(float *lds, int blk, float *__rest
         const int rmax = min(kExColRows, rows - t * kExColRows);
         if (rmax == kExColRows) {
           const float4 *t4[1] = {reinterpret_cast<const float4 *>(T)};
-          ex_chain4<1, kExColBatch>(acc, t4, kExColRows / 4);
+          chain_add4<1, kExColBatch>(acc, t4, kExColRows / 4);
         } else {
           for (int i = 0; i < rmax; i++) acc[0] = acc[0] + T[i];
         }

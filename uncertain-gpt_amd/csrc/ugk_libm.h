@@ -425,6 +425,21 @@ UGK_HD float ugk_logf_normal_t(float x, Tab tab) {
 
 UGK_HD float ugk_logf_normal(float x) { return ugk_logf_normal_t<1>(x, UgkLogfTable{}); }
 
+// logf for every input, glibc's special cases included: -inf at +-0, +inf at
+// +inf, NaN for negative x and NaN, and a subnormal x scaled by 2^23 into the
+// normal range first (the exponent taken back by 23 in the bit pattern, as
+// glibc does); normal x as ugk_logf_normal.
+UGK_HD float ugk_logf(float x) {
+  uint32_t ix = ugk_f2u(x);
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+    if (ix * 2u == 0u) return -ugk_u2f(0x7f800000u);  // +-0: -inf
+    if (ix == 0x7f800000u) return x;                   // +inf
+    if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return ugk_u2f(0x7fc00000u);  // x < 0 or NaN
+    ix = ugk_f2u(x * 0x1p23f) - (23u << 23);            // subnormal
+  }
+  return ugk_logf_normal_t<1>(ugk_u2f(ix), UgkLogfTable{});
+}
+
 // cosf for |x| < 120 (sincosf's fast path): x - n pi/2 with n = round(x 2/pi)
 // (from the product with 2^24 2/pi and an integer shift), then the sine or
 // cosine polynomial of the remainder by n's parity, negated for n mod 4 = 1

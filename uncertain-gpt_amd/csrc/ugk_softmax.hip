@@ -15,8 +15,8 @@
 //   prob  e / sum correctly rounded, from the reciprocal of the sum and one
 //         fma correction (ugk_div_recip; a wavefront holding an e below
 //         2^-86 divides instead), stored non-temporally;
-//   loss  -log(prob[target]) by the thread holding the target, which
-//         recomputes that probability from the logit.
+//   loss  -logf(prob[target]) (glibc's logf, restated) by the thread holding
+//         the target, which recomputes that probability from the logit.
 // Rows are V floats long and V is odd for GPT-2, so rows are not 16-byte
 // aligned: loads and stores are dwords, coalesced across the wavefront.
 // A row's elements are laid on the threads from a 256-byte boundary of probs
@@ -29,9 +29,14 @@
 // and the sum (kept per lane in double and rescaled as the max grows), then a
 // flat map over all rows forms expf(x - max) / sum, 12 bytes per logit.
 //
+// Exact mode (ugk_set_softmax_exact): the row sum in train_bnn.c's order, one
+// element after another, so that every probability and loss is the CPU's bit
+// for bit (the kernels after the backward's).
+//
 // Backward: dlogits[v] += (probs[v] - (v == target)) * (1 / (B*T)), one
 // workgroup per row streaming float4 (dwords for misaligned arrays);
 // bit-identical to the CPU loop.
+#include <atomic>
 #include <type_traits>
 
 #include "ugk_internal.h"
@@ -75,10 +80,8 @@ __device__ __forceinline__ float block_sum(float v, float *lds) {
   return s;
 }
 
-// -logf(p), from the double logarithm rounded to float (the correctly rounded
-// logf but for astronomically rare ties; glibc's logf agrees with it on
-// 99.8% of inputs).
-__device__ __forceinline__ float neg_logf(float p) { return -(float)log((double)p); }
+// -logf(p) with glibc's logf (train_bnn.c:301), restated in ugk_libm.h.
+__device__ __forceinline__ float neg_logf(float p) { return -ugk_logf(p); }
 
 // The loss of a row held in slots (element v in slot v + skew, slot u on
 // thread u % threads): the thread holding the target recomputes its
@@ -397,6 +400,164 @@ __global__ __launch_bounds__(kBwdThreads) void k_xent_softmax_bwd(float *__restr
   }
 }
 
+// ---- exact mode: train_bnn.c's order of the row sum ---------------------------
+// train_bnn.c:286-297 takes the row max (any order gives the same value: the
+// rule x > m from -1e30 skips NaN, and the sign of a zero max does not change
+// x - max), adds expf(x - max) for v = 0, 1, ..., V-1 one at a time, divides
+// each exponential by that sum and takes -logf of the target's quotient. The
+// exact form keeps that order in three launches:
+//   k_softmax_rowmax: one wavefront per row, the max by the CPU's rule;
+//   k_softmax_sum_exact: a workgroup per 32 rows, one serial chain per row in
+//     wavefront 0 (lanes 0-31) fed from LDS, four terms per read, by fifteen
+//     loader wavefronts that stage 240-column tiles of expf(x - max) (the
+//     glibc-exact expf) three tiles ahead in registers; the columns past V are
+//     staged as +0, which leaves a sum of terms >= +0 (or NaN, inf) unchanged;
+//   k_softmax_norm_rows: expf(x - max) / sum (IEEE division) and the loss.
+// Its HBM bytes: the logits three times and the probabilities once (16 per
+// logit, against 8 for the default kernels); the chains' latency bounds the
+// sums.
+constexpr int kSxLoaders = 15, kSxThreads = (kSxLoaders + 1) * kWave, kSxLoadLanes = kSxLoaders * kWave;
+constexpr int kSxRows = 32, kSxTile = 240, kSxPitch = kSxTile + 4;
+constexpr int kSxSlots = kSxRows * kSxTile / kSxLoadLanes;
+constexpr int kSxDepth = 3, kSxBatch = 6;
+constexpr int kSxMaxWaves = 4, kSxMaxUnroll = 8;
+constexpr int kSxNormPer = 16;
+static_assert(kSxRows * kSxTile == kSxSlots * kSxLoadLanes && kSxLoadLanes % kSxTile == 0,
+              "a tile is whole loader slots, and a loader lane keeps its column in every slot");
+static_assert((kSxTile / 4) % (2 * kSxBatch) == 0 && kSxRows <= kWave, "whole batch pairs per tile; chains in one wave");
+
+__global__ __launch_bounds__(kSxMaxWaves * kWave) void k_softmax_rowmax(float2 *__restrict__ stats,
+                                                                        const float *__restrict__ logits, int rows,
+                                                                        int V) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kSxMaxWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *lg = logits + (size_t)row * V;
+  float m = kNegInit;
+  for (int v0 = lane; v0 < V; v0 += kWave * kSxMaxUnroll) {
+    float x[kSxMaxUnroll];
+#pragma unroll
+    for (int k = 0; k < kSxMaxUnroll; k++) {
+      const int v = v0 + k * kWave;
+      x[k] = v < V ? lg[v] : kNegInit;
+    }
+#pragma unroll
+    for (int k = 0; k < kSxMaxUnroll; k++) m = max_rule(m, x[k]);
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m = max_rule(m, __shfl_xor(m, off));
+  if (lane == 0) stats[row] = make_float2(m, 0.0f);
+}
+
+__global__ __launch_bounds__(kSxThreads) void k_softmax_sum_exact(float2 *__restrict__ stats,
+                                                                  const float *__restrict__ logits, int rows, int V) {
+  __shared__ __align__(16) float tile[2][kSxRows * kSxPitch];
+  __shared__ uint64_t tab[32];
+  __shared__ float smax[kSxRows];
+  ugk_exp2_stage(tab);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int r0 = blockIdx.x * kSxRows;
+  if ((int)threadIdx.x < kSxRows) smax[threadIdx.x] = stats[min(r0 + (int)threadIdx.x, rows - 1)].x;
+  __syncthreads();
+  const int nt = (V + kSxTile - 1) / kSxTile;
+  // loader lane L holds, in slot sl, tile row L / 240 + 4 sl, column L % 240
+  const int L = (wave - 1) * kWave + lane;
+  const int rb = L / kSxTile, c = L - rb * kSxTile;
+  constexpr int kRowStep = kSxLoadLanes / kSxTile;
+  const UgkExpfAddends add = ugk_expf_addends_vgpr();
+  float reg[kSxDepth][kSxSlots];
+  auto load_tile = [&](int t, int k) {
+    const int col = min(t * kSxTile + c, V - 1);
+#pragma unroll
+    for (int sl = 0; sl < kSxSlots; sl++) {
+      const int row = min(r0 + rb + kRowStep * sl, rows - 1);
+      reg[k][sl] = logits[(size_t)row * V + col];
+    }
+  };
+  auto store_tile = [&](int t, int k) {
+    float *const T = tile[t & 1];
+    const bool in = t * kSxTile + c < V;
+#pragma unroll
+    for (int sl = 0; sl < kSxSlots; sl++) {
+      const int r = rb + kRowStep * sl;
+      T[r * kSxPitch + c] = in ? ugk_dev_expf_nooverflow(reg[k][sl] - smax[r], UgkExp2Lds{tab}, add) : 0.0f;
+    }
+  };
+  float acc[1] = {0.0f};
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < kSxDepth; k++)
+      if (k < nt) load_tile(k, k);
+  }
+  for (int t0 = 0; t0 < nt; t0 += kSxDepth) {
+#pragma unroll
+    for (int k = 0; k < kSxDepth; k++) {
+      const int t = t0 + k;
+      if (t >= nt) break;  // the same in every thread
+      if (wave > 0) {
+        store_tile(t, k);
+        if (t + kSxDepth < nt) load_tile(t + kSxDepth, k);
+      }
+      // tile t is staged in buffer t & 1; the buffer written next round was
+      // last read before this barrier
+      __syncthreads();
+      if (wave == 0) {
+        const float4 *t4[1] = {reinterpret_cast<const float4 *>(tile[t & 1] + (lane & (kSxRows - 1)) * kSxPitch)};
+        chain_add4<1, kSxBatch>(acc, t4, kSxTile / 4);
+      }
+    }
+  }
+  if (wave == 0 && lane < kSxRows && r0 + lane < rows) stats[r0 + lane] = make_float2(smax[lane], acc[0]);
+}
+
+// grid: rows x chunks of kBlock * kSxNormPer logits, the chunks of a row adjacent
+__global__ __launch_bounds__(kBlock) void k_softmax_norm_rows(float *__restrict__ losses, float *__restrict__ probs,
+                                                              const float *__restrict__ logits,
+                                                              const int *__restrict__ targets,
+                                                              const float2 *__restrict__ stats, int V, int chunks) {
+  __shared__ uint64_t tab[32];
+  ugk_exp2_stage(tab);
+  __syncthreads();
+  const int row = (int)(blockIdx.x / (unsigned)chunks);
+  const int v0 = (int)(blockIdx.x - (unsigned)row * chunks) * (kBlock * kSxNormPer) + threadIdx.x;
+  const size_t base = (size_t)row * V;
+  const float2 st = stats[row];
+  const int tgt = targets[row];
+  float x[kSxNormPer];
+#pragma unroll
+  for (int k = 0; k < kSxNormPer; k++) {
+    const int v = v0 + k * kBlock;
+    x[k] = v < V ? ld_nt(logits + base + v) : 0.0f;
+  }
+  const UgkExpfAddends add = ugk_expf_addends_vgpr();
+  uint32_t lo = 0xffffffffu;
+#pragma unroll
+  for (int k = 0; k < kSxNormPer; k++) {
+    x[k] = v0 + k * kBlock < V ? ugk_dev_expf_nooverflow(x[k] - st.x, UgkExp2Lds{tab}, add) : 0.0f;
+    lo = min(lo, ugk_div_recip_key(x[k]));
+  }
+  // e / sum: the reciprocal form where it is the IEEE quotient (a sum in
+  // [1, 2^16], every e of the thread +0, NaN or in [2^-86, 1]), else division
+  const float y = 1.0f / st.y;
+  auto store = [&](auto recip) {
+#pragma unroll
+    for (int k = 0; k < kSxNormPer; k++) {
+      const int v = v0 + k * kBlock;
+      if (v < V) {
+        const float p = decltype(recip)::value ? ugk_div_recip(x[k], st.y, y) : x[k] / st.y;
+        st_nt(probs + base + v, p);
+        if (v == tgt) losses[row] = neg_logf(p);
+      }
+    }
+  };
+  if (st.y >= 1.0f && st.y <= 0x1p16f && lo >= kUgkDivRecipKeyMin)
+    store(std::true_type{});
+  else
+    store(std::false_type{});
+}
+
+std::atomic<int> g_softmax_exact{0};
+
 template <int kThreads, int kPer>
 void launch_rows(float *losses, float *probs, const float *logits, const int *targets, int rows, int V) {
   hipLaunchKernelGGL((k_softmax_xent<kThreads, kPer>), dim3(rows), dim3(kThreads), 0, stream(), losses, probs,
@@ -410,11 +571,28 @@ void launch_rows(float *losses, float *probs, const float *logits, const int *ta
 constexpr int kSplitSlots = 768 * (42 + 25);
 constexpr int kSplitMaxV = kSplitSlots - 63;
 
-size_t softmax_scratch(int rows, int V) { return V > kSplitMaxV ? (size_t)rows * sizeof(float2) : 0; }
+// The row statistics of the two-pass form and of the exact mode (whichever
+// form the calls take, so that a workspace sized once serves both).
+size_t softmax_scratch(int rows, int V) { return V > 0 ? (size_t)rows * sizeof(float2) : 0; }
+
+void set_softmax_exact(int on) { g_softmax_exact.store(on ? 1 : 0); }
+int softmax_exact() { return g_softmax_exact.load(); }
 
 int launch_softmax_crossentropy(float *losses, float *probs, const float *logits, const int *targets, int rows,
                                 int V) {
   if (rows == 0 || V == 0) return 0;
+  if (softmax_exact()) {
+    float2 *stats = static_cast<float2 *>(workspace(kRegSoftmax, softmax_scratch(rows, V)));
+    if (!stats) return UGK_ENOMEM;
+    hipLaunchKernelGGL(k_softmax_rowmax, dim3(grid_for((size_t)rows, kSxMaxWaves)), dim3(kSxMaxWaves * kWave), 0,
+                       stream(), stats, logits, rows, V);
+    hipLaunchKernelGGL(k_softmax_sum_exact, dim3(grid_for((size_t)rows, kSxRows)), dim3(kSxThreads), 0, stream(),
+                       stats, logits, rows, V);
+    const int chunks = (int)grid_for((size_t)V, (size_t)kBlock * kSxNormPer);
+    hipLaunchKernelGGL(k_softmax_norm_rows, dim3((unsigned)((size_t)rows * chunks)), dim3(kBlock), 0, stream(),
+                       losses, probs, logits, targets, stats, V, chunks);
+    return check_launch("softmax_crossentropy (exact)");
+  }
   // a row takes V + 63 slots at most (the alignment skew)
   const int W = V + 63;
   if (W <= 64 * 2) launch_rows<64, 2>(losses, probs, logits, targets, rows, V);
@@ -423,7 +601,7 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
   else if (W <= 4096) launch_rows<256, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 16384) launch_rows<1024, 16>(losses, probs, logits, targets, rows, V);
   else if (W <= 32768) launch_rows<1024, 32>(losses, probs, logits, targets, rows, V);
-  else if (W <= kSplitSlots) {  // 42 slots per thread in registers, 25 in LDS: two rows per CU
+  else if (V <= kSplitMaxV) {  // 42 slots per thread in registers, 25 in LDS: two rows per CU
     static_assert(32768 - 63 >= 768 * 42, "the split kernel's register slots must lie inside every row it takes");
     hipLaunchKernelGGL((k_softmax_xent_split<768, 42, 25>), dim3(rows), dim3(768), 0, stream(), losses, probs,
                        logits, targets, V);

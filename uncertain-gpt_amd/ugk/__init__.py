@@ -29,7 +29,7 @@ __all__ = [
     "bayes_backward_philox", "kl_forward", "kl_backward", "adamw_update", "bbb_step_fused",
     "Loader", "loader_count", "ckpt_path", "ckpt_save", "ckpt_load",
     "set_stream", "synchronize", "reserve", "scratch_bytes", "reserve_config", "workspace_bytes",
-    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_kl_exact", "kl_exact", "set_layernorm_exact", "layernorm_exact", "set_encoder_exact", "encoder_exact",
+    "set_workspace", "set_sync_checks", "op_timer_start", "op_timer_read", "set_gelu_exact", "gelu_exact", "set_philox_exact", "philox_exact", "set_kl_exact", "kl_exact", "set_softmax_exact", "softmax_exact", "set_layernorm_exact", "layernorm_exact", "set_encoder_exact", "encoder_exact",
     "Config", "DenseOps", "param_count", "act_count", "gpt2_layers_forward",
     "gpt2_layers_backward", "gpt2_layers_backward_zeroed", "version",
 ]
@@ -111,6 +111,8 @@ _SIGS = {
     "ugk_get_philox_exact": [],
     "ugk_set_kl_exact": [_i],
     "ugk_get_kl_exact": [],
+    "ugk_set_softmax_exact": [_i],
+    "ugk_get_softmax_exact": [],
     "ugk_set_layernorm_exact": [_i],
     "ugk_get_layernorm_exact": [],
     "ugk_last_error": [],
@@ -508,6 +510,17 @@ def set_kl_exact(exact: bool) -> None:
 
 def kl_exact() -> bool:
     return bool(lib.ugk_get_kl_exact())
+
+
+def set_softmax_exact(exact: bool) -> None:
+    """Row sum inside softmax_crossentropy: False (default) a fixed tree (probabilities within float
+    rounding of train_bnn.c's); True train_bnn.c's serial order, every probability and loss
+    bit-identical to it."""
+    _check(lib.ugk_set_softmax_exact(1 if exact else 0))
+
+
+def softmax_exact() -> bool:
+    return bool(lib.ugk_get_softmax_exact())
 
 
 def set_layernorm_exact(exact: bool) -> None:
