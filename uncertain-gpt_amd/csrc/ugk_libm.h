@@ -374,7 +374,7 @@ struct UgkLogfEntry {
 };
 
 #if defined(__HIPCC__)
-static __constant__ double ugk_logf_tab_dev[32] = UGK_LOGF_TABLE;
+static __constant__ __align__(16) double ugk_logf_tab_dev[32] = UGK_LOGF_TABLE;  // read as double2
 #endif
 static const double ugk_logf_tab_host[32] = UGK_LOGF_TABLE;
 

@@ -510,7 +510,9 @@ __global__ __launch_bounds__(kSxThreads) void k_softmax_sum_exact(float2 *__rest
   if (wave == 0 && lane < kSxRows && r0 + lane < rows) stats[r0 + lane] = make_float2(smax[lane], acc[0]);
 }
 
-// grid: rows x chunks of kBlock * kSxNormPer logits, the chunks of a row adjacent
+// grid: rows x chunks of kBlock * kSxNormPer logits, the chunks of a row
+// adjacent and laid from the 256-byte boundary of probs at or before the
+// row's start, so that each wavefront's store covers whole lines
 __global__ __launch_bounds__(kBlock) void k_softmax_norm_rows(float *__restrict__ losses, float *__restrict__ probs,
                                                               const float *__restrict__ logits,
                                                               const int *__restrict__ targets,
@@ -519,21 +521,23 @@ __global__ __launch_bounds__(kBlock) void k_softmax_norm_rows(float *__restrict_
   ugk_exp2_stage(tab);
   __syncthreads();
   const int row = (int)(blockIdx.x / (unsigned)chunks);
-  const int v0 = (int)(blockIdx.x - (unsigned)row * chunks) * (kBlock * kSxNormPer) + threadIdx.x;
   const size_t base = (size_t)row * V;
+  const int skew = (int)((reinterpret_cast<uintptr_t>(probs + base) >> 2) & 63);
+  const int v0 = (int)(blockIdx.x - (unsigned)row * chunks) * (kBlock * kSxNormPer) + (int)threadIdx.x - skew;
   const float2 st = stats[row];
   const int tgt = targets[row];
   float x[kSxNormPer];
 #pragma unroll
   for (int k = 0; k < kSxNormPer; k++) {
     const int v = v0 + k * kBlock;
-    x[k] = v < V ? ld_nt(logits + base + v) : 0.0f;
+    x[k] = (unsigned)v < (unsigned)V ? ld_nt(logits + base + v) : 0.0f;
   }
   const UgkExpfAddends add = ugk_expf_addends_vgpr();
   uint32_t lo = 0xffffffffu;
 #pragma unroll
   for (int k = 0; k < kSxNormPer; k++) {
-    x[k] = v0 + k * kBlock < V ? ugk_dev_expf_nooverflow(x[k] - st.x, UgkExp2Lds{tab}, add) : 0.0f;
+    x[k] = (unsigned)(v0 + k * kBlock) < (unsigned)V ? ugk_dev_expf_nooverflow(x[k] - st.x, UgkExp2Lds{tab}, add)
+                                                      : 0.0f;
     lo = min(lo, ugk_div_recip_key(x[k]));
   }
   // e / sum: the reciprocal form where it is the IEEE quotient (a sum in
@@ -543,7 +547,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_norm_rows(float *__restrict_
 #pragma unroll
     for (int k = 0; k < kSxNormPer; k++) {
       const int v = v0 + k * kBlock;
-      if (v < V) {
+      if ((unsigned)v < (unsigned)V) {
         const float p = decltype(recip)::value ? ugk_div_recip(x[k], st.y, y) : x[k] / st.y;
         st_nt(probs + base + v, p);
         if (v == tgt) losses[row] = neg_logf(p);
@@ -588,7 +592,7 @@ int launch_softmax_crossentropy(float *losses, float *probs, const float *logits
                        stream(), stats, logits, rows, V);
     hipLaunchKernelGGL(k_softmax_sum_exact, dim3(grid_for((size_t)rows, kSxRows)), dim3(kSxThreads), 0, stream(),
                        stats, logits, rows, V);
-    const int chunks = (int)grid_for((size_t)V, (size_t)kBlock * kSxNormPer);
+    const int chunks = (int)grid_for((size_t)V + 63, (size_t)kBlock * kSxNormPer);  // the skew: up to 63
     hipLaunchKernelGGL(k_softmax_norm_rows, dim3((unsigned)((size_t)rows * chunks)), dim3(kBlock), 0, stream(),
                        losses, probs, logits, targets, stats, V, chunks);
     return check_launch("softmax_crossentropy (exact)");
