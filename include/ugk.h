@@ -27,8 +27,9 @@
  * The library never allocates inside a kernel. A few entry points need device
  * workspace beyond their arguments: the LayerNorm backward's partial column
  * sums (one slot per call, 2L+1 for the step driver), the encoder backward's
- * bucket state, the KL total's partial sums and the long-row softmax's row
- * statistics, each in a region of its own. By default the library allocates
+ * bucket state, the KL total's partial sums and the softmax's row
+ * statistics (rows too long for one workgroup, and the exact mode's), each in
+ * a region of its own. By default the library allocates
  * a region on the first call that needs it and grows it, after waiting for
  * the device, when a larger shape arrives; ugk_reserve / ugk_reserve_config
  * allocate everything up front, after which calls at those shapes neither
