@@ -391,9 +391,9 @@ int ugk_diag_math_mismatch(int fn, unsigned lo, unsigned long long count,
                            unsigned long long *mismatches, unsigned *first);
 /* out[i] = f(in[i]) on the device; variant 0 = the kernels' math, 1 = the
  * line-by-line restatement. fn: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf,
- * 4 softplus, 5 logf and 6 cosf (variant 0 glibc's, as the glibc-exact
- * form of the Philox ops' Box-Muller transform takes them: on normal x > 0
- * and |x| < 120, the device library's elsewhere; variant 1 the device
+ * 4 softplus, 5 logf and 6 cosf (variant 0 glibc's, as the loss and the
+ * glibc-exact Box-Muller transform take them: logf on every input, cosf on
+ * |x| < 120 and the device library's elsewhere; variant 1 the device
  * library's), 7 sqrtf, 8 GELU, 9 GELU derivative; 10+s, 20+s, 30+s tanhf,
  * log1pf, expm1f with division sequence s. */
 int ugk_diag_math_eval(int fn, int variant, float *out, const float *in, size_t n);

@@ -121,12 +121,14 @@ def test_device_logf_cosf_over_the_u01_domain(gpu, oracle):
 
 @pytest.mark.parametrize("fn", ["logf", "cosf"])
 def test_device_logf_cosf_strided_over_their_domains(gpu, oracle, fn):
-    """The restated logf on every 61st normal float x > 0 and cosf on every 61st float of |x| < 120
-    (the domains of the restatements, which the CPU checks against glibc on every input) equal the
-    host glibc on the device too."""
+    """The restated logf on every 61st bit pattern (zero, subnormal, negative, infinite and NaN
+    inputs included: the softmax loss takes it on any probability) and cosf on every 61st float of
+    |x| < 120 (the domains of the restatements, which the CPU checks against glibc on every input)
+    equal the host glibc on the device too."""
     if fn == "logf":
-        lo, hi = 0x00800000, 0x7F800000
-        x = np.arange(lo, hi, 61, dtype=np.uint64).astype(np.uint32).view(np.float32)
+        x = np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
+        x = np.concatenate([x, np.array([0, 0x80000000, 1, 0x007FFFFF, 0x7F800000, 0xFF800000, 0x7FC00000],
+                                        np.uint32)]).view(np.float32)
         want = oracle.logf(x)
     else:
         top = int(np.array([120.0], np.float32).view(np.uint32)[0])

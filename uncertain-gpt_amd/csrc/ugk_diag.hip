@@ -11,10 +11,9 @@ namespace ugk {
 namespace {
 
 // fn codes: 0 expf, 1 log1pf, 2 expm1f, 3 tanhf, 4 softplus (the kernels'
-// math); 5 logf, 6 cosf (evaluation only: the Box-Muller transform's glibc
-// restatements, ugk_logf_normal on normal finite x > 0 and ugk_cosf_small on
-// |x| < 120, the device library's elsewhere; variant 1 the device library's
-// everywhere), 7 sqrtf (its reference: the double square
+// math); 5 logf, 6 cosf (evaluation only: the glibc restatements, ugk_logf
+// on every input and ugk_cosf_small on |x| < 120, the device library's cosf
+// elsewhere; variant 1 the device library's everywhere), 7 sqrtf (its reference: the double square
 // root rounded to float, which is the correctly rounded result); 8 GELU and
 // 9 its derivative as the GELU kernels evaluate them (reference: the same
 // expressions over ugk_tanhf);
@@ -66,7 +65,7 @@ __device__ __forceinline__ float kernel_math(float x, const uint64_t *tab) {
   if (FN == 2) return ugk_dev_expm1f(x);
   if (FN == 3) return ugk_dev_tanhf(x);
   if (FN == 4) return ugk_dev_softplusf_lds(x, tab);
-  if (FN == 5) return (x >= 0x1p-126f && x <= 0x1.fffffep127f) ? ugk_logf_normal(x) : logf(x);
+  if (FN == 5) return ugk_logf(x);
   if (FN == 6) return fabsf(x) < 120.0f ? ugk_cosf_small(x) : cosf(x);
   if (FN == 7) return sqrtf(x);
   if (FN == 8) return ugk_dev_gelu(x);
