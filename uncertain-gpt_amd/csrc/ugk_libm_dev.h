@@ -457,8 +457,6 @@ __device__ __forceinline__ float ugk_fast_exp_t(float x) {
   return (kKeepOverflow && r != r) ? e : r;
 }
 
-__device__ __forceinline__ float ugk_fast_exp(float x) { return ugk_fast_exp_t<true, true>(x); }
-
 // softplus(x) = log1p(e^x) (train_bnn.c:814-816's formula; x for x > 20 as
 // there). log1p(e): below e = 1/16 its series to e^6 (the remainder is below
 // e^7/7, a tenth of an ulp); above, Goldberg's form log(u) e / (u - 1)
