@@ -376,7 +376,7 @@ def main():
             f"{exact_forms['step (every exact mode)']['GBps']:.1f} GB/s on the reference's bytes")
 
     # ---- each op inside the step: a HIP event pair recorded by the dispatch of
-    # every kernel the step driver issues (ugk_op_timer; the three-kernel
+    # every kernel the step driver issues (ugk_op_timer_start/_read; the three-kernel
     # encoder backward is bracketed by two event records instead), over
     # --op-steps further steps; materialize is bracketed here by two records
     N = B * T * C

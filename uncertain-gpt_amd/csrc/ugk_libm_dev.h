@@ -503,10 +503,6 @@ __device__ __forceinline__ float ugk_fast_sigmoid(float x) {
   return q;
 }
 
-__device__ __forceinline__ float ugk_dev_softplusf(float x) {
-  return x > 20.0f ? x : ugk_dev_log1pf(ugk_expf(x));
-}
-
 // The expf table of ugk_libm.h, read from a copy in LDS: a per-lane lookup in
 // local memory instead of a dependent global load on every element's path.
 struct UgkExp2Lds {
